@@ -1,0 +1,10 @@
+"""MI355X-native (gfx950) Kimi Delta Attention core.
+
+Drop-in replacements for the reference's ``kimi_linear.kda_chunkwise`` and
+``kimi_linear.kda_recurrent`` (kimi_linear/__init__.py:9), running hand-written
+HIP kernels behind the C ABI in ``include/kda_hip.h``.
+"""
+
+from .kda import FP16_MAX_SAFE, KdaError, kda_chunkwise, kda_recurrent  # noqa: F401
+
+__all__ = ["kda_chunkwise", "kda_recurrent", "KdaError", "FP16_MAX_SAFE"]

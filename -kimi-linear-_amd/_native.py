@@ -1,0 +1,93 @@
+"""ctypes binding of ``libkda_hip.so`` (C ABI declared in include/kda_hip.h).
+
+The library is loaded lazily on first use and never replaced by anything else:
+if it is missing or was built for another ABI version, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
+ABI_VERSION = 1
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+
+STATUS_OK = 0
+STATUS_BAD_SHAPE = 2
+STATUS_UNSUPPORTED = 4
+
+_i64x3 = ctypes.c_int64 * 3
+
+
+class KdaFwdArgs(ctypes.Structure):
+    """Mirror of ``struct kda_fwd_args`` (include/kda_hip.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int64), ("T", ctypes.c_int64), ("H", ctypes.c_int64),
+        ("K", ctypes.c_int64), ("V", ctypes.c_int64),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("g", ctypes.c_void_p), ("beta", ctypes.c_void_p),
+        ("q_stride", _i64x3), ("k_stride", _i64x3), ("v_stride", _i64x3),
+        ("g_stride", _i64x3), ("beta_stride", _i64x3),
+        ("qkv_dtype", ctypes.c_int32), ("g_dtype", ctypes.c_int32), ("beta_dtype", ctypes.c_int32),
+        ("state_in", ctypes.c_void_p), ("state_in_dtype", ctypes.c_int32),
+        ("state_out", ctypes.c_void_p), ("state_out_dtype", ctypes.c_int32),
+        ("o", ctypes.c_void_p),
+        ("scale", ctypes.c_float),
+        ("clamp_fp16_out", ctypes.c_int32),
+        ("chunk_size", ctypes.c_int64),
+    ]
+
+
+EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_status_str", "kda_abi_version")
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeLibraryError(RuntimeError):
+    """libkda_hip.so is missing, unloadable or of the wrong ABI version."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the native library, raising if it is unusable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise NativeLibraryError(
+                f"{LIB_PATH} not found: build it with __graft_entry__.build() "
+                "(hipcc, gfx950) before using the HIP KDA kernels")
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:
+            raise NativeLibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+        for name in EXPORTED_SYMBOLS:
+            if not hasattr(lib, name):
+                raise NativeLibraryError(f"{LIB_PATH} does not export {name}")
+        lib.kda_chunkwise_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_void_p]
+        lib.kda_chunkwise_fwd.restype = ctypes.c_int
+        lib.kda_recurrent_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_void_p]
+        lib.kda_recurrent_fwd.restype = ctypes.c_int
+        lib.kda_status_str.argtypes = [ctypes.c_int]
+        lib.kda_status_str.restype = ctypes.c_char_p
+        lib.kda_abi_version.argtypes = []
+        lib.kda_abi_version.restype = ctypes.c_int
+        version = lib.kda_abi_version()
+        if version != ABI_VERSION:
+            raise NativeLibraryError(
+                f"{LIB_PATH} has ABI version {version}, this wrapper expects {ABI_VERSION}; rebuild it")
+        _lib = lib
+        return lib
+
+
+def status_str(code: int) -> str:
+    return load().kda_status_str(int(code)).decode()

@@ -1,0 +1,86 @@
+// C ABI of the KDA core: argument validation and dispatch to the gfx950 kernels.
+// Declared in include/kda_hip.h.  No C++ exception crosses this boundary and no
+// call allocates, frees or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kda_hip.h"
+#include "kda_launch.h"
+
+namespace {
+
+bool dtype_ok(int32_t d) {
+    return d == KDA_DTYPE_F32 || d == KDA_DTYPE_F16 || d == KDA_DTYPE_BF16;
+}
+
+int64_t elem_size(int32_t d) { return d == KDA_DTYPE_F32 ? 4 : 2; }
+
+// Checks shared by both entry points.
+int validate_common(const kda_fwd_args* a) {
+    if (a == nullptr) return KDA_ERR_NULL_POINTER;
+    if (a->B < 0 || a->T < 0 || a->H < 0 || a->K <= 0 || a->V <= 0) return KDA_ERR_BAD_SHAPE;
+    if (!dtype_ok(a->qkv_dtype) || !dtype_ok(a->g_dtype) || !dtype_ok(a->beta_dtype) ||
+        !dtype_ok(a->state_out_dtype) || (a->state_in && !dtype_ok(a->state_in_dtype)))
+        return KDA_ERR_BAD_DTYPE;
+    const bool have_heads = a->B > 0 && a->H > 0;
+    if (have_heads && a->state_out == nullptr) return KDA_ERR_NULL_POINTER;
+    if (have_heads && a->T > 0 &&
+        (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->o))
+        return KDA_ERR_NULL_POINTER;
+    if (have_heads && a->state_in) {
+        const int64_t n = a->B * a->H * a->K * a->V;
+        const auto in0 = reinterpret_cast<uintptr_t>(a->state_in);
+        const auto in1 = in0 + static_cast<uintptr_t>(n * elem_size(a->state_in_dtype));
+        const auto out0 = reinterpret_cast<uintptr_t>(a->state_out);
+        const auto out1 = out0 + static_cast<uintptr_t>(n * elem_size(a->state_out_dtype));
+        if (in0 < out1 && out0 < in1) return KDA_ERR_ALIAS;
+    }
+    return KDA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kda_recurrent_fwd(const kda_fwd_args* args, void* stream) {
+    const int st = validate_common(args);
+    if (st != KDA_OK) return st;
+    if (args->B == 0 || args->H == 0) return KDA_OK;
+    if (!kda::recurrent_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
+    if (args->B * args->H * args->V / 32 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream));
+}
+
+int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) {
+    const int st = validate_common(args);
+    if (st != KDA_OK) return st;
+    if (args->chunk_size <= 0 || args->T % args->chunk_size != 0) return KDA_ERR_BAD_SHAPE;
+    if (args->B == 0 || args->H == 0) return KDA_OK;
+    if (args->T == 0) {
+        // No tokens: the result is the initial state converted to the output
+        // dtype (or zeros); the recurrence kernel with an empty token loop does it.
+        if (!kda::recurrent_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
+        return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream));
+    }
+    if (!kda::chunkwise_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
+    if (args->B * args->H * args->V / 16 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    return kda::chunkwise_launch(*args, static_cast<hipStream_t>(stream));
+}
+
+const char* kda_status_str(int status) {
+    switch (status) {
+        case KDA_OK: return "ok";
+        case KDA_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case KDA_ERR_BAD_SHAPE: return "invalid shape (negative size, T not a multiple of chunk_size, or grid too large)";
+        case KDA_ERR_BAD_DTYPE: return "unsupported dtype code";
+        case KDA_ERR_UNSUPPORTED: return "no kernel for these head dimensions";
+        case KDA_ERR_ALIAS: return "state_out overlaps state_in";
+        case KDA_ERR_LAUNCH: return "kernel launch failed";
+        default: return "unknown kda_status";
+    }
+}
+
+int kda_abi_version(void) { return KDA_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,94 @@
+// Shared device helpers for the gfx950 KDA kernels: element loads/stores for
+// the three boundary dtypes, fp16 hi/lo operand splitting and MFMA vector types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kda_hip.h"
+
+namespace kda {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr float kFp16MaxSafe = 60000.0f;   // kimi_linear/fp16.py:97
+
+// ---- scalar element access for a runtime dtype code ----------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+    switch (dtype) {
+        case KDA_DTYPE_F16: return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+        case KDA_DTYPE_BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+        default: return static_cast<const float*>(p)[i];
+    }
+}
+
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float x) {
+    switch (dtype) {
+        case KDA_DTYPE_F16: static_cast<_Float16*>(p)[i] = static_cast<_Float16>(x); break;
+        case KDA_DTYPE_BF16: static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(x); break;
+        default: static_cast<float*>(p)[i] = x; break;
+    }
+}
+
+// ---- compile-time typed access (hot loops) --------------------------------
+struct bf16_t { uint16_t bits; };
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static __device__ __forceinline__ float ld(const float* p) { return *p; }
+    static __device__ __forceinline__ void st(float* p, float x) { *p = x; }
+    static constexpr int code = KDA_DTYPE_F32;
+};
+template <> struct Elem<_Float16> {
+    static __device__ __forceinline__ float ld(const _Float16* p) { return static_cast<float>(*p); }
+    static __device__ __forceinline__ void st(_Float16* p, float x) { *p = static_cast<_Float16>(x); }
+    static constexpr int code = KDA_DTYPE_F16;
+};
+template <> struct Elem<bf16_t> {
+    static __device__ __forceinline__ float ld(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
+    static __device__ __forceinline__ void st(bf16_t* p, float x) { p->bits = f32_to_bf16_bits(x); }
+    static constexpr int code = KDA_DTYPE_BF16;
+};
+
+// Clamp to +-60000 keeping NaN (the comparisons are false for NaN).
+__device__ __forceinline__ float clamp_fp16_safe(float x) {
+    return x > kFp16MaxSafe ? kFp16MaxSafe : (x < -kFp16MaxSafe ? -kFp16MaxSafe : x);
+}
+
+// exp(x) through the hardware base-2 exponential.
+__device__ __forceinline__ float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// fp16 hi/lo split: x ~= hi + lo with |x - hi - lo| ~ 2^-22 |x|.
+__device__ __forceinline__ void split_h(float x, _Float16& hi, _Float16& lo) {
+    hi = static_cast<_Float16>(x);
+    lo = static_cast<_Float16>(x - static_cast<float>(hi));
+}
+
+// ---- MFMA wrappers (gfx950) ----------------------------------------------
+// 16x16 output tile, f32 accumulate.  Lane l holds A row (l % 16) and B column
+// (l % 16); lane group g = l / 16 supplies the k slots; the accumulator holds
+// D[4g + j][l % 16] in slot j.
+__device__ __forceinline__ f4 mfma16x16x16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace kda

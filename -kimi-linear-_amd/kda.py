@@ -1,0 +1,184 @@
+"""Drop-in ``kda_chunkwise`` / ``kda_recurrent`` backed by the gfx950 HIP kernels.
+
+Same signatures and semantics as the reference kernels
+(``kimi_linear/kda.py:58-59`` and ``kimi_linear/kda.py:188``):
+
+* ``q, k: [B, T, H, K]``, ``v: [B, T, H, V]``, ``g: [B, T, H, K]`` (log decay),
+  ``beta: [B, T, H]``; the optional state is ``[B, H, K, V]``.
+* q is scaled by ``K**-0.5`` inside (``kda.py:132,141,199``).
+* Gates and the state may come in any of fp32 / fp16 / bf16; they are read in
+  that dtype and computed in fp32.
+* Inputs are never modified; ``o`` is a new ``[B, T, H, V]`` tensor in
+  ``v.dtype`` and the state a new ``[B, H, K, V]`` tensor in
+  ``state_dtype or v.dtype`` (``kda.py:185,219``).
+* ``kda_recurrent`` clamps an fp16 ``o`` to +-60000 (``kda.py:217-218``);
+  ``kda_chunkwise`` does not.
+* ``kda_chunkwise`` requires ``T % chunk_size == 0`` (``kda.py:109``); the
+  reference fails in ``reshape`` with a RuntimeError, this wrapper raises
+  :class:`KdaError`, which is both a ValueError and a RuntimeError.
+  ``chunk_size`` has no other effect (the maths is chunk-size invariant) and
+  ``tile_size`` is accepted and ignored (a memory knob, ``kda.py:101-103``).
+
+Differences that are deliberate:
+
+* HIP tensors only.  There is no CPU path and no fallback: CPU tensors, a
+  missing ``libkda_hip.so`` or an unsupported head size raise.
+* Forward only: inputs that require grad under grad mode raise (the reference
+  is differentiable through autograd; a native backward is future work).
+
+Every call is asynchronous on the current stream, allocates only through the
+torch caching allocator and never synchronises, so it can be captured in a
+``torch.cuda.CUDAGraph`` (the reference captures ``kda_recurrent`` at
+``kimi_linear/graph_decode.py:285-287``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+
+FP16_MAX_SAFE = 60000.0     # kimi_linear/fp16.py:97
+
+_DTYPE_CODE = {
+    torch.float32: _native.DTYPE_F32,
+    torch.float16: _native.DTYPE_F16,
+    torch.bfloat16: _native.DTYPE_BF16,
+}
+
+
+class KdaError(ValueError, RuntimeError):
+    """Invalid arguments or a failed native call."""
+
+
+def _check_tensor(name, x):
+    if not isinstance(x, torch.Tensor):
+        raise KdaError(f"{name} must be a torch.Tensor, got {type(x).__name__}")
+
+
+def _as_kernel_input(x: torch.Tensor) -> torch.Tensor:
+    """A view whose last dimension is contiguous (copying only if it is not)."""
+    if x.dim() > 0 and x.shape[-1] > 1 and x.stride(-1) != 1:
+        return x.contiguous()
+    return x
+
+
+def _float_or_f32(x: torch.Tensor) -> torch.Tensor:
+    return x if x.dtype in _DTYPE_CODE else x.float()
+
+
+def _strides3(x: torch.Tensor):
+    return (ctypes.c_int64 * 3)(*x.stride()[:3])
+
+
+def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
+    for name, x in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
+        _check_tensor(name, x)
+    if state is not None:
+        _check_tensor("state", state)
+    if q.dim() != 4 or v.dim() != 4:
+        raise KdaError(f"q and v must be [B, T, H, D]; got q {tuple(q.shape)}, v {tuple(v.shape)}")
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if tuple(k.shape) != (B, T, H, K) or tuple(g.shape) != (B, T, H, K):
+        raise KdaError(f"k and g must match q's shape {tuple(q.shape)}; "
+                       f"got k {tuple(k.shape)}, g {tuple(g.shape)}")
+    if tuple(v.shape[:3]) != (B, T, H):
+        raise KdaError(f"v must be [B, T, H, V] = [{B}, {T}, {H}, V]; got {tuple(v.shape)}")
+    if tuple(beta.shape) != (B, T, H):
+        raise KdaError(f"beta must be [B, T, H] = [{B}, {T}, {H}]; got {tuple(beta.shape)}")
+    if state is not None and tuple(state.shape) != (B, H, K, V):
+        raise KdaError(f"state must be [B, H, K, V] = [{B}, {H}, {K}, {V}]; got {tuple(state.shape)}")
+    if kind == "chunkwise":
+        if chunk_size <= 0:
+            raise KdaError(f"chunk_size must be positive, got {chunk_size}")
+        if T % chunk_size != 0:
+            raise KdaError(f"T={T} must be a multiple of chunk_size={chunk_size} "
+                           "(the caller splits the body and the tail)")
+    if K <= 0 or V <= 0:
+        raise KdaError(f"head dims must be positive, got K={K}, V={V}")
+
+    dev = q.device
+    tensors = [q, k, v, g, beta] + ([state] if state is not None else [])
+    if dev.type != "cuda" or any(x.device != dev for x in tensors):
+        raise KdaError("the HIP KDA kernels need all inputs on one HIP device "
+                       f"(got {', '.join(str(x.device) for x in tensors)}); there is no CPU path")
+    if torch.is_grad_enabled() and any(x.requires_grad for x in tensors):
+        raise KdaError("the HIP KDA kernels are forward-only: call under torch.no_grad() "
+                       "or detach the inputs")
+    if v.dtype not in _DTYPE_CODE:
+        raise KdaError(f"v must be float32, float16 or bfloat16, got {v.dtype}")
+
+    out_dtype = v.dtype
+    s_dtype = state_dtype or out_dtype
+    if not isinstance(s_dtype, torch.dtype) or not s_dtype.is_floating_point:
+        raise KdaError(f"state_dtype must be a floating dtype, got {state_dtype!r}")
+    kernel_s_dtype = s_dtype if s_dtype in _DTYPE_CODE else torch.float32
+
+    o = torch.empty(B, T, H, V, device=dev, dtype=out_dtype)
+    s_out = torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
+    if B * H == 0:
+        if state is not None:
+            s_out.copy_(state)
+        return o, s_out.to(s_dtype)
+
+    qk_dtype = out_dtype
+    q = _as_kernel_input(q if q.dtype == qk_dtype else q.to(qk_dtype))
+    k = _as_kernel_input(k if k.dtype == qk_dtype else k.to(qk_dtype))
+    v = _as_kernel_input(v)
+    g = _as_kernel_input(_float_or_f32(g))
+    beta = _float_or_f32(beta)
+    if state is not None:
+        state = _float_or_f32(state)
+        if not state.is_contiguous():
+            state = state.contiguous()
+
+    args = _native.KdaFwdArgs()
+    args.B, args.T, args.H, args.K, args.V = B, T, H, K, V
+    args.q, args.k, args.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    args.g, args.beta = g.data_ptr(), beta.data_ptr()
+    args.q_stride, args.k_stride, args.v_stride = _strides3(q), _strides3(k), _strides3(v)
+    args.g_stride, args.beta_stride = _strides3(g), _strides3(beta)
+    args.qkv_dtype = _DTYPE_CODE[qk_dtype]
+    args.g_dtype = _DTYPE_CODE[g.dtype]
+    args.beta_dtype = _DTYPE_CODE[beta.dtype]
+    args.state_in = state.data_ptr() if state is not None else None
+    args.state_in_dtype = _DTYPE_CODE[state.dtype] if state is not None else _native.DTYPE_F32
+    args.state_out = s_out.data_ptr()
+    args.state_out_dtype = _DTYPE_CODE[kernel_s_dtype]
+    args.o = o.data_ptr()
+    args.scale = float(K) ** -0.5
+    args.clamp_fp16_out = 1 if kind == "recurrent" else 0
+    args.chunk_size = chunk_size if kind == "chunkwise" else 1
+
+    lib = _native.load()
+    fn = lib.kda_chunkwise_fwd if kind == "chunkwise" else lib.kda_recurrent_fwd
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        status = fn(ctypes.byref(args), ctypes.c_void_p(stream))
+    if status != _native.STATUS_OK:
+        raise KdaError(f"kda_{kind}_fwd failed: {_native.status_str(status)} "
+                       f"(B={B}, T={T}, H={H}, K={K}, V={V})")
+    if kernel_s_dtype != s_dtype:
+        s_out = s_out.to(s_dtype)
+    return o, s_out
+
+
+def kda_chunkwise(q, k, v, g, beta, initial_state=None, chunk_size=64, tile_size=0,
+                  state_dtype=None):
+    """Chunkwise KDA forward on gfx950 (signature of kimi_linear/kda.py:58-59).
+
+    Returns ``(o [B, T, H, V] in v.dtype, state [B, H, K, V] in state_dtype or v.dtype)``.
+    """
+    del tile_size
+    return _forward("chunkwise", q, k, v, g, beta, initial_state, int(chunk_size), state_dtype)
+
+
+def kda_recurrent(q, k, v, g, beta, state=None, state_dtype=None):
+    """Token-by-token KDA recurrence on gfx950 (signature of kimi_linear/kda.py:188).
+
+    Any ``T >= 0``; ``T == 1`` is the decode step.
+    """
+    return _forward("recurrent", q, k, v, g, beta, state, 0, state_dtype)

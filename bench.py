@@ -1,0 +1,217 @@
+"""Benchmark of the MI355X KDA core (one GPU).
+
+A step is one ``kda_chunkwise`` forward over the 1.5B-config layer shape
+(B=8, T=4096, H=16, dk=dv=128, chunk 64; fp16 q/k/v, fp32 g/beta, fp32 state
+from zeros), inputs resident in HBM.  ``value`` is tokens/s (B*T per step).
+
+Also reported on the same line:
+* ``roofline`` of the chunkwise kernel: algorithmic HBM bytes per launch over
+  the mean launch duration (HIP events around every timed launch);
+* ``decode``: the B=64 recurrent decode step (fp32 state N(0, 0.02), fp16
+  q/k/v/g/beta) as 512 chained steps captured in one hipGraph, per-step time,
+  plus a variant rotating 5 independent state sets (320 MiB working set) so
+  the state cannot stay resident in the 256 MB Infinity Cache;
+* ``cpu_baseline``: the CPU oracle (an op-for-op restatement of the
+  reference's PyTorch algorithm) on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "KDA chunkwise fwd tokens/s @H16 d128 T4096 fp16; recurrent decode µs @B64"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+B1, T1, H1, D1, C1 = 8, 4096, 16, 128, 64
+# algorithmic traffic per (token, head): q,k,v fp16 (768 B) + g fp32 (512 B) + beta (4 B)
+# + o fp16 (256 B); per (sequence, head) the fp32 state is written once (S0 = 0 is not read).
+CHUNK_BYTES = B1 * T1 * H1 * 1540 + B1 * H1 * D1 * D1 * 4
+# causal flop count per (token, head): C (3K + 2V) + 6 K V
+CHUNK_FLOPS = B1 * T1 * H1 * (C1 * (3 * D1 + 2 * D1) + 6 * D1 * D1)
+
+B2, H2, STEPS2 = 64, 16, 512
+# per decode step: fp32 state read + write, plus q,k,g,v (fp16) + beta (fp16) in and o (fp16) out
+DECODE_BYTES = 2 * B2 * H2 * D1 * D1 * 4 + B2 * H2 * (4 * D1 * 2 + 2 + D1 * 2)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--only", choices=["chunkwise", "decode"], default=None,
+                   help="run one workload only (for profiling)")
+    return p.parse_args()
+
+
+def chunkwise_bench(pkg, wl, torch, steps, warmup):
+    inp = wl.make_inputs(B1, T1, H1, D1, D1, device="cuda", seed=1, qkv_dtype=torch.float16)
+    args = (inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"])
+
+    def step():
+        return pkg.kda_chunkwise(*args, initial_state=None, chunk_size=C1,
+                                 state_dtype=torch.float32)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        t0 = time.perf_counter()
+        for e0, e1 in ev:
+            e0.record(stream)
+            step()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    launch_ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+    return wall, launch_ms
+
+
+def decode_bench(pkg, wl, torch, n_sets):
+    """512 chained decode steps in one hipGraph; returns (us_per_step, graph)."""
+    inp = wl.make_inputs(B2, STEPS2, H2, D1, D1, device="cuda", seed=2,
+                         qkv_dtype=torch.float16, gate_dtype=torch.float16, state_std=0.02)
+    states = [inp["state"]] + [inp["state"].clone() for _ in range(n_sets - 1)]
+    xs = [inp[n] for n in ("q", "k", "v", "g", "beta")]
+
+    def run_all(sts):
+        cur = list(sts)
+        for t in range(STEPS2):
+            c = t % n_sets
+            x = [a[:, t:t + 1] for a in xs]
+            _, cur[c] = pkg.kda_recurrent(*x, state=cur[c], state_dtype=torch.float32)
+        return cur
+
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run_all(states)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_all(states)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * STEPS2)
+    del graph
+    return us
+
+
+def cpu_baselines(wl, torch, include_decode=True):
+    from oracle import kda_chunkwise_ref, kda_recurrent_ref
+    threads = torch.get_num_threads()
+    # chunkwise sample: one sequence of the same layer shape (all 16 heads), 2048 tokens
+    Ts = 2048
+    s = wl.make_inputs(1, Ts, H1, D1, D1, device="cpu", seed=1, qkv_dtype=torch.float16)
+    t0 = time.perf_counter()
+    kda_chunkwise_ref(s["q"], s["k"], s["v"], s["g"], s["beta"], chunk_size=C1,
+                      state_dtype=torch.float32)
+    tc = time.perf_counter() - t0
+    out = {"value": Ts / tc, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": f"oracle kda_chunkwise_ref, B=1 T={Ts} H=16 dk=dv=128 C=64 (fp16 inputs "
+                     f"upcast to fp32), one run, {tc:.1f} s"}
+    if include_decode:
+        d = wl.make_inputs(B2, 32, H2, D1, D1, device="cpu", seed=2, qkv_dtype=torch.float16,
+                           gate_dtype=torch.float16, state_std=0.02)
+        t0 = time.perf_counter()
+        kda_recurrent_ref(d["q"], d["k"], d["v"], d["g"], d["beta"], state=d["state"],
+                          state_dtype=torch.float32)
+        td = time.perf_counter() - t0
+        out["decode_us_per_step"] = td / 32 * 1e6
+        out["decode_sample"] = f"oracle kda_recurrent_ref, B=64 H=16 dk=dv=128, 32 steps, {td:.1f} s"
+    return out
+
+
+def load_traffic():
+    p = ROOT / "profiles" / "chunkwise_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the KDA core has no multi-GPU path in this "
+              "build (heads shard trivially across GPUs; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    wl = importlib.import_module("kimi_linear_amd.workloads")
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+
+    result = {"metric": METRIC, "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+              "steps": args.steps, "warmup": args.warmup}
+    if args.only in (None, "chunkwise"):
+        wall, launch_ms = chunkwise_bench(pkg, wl, torch, args.steps, args.warmup)
+        ms_per_step = wall * 1e3 / args.steps
+        achieved = CHUNK_BYTES / (launch_ms * 1e-3) / 1e9
+        result.update({
+            "value": B1 * T1 * args.steps / wall,
+            "ms_per_step": ms_per_step,
+            "config": {"workload": "kda_chunkwise forward, B=8 T=4096 H=16 dk=dv=128 "
+                                   "chunk_size=64; fp16 q/k/v, fp32 g/beta, fp32 state from zeros",
+                       "global_batch": B1, "seq_len": T1, "heads": H1, "head_dim": D1,
+                       "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                         "traffic": load_traffic(),
+                         "kernel_ms": launch_ms,
+                         "mfma_frac_causal": CHUNK_FLOPS / (launch_ms * 1e-3) / 1e12
+                         / FP16_PEAK_TFLOPS},
+        })
+    if args.only in (None, "decode"):
+        us_mall = decode_bench(pkg, wl, torch, 1)
+        us_hbm = decode_bench(pkg, wl, torch, 5)
+        result["decode"] = {
+            "workload": "kda_recurrent decode step, B=64 H=16 dk=dv=128, fp32 state, fp16 "
+                        "q/k/v/g/beta; 512 chained steps in one hipGraph",
+            "us_per_step": us_mall,
+            "gbs": DECODE_BYTES / (us_mall * 1e-6) / 1e9,
+            "us_per_step_rotating_320MiB": us_hbm,
+            "gbs_rotating": DECODE_BYTES / (us_hbm * 1e-6) / 1e9,
+            "hbm_frac_rotating": DECODE_BYTES / (us_hbm * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        }
+        if "value" not in result:
+            result.update({"value": us_mall, "unit": "us/step", "higher_is_better": False,
+                           "ms_per_step": us_mall / 1e3})
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baselines(wl, torch, include_decode=args.only != "chunkwise")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

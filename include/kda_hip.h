@@ -1,0 +1,112 @@
+/*
+ * kda_hip.h -- C ABI of the MI355X (gfx950) Kimi Delta Attention core.
+ *
+ * The reference (Lazy-Hakimi/-kimi-linear-) is pure PyTorch: its hot path is
+ * the pair of Python functions
+ *
+ *   kda_chunkwise(q, k, v, g, beta, initial_state=None, chunk_size=64,
+ *                 tile_size=0, state_dtype=None)      kimi_linear/kda.py:58-59
+ *   kda_recurrent(q, k, v, g, beta, state=None,
+ *                 state_dtype=None)                  kimi_linear/kda.py:188
+ *
+ * This library replaces their bodies.  A Python wrapper with the same
+ * signatures allocates the outputs and calls the entry points below through
+ * ctypes; a C/C++ caller fills kda_fwd_args directly.
+ *
+ * Contract shared by both entry points
+ *  - All pointers are device pointers on the current HIP device.
+ *  - q, k, g: [B, T, H, K]; v: [B, T, H, V]; beta: [B, T, H].  Each is a
+ *    strided view whose last dimension is contiguous; the three strides
+ *    (batch, token, head) are given in ELEMENTS.  q, k and v share one dtype.
+ *  - state_in (nullable = zeros), state_out: [B, H, K, V] contiguous.
+ *  - o: [B, T, H, V] contiguous, in the dtype of v.
+ *  - The work is asynchronous and stream-ordered on `stream` (a hipStream_t,
+ *    NULL = the legacy default stream).  The library never allocates, frees,
+ *    synchronises or copies to the host, so a call may be captured in a
+ *    hipGraph.  Inputs are never written; state_out may not alias state_in.
+ *  - Returns KDA_OK (0) or a kda_status code; kda_status_str() names it.
+ *    Argument errors are detected on the host before any launch.
+ */
+#ifndef KDA_HIP_H
+#define KDA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDA_ABI_VERSION 1
+
+/* Element types accepted at the boundary. */
+typedef enum kda_dtype {
+    KDA_DTYPE_F32 = 0,
+    KDA_DTYPE_F16 = 1,
+    KDA_DTYPE_BF16 = 2
+} kda_dtype;
+
+typedef enum kda_status {
+    KDA_OK = 0,
+    KDA_ERR_NULL_POINTER = 1,      /* a required pointer is NULL                 */
+    KDA_ERR_BAD_SHAPE = 2,         /* negative/inconsistent sizes, T % chunk != 0 */
+    KDA_ERR_BAD_DTYPE = 3,         /* dtype code outside kda_dtype / o != v dtype */
+    KDA_ERR_UNSUPPORTED = 4,       /* head dims this build has no kernel for      */
+    KDA_ERR_ALIAS = 5,             /* state_out aliases state_in                  */
+    KDA_ERR_LAUNCH = 6             /* hipGetLastError() after the launch          */
+} kda_status;
+
+/* One call's arguments.  Plain data: pointers, sizes, strides, codes. */
+typedef struct kda_fwd_args {
+    int64_t B, T, H, K, V;
+
+    const void* q;                 /* [B,T,H,K] */
+    const void* k;                 /* [B,T,H,K] */
+    const void* v;                 /* [B,T,H,V] */
+    const void* g;                 /* [B,T,H,K] log decay (<= 0) */
+    const void* beta;              /* [B,T,H]   delta-rule rate  */
+    int64_t q_stride[3];           /* (batch, token, head) strides in elements */
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t g_stride[3];
+    int64_t beta_stride[3];
+    int32_t qkv_dtype;             /* kda_dtype of q, k and v */
+    int32_t g_dtype;               /* kda_dtype of g          */
+    int32_t beta_dtype;            /* kda_dtype of beta       */
+
+    const void* state_in;          /* [B,H,K,V] contiguous, or NULL for zeros */
+    int32_t state_in_dtype;
+    void* state_out;               /* [B,H,K,V] contiguous */
+    int32_t state_out_dtype;
+    void* o;                       /* [B,T,H,V] contiguous, dtype == qkv_dtype */
+
+    float scale;                   /* q multiplier; the reference uses K^-0.5  */
+    int32_t clamp_fp16_out;        /* 1: clamp an fp16 o to +-60000 (kda.py:217-218) */
+    int64_t chunk_size;            /* chunkwise: T must be a multiple of it (kda.py:109);
+                                      it has no other numerical role (the maths is
+                                      chunk-size invariant) */
+} kda_fwd_args;
+
+/*
+ * Chunkwise forward; replaces the body of kda_chunkwise (kimi_linear/kda.py:58-185).
+ * o = per-token outputs, state_out = final state.  T may be 0.
+ */
+int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream);
+
+/*
+ * Token-by-token recurrence; replaces the body of kda_recurrent
+ * (kimi_linear/kda.py:188-219).  Any T >= 0; T == 1 is the decode step.
+ * chunk_size is ignored.
+ */
+int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
+
+/* Human-readable name of a kda_status code (static storage). */
+const char* kda_status_str(int status);
+
+/* KDA_ABI_VERSION of the built library (layout of kda_fwd_args). */
+int kda_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_HIP_H */

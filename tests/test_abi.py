@@ -1,0 +1,130 @@
+"""CPU tests of the C ABI boundary: symbols, struct layout, host-side validation.
+
+No kernel is launched here: every call below is rejected (or is empty) on the
+host before the library touches the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "kda_hip.h"
+
+
+@pytest.fixture(scope="module")
+def native(kda_pkg):
+    import importlib
+    mod = importlib.import_module("kimi_linear_amd._native")
+    mod.load()
+    return mod
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(kda_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol(native):
+    lib = native.load()
+    declared = header_functions()
+    assert declared == sorted(native.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings(native):
+    lib = native.load()
+    assert lib.kda_abi_version() == native.ABI_VERSION
+    for code in range(7):
+        assert native.status_str(code)
+    assert native.status_str(0) == "ok"
+    assert "unknown" in native.status_str(99)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_header(native, tmp_path):
+    fields = [name for name, _ in native.KdaFwdArgs._fields_]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "kda_hip.h"',
+             "int main(void) {", '  printf("size %zu\\n", sizeof(kda_fwd_args));']
+    lines += [f'  printf("{f} %zu\\n", offsetof(kda_fwd_args, {f}));' for f in fields]
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = dict(line.split() for line in out if line)
+    assert int(got["size"]) == ctypes.sizeof(native.KdaFwdArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(native.KdaFwdArgs, f).offset, f
+
+
+def _args(native, **kw):
+    a = native.KdaFwdArgs()
+    a.B, a.T, a.H, a.K, a.V = 1, 16, 1, 64, 64
+    fake = 0x100000   # never dereferenced: every case here fails validation first
+    a.q = a.k = a.v = a.g = a.beta = a.o = fake
+    a.state_out = fake * 4
+    a.state_in = None
+    a.chunk_size = 16
+    a.scale = 0.125
+    for name, val in kw.items():
+        setattr(a, name, val)
+    return a
+
+
+@pytest.mark.parametrize("fn", ["kda_chunkwise_fwd", "kda_recurrent_fwd"])
+def test_host_validation_codes(native, fn):
+    lib = native.load()
+    call = getattr(lib, fn)
+    assert call(None, None) == 1                                          # NULL args
+    assert call(ctypes.byref(_args(native, B=-1)), None) == 2            # bad shape
+    assert call(ctypes.byref(_args(native, qkv_dtype=7)), None) == 3     # bad dtype
+    assert call(ctypes.byref(_args(native, K=48)), None) == 4            # no kernel for K
+    assert call(ctypes.byref(_args(native, q=None)), None) == 1          # missing input
+    assert call(ctypes.byref(_args(native, state_out=None)), None) == 1
+    overlap = _args(native)
+    overlap.state_in = overlap.state_out + 8
+    assert call(ctypes.byref(overlap), None) == 5                        # aliasing
+    assert call(ctypes.byref(_args(native, B=0)), None) == 0             # empty: no launch
+    assert call(ctypes.byref(_args(native, H=0)), None) == 0
+
+
+def test_chunk_contract(native):
+    lib = native.load()
+    assert lib.kda_chunkwise_fwd(ctypes.byref(_args(native, T=20, chunk_size=16)), None) == 2
+    assert lib.kda_chunkwise_fwd(ctypes.byref(_args(native, chunk_size=0)), None) == 2
+    # the recurrence ignores chunk_size
+    assert lib.kda_recurrent_fwd(ctypes.byref(_args(native, T=20, chunk_size=16, K=48)), None) == 4
+
+
+def test_wrapper_rejects_cpu_tensors(kda_pkg):
+    B, T, H, K, V = 1, 16, 1, 64, 64
+    q = torch.zeros(B, T, H, K)
+    beta = torch.zeros(B, T, H)
+    with pytest.raises(kda_pkg.KdaError, match="no CPU path"):
+        kda_pkg.kda_chunkwise(q, q, torch.zeros(B, T, H, V), q, beta, chunk_size=16)
+    with pytest.raises(kda_pkg.KdaError, match="no CPU path"):
+        kda_pkg.kda_recurrent(q, q, torch.zeros(B, T, H, V), q, beta)
+
+
+def test_wrapper_shape_and_chunk_errors(kda_pkg):
+    q = torch.zeros(1, 20, 1, 64)
+    beta = torch.zeros(1, 20, 1)
+    v = torch.zeros(1, 20, 1, 64)
+    with pytest.raises(ValueError, match="multiple of chunk_size"):
+        kda_pkg.kda_chunkwise(q, q, v, q, beta, chunk_size=16)
+    with pytest.raises(RuntimeError):       # the reference's reshape raises RuntimeError
+        kda_pkg.kda_chunkwise(q, q, v, q, beta, chunk_size=16)
+    with pytest.raises(kda_pkg.KdaError, match="beta must be"):
+        kda_pkg.kda_recurrent(q, q, v, q, torch.zeros(1, 20, 2))
+    with pytest.raises(kda_pkg.KdaError, match="state must be"):
+        kda_pkg.kda_recurrent(q, q, v, q, beta, state=torch.zeros(1, 1, 64, 32))
