@@ -1,8 +1,8 @@
 // Chunkwise KDA forward for gfx950: fp16 MFMA, fp32 accumulation, fp32 state.
 //
 // Replaces the body of kda_chunkwise (kimi_linear/kda.py:111-185).  The maths
-// is the same UT-transform form (paper Eq. 6-9), evaluated per internal chunk
-// of BT = 16 tokens; because the recurrence is chunk-size invariant the
+// is the reference's UT-transform form (paper Eq. 6-9) evaluated per internal
+// chunk of BT = 16 tokens; the recurrence is chunk-size invariant, so the
 // caller's chunk_size only fixes the T % chunk_size == 0 contract.
 //
 // Per (b, h) and internal chunk (rows c, i in [0, 16)), with a_t = exp(g_t):
@@ -13,24 +13,34 @@
 //   P      = U - W S,   O = scale (E * Q) S + A P
 //   S     <- Diag(E[15]) S + ((E[15]/E) * K)^T P
 //
-// Decay factoring without pairwise exponentials.  Every pair i < c inside a
-// 16-token chunk has a unique highest differing bit b: c has it set, i has it
-// clear, and both lie in the same aligned block of 2^(b+1) rows whose upper
-// half starts at ref.  Then
-//   prod_{t=i+1..c} a_t = (prod_{t=ref+1..c} a_t) * (prod_{t=i+1..ref} a_t)
-// and both factors are <= 1, so per level b one [16 x K] operand X_b holds
-// k_r times its factor (query rows: the first product, key rows: the second)
-// and L_b = X_b X_b^T is a plain MFMA product; entries outside level b's pairs
-// are masked.  Factors only underflow when the true decay is smaller still.
-// Level "d" (the diagonal, factor 1) gives A[c,c].
+// Decay factoring without pairwise exponentials: every pair i < c of a chunk
+// has a unique highest differing bit b; c has it set, i clear, and both sit in
+// the aligned block of 2^(b+1) rows whose upper half starts at ref.  Then
+//   prod_{t=i+1..c} a_t = (prod_{t=ref+1..c} a_t) * (prod_{t=i+1..ref} a_t),
+// both factors <= 1, so per level b one [16 x K] operand X_b (row r = k_r times
+// its factor) gives L_b = X_b X_b^T as a plain MFMA product, masked to level
+// b's pairs.  A factor only underflows when the true decay is smaller still.
+// Level "diag" (factor 1) gives A[c, c].
 //
-// Work split: one workgroup of NW waves per (b, h, 16*NW state columns).  Wave
-// w owns state columns [16w, 16w+16) as four-float MFMA accumulator tiles
-// (rows 16t + 4*(lane/16) + j, column lane%16) for all K rows, so W S, Q S,
-// A P and K^T P need no cross-wave reduction.  The V-independent work
-// (operands, L, A, solve, W) is shared by the waves through LDS.
-// Operands that are not exact in fp16 (S, P, W, QE, K-hat, A, M) are split
-// into fp16 hi + lo and multiplied as hi*hi + hi*lo + lo*hi.
+// (I + L)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8) for the nilpotent L: four
+// 16x16 products and three squarings on MFMA (fp16 hi/lo split operands),
+// entirely in registers.  An MFMA accumulator holds X[4g+j][n] in lane n+16g,
+// slot j -- the B-operand layout of X and the A-operand layout of X^T -- so a
+// chain that keeps X and X^T side by side needs no data movement.
+//
+// Software pipeline, one workgroup per (b, h, 16*NC state columns):
+//   NC consumer waves: wave w owns state columns [16w, 16w+16) for all K rows
+//     as MFMA accumulators and runs the sequential chain of chunk n.
+//   NP = K/32 producer waves: two lanes per channel (8 rows each) build the
+//     operands of chunk n+2 straight from prefetched global loads; producer
+//     wave 0 then inverts (I + L) and forms W for chunk n+1 while the others
+//     compute the level products of chunk n+2.
+// Each step has two phases separated by workgroup barriers:
+//   A: producers: operands(n+2) | consumers: U = M V, P = U - W S, O = QE S
+//   B: producer 0: solve + W (n+1), others: levels (n+2)
+//      | consumers: O += A P, store O, S <- E15 S + Khat^T P
+// Operands that are not exact in fp16 and carry the state (S, P, M) are split
+// into fp16 hi + lo; the others are single fp16 with fp32 accumulation.
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -38,29 +48,54 @@ namespace kda {
 
 namespace {
 
-constexpr int BT = 16;   // tokens per internal chunk
-constexpr int RP = 24;   // padded row (halfs) of the [*][16] operand matrices
-constexpr int NLEV = 5;  // operand levels: 0 = diagonal, 1 + b for bit b = 0..3
+constexpr int BT = 16;    // tokens per internal chunk
+constexpr int RP = 24;    // padded row (halfs) of the [*][16] fp16 matrices (48 B rows)
+constexpr int LP = 20;    // padded row (floats) of the 16x16 fp32 L
+constexpr int NLEV = 5;   // operand levels: 0 = diagonal, 1 + b for bit b = 0..3
 
-template <int K, int NW>
-struct __align__(16) ChunkSmem {
-    static constexpr int VT = 16 * NW;
-    static constexpr int KP = K + 16;      // padded row (halfs) of [16][K] operands
-    float alpha[BT][K];                    // exp(g)
-    float qv[BT][K];                       // q (unscaled)
-    float kv[BT][K];
-    float beta[BT];
-    float elast[K];                        // exp(gc) at the chunk's last row
-    float L[BT][BT + 1];                   // beta-scaled strictly-lower L
-    _Float16 X[NLEV][BT][KP];              // key-side level operands
+// Input element access.  Raw values are held one per 32-bit register and
+// converted only at use, so a prefetch load is never followed by a wait.
+template <typename TQ> struct QIn;
+template <> struct QIn<_Float16> {
+    static constexpr bool exact = true;   // values are exact in fp16
+    using Raw = uint32_t;
+    static __device__ __forceinline__ Raw ld(const _Float16* p) {
+        return *reinterpret_cast<const uint16_t*>(p);
+    }
+    static __device__ __forceinline__ float f(Raw r) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+    }
+};
+template <> struct QIn<bf16_t> {
+    static constexpr bool exact = false;
+    using Raw = uint32_t;
+    static __device__ __forceinline__ Raw ld(const bf16_t* p) {
+        return *reinterpret_cast<const uint16_t*>(p);
+    }
+    static __device__ __forceinline__ float f(Raw r) { return __uint_as_float(r << 16); }
+};
+template <> struct QIn<float> {
+    static constexpr bool exact = false;
+    using Raw = float;
+    static __device__ __forceinline__ Raw ld(const float* p) { return *p; }
+    static __device__ __forceinline__ float f(Raw r) { return r; }
+};
+
+template <int K>
+struct __align__(16) Smem {
+    static constexpr int KP = K + 4;       // padded row (halfs) of [16][K] operands
+    _Float16 X[NLEV][BT][KP];              // level operands (k * factor)
     _Float16 Y[NLEV][BT][KP];              // query-side level operands (q * factor)
-    _Float16 QE[2][BT][KP];                // q * E, hi/lo
-    _Float16 WN[2][BT][KP];                // -W, hi/lo
-    _Float16 KET[2][K][RP];                // (k * E)^T, hi/lo
-    _Float16 KHT[2][K][RP];                // (k * E[15] / E)^T, hi/lo
-    _Float16 VTt[2][VT][RP];               // V^T, hi/lo
-    _Float16 AM[2][BT][RP];                // A (scaled), hi/lo
-    _Float16 MM[2][BT][RP];                // M, hi/lo
+    _Float16 QE[3][BT][KP];                // q * E                  (chunk % 3)
+    _Float16 WN[BT][KP];                   // -W                     (single)
+    _Float16 KET[2][K][RP];                // (k * E)^T              (chunk % 2)
+    _Float16 KHT[3][K][RP];                // (k * E15 / E)^T        (chunk % 3)
+    _Float16 AM[3][BT][RP];                // scale * A              (chunk % 3)
+    _Float16 MH[BT][RP];                   // M hi                   (single)
+    _Float16 ML[BT][RP];                   // M lo
+    float L[2][BT][LP];                    // beta-scaled L          (chunk % 2)
+    float elast[3][K];                     // E[15]                  (chunk % 3)
+    float beta[2][BT];                     //                        (chunk % 2)
 };
 
 __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, int lg) {
@@ -77,302 +112,529 @@ __device__ __forceinline__ h8 frag32(const _Float16* base, int stride, int row, 
     return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Level b operands of channel c: every row r of the chunk gets k_r times its
-// decay factor relative to the upper half-block start ref of its level block.
-template <int B, int K, int NW>
-__device__ __forceinline__ void level_operands(ChunkSmem<K, NW>& sm, int c) {
-    constexpr int Lh = 1 << B;       // half-block size
-    constexpr int lev = 1 + B;
+__device__ __forceinline__ void split4(const f4& x, h4& hi, h4& lo) {
 #pragma unroll
-    for (int s0 = 0; s0 < BT; s0 += 2 * Lh) {
-        const int ref = s0 + Lh;
-        float f = 1.f;
-#pragma unroll
-        for (int r = ref; r < s0 + 2 * Lh; ++r) {      // query rows: prod_{ref+1..r}
-            if (r > ref) f *= sm.alpha[r][c];
-            sm.X[lev][r][c] = static_cast<_Float16>(sm.kv[r][c] * f);
-            sm.Y[lev][r][c] = static_cast<_Float16>(sm.qv[r][c] * f);
-        }
-        f = 1.f;
-#pragma unroll
-        for (int r = ref - 1; r >= s0; --r) {          // key rows: prod_{r+1..ref}
-            f *= sm.alpha[r + 1][c];
-            sm.X[lev][r][c] = static_cast<_Float16>(sm.kv[r][c] * f);
-            sm.Y[lev][r][c] = static_cast<_Float16>(0.f);
-        }
+    for (int j = 0; j < 4; ++j) {
+        const _Float16 h = static_cast<_Float16>(x[j]);
+        hi[j] = h;
+        lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(h));
     }
 }
 
-template <int K, int NW>
-__global__ __launch_bounds__(64 * NW) void chunkwise_kernel(const kda_fwd_args a) {
-    using Sm = ChunkSmem<K, NW>;
-    constexpr int VT = Sm::VT, KP = Sm::KP, NT = 64 * NW;
-    constexpr int KT = K / 16;     // 16-row state tiles
-    constexpr int KU = K / 32;     // 32-wide k blocks
-    static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
-    __shared__ Sm sm;
+// An fp32 accumulator tile split into fp16 hi + lo operands.
+struct Split4 {
+    h4 hi, lo;
+    __device__ explicit Split4(const f4& x) { split4(x, hi, lo); }
+};
 
-    const int64_t H = a.H, T = a.T, V = a.V;
-    const int nvt = static_cast<int>(V / VT);
-    int bid = blockIdx.x;
-    const int vt = bid % nvt;
-    bid /= nvt;
-    const int64_t h = bid % H;
-    const int64_t b = bid / H;
+// acc(A_layout(a) * B_layout(b)) with both operands split: hi*hi + hi*lo + lo*hi.
+__device__ __forceinline__ f4 mm3(const Split4& a, const Split4& b) {
+    f4 d = {0.f, 0.f, 0.f, 0.f};
+    d = mfma16x16x16(a.hi, b.hi, d);
+    d = mfma16x16x16(a.hi, b.lo, d);
+    d = mfma16x16x16(a.lo, b.hi, d);
+    return d;
+}
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int ln = lane & 15, lg = lane >> 4;
-    const int64_t v0 = static_cast<int64_t>(vt) * VT;
-    const int64_t ncol = v0 + 16 * wave + ln;        // this lane's state / output column
-    const float scale = a.scale;
-    const bool v_exact = a.qkv_dtype == KDA_DTYPE_F16;
+// Raw per-lane inputs of one chunk for a producer lane (one channel, 8 rows).
+// Loaded values stay unconverted until use, so the loads remain in flight
+// across the pipeline steps instead of stalling at issue.
+template <typename TQ>
+struct PrepIn {
+    float g[8];
+    typename QIn<TQ>::Raw q[8], k[8];
+    float beta;
+};
 
-    // ---- initial state, accumulator layout: Sacc[t][j] = S[16t + 4lg + j][ncol]
-    const int64_t sbase = (b * H + h) * static_cast<int64_t>(K) * V;
-    f4 Sacc[KT];
+// Accumulator-layout state tiles: S[t][j] = state[16t + 4lg + j][col]; `off`
+// is the element offset of (row 4lg, col) and rows are V apart.  All loads
+// are issued before any is used.
+template <int KT, typename TS>
+__device__ __forceinline__ void load_state_t(f4 (&S)[KT], const TS* p, int64_t off, int64_t V) {
 #pragma unroll
     for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t r = 16 * t + 4 * lg + j;
-            Sacc[t][j] = a.state_in ? load_elem(a.state_in, sbase + r * V + ncol, a.state_in_dtype) : 0.f;
-        }
+        for (int j = 0; j < 4; ++j) S[t][j] = Elem<TS>::ld(p + off + (16 * t + j) * V);
+}
+template <int KT>
+__device__ __forceinline__ void load_state(f4 (&S)[KT], const void* p, int dtype, int64_t off, int64_t V) {
+    if (p == nullptr) {
+#pragma unroll
+        for (int t = 0; t < KT; ++t) S[t] = f4{0.f, 0.f, 0.f, 0.f};
+    } else if (dtype == KDA_DTYPE_F32) {
+        load_state_t<KT>(S, static_cast<const float*>(p), off, V);
+    } else if (dtype == KDA_DTYPE_F16) {
+        load_state_t<KT>(S, static_cast<const _Float16*>(p), off, V);
+    } else {
+        load_state_t<KT>(S, static_cast<const bf16_t*>(p), off, V);
+    }
+}
+template <int KT, typename TS>
+__device__ __forceinline__ void store_state_t(const f4 (&S)[KT], TS* p, int64_t off, int64_t V) {
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Elem<TS>::st(p + off + (16 * t + j) * V, S[t][j]);
+}
+template <int KT>
+__device__ __forceinline__ void store_state(const f4 (&S)[KT], void* p, int dtype, int64_t off, int64_t V) {
+    if (dtype == KDA_DTYPE_F32) store_state_t<KT>(S, static_cast<float*>(p), off, V);
+    else if (dtype == KDA_DTYPE_F16) store_state_t<KT>(S, static_cast<_Float16*>(p), off, V);
+    else store_state_t<KT>(S, static_cast<bf16_t*>(p), off, V);
+}
 
-    for (int64_t t0 = 0; t0 < T; t0 += BT) {
-        // ---- stage the chunk (rows past T are neutral: k = q = v = beta = 0, a = 1)
-        for (int idx = tid; idx < BT * K; idx += NT) {
-            const int r = idx / K, c = idx % K;
-            const int64_t tt = t0 + r;
-            float qx = 0.f, kx = 0.f, al = 1.f;
-            if (tt < T) {
-                qx = load_elem(a.q, b * a.q_stride[0] + tt * a.q_stride[1] + h * a.q_stride[2] + c, a.qkv_dtype);
-                kx = load_elem(a.k, b * a.k_stride[0] + tt * a.k_stride[1] + h * a.k_stride[2] + c, a.qkv_dtype);
-                al = fast_exp(load_elem(a.g, b * a.g_stride[0] + tt * a.g_stride[1] + h * a.g_stride[2] + c, a.g_dtype));
-            }
-            sm.qv[r][c] = qx;
-            sm.kv[r][c] = kx;
-            sm.alpha[r][c] = al;
-        }
-        for (int idx = tid; idx < BT * VT; idx += NT) {
-            const int n = idx % VT, r = idx / VT;
-            const int64_t tt = t0 + r;
-            float vx = 0.f;
-            if (tt < T)
-                vx = load_elem(a.v, b * a.v_stride[0] + tt * a.v_stride[1] + h * a.v_stride[2] + v0 + n, a.qkv_dtype);
-            split_h(vx, sm.VTt[0][n][r], sm.VTt[1][n][r]);
-        }
-        if (tid < BT) {
-            const int64_t tt = t0 + tid;
-            sm.beta[tid] = tt < T ? load_elem(a.beta, b * a.beta_stride[0] + tt * a.beta_stride[1] +
-                                                          h * a.beta_stride[2], a.beta_dtype)
-                                  : 0.f;
-        }
-        __syncthreads();
+template <int K, int NC, typename TQ>
+struct Kern {
+    static constexpr int KP = Smem<K>::KP;
+    static constexpr int KT = K / 16;       // 16-row state tiles
+    static constexpr int KU = K / 32;       // 32-wide k blocks
+    static constexpr int NP = K / 32;       // producer waves
+    static constexpr int NWAVE = NC + NP;
+    static constexpr int VT = 16 * NC;
 
-        // ---- per-channel operands: 6 tasks per channel
-        for (int idx = tid; idx < 6 * K; idx += NT) {
-            const int c = idx % K, task = idx / K;
-            switch (task) {
-                case 0: {
-                    float e = 1.f;
-#pragma unroll
-                    for (int r = 0; r < BT; ++r) {
-                        e *= sm.alpha[r][c];
-                        split_h(sm.qv[r][c] * e, sm.QE[0][r][c], sm.QE[1][r][c]);
-                        split_h(sm.kv[r][c] * e, sm.KET[0][c][r], sm.KET[1][c][r]);
-                    }
-                    sm.elast[c] = e;
-                    float s = 1.f;
-#pragma unroll
-                    for (int r = BT - 1; r >= 0; --r) {
-                        split_h(sm.kv[r][c] * s, sm.KHT[0][c][r], sm.KHT[1][c][r]);
-                        s *= sm.alpha[r][c];
-                    }
-                    break;
-                }
-                case 1: level_operands<0>(sm, c); break;
-                case 2: level_operands<1>(sm, c); break;
-                case 3: level_operands<2>(sm, c); break;
-                case 4: level_operands<3>(sm, c); break;
-                default: {
-#pragma unroll
-                    for (int r = 0; r < BT; ++r) {
-                        sm.X[0][r][c] = static_cast<_Float16>(sm.kv[r][c]);
-                        sm.Y[0][r][c] = static_cast<_Float16>(sm.qv[r][c]);
-                    }
-                    break;
-                }
-            }
-        }
-        __syncthreads();
+    const kda_fwd_args& a;
+    Smem<K>& sm;
+    int64_t b, h, T;
+    int nch;
+    float scale;
+    int lane, ln, lg;
+    // per-lane column byte offsets, first rows and per-row byte strides; a
+    // lane's element (row r, its column) of a chunk is at base + r * rs + col
+    uint32_t col_q, col_k, col_g, col_v;
+    uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;
+    int prow0, vrow0;
 
-        // ---- L and A by level: each (c, i) is written by exactly one level
-        for (int lev = wave; lev < NLEV; lev += NW) {
-            f4 accL = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int u = 0; u < KU; ++u) {
-                const h8 xf = frag32(&sm.X[lev][0][0], KP, ln, lg, u);
-                const h8 yf = frag32(&sm.Y[lev][0][0], KP, ln, lg, u);
-                accL = mfma16x16x32(xf, xf, accL);
-                accA = mfma16x16x32(yf, xf, accA);
-            }
-            const int i = ln;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = 4 * lg + j;
-                if (lev == 0) {
-                    if (i == c) {
-                        split_h(accA[j] * scale, sm.AM[0][c][i], sm.AM[1][c][i]);
-                    } else if (i > c) {
-                        sm.AM[0][c][i] = static_cast<_Float16>(0.f);
-                        sm.AM[1][c][i] = static_cast<_Float16>(0.f);
-                    }
-                } else {
-                    const int bb = lev - 1;
-                    const bool pair = ((c >> (bb + 1)) == (i >> (bb + 1))) && ((c >> bb) & 1) && !((i >> bb) & 1);
-                    if (pair) {
-                        sm.L[c][i] = sm.beta[c] * accL[j];
-                        split_h(accA[j] * scale, sm.AM[0][c][i], sm.AM[1][c][i]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
+    __device__ Kern(const kda_fwd_args& args, Smem<K>& s) : a(args), sm(s) {}
 
-        // ---- M = (I + L)^-1 Diag(beta): forward substitution, one column per lane
-        if (tid < BT) {
-            const int jc = tid;
-            float m[BT];
-#pragma unroll
-            for (int r = 0; r < BT; ++r) {
-                float s = (r == jc) ? 1.f : 0.f;
-#pragma unroll
-                for (int t = 0; t < r; ++t) s = fmaf(-sm.L[r][t], m[t], s);
-                m[r] = s;
-            }
-            const float bj = sm.beta[jc];
-#pragma unroll
-            for (int r = 0; r < BT; ++r) split_h(m[r] * bj, sm.MM[0][r][jc], sm.MM[1][r][jc]);
-        }
-        __syncthreads();
+    // ------------------------------------------------------------ producers
+    // Rows of chunk `chunk` that lie before T (1..BT).
+    __device__ int rows_in(int chunk) const {
+        const int64_t left = T - static_cast<int64_t>(chunk) * BT;
+        return left < BT ? static_cast<int>(left) : BT;
+    }
 
-        // ---- W = M (E*K) (shared, written as -W) and U = M V (this wave's columns)
-        const h4 mh = frag16(&sm.MM[0][0][0], RP, ln, lg);
-        const h4 ml = frag16(&sm.MM[1][0][0], RP, ln, lg);
-        for (int tt = wave; tt < KT; tt += NW) {
-            const h4 kh = frag16(&sm.KET[0][16 * tt][0], RP, ln, lg);
-            const h4 kl = frag16(&sm.KET[1][16 * tt][0], RP, ln, lg);
-            f4 w = {0.f, 0.f, 0.f, 0.f};
-            w = mfma16x16x16(mh, kh, w);
-            w = mfma16x16x16(ml, kh, w);
-            w = mfma16x16x16(mh, kl, w);
+    // Element offset of (b, t0, h, 0) of a [B, T, H, D] view.
+    __device__ int64_t base(const int64_t (&st)[3], int chunk) const {
+        return b * st[0] + static_cast<int64_t>(chunk) * BT * st[1] + h * st[2];
+    }
+
+    template <typename T>
+    static __device__ __forceinline__ const char* cbase(const void* p, int64_t elems) {
+        return reinterpret_cast<const char*>(static_cast<const T*>(p) + elems);
+    }
+    template <typename T>
+    static __device__ __forceinline__ T at(const char* base, uint32_t off) {
+        return *reinterpret_cast<const T*>(base + off);
+    }
+
+    // Issue the loads of one chunk (rows past T read the last row; masked at use).
+    // Chunk bases are wave-uniform; every per-lane offset is a non-negative
+    // 32-bit byte offset formed before it is added to the base.
+    __device__ void prep_load(PrepIn<TQ>& in, int chunk, bool beta_lane) const {
+        const int last = rows_in(chunk) - 1;
+        const char* q = cbase<TQ>(a.q, base(a.q_stride, chunk));
+        const char* k = cbase<TQ>(a.k, base(a.k_stride, chunk));
+        const char* g = cbase<float>(a.g, base(a.g_stride, chunk));
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                split_h(-w[j], sm.WN[0][4 * lg + j][16 * tt + ln], sm.WN[1][4 * lg + j][16 * tt + ln]);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = static_cast<uint32_t>(min(prow0 + i, last));
+            const uint32_t og = r * rs_g + col_g, oq = r * rs_q + col_q, ok = r * rs_k + col_k;
+            in.g[i] = at<float>(g, og);
+            in.q[i] = QIn<TQ>::ld(reinterpret_cast<const TQ*>(q + oq));
+            in.k[i] = QIn<TQ>::ld(reinterpret_cast<const TQ*>(k + ok));
         }
-        f4 P = {0.f, 0.f, 0.f, 0.f};
+        if (beta_lane) {
+            const char* bp = cbase<float>(a.beta, base(a.beta_stride, chunk));
+            const uint32_t ob = static_cast<uint32_t>(min(lane, last)) * rs_b;
+            in.beta = at<float>(bp, ob);
+        }
+    }
+
+    // Operands of one chunk for channel c, rows 8*hf .. 8*hf+7.
+    __device__ void prep_compute(const PrepIn<TQ>& pin, int chunk, int c, int hf, bool beta_lane) const {
+        struct { float g[8], q[8], k[8], beta; } in;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            in.g[i] = pin.g[i];
+            in.q[i] = QIn<TQ>::f(pin.q[i]);
+            in.k[i] = QIn<TQ>::f(pin.k[i]);
+        }
+        in.beta = pin.beta;
+        const int nrow = rows_in(chunk);
+        if (nrow < BT) {                                // tail chunk: neutral padding rows
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (8 * hf + i >= nrow) { in.g[i] = 0.f; in.q[i] = 0.f; in.k[i] = 0.f; }
+            if (lane >= nrow) in.beta = 0.f;
+        }
+        float al[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) al[i] = fast_exp(in.g[i]);
+        float pre[8];                                   // prod_{t<=i} within the half
+        pre[0] = al[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) pre[i] = pre[i - 1] * al[i];
+        float suf[8];                                   // prod_{t=i+1..7} within the half
+        suf[7] = 1.f;
+#pragma unroll
+        for (int i = 6; i >= 0; --i) suf[i] = suf[i + 1] * al[i + 1];
+        const float other = __shfl_xor(pre[7], 32);    // product over the other half
+        const float a8 = __shfl_xor(al[0], 32);        // lower half: a of row 8
+        const bool up = hf != 0;
+        const float emul = up ? other : 1.f;            // E = exp(gc) = prefix over the chunk
+        const float kmul = up ? 1.f : other;            // E15 / E = suffix over the chunk
+        const int r0 = 8 * hf;
+        const int b3 = chunk % 3, b2 = chunk % 2;
+
+        h8 ke8, kh8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float e = pre[i] * emul;
+            sm.QE[b3][r0 + i][c] = static_cast<_Float16>(in.q[i] * e);
+            ke8[i] = static_cast<_Float16>(in.k[i] * e);
+            kh8[i] = static_cast<_Float16>(in.k[i] * (suf[i] * kmul));
+        }
+        *reinterpret_cast<h8*>(&sm.KET[b2][c][r0]) = ke8;
+        *reinterpret_cast<h8*>(&sm.KHT[b3][c][r0]) = kh8;
+        if (up) sm.elast[b3][c] = pre[7] * emul;
+        if (beta_lane) sm.beta[b2][lane] = in.beta;
+
+        // level "diag": factor 1
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sm.X[0][r0 + i][c] = static_cast<_Float16>(in.k[i]);
+            sm.Y[0][r0 + i][c] = static_cast<_Float16>(in.q[i]);
+        }
+        // level b = 0: query rows odd (factor 1), key rows even (a_{i+1})
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            sm.X[1][r0 + i][c] = static_cast<_Float16>(in.k[i] * al[i + 1]);
+            sm.X[1][r0 + i + 1][c] = static_cast<_Float16>(in.k[i + 1]);
+            sm.Y[1][r0 + i + 1][c] = static_cast<_Float16>(in.q[i + 1]);
+        }
+        // level b = 1: ref = 2 mod 4
+#pragma unroll
+        for (int i = 0; i < 8; i += 4) {
+            const float f1 = al[i + 2];
+            const float f0 = al[i + 1] * f1;
+            const float f3 = al[i + 3];
+            sm.X[2][r0 + i][c] = static_cast<_Float16>(in.k[i] * f0);
+            sm.X[2][r0 + i + 1][c] = static_cast<_Float16>(in.k[i + 1] * f1);
+            sm.X[2][r0 + i + 2][c] = static_cast<_Float16>(in.k[i + 2]);
+            sm.X[2][r0 + i + 3][c] = static_cast<_Float16>(in.k[i + 3] * f3);
+            sm.Y[2][r0 + i + 2][c] = static_cast<_Float16>(in.q[i + 2]);
+            sm.Y[2][r0 + i + 3][c] = static_cast<_Float16>(in.q[i + 3] * f3);
+        }
+        // level b = 2: ref = 4 within the half
         {
-            const h4 vh = frag16(&sm.VTt[0][16 * wave][0], RP, ln, lg);
-            P = mfma16x16x16(mh, vh, P);
-            P = mfma16x16x16(ml, vh, P);
-            if (!v_exact) {
-                const h4 vl = frag16(&sm.VTt[1][16 * wave][0], RP, ln, lg);
-                P = mfma16x16x16(mh, vl, P);
+            const float f3 = al[4], f2 = al[3] * f3, f1 = al[2] * f2, f0 = al[1] * f1;
+            const float f5 = al[5], f6 = f5 * al[6], f7 = f6 * al[7];
+            sm.X[3][r0 + 0][c] = static_cast<_Float16>(in.k[0] * f0);
+            sm.X[3][r0 + 1][c] = static_cast<_Float16>(in.k[1] * f1);
+            sm.X[3][r0 + 2][c] = static_cast<_Float16>(in.k[2] * f2);
+            sm.X[3][r0 + 3][c] = static_cast<_Float16>(in.k[3] * f3);
+            sm.X[3][r0 + 4][c] = static_cast<_Float16>(in.k[4]);
+            sm.X[3][r0 + 5][c] = static_cast<_Float16>(in.k[5] * f5);
+            sm.X[3][r0 + 6][c] = static_cast<_Float16>(in.k[6] * f6);
+            sm.X[3][r0 + 7][c] = static_cast<_Float16>(in.k[7] * f7);
+            sm.Y[3][r0 + 4][c] = static_cast<_Float16>(in.q[4]);
+            sm.Y[3][r0 + 5][c] = static_cast<_Float16>(in.q[5] * f5);
+            sm.Y[3][r0 + 6][c] = static_cast<_Float16>(in.q[6] * f6);
+            sm.Y[3][r0 + 7][c] = static_cast<_Float16>(in.q[7] * f7);
+        }
+        // level b = 3: ref = 8; upper half = query rows (prod_{9..r}), lower = key rows
+        {
+            float f = 1.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (i > 0) f *= al[i];
+                const float fr = up ? f : suf[i] * a8;
+                sm.X[4][r0 + i][c] = static_cast<_Float16>(in.k[i] * fr);
+                sm.Y[4][r0 + i][c] = static_cast<_Float16>(in.q[i] * fr);   // key rows: masked later
             }
         }
-        __syncthreads();
+    }
 
-        // ---- state chain of this wave's 16 columns
+    // Level product of one chunk: writes the level's pairs of L and A.
+    __device__ void level_mfma(int lev, int chunk) const {
+        f4 accL = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            const h8 xf = frag32(&sm.X[lev][0][0], KP, ln, lg, u);
+            const h8 yf = frag32(&sm.Y[lev][0][0], KP, ln, lg, u);
+            if (lev != 0) accL = mfma16x16x32(xf, xf, accL);
+            accA = mfma16x16x32(yf, xf, accA);
+        }
+        const int i = ln;
+        const int lb = chunk % 2, ab = chunk % 3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 4 * lg + j;
+            if (lev == 0) {
+                if (i >= c) {
+                    sm.L[lb][c][i] = 0.f;
+                    sm.AM[ab][c][i] = static_cast<_Float16>(i == c ? accA[j] * scale : 0.f);
+                }
+            } else {
+                const int bb = lev - 1;
+                const bool pair = ((c >> (bb + 1)) == (i >> (bb + 1))) && ((c >> bb) & 1) && !((i >> bb) & 1);
+                if (pair) {
+                    sm.L[lb][c][i] = sm.beta[lb][c] * accL[j];
+                    sm.AM[ab][c][i] = static_cast<_Float16>(accA[j] * scale);
+                }
+            }
+        }
+    }
+
+    // M = (I + L)^-1 Diag(beta) and W = M (E * K) of one chunk (one wave).
+    __device__ void solve_w(int chunk) const {
+        const int lb = chunk % 2;
+        f4 Lc, Lt;                                       // acc(L), acc(L^T)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Lc[j] = sm.L[lb][4 * lg + j][ln];
+        {
+            const float4 r = *reinterpret_cast<const float4*>(&sm.L[lb][ln][4 * lg]);
+            Lt[0] = r.x; Lt[1] = r.y; Lt[2] = r.z; Lt[3] = r.w;
+        }
+        const Split4 lc(Lc), lt(Lt);
+        const Split4 l2(mm3(lt, lc)), l2t(mm3(lc, lt));  // L^2, (L^2)^T
+        const Split4 l4(mm3(l2t, l2)), l4t(mm3(l2, l2t));
+        const Split4 l8(mm3(l4t, l4));
+        f4 Q;                                            // acc(I - L^T)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Q[j] = (4 * lg + j == ln ? 1.f : 0.f) - Lt[j];
+        Q += mm3(l2, Split4(Q));
+        Q += mm3(l4, Split4(Q));
+        Q += mm3(l8, Split4(Q));                         // acc(Minv^T) = A-layout of Minv
+        const float4 bt = *reinterpret_cast<const float4*>(&sm.beta[lb][4 * lg]);
+        Q[0] *= bt.x; Q[1] *= bt.y; Q[2] *= bt.z; Q[3] *= bt.w;
+        h4 mh, ml;
+        split4(Q, mh, ml);
+        *reinterpret_cast<h4*>(&sm.MH[ln][4 * lg]) = mh;
+        *reinterpret_cast<h4*>(&sm.ML[ln][4 * lg]) = ml;
+#pragma unroll
+        for (int t = 0; t < KT; ++t) {
+            const h4 kf = frag16(&sm.KET[lb][16 * t][0], RP, ln, lg);
+            f4 w = {0.f, 0.f, 0.f, 0.f};
+            w = mfma16x16x16(mh, kf, w);
+            w = mfma16x16x16(ml, kf, w);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.WN[4 * lg + j][16 * t + ln] = static_cast<_Float16>(-w[j]);
+        }
+    }
+
+    // ------------------------------------------------------------ consumers
+    __device__ void v_load(typename QIn<TQ>::Raw (&vr)[4], int chunk) const {
+        const int last = rows_in(chunk) - 1;
+        const char* v = cbase<TQ>(a.v, base(a.v_stride, chunk));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t ov = static_cast<uint32_t>(min(vrow0 + j, last)) * rs_v + col_v;
+            vr[j] = QIn<TQ>::ld(reinterpret_cast<const TQ*>(v + ov));
+        }
+    }
+
+    __device__ void consumer_a(int chunk, const typename QIn<TQ>::Raw (&vraw)[4], f4 (&S)[KT], f4& P,
+                               f4& O) const {
+        float vr[4];
+        const int nrow = rows_in(chunk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vr[j] = (4 * lg + j < nrow) ? QIn<TQ>::f(vraw[j]) : 0.f;
         h8 shi[KU], slo[KU];
 #pragma unroll
         for (int u = 0; u < KU; ++u)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                _Float16 x0, x1, y0, y1;
-                split_h(Sacc[2 * u][j], x0, y0);
-                split_h(Sacc[2 * u + 1][j], x1, y1);
-                shi[u][j] = x0; slo[u][j] = y0;
-                shi[u][4 + j] = x1; slo[u][4 + j] = y1;
+                const _Float16 x0 = static_cast<_Float16>(S[2 * u][j]);
+                const _Float16 x1 = static_cast<_Float16>(S[2 * u + 1][j]);
+                shi[u][j] = x0;
+                shi[u][4 + j] = x1;
+                slo[u][j] = static_cast<_Float16>(S[2 * u][j] - static_cast<float>(x0));
+                slo[u][4 + j] = static_cast<_Float16>(S[2 * u + 1][j] - static_cast<float>(x1));
             }
-        // P = U - W S
+        // U = M V
+        const h4 mh = frag16(&sm.MH[0][0], RP, ln, lg);
+        const h4 ml = frag16(&sm.ML[0][0], RP, ln, lg);
+        h4 vh, vl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            vh[j] = static_cast<_Float16>(vr[j]);
+            vl[j] = static_cast<_Float16>(vr[j] - static_cast<float>(vh[j]));
+        }
+        P = f4{0.f, 0.f, 0.f, 0.f};
+        P = mfma16x16x16(mh, vh, P);
+        P = mfma16x16x16(ml, vh, P);
+        if (!QIn<TQ>::exact) P = mfma16x16x16(mh, vl, P);
+        // P = U - W S ;  O = (Q * E) S
+        O = f4{0.f, 0.f, 0.f, 0.f};
+        const int qb = chunk % 3;
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
-            const h8 wh = frag32(&sm.WN[0][0][0], KP, ln, lg, u);
-            const h8 wl = frag32(&sm.WN[1][0][0], KP, ln, lg, u);
-            P = mfma16x16x32(wh, shi[u], P);
-            P = mfma16x16x32(wh, slo[u], P);
-            P = mfma16x16x32(wl, shi[u], P);
+            const h8 wf = frag32(&sm.WN[0][0], KP, ln, lg, u);
+            P = mfma16x16x32(wf, shi[u], P);
+            P = mfma16x16x32(wf, slo[u], P);
+            const h8 qf = frag32(&sm.QE[qb][0][0], KP, ln, lg, u);
+            O = mfma16x16x32(qf, shi[u], O);
+            O = mfma16x16x32(qf, slo[u], O);
         }
-        // O = scale (Q*E) S + A P
-        f4 O = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            const h8 qh = frag32(&sm.QE[0][0][0], KP, ln, lg, u);
-            const h8 ql = frag32(&sm.QE[1][0][0], KP, ln, lg, u);
-            O = mfma16x16x32(qh, shi[u], O);
-            O = mfma16x16x32(qh, slo[u], O);
-            O = mfma16x16x32(ql, shi[u], O);
-        }
+    }
+
+    __device__ void consumer_b(int chunk, f4 (&S)[KT], const f4& P, f4 O, int64_t col0, uint32_t ocol) const {
+        const int cb = chunk % 3;
 #pragma unroll
         for (int j = 0; j < 4; ++j) O[j] *= scale;
         h4 ph, pl;
+        split4(P, ph, pl);
+        const h4 af = frag16(&sm.AM[cb][0][0], RP, ln, lg);
+        O = mfma16x16x16(af, ph, O);
+        O = mfma16x16x16(af, pl, O);
+        // o[b, t, h, col]: wave-uniform chunk base + 32-bit lane offset
+        TQ* o = static_cast<TQ*>(a.o) + ((b * T + static_cast<int64_t>(chunk) * BT) * a.H + h) * a.V + col0;
+        const uint32_t orow = static_cast<uint32_t>(a.H * a.V);
+        const int nrow = rows_in(chunk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            _Float16 x, y;
-            split_h(P[j], x, y);
-            ph[j] = x; pl[j] = y;
-        }
-        {
-            const h4 ah = frag16(&sm.AM[0][0][0], RP, ln, lg);
-            const h4 al = frag16(&sm.AM[1][0][0], RP, ln, lg);
-            O = mfma16x16x16(ah, ph, O);
-            O = mfma16x16x16(ah, pl, O);
-            O = mfma16x16x16(al, ph, O);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t tt = t0 + 4 * lg + j;
-            if (tt < T) store_elem(a.o, ((b * T + tt) * H + h) * V + ncol, a.qkv_dtype, O[j]);
-        }
-        // S <- Diag(E[15]) S + Khat^T P
+        for (int j = 0; j < 4; ++j)
+            if (4 * lg + j < nrow) Elem<TQ>::st(o + (4 * lg + j) * orow + ocol, O[j]);
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
-            const float4 e = *reinterpret_cast<const float4*>(&sm.elast[16 * t + 4 * lg]);
-            Sacc[t][0] *= e.x; Sacc[t][1] *= e.y; Sacc[t][2] *= e.z; Sacc[t][3] *= e.w;
-            const h4 kh = frag16(&sm.KHT[0][16 * t][0], RP, ln, lg);
-            const h4 kl = frag16(&sm.KHT[1][16 * t][0], RP, ln, lg);
-            Sacc[t] = mfma16x16x16(kh, ph, Sacc[t]);
-            Sacc[t] = mfma16x16x16(kh, pl, Sacc[t]);
-            Sacc[t] = mfma16x16x16(kl, ph, Sacc[t]);
+            const float4 e = *reinterpret_cast<const float4*>(&sm.elast[cb][16 * t + 4 * lg]);
+            S[t][0] *= e.x; S[t][1] *= e.y; S[t][2] *= e.z; S[t][3] *= e.w;
+            const h4 kf = frag16(&sm.KHT[cb][16 * t][0], RP, ln, lg);
+            S[t] = mfma16x16x16(kf, ph, S[t]);
+            S[t] = mfma16x16x16(kf, pl, S[t]);
         }
-        // No barrier needed here: the next chunk's staging writes only alpha,
-        // qv, kv, beta and VTt, none of which this phase reads; the barrier
-        // after staging orders everything else.
+    }
+};
+
+template <int K, int NC, typename TQ>
+__global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda_fwd_args a) {
+    using KN = Kern<K, NC, TQ>;
+    constexpr int NP = KN::NP, KT = KN::KT, VT = KN::VT;
+    static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
+    __shared__ Smem<K> sm;
+    KN kn(a, sm);
+
+    const int64_t H = a.H, V = a.V;
+    const int nvt = static_cast<int>(V / VT);
+    int bid = blockIdx.x;
+    const int vt = bid % nvt;
+    bid /= nvt;
+    kn.h = bid % H;
+    kn.b = bid / H;
+    kn.T = a.T;
+    kn.nch = static_cast<int>((a.T + BT - 1) / BT);
+    kn.scale = a.scale;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    kn.lane = tid & 63;
+    kn.ln = kn.lane & 15;
+    kn.lg = kn.lane >> 4;
+    const int nch = kn.nch;
+
+    const bool consumer = wave < NC;
+    // consumer state: S[t][j] = S[16t + 4lg + j][col], col = col0 + ocol
+    const int64_t col0 = static_cast<int64_t>(vt) * VT;
+    const uint32_t ocol = static_cast<uint32_t>(16 * (consumer ? wave : 0) + kn.ln);
+    const int64_t col = col0 + ocol;
+    const int64_t sbase = (kn.b * H + kn.h) * static_cast<int64_t>(K) * V;
+    // producer lane: channel c, rows 8*hf .. 8*hf+7
+    const int pw = wave - NC;
+    const int pc = 32 * (consumer ? 0 : pw) + (kn.lane & 31);
+    const int phf = kn.lane >> 5;
+    const bool beta_lane = !consumer && pw == 0 && kn.lane < BT;
+    {
+        const uint32_t eq = static_cast<uint32_t>(sizeof(TQ));
+        kn.rs_q = static_cast<uint32_t>(a.q_stride[1]) * eq;
+        kn.rs_k = static_cast<uint32_t>(a.k_stride[1]) * eq;
+        kn.rs_v = static_cast<uint32_t>(a.v_stride[1]) * eq;
+        kn.rs_g = static_cast<uint32_t>(a.g_stride[1]) * 4u;
+        kn.rs_b = static_cast<uint32_t>(a.beta_stride[1]) * 4u;
+        kn.col_q = static_cast<uint32_t>(pc) * eq;
+        kn.col_k = static_cast<uint32_t>(pc) * eq;
+        kn.col_g = static_cast<uint32_t>(pc) * 4u;
+        kn.col_v = static_cast<uint32_t>(col) * eq;
+        kn.prow0 = 8 * phf;
+        kn.vrow0 = 4 * kn.lg;
     }
 
-#pragma unroll
-    for (int t = 0; t < KT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t r = 16 * t + 4 * lg + j;
-            store_elem(a.state_out, sbase + r * V + ncol, a.state_out_dtype, Sacc[t][j]);
+    f4 S[KT];
+    typename QIn<TQ>::Raw vr0[4], vr1[4];
+    PrepIn<TQ> pin0, pin1;
+    if (consumer) {
+        load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
+        kn.v_load(vr0, 0);
+        if (nch > 1) kn.v_load(vr1, 1);
+    } else {
+        kn.prep_load(pin0, 0, beta_lane);
+        if (nch > 1) kn.prep_load(pin1, 1, beta_lane);
+    }
+
+    f4 P = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
+    // step sp: producers build chunk sp, producer 0 solves chunk sp-1,
+    // consumers run chunk sp-2.  Register sets alternate with sp's parity.
+    auto step = [&](int sp, PrepIn<TQ>& pin, typename QIn<TQ>::Raw (&vr)[4]) {
+        const int cp = sp, cs = sp - 1, cc = sp - 2;
+        // ---- phase A
+        if (consumer) {
+            if (cc >= 0) {
+                kn.consumer_a(cc, vr, S, P, O);
+                if (cc + 2 < nch) kn.v_load(vr, cc + 2);
+            }
+        } else if (cp < nch) {
+            kn.prep_compute(pin, cp, pc, phf, beta_lane);
+            if (cp + 2 < nch) kn.prep_load(pin, cp + 2, beta_lane);
         }
+        __syncthreads();
+        // ---- phase B
+        if (consumer) {
+            if (cc >= 0) kn.consumer_b(cc, S, P, O, col0, ocol);
+        } else {
+            if (pw == 0 && cs >= 0 && cs < nch) kn.solve_w(cs);
+            if (cp < nch) {
+                if (NP == 1) {
+#pragma unroll
+                    for (int lev = 0; lev < NLEV; ++lev) kn.level_mfma(lev, cp);
+                } else {
+#pragma unroll
+                    for (int lev = 0; lev < NLEV; ++lev)
+                        if (1 + lev % (NP - 1) == pw) kn.level_mfma(lev, cp);
+                }
+            }
+        }
+        __syncthreads();
+    };
+    const int nsteps = nch + 2;
+    for (int sp = 0; sp < nsteps; sp += 2) {
+        step(sp, pin0, vr0);
+        if (sp + 1 < nsteps) step(sp + 1, pin1, vr1);
+    }
+
+    if (consumer) store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
 }
 
-template <int K, int NW>
-int launch_knw(const kda_fwd_args& a, hipStream_t stream) {
-    const int64_t blocks = a.B * a.H * (a.V / (16 * NW));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NW>), dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
-                       stream, a);
+template <int K, int NC, typename TQ>
+int launch_knq(const kda_fwd_args& a, hipStream_t stream) {
+    const int64_t blocks = a.B * a.H * (a.V / (16 * NC));
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(64 * (NC + K / 32)), 0, stream, a);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
+}
+
+template <int K, typename TQ>
+int launch_kq(const kda_fwd_args& a, hipStream_t stream) {
+    if (a.V % 64 == 0) return launch_knq<K, 4, TQ>(a, stream);
+    if (a.V % 32 == 0) return launch_knq<K, 2, TQ>(a, stream);
+    return launch_knq<K, 1, TQ>(a, stream);
 }
 
 template <int K>
 int launch_k(const kda_fwd_args& a, hipStream_t stream) {
-    if (a.V % 64 == 0) return launch_knw<K, 4>(a, stream);
-    if (a.V % 32 == 0) return launch_knw<K, 2>(a, stream);
-    return launch_knw<K, 1>(a, stream);
+    switch (a.qkv_dtype) {
+        case KDA_DTYPE_F16: return launch_kq<K, _Float16>(a, stream);
+        case KDA_DTYPE_BF16: return launch_kq<K, bf16_t>(a, stream);
+        case KDA_DTYPE_F32: return launch_kq<K, float>(a, stream);
+        default: return KDA_ERR_BAD_DTYPE;
+    }
 }
 
 }  // namespace
@@ -382,6 +644,14 @@ bool chunkwise_supported(int64_t K, int64_t V) {
 }
 
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream) {
+    // the pipeline reads gates in fp32 (the wrapper converts other dtypes)
+    if (a.g_dtype != KDA_DTYPE_F32 || a.beta_dtype != KDA_DTYPE_F32) return KDA_ERR_BAD_DTYPE;
+    // in-chunk offsets are 32-bit byte offsets: 16 token strides + one row must fit
+    const int64_t lim = int64_t(1) << 31;
+    const int64_t ts[5] = {a.q_stride[1], a.k_stride[1], a.v_stride[1], a.g_stride[1], a.beta_stride[1]};
+    for (int64_t st : ts)
+        if (st < 0 || (BT + 1) * st * 4 + a.V * 4 >= lim) return KDA_ERR_UNSUPPORTED;
+    if ((BT + 1) * a.H * a.V * 4 >= lim) return KDA_ERR_UNSUPPORTED;
     switch (a.K) {
         case 32: return launch_k<32>(a, stream);
         case 64: return launch_k<64>(a, stream);

@@ -128,6 +128,10 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
     q = _as_kernel_input(q if q.dtype == qk_dtype else q.to(qk_dtype))
     k = _as_kernel_input(k if k.dtype == qk_dtype else k.to(qk_dtype))
     v = _as_kernel_input(v)
+    if kind == "chunkwise":
+        # the chunkwise pipeline reads fp32 gates (the reference upcasts them too, kda.py:119-120)
+        g = g.float()
+        beta = beta.float()
     g = _as_kernel_input(_float_or_f32(g))
     beta = _float_or_f32(beta)
     if state is not None:

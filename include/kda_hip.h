@@ -89,6 +89,8 @@ typedef struct kda_fwd_args {
 /*
  * Chunkwise forward; replaces the body of kda_chunkwise (kimi_linear/kda.py:58-185).
  * o = per-token outputs, state_out = final state.  T may be 0.
+ * For T > 0, g and beta must be fp32 (KDA_ERR_BAD_DTYPE otherwise): the
+ * reference upcasts both before use (kda.py:119-120).
  */
 int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream);
 
