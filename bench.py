@@ -53,8 +53,9 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--only", choices=["chunkwise", "decode"], default=None,
-                   help="run one workload only (for profiling)")
+    p.add_argument("--only", choices=["chunkwise", "decode", "copy"], default=None,
+                   help="run one workload only (for profiling); 'copy' runs a plain 1 GiB "
+                        "device copy used to calibrate the HBM byte counters")
     return p.parse_args()
 
 
@@ -125,25 +126,27 @@ def decode_bench(pkg, wl, torch, n_sets):
 def cpu_baselines(wl, torch, include_decode=True):
     from oracle import kda_chunkwise_ref, kda_recurrent_ref
     threads = torch.get_num_threads()
-    # chunkwise sample: one sequence of the same layer shape (all 16 heads), 2048 tokens
-    Ts = 2048
-    s = wl.make_inputs(1, Ts, H1, D1, D1, device="cpu", seed=1, qkv_dtype=torch.float16)
+    # chunkwise sample: two sequences of the same layer shape (all 16 heads), 8192 tokens each
+    Bs, Ts = 2, 8192
+    s = wl.make_inputs(Bs, Ts, H1, D1, D1, device="cpu", seed=1, qkv_dtype=torch.float16)
     t0 = time.perf_counter()
     kda_chunkwise_ref(s["q"], s["k"], s["v"], s["g"], s["beta"], chunk_size=C1,
                       state_dtype=torch.float32)
     tc = time.perf_counter() - t0
-    out = {"value": Ts / tc, "unit": "tokens/s", "cores": threads, "kind": "port",
-           "sample": f"oracle kda_chunkwise_ref, B=1 T={Ts} H=16 dk=dv=128 C=64 (fp16 inputs "
+    out = {"value": Bs * Ts / tc, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": f"oracle kda_chunkwise_ref, B={Bs} T={Ts} H=16 dk=dv=128 C=64 (fp16 inputs "
                      f"upcast to fp32), one run, {tc:.1f} s"}
     if include_decode:
-        d = wl.make_inputs(B2, 32, H2, D1, D1, device="cpu", seed=2, qkv_dtype=torch.float16,
+        nst = 96
+        d = wl.make_inputs(B2, nst, H2, D1, D1, device="cpu", seed=2, qkv_dtype=torch.float16,
                            gate_dtype=torch.float16, state_std=0.02)
         t0 = time.perf_counter()
         kda_recurrent_ref(d["q"], d["k"], d["v"], d["g"], d["beta"], state=d["state"],
                           state_dtype=torch.float32)
         td = time.perf_counter() - t0
-        out["decode_us_per_step"] = td / 32 * 1e6
-        out["decode_sample"] = f"oracle kda_recurrent_ref, B=64 H=16 dk=dv=128, 32 steps, {td:.1f} s"
+        out["decode_us_per_step"] = td / nst * 1e6
+        out["decode_sample"] = (f"oracle kda_recurrent_ref, B=64 H=16 dk=dv=128, {nst} chained "
+                                f"steps, {td:.1f} s")
     return out
 
 
@@ -171,6 +174,15 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
+
+    if args.only == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 1 << 30, "copies": args.steps}), flush=True)
+        return
 
     result = {"metric": METRIC, "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
               "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
