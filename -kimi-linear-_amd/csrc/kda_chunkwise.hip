@@ -9,8 +9,9 @@
 //   E[r]   = prod_{t<=r} a_t              (= exp(gc_r), per channel)
 //   L[c,i] = beta_c <k_c, k_i * prod_{t=i+1..c} a_t>,  i < c
 //   A[c,i] = scale <q_c, k_i * prod_{t=i+1..c} a_t>,   i <= c
-//   M      = (I + L)^-1 Diag(beta),  W = M (E * K),  U = M V
-//   P      = U - W S,   O = scale (E * Q) S + A P
+//   M      = (I + L)^-1 Diag(beta)
+//   P      = M (V - (E * K) S)           (= U - W S with U = M V, W = M (E * K))
+//   O      = scale (E * Q) S + A P
 //   S     <- Diag(E[15]) S + ((E[15]/E) * K)^T P
 //
 // Decay factoring without pairwise exponentials: every pair i < c of a chunk
@@ -33,14 +34,19 @@
 //     as MFMA accumulators and runs the sequential chain of chunk n.
 //   NP = K/32 producer waves: two lanes per channel (8 rows each) build the
 //     operands of chunk n+2 straight from prefetched global loads; producer
-//     wave 0 then inverts (I + L) and forms W for chunk n+1 while the others
-//     compute the level products of chunk n+2.
+//     wave 0 inverts (I + L) of chunk n+1 while the others compute the level
+//     products of chunk n+2.
 // Each step has two phases separated by workgroup barriers:
-//   A: producers: operands(n+2) | consumers: U = M V, P = U - W S, O = QE S
-//   B: producer 0: solve + W (n+1), others: levels (n+2)
-//      | consumers: O += A P, store O, S <- E15 S + Khat^T P
-// Operands that are not exact in fp16 and carry the state (S, P, M) are split
-// into fp16 hi + lo; the others are single fp16 with fp32 accumulation.
+//   A: producers: decays + level operands (n+2)
+//      | consumers: Z = (E*K) S, O = (E*Q) S, P = M (V - Z)   (n)
+//   B: producer 0: (I + L)^-1 (n+1); others: level products (n+2); all
+//      producers: E-scaled operands (n+2)
+//      | consumers: O += A P, store O, S <- E15 S + Khat^T P   (n)
+// Operands that are not exact in fp16 and carry the state (S, P, M and
+// V - Z) are split into fp16 hi + lo; the others are single fp16 with fp32
+// accumulation.  Operands read through LDS transpose loads are stored
+// k-major, so each producer lane stores a channel's 8 rows with one 16-byte
+// write.
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -52,12 +58,12 @@ constexpr int BT = 16;    // tokens per internal chunk
 constexpr int RP = 24;    // padded row (halfs) of the [*][16] fp16 matrices (48 B rows)
 constexpr int LP = 20;    // padded row (floats) of the 16x16 fp32 L
 constexpr int NLEV = 5;   // operand levels: 0 = diagonal, 1 + b for bit b = 0..3
+constexpr int kXcds = 8;  // accelerator complex dies on MI355X
 
 // Input element access.  Raw values are held one per 32-bit register and
 // converted only at use, so a prefetch load is never followed by a wait.
 template <typename TQ> struct QIn;
 template <> struct QIn<_Float16> {
-    static constexpr bool exact = true;   // values are exact in fp16
     using Raw = uint32_t;
     static __device__ __forceinline__ Raw ld(const _Float16* p) {
         return *reinterpret_cast<const uint16_t*>(p);
@@ -67,7 +73,6 @@ template <> struct QIn<_Float16> {
     }
 };
 template <> struct QIn<bf16_t> {
-    static constexpr bool exact = false;
     using Raw = uint32_t;
     static __device__ __forceinline__ Raw ld(const bf16_t* p) {
         return *reinterpret_cast<const uint16_t*>(p);
@@ -75,20 +80,20 @@ template <> struct QIn<bf16_t> {
     static __device__ __forceinline__ float f(Raw r) { return __uint_as_float(r << 16); }
 };
 template <> struct QIn<float> {
-    static constexpr bool exact = false;
     using Raw = float;
     static __device__ __forceinline__ Raw ld(const float* p) { return *p; }
     static __device__ __forceinline__ float f(Raw r) { return r; }
 };
 
+// Operands consumed through LDS transpose reads are stored k-major ([K][16]:
+// the 16 chunk rows of one channel are contiguous), so a producer lane writes
+// its 8 rows of a channel with one 16-byte store.
 template <int K>
 struct __align__(16) Smem {
-    static constexpr int KP = K + 4;       // padded row (halfs) of [16][K] operands
-    _Float16 X[NLEV][BT][KP];              // level operands (k * factor)
-    _Float16 Y[NLEV][BT][KP];              // query-side level operands (q * factor)
-    _Float16 QE[3][BT][KP];                // q * E                  (chunk % 3)
-    _Float16 WN[BT][KP];                   // -W                     (single)
-    _Float16 KET[2][K][RP];                // (k * E)^T              (chunk % 2)
+    _Float16 XT[NLEV][K][BT];              // level operands (k * factor), k-major
+    _Float16 YT[NLEV][K][BT];              // query-side level operands (q * factor)
+    _Float16 QET[3][K][BT];                // q * E                  (chunk % 3)
+    _Float16 KET[3][K][BT];                // k * E                  (chunk % 3)
     _Float16 KHT[3][K][RP];                // (k * E15 / E)^T        (chunk % 3)
     _Float16 AM[3][BT][RP];                // scale * A              (chunk % 3)
     _Float16 MH[BT][RP];                   // M hi                   (single)
@@ -102,13 +107,26 @@ __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, 
     return *reinterpret_cast<const h4*>(base + row * stride + 4 * lg);
 }
 
-// 16x16x32 operand fragment: slots 0-3 hold k = 32u + 4lg + j, slots 4-7 hold
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
+
+// MFMA row fragment from a k-major [K][16] fp16 matrix X^T through the LDS
+// transpose read (ds_read_b64_tr_b16): within each 16-lane group, lane 4j+q
+// supplies the four rows 4q..4q+3 of channel kbase+j, and lane i receives
+// X[i][kbase + 0..3] -- the A-operand fragment of row i, which is also the
+// B-operand fragment of column i of X^T.
+__device__ __forceinline__ h4 frag16_tr(const _Float16* xt, int kbase, int ln) {
+    const _Float16* p = xt + (kbase + (ln >> 2)) * BT + 4 * (ln & 3);
+    return __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
+}
+
+// 16x16x32 fragment: slots 0-3 hold k = 32u + 4lg + j, slots 4-7 hold
 // k = 32u + 16 + 4lg + j.  A and B fragments use the same assignment, so the
-// product is the full 32-wide dot product whatever slot order the unit uses.
-__device__ __forceinline__ h8 frag32(const _Float16* base, int stride, int row, int lg, int u) {
-    const _Float16* p = base + row * stride + 32 * u + 4 * lg;
-    const h4 lo = *reinterpret_cast<const h4*>(p);
-    const h4 hi = *reinterpret_cast<const h4*>(p + 16);
+// product is the full 32-wide dot product whatever slot order the unit uses;
+// it also matches the two state tiles 2u, 2u+1 held by a consumer lane group.
+__device__ __forceinline__ h8 frag32_tr(const _Float16* xt, int lg, int ln, int u) {
+    const h4 lo = frag16_tr(xt, 32 * u + 4 * lg, ln);
+    const h4 hi = frag16_tr(xt, 32 * u + 16 + 4 * lg, ln);
     return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -119,6 +137,15 @@ __device__ __forceinline__ void split4(const f4& x, h4& hi, h4& lo) {
         hi[j] = h;
         lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(h));
     }
+}
+
+// x of lane (lane ^ 32), through the VALU cross-half swap (no LDS traffic):
+// permlane32_swap(x, x) returns {x of lane l-32 in the upper half,
+// x of lane l+32 in the lower half} as its two results.
+__device__ __forceinline__ float xor32(float x, int lane) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
 }
 
 // An fp32 accumulator tile split into fp16 hi + lo operands.
@@ -185,7 +212,6 @@ __device__ __forceinline__ void store_state(const f4 (&S)[KT], void* p, int dtyp
 
 template <int K, int NC, typename TQ>
 struct Kern {
-    static constexpr int KP = Smem<K>::KP;
     static constexpr int KT = K / 16;       // 16-row state tiles
     static constexpr int KU = K / 32;       // 32-wide k blocks
     static constexpr int NP = K / 32;       // producer waves
@@ -250,109 +276,110 @@ struct Kern {
         }
     }
 
-    // Operands of one chunk for channel c, rows 8*hf .. 8*hf+7.
-    __device__ void prep_compute(const PrepIn<TQ>& pin, int chunk, int c, int hf, bool beta_lane) const {
-        struct { float g[8], q[8], k[8], beta; } in;
+    // Producer values of one chunk carried from phase A to phase B.
+    struct PrepMid {
+        float q[8], k[8], pre[8], suf[8];
+        float emul, kmul;
+    };
+
+    // Phase A operands of one chunk for channel c, rows 8*hf .. 8*hf+7: the
+    // decays, the level operands X_b, Y_b (k-major, one 16-byte store each)
+    // and beta.
+    __device__ void prep_levels(const PrepIn<TQ>& pin, PrepMid& mid, int chunk, int c, int hf,
+                                bool beta_lane) const {
+        float gv[8];
+        float beta = pin.beta;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            in.g[i] = pin.g[i];
-            in.q[i] = QIn<TQ>::f(pin.q[i]);
-            in.k[i] = QIn<TQ>::f(pin.k[i]);
+            gv[i] = pin.g[i];
+            mid.q[i] = QIn<TQ>::f(pin.q[i]);
+            mid.k[i] = QIn<TQ>::f(pin.k[i]);
         }
-        in.beta = pin.beta;
         const int nrow = rows_in(chunk);
         if (nrow < BT) {                                // tail chunk: neutral padding rows
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (8 * hf + i >= nrow) { in.g[i] = 0.f; in.q[i] = 0.f; in.k[i] = 0.f; }
-            if (lane >= nrow) in.beta = 0.f;
+                if (8 * hf + i >= nrow) { gv[i] = 0.f; mid.q[i] = 0.f; mid.k[i] = 0.f; }
+            if (lane >= nrow) beta = 0.f;
         }
         float al[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) al[i] = fast_exp(in.g[i]);
-        float pre[8];                                   // prod_{t<=i} within the half
-        pre[0] = al[0];
+        for (int i = 0; i < 8; ++i) al[i] = fast_exp(gv[i]);
+        mid.pre[0] = al[0];                             // prod_{t<=i} within the half
 #pragma unroll
-        for (int i = 1; i < 8; ++i) pre[i] = pre[i - 1] * al[i];
-        float suf[8];                                   // prod_{t=i+1..7} within the half
-        suf[7] = 1.f;
+        for (int i = 1; i < 8; ++i) mid.pre[i] = mid.pre[i - 1] * al[i];
+        mid.suf[7] = 1.f;                               // prod_{t=i+1..7} within the half
 #pragma unroll
-        for (int i = 6; i >= 0; --i) suf[i] = suf[i + 1] * al[i + 1];
-        const float other = __shfl_xor(pre[7], 32);    // product over the other half
-        const float a8 = __shfl_xor(al[0], 32);        // lower half: a of row 8
+        for (int i = 6; i >= 0; --i) mid.suf[i] = mid.suf[i + 1] * al[i + 1];
+        const float other = xor32(mid.pre[7], lane);    // product over the other half
+        const float a8 = xor32(al[0], lane);            // lower half: a of row 8
         const bool up = hf != 0;
-        const float emul = up ? other : 1.f;            // E = exp(gc) = prefix over the chunk
-        const float kmul = up ? 1.f : other;            // E15 / E = suffix over the chunk
+        mid.emul = up ? other : 1.f;                    // E = exp(gc): prefix over the chunk
+        mid.kmul = up ? 1.f : other;                    // E15 / E: suffix over the chunk
+        if (beta_lane) sm.beta[chunk % 2][lane] = beta;
+
         const int r0 = 8 * hf;
-        const int b3 = chunk % 3, b2 = chunk % 2;
-
-        h8 ke8, kh8;
+        // level factors F_b(row); query-side operands of key rows are never
+        // read unmasked, so Y is written for every row with the same factor
+        float f[8];
+        auto level = [&](int lev) {
+            h8 x, y;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float e = pre[i] * emul;
-            sm.QE[b3][r0 + i][c] = static_cast<_Float16>(in.q[i] * e);
-            ke8[i] = static_cast<_Float16>(in.k[i] * e);
-            kh8[i] = static_cast<_Float16>(in.k[i] * (suf[i] * kmul));
-        }
-        *reinterpret_cast<h8*>(&sm.KET[b2][c][r0]) = ke8;
-        *reinterpret_cast<h8*>(&sm.KHT[b3][c][r0]) = kh8;
-        if (up) sm.elast[b3][c] = pre[7] * emul;
-        if (beta_lane) sm.beta[b2][lane] = in.beta;
-
+            for (int i = 0; i < 8; ++i) {
+                x[i] = static_cast<_Float16>(mid.k[i] * f[i]);
+                y[i] = static_cast<_Float16>(mid.q[i] * f[i]);
+            }
+            *reinterpret_cast<h8*>(&sm.XT[lev][c][r0]) = x;
+            *reinterpret_cast<h8*>(&sm.YT[lev][c][r0]) = y;
+        };
         // level "diag": factor 1
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            sm.X[0][r0 + i][c] = static_cast<_Float16>(in.k[i]);
-            sm.Y[0][r0 + i][c] = static_cast<_Float16>(in.q[i]);
-        }
-        // level b = 0: query rows odd (factor 1), key rows even (a_{i+1})
+        for (int i = 0; i < 8; ++i) f[i] = 1.f;
+        level(0);
+        // level b = 0: ref = odd rows; key rows even -> a_{i+1}
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            sm.X[1][r0 + i][c] = static_cast<_Float16>(in.k[i] * al[i + 1]);
-            sm.X[1][r0 + i + 1][c] = static_cast<_Float16>(in.k[i + 1]);
-            sm.Y[1][r0 + i + 1][c] = static_cast<_Float16>(in.q[i + 1]);
-        }
+        for (int i = 0; i < 8; i += 2) { f[i] = al[i + 1]; f[i + 1] = 1.f; }
+        level(1);
         // level b = 1: ref = 2 mod 4
 #pragma unroll
         for (int i = 0; i < 8; i += 4) {
-            const float f1 = al[i + 2];
-            const float f0 = al[i + 1] * f1;
-            const float f3 = al[i + 3];
-            sm.X[2][r0 + i][c] = static_cast<_Float16>(in.k[i] * f0);
-            sm.X[2][r0 + i + 1][c] = static_cast<_Float16>(in.k[i + 1] * f1);
-            sm.X[2][r0 + i + 2][c] = static_cast<_Float16>(in.k[i + 2]);
-            sm.X[2][r0 + i + 3][c] = static_cast<_Float16>(in.k[i + 3] * f3);
-            sm.Y[2][r0 + i + 2][c] = static_cast<_Float16>(in.q[i + 2]);
-            sm.Y[2][r0 + i + 3][c] = static_cast<_Float16>(in.q[i + 3] * f3);
+            f[i + 1] = al[i + 2];
+            f[i] = al[i + 1] * f[i + 1];
+            f[i + 2] = 1.f;
+            f[i + 3] = al[i + 3];
         }
+        level(2);
         // level b = 2: ref = 4 within the half
-        {
-            const float f3 = al[4], f2 = al[3] * f3, f1 = al[2] * f2, f0 = al[1] * f1;
-            const float f5 = al[5], f6 = f5 * al[6], f7 = f6 * al[7];
-            sm.X[3][r0 + 0][c] = static_cast<_Float16>(in.k[0] * f0);
-            sm.X[3][r0 + 1][c] = static_cast<_Float16>(in.k[1] * f1);
-            sm.X[3][r0 + 2][c] = static_cast<_Float16>(in.k[2] * f2);
-            sm.X[3][r0 + 3][c] = static_cast<_Float16>(in.k[3] * f3);
-            sm.X[3][r0 + 4][c] = static_cast<_Float16>(in.k[4]);
-            sm.X[3][r0 + 5][c] = static_cast<_Float16>(in.k[5] * f5);
-            sm.X[3][r0 + 6][c] = static_cast<_Float16>(in.k[6] * f6);
-            sm.X[3][r0 + 7][c] = static_cast<_Float16>(in.k[7] * f7);
-            sm.Y[3][r0 + 4][c] = static_cast<_Float16>(in.q[4]);
-            sm.Y[3][r0 + 5][c] = static_cast<_Float16>(in.q[5] * f5);
-            sm.Y[3][r0 + 6][c] = static_cast<_Float16>(in.q[6] * f6);
-            sm.Y[3][r0 + 7][c] = static_cast<_Float16>(in.q[7] * f7);
-        }
+        f[3] = al[4]; f[2] = al[3] * f[3]; f[1] = al[2] * f[2]; f[0] = al[1] * f[1];
+        f[4] = 1.f; f[5] = al[5]; f[6] = f[5] * al[6]; f[7] = f[6] * al[7];
+        level(3);
         // level b = 3: ref = 8; upper half = query rows (prod_{9..r}), lower = key rows
         {
-            float f = 1.f;
+            float q = 1.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (i > 0) f *= al[i];
-                const float fr = up ? f : suf[i] * a8;
-                sm.X[4][r0 + i][c] = static_cast<_Float16>(in.k[i] * fr);
-                sm.Y[4][r0 + i][c] = static_cast<_Float16>(in.q[i] * fr);   // key rows: masked later
+                if (i > 0) q *= al[i];
+                f[i] = up ? q : mid.suf[i] * a8;
             }
         }
+        level(4);
+    }
+
+    // Phase B operands of one chunk: q * E, k * E, k * E15 / E and E15.
+    __device__ void prep_e(const PrepMid& mid, int chunk, int c, int hf) const {
+        const int b3 = chunk % 3, r0 = 8 * hf;
+        h8 qe, ke, kh;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float e = mid.pre[i] * mid.emul;
+            qe[i] = static_cast<_Float16>(mid.q[i] * e);
+            ke[i] = static_cast<_Float16>(mid.k[i] * e);
+            kh[i] = static_cast<_Float16>(mid.k[i] * (mid.suf[i] * mid.kmul));
+        }
+        *reinterpret_cast<h8*>(&sm.QET[b3][c][r0]) = qe;
+        *reinterpret_cast<h8*>(&sm.KET[b3][c][r0]) = ke;
+        *reinterpret_cast<h8*>(&sm.KHT[b3][c][r0]) = kh;
+        if (hf) sm.elast[b3][c] = mid.pre[7] * mid.emul;
     }
 
     // Level product of one chunk: writes the level's pairs of L and A.
@@ -360,8 +387,8 @@ struct Kern {
         f4 accL = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
-            const h8 xf = frag32(&sm.X[lev][0][0], KP, ln, lg, u);
-            const h8 yf = frag32(&sm.Y[lev][0][0], KP, ln, lg, u);
+            const h8 xf = frag32_tr(&sm.XT[lev][0][0], lg, ln, u);
+            const h8 yf = frag32_tr(&sm.YT[lev][0][0], lg, ln, u);
             if (lev != 0) accL = mfma16x16x32(xf, xf, accL);
             accA = mfma16x16x32(yf, xf, accA);
         }
@@ -386,8 +413,9 @@ struct Kern {
         }
     }
 
-    // M = (I + L)^-1 Diag(beta) and W = M (E * K) of one chunk (one wave).
-    __device__ void solve_w(int chunk) const {
+    // M = (I + L)^-1 Diag(beta) of one chunk (one wave), stored as hi/lo
+    // A-operand fragments for the consumers.
+    __device__ void solve_m(int chunk) const {
         const int lb = chunk % 2;
         f4 Lc, Lt;                                       // acc(L), acc(L^T)
 #pragma unroll
@@ -412,15 +440,6 @@ struct Kern {
         split4(Q, mh, ml);
         *reinterpret_cast<h4*>(&sm.MH[ln][4 * lg]) = mh;
         *reinterpret_cast<h4*>(&sm.ML[ln][4 * lg]) = ml;
-#pragma unroll
-        for (int t = 0; t < KT; ++t) {
-            const h4 kf = frag16(&sm.KET[lb][16 * t][0], RP, ln, lg);
-            f4 w = {0.f, 0.f, 0.f, 0.f};
-            w = mfma16x16x16(mh, kf, w);
-            w = mfma16x16x16(ml, kf, w);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sm.WN[4 * lg + j][16 * t + ln] = static_cast<_Float16>(-w[j]);
-        }
     }
 
     // ------------------------------------------------------------ consumers
@@ -452,31 +471,30 @@ struct Kern {
                 slo[u][j] = static_cast<_Float16>(S[2 * u][j] - static_cast<float>(x0));
                 slo[u][4 + j] = static_cast<_Float16>(S[2 * u + 1][j] - static_cast<float>(x1));
             }
-        // U = M V
-        const h4 mh = frag16(&sm.MH[0][0], RP, ln, lg);
-        const h4 ml = frag16(&sm.ML[0][0], RP, ln, lg);
-        h4 vh, vl;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            vh[j] = static_cast<_Float16>(vr[j]);
-            vl[j] = static_cast<_Float16>(vr[j] - static_cast<float>(vh[j]));
-        }
-        P = f4{0.f, 0.f, 0.f, 0.f};
-        P = mfma16x16x16(mh, vh, P);
-        P = mfma16x16x16(ml, vh, P);
-        if (!QIn<TQ>::exact) P = mfma16x16x16(mh, vl, P);
-        // P = U - W S ;  O = (Q * E) S
+        // Z = (k * E) S and O = (q * E) S over the K channels
+        const int cb = chunk % 3;
+        f4 Z = {0.f, 0.f, 0.f, 0.f};
         O = f4{0.f, 0.f, 0.f, 0.f};
-        const int qb = chunk % 3;
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
-            const h8 wf = frag32(&sm.WN[0][0], KP, ln, lg, u);
-            P = mfma16x16x32(wf, shi[u], P);
-            P = mfma16x16x32(wf, slo[u], P);
-            const h8 qf = frag32(&sm.QE[qb][0][0], KP, ln, lg, u);
+            const h8 kf = frag32_tr(&sm.KET[cb][0][0], lg, ln, u);
+            Z = mfma16x16x32(kf, shi[u], Z);
+            Z = mfma16x16x32(kf, slo[u], Z);
+            const h8 qf = frag32_tr(&sm.QET[cb][0][0], lg, ln, u);
             O = mfma16x16x32(qf, shi[u], O);
             O = mfma16x16x32(qf, slo[u], O);
         }
+        // P = U - W S = M (V - Z)
+        f4 R;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) R[j] = vr[j] - Z[j];
+        const Split4 r(R);
+        const h4 mh = frag16(&sm.MH[0][0], RP, ln, lg);
+        const h4 ml = frag16(&sm.ML[0][0], RP, ln, lg);
+        P = f4{0.f, 0.f, 0.f, 0.f};
+        P = mfma16x16x16(mh, r.hi, P);
+        P = mfma16x16x16(mh, r.lo, P);
+        P = mfma16x16x16(ml, r.hi, P);
     }
 
     __device__ void consumer_b(int chunk, f4 (&S)[KT], const f4& P, f4 O, int64_t col0, uint32_t ocol) const {
@@ -516,7 +534,11 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
 
     const int64_t H = a.H, V = a.V;
     const int nvt = static_cast<int>(V / VT);
+    // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs, so
+    // renumber them to put consecutive logical workgroups -- the V-tiles of
+    // one head, which all read the head's q, k and g -- on one XCD and its L2.
     int bid = blockIdx.x;
+    if (gridDim.x % kXcds == 0) bid = (bid % kXcds) * (gridDim.x / kXcds) + bid / kXcds;
     const int vt = bid % nvt;
     bid /= nvt;
     kn.h = bid % H;
@@ -557,39 +579,49 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
         kn.vrow0 = 4 * kn.lg;
     }
 
-    f4 S[KT];
-    typename QIn<TQ>::Raw vr0[4], vr1[4];
-    PrepIn<TQ> pin0, pin1;
+    // step sp: producers build chunk sp, producer 0 inverts chunk sp-1,
+    // consumers run chunk sp-2.  Each role runs its own loop with the same
+    // two barriers per step; register sets alternate with sp's parity and
+    // every prefetch is issued unconditionally (chunk index clamped), so the
+    // compiler's load accounting stays exact and a wait covers only the chunk
+    // being consumed.
+    const int nsteps = nch + 2;
+    const int last = nch - 1;
     if (consumer) {
+        f4 S[KT];
+        typename QIn<TQ>::Raw vr0[4], vr1[4];
         load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
         kn.v_load(vr0, 0);
-        if (nch > 1) kn.v_load(vr1, 1);
-    } else {
-        kn.prep_load(pin0, 0, beta_lane);
-        if (nch > 1) kn.prep_load(pin1, 1, beta_lane);
-    }
-
-    f4 P = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
-    // step sp: producers build chunk sp, producer 0 solves chunk sp-1,
-    // consumers run chunk sp-2.  Register sets alternate with sp's parity.
-    auto step = [&](int sp, PrepIn<TQ>& pin, typename QIn<TQ>::Raw (&vr)[4]) {
-        const int cp = sp, cs = sp - 1, cc = sp - 2;
-        // ---- phase A
-        if (consumer) {
+        kn.v_load(vr1, min(1, last));
+        f4 P = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
+        auto step = [&](int sp, typename QIn<TQ>::Raw (&vr)[4]) {
+            const int cc = sp - 2;
             if (cc >= 0) {
                 kn.consumer_a(cc, vr, S, P, O);
-                if (cc + 2 < nch) kn.v_load(vr, cc + 2);
+                kn.v_load(vr, min(cc + 2, last));
             }
-        } else if (cp < nch) {
-            kn.prep_compute(pin, cp, pc, phf, beta_lane);
-            if (cp + 2 < nch) kn.prep_load(pin, cp + 2, beta_lane);
-        }
-        __syncthreads();
-        // ---- phase B
-        if (consumer) {
+            __syncthreads();
             if (cc >= 0) kn.consumer_b(cc, S, P, O, col0, ocol);
-        } else {
-            if (pw == 0 && cs >= 0 && cs < nch) kn.solve_w(cs);
+            __syncthreads();
+        };
+        for (int sp = 0; sp < nsteps; sp += 2) {
+            step(sp, vr0);
+            if (sp + 1 < nsteps) step(sp + 1, vr1);
+        }
+        store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
+    } else {
+        PrepIn<TQ> pin0, pin1;
+        kn.prep_load(pin0, 0, beta_lane);
+        kn.prep_load(pin1, min(1, last), beta_lane);
+        typename KN::PrepMid mid;
+        auto step = [&](int sp, PrepIn<TQ>& pin) {
+            const int cp = sp, cs = sp - 1;
+            if (cp < nch) {
+                kn.prep_levels(pin, mid, cp, pc, phf, beta_lane);
+                kn.prep_load(pin, min(cp + 2, last), beta_lane);
+            }
+            __syncthreads();
+            if (pw == 0 && cs >= 0 && cs < nch) kn.solve_m(cs);
             if (cp < nch) {
                 if (NP == 1) {
 #pragma unroll
@@ -599,17 +631,15 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
                     for (int lev = 0; lev < NLEV; ++lev)
                         if (1 + lev % (NP - 1) == pw) kn.level_mfma(lev, cp);
                 }
+                kn.prep_e(mid, cp, pc, phf);
             }
+            __syncthreads();
+        };
+        for (int sp = 0; sp < nsteps; sp += 2) {
+            step(sp, pin0);
+            if (sp + 1 < nsteps) step(sp + 1, pin1);
         }
-        __syncthreads();
-    };
-    const int nsteps = nch + 2;
-    for (int sp = 0; sp < nsteps; sp += 2) {
-        step(sp, pin0, vr0);
-        if (sp + 1 < nsteps) step(sp + 1, pin1, vr1);
     }
-
-    if (consumer) store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
 }
 
 template <int K, int NC, typename TQ>
