@@ -60,30 +60,65 @@ constexpr int LP = 20;    // padded row (floats) of the 16x16 fp32 L
 constexpr int NLEV = 5;   // operand levels: 0 = diagonal, 1 + b for bit b = 0..3
 constexpr int kXcds = 8;  // accelerator complex dies on MI355X
 
-// Input element access.  Raw values are held one per 32-bit register and
-// converted only at use, so a prefetch load is never followed by a wait.
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Input element access through raw buffer loads.  A chunk's descriptor covers
+// exactly its rows before T, so rows past T read as zero -- the neutral
+// padding (k = q = v = g = beta = 0) -- with no clamping or masking.  Loaded
+// values are held one per 32-bit register and converted only at use, so a
+// prefetch load is never followed by a wait.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(nbytes), 0x00020000);
+}
+__device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+}
+
 template <typename TQ> struct QIn;
 template <> struct QIn<_Float16> {
-    using Raw = uint32_t;
-    static __device__ __forceinline__ Raw ld(const _Float16* p) {
-        return *reinterpret_cast<const uint16_t*>(p);
-    }
-    static __device__ __forceinline__ float f(Raw r) {
+    static __device__ __forceinline__ uint32_t ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return bload16(r, off); }
+    static __device__ __forceinline__ float f(uint32_t r) {
         return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+    }
+    static __device__ __forceinline__ h8 oct(const uint32_t (&r)[8]) {   // exact: repack the bits
+        h8 x;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(r[i]));
+        return x;
     }
 };
 template <> struct QIn<bf16_t> {
-    using Raw = uint32_t;
-    static __device__ __forceinline__ Raw ld(const bf16_t* p) {
-        return *reinterpret_cast<const uint16_t*>(p);
+    static __device__ __forceinline__ uint32_t ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return bload16(r, off); }
+    static __device__ __forceinline__ float f(uint32_t r) { return __uint_as_float(r << 16); }
+    static __device__ __forceinline__ h8 oct(const uint32_t (&r)[8]) {
+        h8 x;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(f(r[i]));
+        return x;
     }
-    static __device__ __forceinline__ float f(Raw r) { return __uint_as_float(r << 16); }
 };
 template <> struct QIn<float> {
-    using Raw = float;
-    static __device__ __forceinline__ Raw ld(const float* p) { return *p; }
-    static __device__ __forceinline__ float f(Raw r) { return r; }
+    static __device__ __forceinline__ uint32_t ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return bload32(r, off); }
+    static __device__ __forceinline__ float f(uint32_t r) { return __uint_as_float(r); }
+    static __device__ __forceinline__ h8 oct(const uint32_t (&r)[8]) {
+        h8 x;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(f(r[i]));
+        return x;
+    }
 };
+
+// Eight fp32 values rounded to fp16.
+__device__ __forceinline__ h8 to_h8(const float (&x)[8]) {
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(x[i]);
+    return r;
+}
 
 // Operands consumed through LDS transpose reads are stored k-major ([K][16]:
 // the 16 chunk rows of one channel are contiguous), so a producer lane writes
@@ -130,13 +165,24 @@ __device__ __forceinline__ h8 frag32_tr(const _Float16* xt, int lg, int ln, int 
     return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// fp16 lo halves of two fp32 values given their fp16 hi halves: f16(x - hi).
+// The compiler forms x - hi with v_fma_mix_f32 (hi read as fp16 in place) and
+// packs the pair with one conversion.  (A hand-written v_fma_mixlo/mixhi
+// pair on one register is left out: the compiler's hazard pass does not see
+// inside inline asm, and that sequence gave run-to-run differences.)
+__device__ __forceinline__ h2 split_lo_pair(float x0, float x1, h2 hi) {
+    return h2{static_cast<_Float16>(x0 - static_cast<float>(hi[0])),
+              static_cast<_Float16>(x1 - static_cast<float>(hi[1]))};
+}
+
+// Four fp32 values as fp16 hi + lo (x ~= hi + lo to ~2^-22 relative).
 __device__ __forceinline__ void split4(const f4& x, h4& hi, h4& lo) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const _Float16 h = static_cast<_Float16>(x[j]);
-        hi[j] = h;
-        lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(h));
-    }
+    const h2 h01 = h2{static_cast<_Float16>(x[0]), static_cast<_Float16>(x[1])};
+    const h2 h23 = h2{static_cast<_Float16>(x[2]), static_cast<_Float16>(x[3])};
+    const h2 l01 = split_lo_pair(x[0], x[1], h01);
+    const h2 l23 = split_lo_pair(x[2], x[3], h23);
+    hi = h4{h01[0], h01[1], h23[0], h23[1]};
+    lo = h4{l01[0], l01[1], l23[0], l23[1]};
 }
 
 // x of lane (lane ^ 32), through the VALU cross-half swap (no LDS traffic):
@@ -164,14 +210,27 @@ __device__ __forceinline__ f4 mm3(const Split4& a, const Split4& b) {
 }
 
 // Raw per-lane inputs of one chunk for a producer lane (one channel, 8 rows).
-// Loaded values stay unconverted until use, so the loads remain in flight
-// across the pipeline steps instead of stalling at issue.
-template <typename TQ>
 struct PrepIn {
-    float g[8];
-    typename QIn<TQ>::Raw q[8], k[8];
-    float beta;
+    uint32_t g[8], q[8], k[8];
+    uint32_t beta;
 };
+
+// Prefetched values are converted only where they are used.  Left alone, the
+// compiler hoists a conversion (or the packing of two fp16 loads into one
+// register) up to the load, which puts a wait for the whole prefetch right
+// after it is issued.  An empty volatile asm that "modifies" the registers at
+// the point of use keeps every such instruction, and the wait, there.
+template <int N>
+__device__ __forceinline__ void use_here(uint32_t (&r)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
+}
+__device__ __forceinline__ void use_here(PrepIn& p) {
+    use_here(p.g);
+    use_here(p.q);
+    use_here(p.k);
+    asm volatile("" : "+v"(p.beta));
+}
 
 // Accumulator-layout state tiles: S[t][j] = state[16t + 4lg + j][col]; `off`
 // is the element offset of (row 4lg, col) and rows are V apart.  All loads
@@ -224,87 +283,60 @@ struct Kern {
     int nch;
     float scale;
     int lane, ln, lg;
-    // per-lane column byte offsets, first rows and per-row byte strides; a
-    // lane's element (row r, its column) of a chunk is at base + r * rs + col
-    uint32_t col_q, col_k, col_g, col_v;
+    // per-row byte strides and this lane's byte offsets inside a chunk
     uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;
-    int prow0, vrow0;
+    uint32_t off_q[8], off_k[8], off_g[8], off_v[4], off_b;
 
     __device__ Kern(const kda_fwd_args& args, Smem<K>& s) : a(args), sm(s) {}
 
-    // ------------------------------------------------------------ producers
     // Rows of chunk `chunk` that lie before T (1..BT).
     __device__ int rows_in(int chunk) const {
         const int64_t left = T - static_cast<int64_t>(chunk) * BT;
         return left < BT ? static_cast<int>(left) : BT;
     }
 
-    // Element offset of (b, t0, h, 0) of a [B, T, H, D] view.
-    __device__ int64_t base(const int64_t (&st)[3], int chunk) const {
-        return b * st[0] + static_cast<int64_t>(chunk) * BT * st[1] + h * st[2];
+    // Buffer descriptor over the rows of one chunk of a [B, T, H, D] view
+    // (elements of size es, token stride rs bytes) at (b, t0, h, 0).
+    __device__ __amdgpu_buffer_rsrc_t chunk_rsrc(const void* p, const int64_t (&st)[3], int es, uint32_t rs,
+                                                 int chunk) const {
+        const int64_t e = b * st[0] + static_cast<int64_t>(chunk) * BT * st[1] + h * st[2];
+        return make_rsrc(static_cast<const char*>(p) + e * es, static_cast<uint32_t>(rows_in(chunk)) * rs);
     }
 
-    template <typename T>
-    static __device__ __forceinline__ const char* cbase(const void* p, int64_t elems) {
-        return reinterpret_cast<const char*>(static_cast<const T*>(p) + elems);
-    }
-    template <typename T>
-    static __device__ __forceinline__ T at(const char* base, uint32_t off) {
-        return *reinterpret_cast<const T*>(base + off);
-    }
-
-    // Issue the loads of one chunk (rows past T read the last row; masked at use).
-    // Chunk bases are wave-uniform; every per-lane offset is a non-negative
-    // 32-bit byte offset formed before it is added to the base.
-    __device__ void prep_load(PrepIn<TQ>& in, int chunk, bool beta_lane) const {
-        const int last = rows_in(chunk) - 1;
-        const char* q = cbase<TQ>(a.q, base(a.q_stride, chunk));
-        const char* k = cbase<TQ>(a.k, base(a.k_stride, chunk));
-        const char* g = cbase<float>(a.g, base(a.g_stride, chunk));
+    // ------------------------------------------------------------ producers
+    __device__ void prep_load(PrepIn& in, int chunk, bool beta_lane) const {
+        const auto rq = chunk_rsrc(a.q, a.q_stride, sizeof(TQ), rs_q, chunk);
+        const auto rk = chunk_rsrc(a.k, a.k_stride, sizeof(TQ), rs_k, chunk);
+        const auto rg = chunk_rsrc(a.g, a.g_stride, 4, rs_g, chunk);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t r = static_cast<uint32_t>(min(prow0 + i, last));
-            const uint32_t og = r * rs_g + col_g, oq = r * rs_q + col_q, ok = r * rs_k + col_k;
-            in.g[i] = at<float>(g, og);
-            in.q[i] = QIn<TQ>::ld(reinterpret_cast<const TQ*>(q + oq));
-            in.k[i] = QIn<TQ>::ld(reinterpret_cast<const TQ*>(k + ok));
+            in.g[i] = bload32(rg, off_g[i]);
+            in.q[i] = QIn<TQ>::ld(rq, off_q[i]);
+            in.k[i] = QIn<TQ>::ld(rk, off_k[i]);
         }
-        if (beta_lane) {
-            const char* bp = cbase<float>(a.beta, base(a.beta_stride, chunk));
-            const uint32_t ob = static_cast<uint32_t>(min(lane, last)) * rs_b;
-            in.beta = at<float>(bp, ob);
-        }
+        if (beta_lane) in.beta = bload32(chunk_rsrc(a.beta, a.beta_stride, 4, rs_b, chunk), off_b);
     }
 
     // Producer values of one chunk carried from phase A to phase B.
     struct PrepMid {
-        float q[8], k[8], pre[8], suf[8];
+        h8 qh, kh;                                  // the 8 rows as fp16
+        float pre[8], suf[8];
         float emul, kmul;
     };
 
     // Phase A operands of one chunk for channel c, rows 8*hf .. 8*hf+7: the
     // decays, the level operands X_b, Y_b (k-major, one 16-byte store each)
-    // and beta.
-    __device__ void prep_levels(const PrepIn<TQ>& pin, PrepMid& mid, int chunk, int c, int hf,
+    // and beta.  Products are packed fp16: factor pairs (fp32 chains rounded
+    // once) times the fp16 k / q pairs.
+    __device__ void prep_levels(const PrepIn& pin_, PrepMid& mid, int chunk, int c, int hf,
                                 bool beta_lane) const {
-        float gv[8];
-        float beta = pin.beta;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            gv[i] = pin.g[i];
-            mid.q[i] = QIn<TQ>::f(pin.q[i]);
-            mid.k[i] = QIn<TQ>::f(pin.k[i]);
-        }
-        const int nrow = rows_in(chunk);
-        if (nrow < BT) {                                // tail chunk: neutral padding rows
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (8 * hf + i >= nrow) { gv[i] = 0.f; mid.q[i] = 0.f; mid.k[i] = 0.f; }
-            if (lane >= nrow) beta = 0.f;
-        }
+        PrepIn pin = pin_;
+        use_here(pin);
         float al[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) al[i] = fast_exp(gv[i]);
+        for (int i = 0; i < 8; ++i) al[i] = fast_exp(__uint_as_float(pin.g[i]));
+        mid.qh = QIn<TQ>::oct(pin.q);
+        mid.kh = QIn<TQ>::oct(pin.k);
         mid.pre[0] = al[0];                             // prod_{t<=i} within the half
 #pragma unroll
         for (int i = 1; i < 8; ++i) mid.pre[i] = mid.pre[i - 1] * al[i];
@@ -316,26 +348,22 @@ struct Kern {
         const bool up = hf != 0;
         mid.emul = up ? other : 1.f;                    // E = exp(gc): prefix over the chunk
         mid.kmul = up ? 1.f : other;                    // E15 / E: suffix over the chunk
-        if (beta_lane) sm.beta[chunk % 2][lane] = beta;
+        if (beta_lane) sm.beta[chunk % 2][lane] = __uint_as_float(pin.beta);
 
         const int r0 = 8 * hf;
         // level factors F_b(row); query-side operands of key rows are never
         // read unmasked, so Y is written for every row with the same factor
-        float f[8];
-        auto level = [&](int lev) {
-            h8 x, y;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                x[i] = static_cast<_Float16>(mid.k[i] * f[i]);
-                y[i] = static_cast<_Float16>(mid.q[i] * f[i]);
-            }
+        auto store = [&](int lev, h8 x, h8 y) {
             *reinterpret_cast<h8*>(&sm.XT[lev][c][r0]) = x;
             *reinterpret_cast<h8*>(&sm.YT[lev][c][r0]) = y;
         };
+        float f[8];
+        auto level = [&](int lev) {
+            const h8 fh = to_h8(f);
+            store(lev, mid.kh * fh, mid.qh * fh);
+        };
         // level "diag": factor 1
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = 1.f;
-        level(0);
+        store(0, mid.kh, mid.qh);
         // level b = 0: ref = odd rows; key rows even -> a_{i+1}
 #pragma unroll
         for (int i = 0; i < 8; i += 2) { f[i] = al[i + 1]; f[i + 1] = 1.f; }
@@ -368,17 +396,16 @@ struct Kern {
     // Phase B operands of one chunk: q * E, k * E, k * E15 / E and E15.
     __device__ void prep_e(const PrepMid& mid, int chunk, int c, int hf) const {
         const int b3 = chunk % 3, r0 = 8 * hf;
-        h8 qe, ke, kh;
+        float e[8], sf[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float e = mid.pre[i] * mid.emul;
-            qe[i] = static_cast<_Float16>(mid.q[i] * e);
-            ke[i] = static_cast<_Float16>(mid.k[i] * e);
-            kh[i] = static_cast<_Float16>(mid.k[i] * (mid.suf[i] * mid.kmul));
+            e[i] = mid.pre[i] * mid.emul;
+            sf[i] = mid.suf[i] * mid.kmul;
         }
-        *reinterpret_cast<h8*>(&sm.QET[b3][c][r0]) = qe;
-        *reinterpret_cast<h8*>(&sm.KET[b3][c][r0]) = ke;
-        *reinterpret_cast<h8*>(&sm.KHT[b3][c][r0]) = kh;
+        const h8 eh = to_h8(e), sh = to_h8(sf);
+        *reinterpret_cast<h8*>(&sm.QET[b3][c][r0]) = mid.qh * eh;
+        *reinterpret_cast<h8*>(&sm.KET[b3][c][r0]) = mid.kh * eh;
+        *reinterpret_cast<h8*>(&sm.KHT[b3][c][r0]) = mid.kh * sh;
         if (hf) sm.elast[b3][c] = mid.pre[7] * mid.emul;
     }
 
@@ -443,34 +470,27 @@ struct Kern {
     }
 
     // ------------------------------------------------------------ consumers
-    __device__ void v_load(typename QIn<TQ>::Raw (&vr)[4], int chunk) const {
-        const int last = rows_in(chunk) - 1;
-        const char* v = cbase<TQ>(a.v, base(a.v_stride, chunk));
+    __device__ void v_load(uint32_t (&vr)[4], int chunk) const {
+        const auto rv = chunk_rsrc(a.v, a.v_stride, sizeof(TQ), rs_v, chunk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t ov = static_cast<uint32_t>(min(vrow0 + j, last)) * rs_v + col_v;
-            vr[j] = QIn<TQ>::ld(reinterpret_cast<const TQ*>(v + ov));
-        }
+        for (int j = 0; j < 4; ++j) vr[j] = QIn<TQ>::ld(rv, off_v[j]);
     }
 
-    __device__ void consumer_a(int chunk, const typename QIn<TQ>::Raw (&vraw)[4], f4 (&S)[KT], f4& P,
-                               f4& O) const {
+    __device__ void consumer_a(int chunk, const uint32_t (&vraw_)[4], f4 (&S)[KT], f4& P, f4& O) const {
+        uint32_t vraw[4] = {vraw_[0], vraw_[1], vraw_[2], vraw_[3]};
+        use_here(vraw);
         float vr[4];
-        const int nrow = rows_in(chunk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vr[j] = (4 * lg + j < nrow) ? QIn<TQ>::f(vraw[j]) : 0.f;
+        for (int j = 0; j < 4; ++j) vr[j] = QIn<TQ>::f(vraw[j]);
         h8 shi[KU], slo[KU];
 #pragma unroll
-        for (int u = 0; u < KU; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const _Float16 x0 = static_cast<_Float16>(S[2 * u][j]);
-                const _Float16 x1 = static_cast<_Float16>(S[2 * u + 1][j]);
-                shi[u][j] = x0;
-                shi[u][4 + j] = x1;
-                slo[u][j] = static_cast<_Float16>(S[2 * u][j] - static_cast<float>(x0));
-                slo[u][4 + j] = static_cast<_Float16>(S[2 * u + 1][j] - static_cast<float>(x1));
-            }
+        for (int u = 0; u < KU; ++u) {
+            h4 h0, l0, h1, l1;
+            split4(S[2 * u], h0, l0);
+            split4(S[2 * u + 1], h1, l1);
+            shi[u] = h8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+            slo[u] = h8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+        }
         // Z = (k * E) S and O = (q * E) S over the K channels
         const int cb = chunk % 3;
         f4 Z = {0.f, 0.f, 0.f, 0.f};
@@ -571,12 +591,20 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
         kn.rs_v = static_cast<uint32_t>(a.v_stride[1]) * eq;
         kn.rs_g = static_cast<uint32_t>(a.g_stride[1]) * 4u;
         kn.rs_b = static_cast<uint32_t>(a.beta_stride[1]) * 4u;
-        kn.col_q = static_cast<uint32_t>(pc) * eq;
-        kn.col_k = static_cast<uint32_t>(pc) * eq;
-        kn.col_g = static_cast<uint32_t>(pc) * 4u;
-        kn.col_v = static_cast<uint32_t>(col) * eq;
-        kn.prow0 = 8 * phf;
-        kn.vrow0 = 4 * kn.lg;
+        // lane byte offsets inside a chunk; rows past T fall outside the
+        // chunk's descriptor and read as zero
+        const uint32_t pcol = static_cast<uint32_t>(pc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = static_cast<uint32_t>(8 * phf + i);
+            kn.off_q[i] = r * kn.rs_q + pcol * eq;
+            kn.off_k[i] = r * kn.rs_k + pcol * eq;
+            kn.off_g[i] = r * kn.rs_g + pcol * 4u;
+        }
+        kn.off_b = static_cast<uint32_t>(kn.lane) * kn.rs_b;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            kn.off_v[j] = static_cast<uint32_t>(4 * kn.lg + j) * kn.rs_v + static_cast<uint32_t>(col) * eq;
     }
 
     // step sp: producers build chunk sp, producer 0 inverts chunk sp-1,
@@ -589,12 +617,12 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
     const int last = nch - 1;
     if (consumer) {
         f4 S[KT];
-        typename QIn<TQ>::Raw vr0[4], vr1[4];
+        uint32_t vr0[4], vr1[4];
         load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
         kn.v_load(vr0, 0);
         kn.v_load(vr1, min(1, last));
         f4 P = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
-        auto step = [&](int sp, typename QIn<TQ>::Raw (&vr)[4]) {
+        auto step = [&](int sp, uint32_t (&vr)[4]) {
             const int cc = sp - 2;
             if (cc >= 0) {
                 kn.consumer_a(cc, vr, S, P, O);
@@ -610,11 +638,11 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
         }
         store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
     } else {
-        PrepIn<TQ> pin0, pin1;
+        PrepIn pin0, pin1;
         kn.prep_load(pin0, 0, beta_lane);
         kn.prep_load(pin1, min(1, last), beta_lane);
         typename KN::PrepMid mid;
-        auto step = [&](int sp, PrepIn<TQ>& pin) {
+        auto step = [&](int sp, PrepIn& pin) {
             const int cp = sp, cs = sp - 1;
             if (cp < nch) {
                 kn.prep_levels(pin, mid, cp, pc, phf, beta_lane);
@@ -682,6 +710,11 @@ int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream) {
     for (int64_t st : ts)
         if (st < 0 || (BT + 1) * st * 4 + a.V * 4 >= lim) return KDA_ERR_UNSUPPORTED;
     if ((BT + 1) * a.H * a.V * 4 >= lim) return KDA_ERR_UNSUPPORTED;
+    // a chunk's buffer descriptor spans rows_in * token stride bytes, so every
+    // token row must be disjoint from the next (stride >= row length)
+    if (a.T > 1 && (a.q_stride[1] < a.K || a.k_stride[1] < a.K || a.g_stride[1] < a.K ||
+                    a.v_stride[1] < a.V || a.beta_stride[1] < 1))
+        return KDA_ERR_UNSUPPORTED;
     switch (a.K) {
         case 32: return launch_k<32>(a, stream);
         case 64: return launch_k<64>(a, stream);
