@@ -1,11 +1,11 @@
 // Chunkwise KDA forward for gfx950: fp16 MFMA, fp32 accumulation, fp32 state.
 //
 // Replaces the body of kda_chunkwise (kimi_linear/kda.py:111-185).  The maths
-// is the reference's UT-transform form (paper Eq. 6-9) evaluated per internal
-// chunk of BT = 16 tokens; the recurrence is chunk-size invariant, so the
-// caller's chunk_size only fixes the T % chunk_size == 0 contract.
+// is the reference's UT-transform form (paper Eq. 6-9) evaluated per block of
+// BT = 16 tokens; the recurrence is chunk-size invariant, so the caller's
+// chunk_size only fixes the T % chunk_size == 0 contract.
 //
-// Per (b, h) and internal chunk (rows c, i in [0, 16)), with a_t = exp(g_t):
+// Per (b, h) and block (rows c, i in [0, 16)), with a_t = exp(g_t):
 //   E[r]   = prod_{t<=r} a_t              (= exp(gc_r), per channel)
 //   L[c,i] = beta_c <k_c, k_i * prod_{t=i+1..c} a_t>,  i < c
 //   A[c,i] = scale <q_c, k_i * prod_{t=i+1..c} a_t>,   i <= c
@@ -14,9 +14,9 @@
 //   O      = scale (E * Q) S + A P
 //   S     <- Diag(E[15]) S + ((E[15]/E) * K)^T P
 //
-// Decay factoring without pairwise exponentials: every pair i < c of a chunk
+// Decay factoring without pairwise exponentials: every pair i < c of a block
 // has a unique highest differing bit b; c has it set, i clear, and both sit in
-// the aligned block of 2^(b+1) rows whose upper half starts at ref.  Then
+// the aligned group of 2^(b+1) rows whose upper half starts at ref + 1.  Then
 //   prod_{t=i+1..c} a_t = (prod_{t=ref+1..c} a_t) * (prod_{t=i+1..ref} a_t),
 // both factors <= 1, so per level b one [16 x K] operand X_b (row r = k_r times
 // its factor) gives L_b = X_b X_b^T as a plain MFMA product, masked to level
@@ -29,24 +29,23 @@
 // slot j -- the B-operand layout of X and the A-operand layout of X^T -- so a
 // chain that keeps X and X^T side by side needs no data movement.
 //
-// Software pipeline, one workgroup per (b, h, 16*NC state columns):
+// Pipeline, one workgroup per (b, h, 16*NC state columns), in supersteps of
+// NB = 4 blocks (64 tokens), each split in two halves by workgroup barriers:
 //   NC consumer waves: wave w owns state columns [16w, 16w+16) for all K rows
-//     as MFMA accumulators and runs the sequential chain of chunk n.
-//   NP = K/32 producer waves: two lanes per channel (8 rows each) build the
-//     operands of chunk n+2 straight from prefetched global loads; producer
-//     wave 0 inverts (I + L) of chunk n+1 while the others compute the level
-//     products of chunk n+2.
-// Each step has two phases separated by workgroup barriers:
-//   A: producers: decays + level operands (n+2)
-//      | consumers: Z = (E*K) S, O = (E*Q) S, P = M (V - Z)   (n)
-//   B: producer 0: (I + L)^-1 (n+1); others: level products (n+2); all
-//      producers: E-scaled operands (n+2)
-//      | consumers: O += A P, store O, S <- E15 S + Khat^T P   (n)
-// Operands that are not exact in fp16 and carry the state (S, P, M and
+//     as MFMA accumulators and runs the sequential chain over blocks 0-1 of
+//     superstep s in the first half and blocks 2-3 in the second.
+//   NB * PW producer waves (PW = 2 for K = 128, else 1): the PW waves of
+//     block p build every operand of block NB*(s+1) + p, each over its own
+//     channels -- decays, level operands (staged k-major in the slot's own
+//     q*E / k*E rows before those receive their final values), partial L
+//     and A -- in the first half; in the second the first wave adds the
+//     partial sums, writes A and inverts (I + L), the other writes its
+//     E-scaled operands.  The next block's loads are issued between levels.
+// Operand slots alternate between two sets of NB, so the producers of
+// superstep s+1 and the consumers of superstep s never touch the same slot.
+// Operands that are not exact in fp16 and carry the state (S, P, M, L and
 // V - Z) are split into fp16 hi + lo; the others are single fp16 with fp32
-// accumulation.  Operands read through LDS transpose loads are stored
-// k-major, so each producer lane stores a channel's 8 rows with one 16-byte
-// write.
+// accumulation.
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -54,88 +53,134 @@ namespace kda {
 
 namespace {
 
-constexpr int BT = 16;    // tokens per internal chunk
-constexpr int RP = 24;    // padded row (halfs) of the [*][16] fp16 matrices (48 B rows)
-constexpr int LP = 20;    // padded row (floats) of the 16x16 fp32 L
-constexpr int NLEV = 5;   // operand levels: 0 = diagonal, 1 + b for bit b = 0..3
-constexpr int kXcds = 8;  // accelerator complex dies on MI355X
+constexpr int BT = 16;          // tokens per block
+constexpr int NB = 4;           // blocks per superstep = producer waves
+constexpr int NSLOT = 2 * NB;   // operand slots (two supersteps)
+constexpr int RP = 24;          // padded row (halfs) of the [16][16] fp16 A-operand matrices
+constexpr int LP = 20;          // padded row (floats) of the 16x16 fp32 L
+constexpr int kXcds = 8;        // accelerator complex dies on MI355X
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-// Input element access through raw buffer loads.  A chunk's descriptor covers
-// exactly its rows before T, so rows past T read as zero -- the neutral
-// padding (k = q = v = g = beta = 0) -- with no clamping or masking.  Loaded
-// values are held one per 32-bit register and converted only at use, so a
-// prefetch load is never followed by a wait.
+// Raw buffer loads.  A block's descriptor spans exactly its rows before T;
+// the range check covers the whole offset (lane offset + row offset), so
+// rows past T read as zero -- the neutral padding (k = q = v = g = beta = 0)
+// -- with no clamping or masking.  The row offset is wave-uniform and goes in
+// the scalar offset; the lane offset is one register per tensor.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                              static_cast<int>(nbytes), 0x00020000);
 }
-__device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
-}
-__device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
-}
-
-template <typename TQ> struct QIn;
-template <> struct QIn<_Float16> {
-    static __device__ __forceinline__ uint32_t ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return bload16(r, off); }
-    static __device__ __forceinline__ float f(uint32_t r) {
-        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
-    }
-    static __device__ __forceinline__ h8 oct(const uint32_t (&r)[8]) {   // exact: repack the bits
-        h8 x;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(r[i]));
-        return x;
+template <int BYTES> struct BLoad;
+template <> struct BLoad<2> {
+    static constexpr int W = 1;
+    static __device__ __forceinline__ void ld(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(vo), static_cast<int>(so), 0);
     }
 };
-template <> struct QIn<bf16_t> {
-    static __device__ __forceinline__ uint32_t ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return bload16(r, off); }
-    static __device__ __forceinline__ float f(uint32_t r) { return __uint_as_float(r << 16); }
-    static __device__ __forceinline__ h8 oct(const uint32_t (&r)[8]) {
-        h8 x;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(f(r[i]));
-        return x;
+template <> struct BLoad<4> {
+    static constexpr int W = 1;
+    static __device__ __forceinline__ void ld(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(vo), static_cast<int>(so), 0);
     }
 };
-template <> struct QIn<float> {
-    static __device__ __forceinline__ uint32_t ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return bload32(r, off); }
-    static __device__ __forceinline__ float f(uint32_t r) { return __uint_as_float(r); }
-    static __device__ __forceinline__ h8 oct(const uint32_t (&r)[8]) {
-        h8 x;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(f(r[i]));
-        return x;
+template <> struct BLoad<8> {
+    static constexpr int W = 2;
+    static __device__ __forceinline__ void ld(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(vo), static_cast<int>(so), 0);
+        w[0] = x[0];
+        w[1] = x[1];
     }
 };
 
-// Eight fp32 values rounded to fp16.
-__device__ __forceinline__ h8 to_h8(const float (&x)[8]) {
-    h8 r;
+// Values are held raw, one load per register set, and converted only where
+// they are used.  Left alone, the compiler hoists a conversion (or the
+// packing of two fp16 loads into one register) up to the load, which puts a
+// wait for the whole prefetch right after it is issued.  An empty volatile
+// asm that "modifies" the registers at the point of use keeps every such
+// instruction, and the wait, there.
+template <int N>
+__device__ __forceinline__ void use_here(uint32_t (&r)[N]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(x[i]);
-    return r;
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
+}
+template <int N, int M>
+__device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) use_here(r[i]);
 }
 
-// Operands consumed through LDS transpose reads are stored k-major ([K][16]:
-// the 16 chunk rows of one channel are contiguous), so a producer lane writes
-// its 8 rows of a channel with one 16-byte store.
+// Element type of q, k and v: CH adjacent channels of one token row.
+template <typename TQ, int CH>
+struct QRow {
+    static constexpr int BYTES = CH * static_cast<int>(sizeof(TQ));
+    static constexpr int W = BLoad<BYTES>::W;
+    // channel j of a raw row
+    static __device__ __forceinline__ float val(const uint32_t (&w)[W], int j) {
+        if constexpr (sizeof(TQ) == 4) {
+            return __uint_as_float(w[j]);
+        } else {
+            const uint32_t hbits = (w[0] >> (16 * j)) & 0xffffu;
+            if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+                return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hbits)));
+            } else {
+                return __uint_as_float(hbits << 16);
+            }
+        }
+    }
+    // channel j of rows (r0, r1) as an fp16 pair (exact repacking for fp16)
+    static __device__ __forceinline__ h2 pair(const uint32_t (&w0)[W], const uint32_t (&w1)[W], int j) {
+        if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+            const uint32_t lo = (w0[0] >> (16 * j)) & 0xffffu;
+            const uint32_t hi = (w1[0] >> (16 * j)) << 16;
+            return __builtin_bit_cast(h2, lo | hi);
+        } else {
+            return h2{static_cast<_Float16>(val(w0, j)), static_cast<_Float16>(val(w1, j))};
+        }
+    }
+};
+
+// Sixteen fp32 values rounded to fp16, as two h8 (rows 0-7, 8-15).
+__device__ __forceinline__ void to_h16(const float (&x)[BT], h8& lo, h8& hi) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        lo[i] = static_cast<_Float16>(x[i]);
+        hi[i] = static_cast<_Float16>(x[8 + i]);
+    }
+}
+
+// Within one wave, LDS serves requests in issue order, so a wave reads back
+// what its own lanes wrote (and reads complete before later overwrites)
+// without any barrier; the compiler keeps the order of the possibly
+// aliasing LDS accesses.  The per-producer staging areas rely on this.
+
+// Operands of one block, as the consumers read them.  Matrices read through
+// LDS transpose loads are stored k-major ([K][16]: the 16 rows of a channel
+// contiguous); KHT holds channel rows read as A operands, with the two 8-byte
+// halves of each 16-byte group swapped on channels with bit 3 set, so the
+// 16 lanes of a read hit distinct banks without padding.
+template <int K>
+struct __align__(16) Slot {
+    _Float16 QET[K][BT];                   // q * E
+    _Float16 KET[K][BT];                   // k * E
+    _Float16 KHT[K][BT];                   // k * E15 / E (swizzled)
+    _Float16 AM[BT][RP];                   // scale * A
+    _Float16 MH[BT][RP];                   // M hi
+    _Float16 ML[BT][RP];                   // M lo
+    float elast[K];                        // E[15]
+};
+
+// Producer waves per block: for K = 128 two, each with half of the channels
+// (one channel per lane); one otherwise.
+template <int K>
+constexpr int kPW = K == 128 ? 2 : 1;
+
 template <int K>
 struct __align__(16) Smem {
-    _Float16 XT[NLEV][K][BT];              // level operands (k * factor), k-major
-    _Float16 YT[NLEV][K][BT];              // query-side level operands (q * factor)
-    _Float16 QET[3][K][BT];                // q * E                  (chunk % 3)
-    _Float16 KET[3][K][BT];                // k * E                  (chunk % 3)
-    _Float16 KHT[3][K][RP];                // (k * E15 / E)^T        (chunk % 3)
-    _Float16 AM[3][BT][RP];                // scale * A              (chunk % 3)
-    _Float16 MH[BT][RP];                   // M hi                   (single)
-    _Float16 ML[BT][RP];                   // M lo
-    float L[2][BT][LP];                    // beta-scaled L          (chunk % 2)
-    float elast[3][K];                     // E[15]                  (chunk % 3)
-    float beta[2][BT];                     //                        (chunk % 2)
+    Slot<K> slot[NSLOT];
+    // per block: the second producer's partial L and A (lane-major), then
+    // the first producer's L for its transpose
+    float XCH[NB][2][64][4];
 };
 
 __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, int lg) {
@@ -165,33 +210,21 @@ __device__ __forceinline__ h8 frag32_tr(const _Float16* xt, int lg, int ln, int 
     return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// fp16 lo halves of two fp32 values given their fp16 hi halves: f16(x - hi).
-// The compiler forms x - hi with v_fma_mix_f32 (hi read as fp16 in place) and
-// packs the pair with one conversion.  (A hand-written v_fma_mixlo/mixhi
-// pair on one register is left out: the compiler's hazard pass does not see
-// inside inline asm, and that sequence gave run-to-run differences.)
-__device__ __forceinline__ h2 split_lo_pair(float x0, float x1, h2 hi) {
-    return h2{static_cast<_Float16>(x0 - static_cast<float>(hi[0])),
-              static_cast<_Float16>(x1 - static_cast<float>(hi[1]))};
-}
-
-// Four fp32 values as fp16 hi + lo (x ~= hi + lo to ~2^-22 relative).
+// Four fp32 values as fp16 hi + lo, x ~= hi + lo to ~2^-21 relative: hi is x
+// truncated to fp16's 11 significant bits (exact in fp16 and in fp32), so
+// lo = x - hi is exact in fp32 and is rounded once.  Three VALU operations
+// per value, no conversion back from fp16.
 __device__ __forceinline__ void split4(const f4& x, h4& hi, h4& lo) {
-    const h2 h01 = h2{static_cast<_Float16>(x[0]), static_cast<_Float16>(x[1])};
-    const h2 h23 = h2{static_cast<_Float16>(x[2]), static_cast<_Float16>(x[3])};
-    const h2 l01 = split_lo_pair(x[0], x[1], h01);
-    const h2 l23 = split_lo_pair(x[2], x[3], h23);
-    hi = h4{h01[0], h01[1], h23[0], h23[1]};
-    lo = h4{l01[0], l01[1], l23[0], l23[1]};
-}
-
-// x of lane (lane ^ 32), through the VALU cross-half swap (no LDS traffic):
-// permlane32_swap(x, x) returns {x of lane l-32 in the upper half,
-// x of lane l+32 in the lower half} as its two results.
-__device__ __forceinline__ float xor32(float x, int lane) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return __uint_as_float((lane & 32) ? r[0] : r[1]);
+    float t[4], r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        t[i] = __uint_as_float(__float_as_uint(x[i]) & 0xffffe000u);
+        r[i] = x[i] - t[i];
+    }
+    hi = h4{static_cast<_Float16>(t[0]), static_cast<_Float16>(t[1]), static_cast<_Float16>(t[2]),
+            static_cast<_Float16>(t[3])};
+    lo = h4{static_cast<_Float16>(r[0]), static_cast<_Float16>(r[1]), static_cast<_Float16>(r[2]),
+            static_cast<_Float16>(r[3])};
 }
 
 // An fp32 accumulator tile split into fp16 hi + lo operands.
@@ -207,29 +240,6 @@ __device__ __forceinline__ f4 mm3(const Split4& a, const Split4& b) {
     d = mfma16x16x16(a.hi, b.lo, d);
     d = mfma16x16x16(a.lo, b.hi, d);
     return d;
-}
-
-// Raw per-lane inputs of one chunk for a producer lane (one channel, 8 rows).
-struct PrepIn {
-    uint32_t g[8], q[8], k[8];
-    uint32_t beta;
-};
-
-// Prefetched values are converted only where they are used.  Left alone, the
-// compiler hoists a conversion (or the packing of two fp16 loads into one
-// register) up to the load, which puts a wait for the whole prefetch right
-// after it is issued.  An empty volatile asm that "modifies" the registers at
-// the point of use keeps every such instruction, and the wait, there.
-template <int N>
-__device__ __forceinline__ void use_here(uint32_t (&r)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
-}
-__device__ __forceinline__ void use_here(PrepIn& p) {
-    use_here(p.g);
-    use_here(p.q);
-    use_here(p.k);
-    asm volatile("" : "+v"(p.beta));
 }
 
 // Accumulator-layout state tiles: S[t][j] = state[16t + 4lg + j][col]; `off`
@@ -271,11 +281,30 @@ __device__ __forceinline__ void store_state(const f4 (&S)[KT], void* p, int dtyp
 
 template <int K, int NC, typename TQ>
 struct Kern {
-    static constexpr int KT = K / 16;       // 16-row state tiles
-    static constexpr int KU = K / 32;       // 32-wide k blocks
-    static constexpr int NP = K / 32;       // producer waves
-    static constexpr int NWAVE = NC + NP;
+    static constexpr int KT = K / 16;                   // 16-row state tiles
+    static constexpr int KU = K / 32;                   // 32-wide k blocks
+    static constexpr int PW = kPW<K>;                   // producer waves per block
+    static constexpr int KW = K / PW;                   // channels per producer wave
+    static constexpr int KUW = KW / 32;                 // 32-wide k blocks per producer wave
+    static constexpr int CH = 1;                        // channels per producer lane
     static constexpr int VT = 16 * NC;
+    using QR = QRow<TQ, CH>;                            // producer rows of q / k
+    using VR = QRow<TQ, 1>;                             // consumer elements of v
+    static constexpr int QW = QR::W;
+
+    // One block's raw inputs for a producer lane: channels chan(0..CH-1),
+    // rows 0..15, and beta of rows 4lg..4lg+3.
+    struct Raw {
+        uint32_t q[BT][QW], k[BT][QW];
+        uint32_t g[BT][CH];
+        uint32_t beta[4];
+    };
+    // The same block, converted: decays, fp16 q and k (rows 0-7 / 8-15), beta.
+    struct Work {
+        float al[CH][BT];
+        h8 qh[CH][2], kh[CH][2];
+        float beta[4];
+    };
 
     const kda_fwd_args& a;
     Smem<K>& sm;
@@ -283,176 +312,167 @@ struct Kern {
     int nch;
     float scale;
     int lane, ln, lg;
-    // per-row byte strides and this lane's byte offsets inside a chunk
-    uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;
-    uint32_t off_q[8], off_k[8], off_g[8], off_v[4], off_b;
+    int hh;                                  // producer: channel part (0 .. PW-1)
+    uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;   // token-row strides in bytes
+    uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets (v, beta: from row 4lg)
 
     __device__ Kern(const kda_fwd_args& args, Smem<K>& s) : a(args), sm(s) {}
 
-    // Rows of chunk `chunk` that lie before T (1..BT).
-    __device__ int rows_in(int chunk) const {
-        const int64_t left = T - static_cast<int64_t>(chunk) * BT;
+    // Channel c of this producer lane (lanes 32-63 repeat lanes 0-31 when K = 32).
+    __device__ int chan(int c) const { return hh * KW + CH * (KW < 64 ? (lane % KW) : lane) + c; }
+
+    // Rows of block `blk` that lie before T (1..BT).
+    __device__ int rows_in(int blk) const {
+        const int64_t left = T - static_cast<int64_t>(blk) * BT;
         return left < BT ? static_cast<int>(left) : BT;
     }
 
-    // Buffer descriptor over the rows of one chunk of a [B, T, H, D] view
-    // (elements of size es, token stride rs bytes) at (b, t0, h, 0).
-    __device__ __amdgpu_buffer_rsrc_t chunk_rsrc(const void* p, const int64_t (&st)[3], int es, uint32_t rs,
-                                                 int chunk) const {
-        const int64_t e = b * st[0] + static_cast<int64_t>(chunk) * BT * st[1] + h * st[2];
-        return make_rsrc(static_cast<const char*>(p) + e * es, static_cast<uint32_t>(rows_in(chunk)) * rs);
+    // Descriptor over the rows of one block of a [B, T, H, D] view (elements
+    // of es bytes, token stride rs bytes), based at (b, 16 blk, h, 0).
+    __device__ __amdgpu_buffer_rsrc_t block_rsrc(const void* p, const int64_t (&st)[3], int es, uint32_t rs,
+                                                 int blk) const {
+        const int64_t e = b * st[0] + static_cast<int64_t>(blk) * BT * st[1] + h * st[2];
+        return make_rsrc(static_cast<const char*>(p) + e * es, static_cast<uint32_t>(rows_in(blk)) * rs);
     }
 
     // ------------------------------------------------------------ producers
-    __device__ void prep_load(PrepIn& in, int chunk, bool beta_lane) const {
-        const auto rq = chunk_rsrc(a.q, a.q_stride, sizeof(TQ), rs_q, chunk);
-        const auto rk = chunk_rsrc(a.k, a.k_stride, sizeof(TQ), rs_k, chunk);
-        const auto rg = chunk_rsrc(a.g, a.g_stride, 4, rs_g, chunk);
+    // Loads of rows [R0, R1) of one block (and beta with the last rows).
+    // The loads of the next block are issued in four parts between the
+    // levels of the current one, so they never queue up in one burst.
+    template <int R0, int R1>
+    __device__ void load_rows(Raw& r, int blk) const {
+        const auto rq = block_rsrc(a.q, a.q_stride, sizeof(TQ), rs_q, blk);
+        const auto rk = block_rsrc(a.k, a.k_stride, sizeof(TQ), rs_k, blk);
+        const auto rg = block_rsrc(a.g, a.g_stride, 4, rs_g, blk);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            in.g[i] = bload32(rg, off_g[i]);
-            in.q[i] = QIn<TQ>::ld(rq, off_q[i]);
-            in.k[i] = QIn<TQ>::ld(rk, off_k[i]);
+        for (int i = R0; i < R1; ++i) {
+            BLoad<4 * CH>::ld(r.g[i], rg, vo_g, i * rs_g);
+            BLoad<QR::BYTES>::ld(r.q[i], rq, vo_q, i * rs_q);
+            BLoad<QR::BYTES>::ld(r.k[i], rk, vo_k, i * rs_k);
         }
-        if (beta_lane) in.beta = bload32(chunk_rsrc(a.beta, a.beta_stride, 4, rs_b, chunk), off_b);
+        if constexpr (R1 == BT) {
+            const auto rb = block_rsrc(a.beta, a.beta_stride, 4, rs_b, blk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) BLoad<4>::ld(&r.beta[j], rb, vo_b, j * rs_b);
+        }
     }
+    __device__ void load_raw(Raw& r, int blk) const { load_rows<0, BT>(r, blk); }
 
-    // Producer values of one chunk carried from phase A to phase B.
-    struct PrepMid {
-        h8 qh, kh;                                  // the 8 rows as fp16
-        float pre[8], suf[8];
-        float emul, kmul;
-    };
-
-    // Phase A operands of one chunk for channel c, rows 8*hf .. 8*hf+7: the
-    // decays, the level operands X_b, Y_b (k-major, one 16-byte store each)
-    // and beta.  Products are packed fp16: factor pairs (fp32 chains rounded
-    // once) times the fp16 k / q pairs.
-    __device__ void prep_levels(const PrepIn& pin_, PrepMid& mid, int chunk, int c, int hf,
-                                bool beta_lane) const {
-        PrepIn pin = pin_;
-        use_here(pin);
-        float al[8];
+    __device__ void unpack(Raw& r, Work& w) const {
+        use_here(r.q);
+        use_here(r.k);
+        use_here(r.g);
+        use_here(r.beta);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) al[i] = fast_exp(__uint_as_float(pin.g[i]));
-        mid.qh = QIn<TQ>::oct(pin.q);
-        mid.kh = QIn<TQ>::oct(pin.k);
-        mid.pre[0] = al[0];                             // prod_{t<=i} within the half
+        for (int c = 0; c < CH; ++c) {
 #pragma unroll
-        for (int i = 1; i < 8; ++i) mid.pre[i] = mid.pre[i - 1] * al[i];
-        mid.suf[7] = 1.f;                               // prod_{t=i+1..7} within the half
+            for (int i = 0; i < BT; ++i) w.al[c][i] = fast_exp(__uint_as_float(r.g[i][c]));
 #pragma unroll
-        for (int i = 6; i >= 0; --i) mid.suf[i] = mid.suf[i + 1] * al[i + 1];
-        const float other = xor32(mid.pre[7], lane);    // product over the other half
-        const float a8 = xor32(al[0], lane);            // lower half: a of row 8
-        const bool up = hf != 0;
-        mid.emul = up ? other : 1.f;                    // E = exp(gc): prefix over the chunk
-        mid.kmul = up ? 1.f : other;                    // E15 / E: suffix over the chunk
-        if (beta_lane) sm.beta[chunk % 2][lane] = __uint_as_float(pin.beta);
-
-        const int r0 = 8 * hf;
-        // level factors F_b(row); query-side operands of key rows are never
-        // read unmasked, so Y is written for every row with the same factor
-        auto store = [&](int lev, h8 x, h8 y) {
-            *reinterpret_cast<h8*>(&sm.XT[lev][c][r0]) = x;
-            *reinterpret_cast<h8*>(&sm.YT[lev][c][r0]) = y;
-        };
-        float f[8];
-        auto level = [&](int lev) {
-            const h8 fh = to_h8(f);
-            store(lev, mid.kh * fh, mid.qh * fh);
-        };
-        // level "diag": factor 1
-        store(0, mid.kh, mid.qh);
-        // level b = 0: ref = odd rows; key rows even -> a_{i+1}
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) { f[i] = al[i + 1]; f[i + 1] = 1.f; }
-        level(1);
-        // level b = 1: ref = 2 mod 4
-#pragma unroll
-        for (int i = 0; i < 8; i += 4) {
-            f[i + 1] = al[i + 2];
-            f[i] = al[i + 1] * f[i + 1];
-            f[i + 2] = 1.f;
-            f[i + 3] = al[i + 3];
-        }
-        level(2);
-        // level b = 2: ref = 4 within the half
-        f[3] = al[4]; f[2] = al[3] * f[3]; f[1] = al[2] * f[2]; f[0] = al[1] * f[1];
-        f[4] = 1.f; f[5] = al[5]; f[6] = f[5] * al[6]; f[7] = f[6] * al[7];
-        level(3);
-        // level b = 3: ref = 8; upper half = query rows (prod_{9..r}), lower = key rows
-        {
-            float q = 1.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (i > 0) q *= al[i];
-                f[i] = up ? q : mid.suf[i] * a8;
+            for (int p = 0; p < BT / 2; ++p) {
+                const h2 qp = QR::pair(r.q[2 * p], r.q[2 * p + 1], c);
+                const h2 kp = QR::pair(r.k[2 * p], r.k[2 * p + 1], c);
+                w.qh[c][p / 4][2 * (p % 4)] = qp[0];
+                w.qh[c][p / 4][2 * (p % 4) + 1] = qp[1];
+                w.kh[c][p / 4][2 * (p % 4)] = kp[0];
+                w.kh[c][p / 4][2 * (p % 4) + 1] = kp[1];
             }
         }
-        level(4);
-    }
-
-    // Phase B operands of one chunk: q * E, k * E, k * E15 / E and E15.
-    __device__ void prep_e(const PrepMid& mid, int chunk, int c, int hf) const {
-        const int b3 = chunk % 3, r0 = 8 * hf;
-        float e[8], sf[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            e[i] = mid.pre[i] * mid.emul;
-            sf[i] = mid.suf[i] * mid.kmul;
-        }
-        const h8 eh = to_h8(e), sh = to_h8(sf);
-        *reinterpret_cast<h8*>(&sm.QET[b3][c][r0]) = mid.qh * eh;
-        *reinterpret_cast<h8*>(&sm.KET[b3][c][r0]) = mid.kh * eh;
-        *reinterpret_cast<h8*>(&sm.KHT[b3][c][r0]) = mid.kh * sh;
-        if (hf) sm.elast[b3][c] = mid.pre[7] * mid.emul;
+        for (int j = 0; j < 4; ++j) w.beta[j] = __uint_as_float(r.beta[j]);
     }
 
-    // Level product of one chunk: writes the level's pairs of L and A.
-    __device__ void level_mfma(int lev, int chunk) const {
+    // Level factors F_b(r), r = 0..15, of one channel: in each aligned group of
+    // 2^(b+1) rows, upper-half rows c get prod_{t=ref+1..c} a_t and lower-half
+    // rows i get prod_{t=i+1..ref} a_t, ref = the group's last lower row.
+    template <int B>
+    static __device__ __forceinline__ void level_factors(const float (&al)[BT], float (&f)[BT]) {
+        constexpr int S = 2 << B, HALF = 1 << B;
+#pragma unroll
+        for (int st = 0; st < BT; st += S) {
+            float run = al[st + HALF];
+            f[st + HALF] = run;
+#pragma unroll
+            for (int c = st + HALF + 1; c < st + S; ++c) {
+                run *= al[c];
+                f[c] = run;
+            }
+            f[st + HALF - 1] = 1.f;
+            run = al[st + HALF - 1];
+#pragma unroll
+            for (int i = st + HALF - 2; i >= st; --i) {
+                f[i] = run;
+                run *= al[i];
+            }
+        }
+    }
+
+    // One operand level of a block (producer p): stage X_b and Y_b k-major,
+    // read them back as MFMA fragments, form L_b = X_b X_b^T and
+    // A_b = Y_b X_b^T, and keep the level's pairs (accumulator layout: row
+    // 4lg + j, column ln).
+    template <int LEV>
+    __device__ void level(const Work& w, Slot<K>& sl, f4& Lacc, f4& Aacc) const {
+        // staged in this part's rows of the slot's QET / KET, which are
+        // written with their final values only after the last level
+        _Float16* xs = &sl.QET[0][0];
+        _Float16* ys = &sl.KET[0][0];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            h8 x0 = w.kh[c][0], x1 = w.kh[c][1], y0 = w.qh[c][0], y1 = w.qh[c][1];
+            if constexpr (LEV > 0) {
+                float f[BT];
+                level_factors<LEV - 1>(w.al[c], f);
+                h8 f0, f1;
+                to_h16(f, f0, f1);
+                x0 *= f0;
+                x1 *= f1;
+                y0 *= f0;
+                y1 *= f1;
+            }
+            const int ch = chan(c);
+            *reinterpret_cast<h8*>(xs + ch * BT) = x0;
+            *reinterpret_cast<h8*>(xs + ch * BT + 8) = x1;
+            *reinterpret_cast<h8*>(ys + ch * BT) = y0;
+            *reinterpret_cast<h8*>(ys + ch * BT + 8) = y1;
+        }
         f4 accL = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            const h8 xf = frag32_tr(&sm.XT[lev][0][0], lg, ln, u);
-            const h8 yf = frag32_tr(&sm.YT[lev][0][0], lg, ln, u);
-            if (lev != 0) accL = mfma16x16x32(xf, xf, accL);
+        for (int u = 0; u < KUW; ++u) {
+            const h8 xf = frag32_tr(xs + hh * KW * BT, lg, ln, u);
+            const h8 yf = frag32_tr(ys + hh * KW * BT, lg, ln, u);
+            if constexpr (LEV > 0) accL = mfma16x16x32(xf, xf, accL);
             accA = mfma16x16x32(yf, xf, accA);
         }
         const int i = ln;
-        const int lb = chunk % 2, ab = chunk % 3;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = 4 * lg + j;
-            if (lev == 0) {
-                if (i >= c) {
-                    sm.L[lb][c][i] = 0.f;
-                    sm.AM[ab][c][i] = static_cast<_Float16>(i == c ? accA[j] * scale : 0.f);
-                }
+            if constexpr (LEV == 0) {
+                if (i == c) Aacc[j] = accA[j];
             } else {
-                const int bb = lev - 1;
+                constexpr int bb = LEV - 1;
                 const bool pair = ((c >> (bb + 1)) == (i >> (bb + 1))) && ((c >> bb) & 1) && !((i >> bb) & 1);
                 if (pair) {
-                    sm.L[lb][c][i] = sm.beta[lb][c] * accL[j];
-                    sm.AM[ab][c][i] = static_cast<_Float16>(accA[j] * scale);
+                    Lacc[j] = w.beta[j] * accL[j];
+                    Aacc[j] = accA[j];
                 }
             }
         }
     }
 
-    // M = (I + L)^-1 Diag(beta) of one chunk (one wave), stored as hi/lo
-    // A-operand fragments for the consumers.
-    __device__ void solve_m(int chunk) const {
-        const int lb = chunk % 2;
-        f4 Lc, Lt;                                       // acc(L), acc(L^T)
+    // M = (I + L)^-1 Diag(beta) of one block (producer p), stored as hi/lo
+    // A-operand fragments.
+    __device__ void solve(const f4& Lc, const float (&beta)[4], Slot<K>& sl, int p) const {
+        float* lt = &sm.XCH[p][0][0][0];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) Lc[j] = sm.L[lb][4 * lg + j][ln];
+        for (int j = 0; j < 4; ++j) lt[(4 * lg + j) * LP + ln] = Lc[j];
+        f4 Lt;                                           // acc(L^T)
         {
-            const float4 r = *reinterpret_cast<const float4*>(&sm.L[lb][ln][4 * lg]);
+            const float4 r = *reinterpret_cast<const float4*>(lt + ln * LP + 4 * lg);
             Lt[0] = r.x; Lt[1] = r.y; Lt[2] = r.z; Lt[3] = r.w;
         }
-        const Split4 lc(Lc), lt(Lt);
-        const Split4 l2(mm3(lt, lc)), l2t(mm3(lc, lt));  // L^2, (L^2)^T
+        const Split4 lc(Lc), ltt(Lt);
+        const Split4 l2(mm3(ltt, lc)), l2t(mm3(lc, ltt));  // L^2, (L^2)^T
         const Split4 l4(mm3(l2t, l2)), l4t(mm3(l2, l2t));
         const Split4 l8(mm3(l4t, l4));
         f4 Q;                                            // acc(I - L^T)
@@ -461,27 +481,101 @@ struct Kern {
         Q += mm3(l2, Split4(Q));
         Q += mm3(l4, Split4(Q));
         Q += mm3(l8, Split4(Q));                         // acc(Minv^T) = A-layout of Minv
-        const float4 bt = *reinterpret_cast<const float4*>(&sm.beta[lb][4 * lg]);
-        Q[0] *= bt.x; Q[1] *= bt.y; Q[2] *= bt.z; Q[3] *= bt.w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Q[j] *= beta[j];
         h4 mh, ml;
         split4(Q, mh, ml);
-        *reinterpret_cast<h4*>(&sm.MH[ln][4 * lg]) = mh;
-        *reinterpret_cast<h4*>(&sm.ML[ln][4 * lg]) = ml;
+        *reinterpret_cast<h4*>(&sl.MH[ln][4 * lg]) = mh;
+        *reinterpret_cast<h4*>(&sl.ML[ln][4 * lg]) = ml;
+    }
+
+    // q * E, k * E, k * E15 / E and E15 of one block.
+    __device__ void escaled(const Work& w, Slot<K>& sl) const {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float (&al)[BT] = w.al[c];
+            float pre[BT], suf[BT];
+            pre[0] = al[0];
+#pragma unroll
+            for (int i = 1; i < BT; ++i) pre[i] = pre[i - 1] * al[i];
+            suf[BT - 1] = 1.f;
+#pragma unroll
+            for (int i = BT - 2; i >= 0; --i) suf[i] = suf[i + 1] * al[i + 1];
+            h8 e0, e1, s0, s1;
+            to_h16(pre, e0, e1);
+            to_h16(suf, s0, s1);
+            const int ch = chan(c);
+            *reinterpret_cast<h8*>(&sl.QET[ch][0]) = w.qh[c][0] * e0;
+            *reinterpret_cast<h8*>(&sl.QET[ch][8]) = w.qh[c][1] * e1;
+            *reinterpret_cast<h8*>(&sl.KET[ch][0]) = w.kh[c][0] * e0;
+            *reinterpret_cast<h8*>(&sl.KET[ch][8]) = w.kh[c][1] * e1;
+            const int sw = ((ch >> 3) & 1) * 8;          // 16-byte halves swapped on channel bit 3
+            *reinterpret_cast<h8*>(&sl.KHT[ch][sw]) = w.kh[c][0] * s0;
+            *reinterpret_cast<h8*>(&sl.KHT[ch][8 - sw]) = w.kh[c][1] * s1;
+            sl.elast[ch] = pre[BT - 1];
+        }
+    }
+
+    // First half of a superstep: the level products of this wave's channels
+    // (partial L and A over them), with the next block's loads issued in
+    // between; the first part also writes its E-scaled operands, the second
+    // part hands its partial sums to the first.
+    __device__ void phase1(Raw& raw, Work& w, f4& Lacc, f4& Aacc, int p, Slot<K>& sl, int next) const {
+        unpack(raw, w);
+        Lacc = f4{0.f, 0.f, 0.f, 0.f};
+        Aacc = f4{0.f, 0.f, 0.f, 0.f};
+        level<0>(w, sl, Lacc, Aacc);
+        load_rows<0, 4>(raw, next);
+        level<1>(w, sl, Lacc, Aacc);
+        load_rows<4, 8>(raw, next);
+        level<2>(w, sl, Lacc, Aacc);
+        load_rows<8, 12>(raw, next);
+        level<3>(w, sl, Lacc, Aacc);
+        load_rows<12, BT>(raw, next);
+        level<4>(w, sl, Lacc, Aacc);
+        if (hh == 0) {
+            escaled(w, sl);
+        } else {
+            *reinterpret_cast<f4*>(&sm.XCH[p][0][lane][0]) = Lacc;
+            *reinterpret_cast<f4*>(&sm.XCH[p][1][lane][0]) = Aacc;
+        }
+    }
+
+    // Second half: the first part completes L and A, writes A and inverts
+    // (I + L); the second part writes its E-scaled operands.
+    __device__ void phase2(const Work& w, const f4& Lacc, const f4& Aacc, int p, Slot<K>& sl) const {
+        if (hh != 0) {
+            escaled(w, sl);
+            return;
+        }
+        f4 L = Lacc, A = Aacc;
+        if constexpr (PW == 2) {
+            L += *reinterpret_cast<const f4*>(&sm.XCH[p][0][lane][0]);
+            A += *reinterpret_cast<const f4*>(&sm.XCH[p][1][lane][0]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sl.AM[4 * lg + j][ln] = static_cast<_Float16>(A[j] * scale);
+        solve(L, w.beta, sl, p);
     }
 
     // ------------------------------------------------------------ consumers
-    __device__ void v_load(uint32_t (&vr)[4], int chunk) const {
-        const auto rv = chunk_rsrc(a.v, a.v_stride, sizeof(TQ), rs_v, chunk);
+    __device__ void v_load(uint32_t (&vr)[4], int blk) const {
+        const auto rv = block_rsrc(a.v, a.v_stride, sizeof(TQ), rs_v, blk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vr[j] = QIn<TQ>::ld(rv, off_v[j]);
+        for (int j = 0; j < 4; ++j) BLoad<sizeof(TQ)>::ld(&vr[j], rv, vo_v, j * rs_v);
     }
 
-    __device__ void consumer_a(int chunk, const uint32_t (&vraw_)[4], f4 (&S)[KT], f4& P, f4& O) const {
-        uint32_t vraw[4] = {vraw_[0], vraw_[1], vraw_[2], vraw_[3]};
+    // One block of the chain for this wave's 16 state columns.
+    __device__ void consume(const Slot<K>& sl, int blk, uint32_t (&vraw)[4], int next, f4 (&S)[KT],
+                            int64_t col0, uint32_t ocol) const {
         use_here(vraw);
         float vr[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vr[j] = QIn<TQ>::f(vraw[j]);
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w1[1] = {vraw[j]};
+            vr[j] = VR::val(w1, 0);
+        }
+        v_load(vraw, next);
         h8 shi[KU], slo[KU];
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
@@ -492,15 +586,13 @@ struct Kern {
             slo[u] = h8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
         }
         // Z = (k * E) S and O = (q * E) S over the K channels
-        const int cb = chunk % 3;
-        f4 Z = {0.f, 0.f, 0.f, 0.f};
-        O = f4{0.f, 0.f, 0.f, 0.f};
+        f4 Z = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
-            const h8 kf = frag32_tr(&sm.KET[cb][0][0], lg, ln, u);
+            const h8 kf = frag32_tr(&sl.KET[0][0], lg, ln, u);
             Z = mfma16x16x32(kf, shi[u], Z);
             Z = mfma16x16x32(kf, slo[u], Z);
-            const h8 qf = frag32_tr(&sm.QET[cb][0][0], lg, ln, u);
+            const h8 qf = frag32_tr(&sl.QET[0][0], lg, ln, u);
             O = mfma16x16x32(qf, shi[u], O);
             O = mfma16x16x32(qf, slo[u], O);
         }
@@ -509,45 +601,49 @@ struct Kern {
 #pragma unroll
         for (int j = 0; j < 4; ++j) R[j] = vr[j] - Z[j];
         const Split4 r(R);
-        const h4 mh = frag16(&sm.MH[0][0], RP, ln, lg);
-        const h4 ml = frag16(&sm.ML[0][0], RP, ln, lg);
-        P = f4{0.f, 0.f, 0.f, 0.f};
+        const h4 mh = frag16(&sl.MH[0][0], RP, ln, lg);
+        const h4 ml = frag16(&sl.ML[0][0], RP, ln, lg);
+        f4 P = {0.f, 0.f, 0.f, 0.f};
         P = mfma16x16x16(mh, r.hi, P);
         P = mfma16x16x16(mh, r.lo, P);
         P = mfma16x16x16(ml, r.hi, P);
-    }
-
-    __device__ void consumer_b(int chunk, f4 (&S)[KT], const f4& P, f4 O, int64_t col0, uint32_t ocol) const {
-        const int cb = chunk % 3;
+        // O = scale (q * E) S + A P
 #pragma unroll
         for (int j = 0; j < 4; ++j) O[j] *= scale;
         h4 ph, pl;
         split4(P, ph, pl);
-        const h4 af = frag16(&sm.AM[cb][0][0], RP, ln, lg);
+        const h4 af = frag16(&sl.AM[0][0], RP, ln, lg);
         O = mfma16x16x16(af, ph, O);
         O = mfma16x16x16(af, pl, O);
-        // o[b, t, h, col]: wave-uniform chunk base + 32-bit lane offset
-        TQ* o = static_cast<TQ*>(a.o) + ((b * T + static_cast<int64_t>(chunk) * BT) * a.H + h) * a.V + col0;
+        // o[b, t, h, col]: wave-uniform block base + 32-bit lane offset
+        TQ* o = static_cast<TQ*>(a.o) + ((b * T + static_cast<int64_t>(blk) * BT) * a.H + h) * a.V + col0;
         const uint32_t orow = static_cast<uint32_t>(a.H * a.V);
-        const int nrow = rows_in(chunk);
+        const int nrow = rows_in(blk);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (4 * lg + j < nrow) Elem<TQ>::st(o + (4 * lg + j) * orow + ocol, O[j]);
+        // S <- E15 S + Khat^T P
+        const int kg = lg ^ (((ln >> 3) & 1) * 2);       // KHT halves swapped on channel bit 3
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
-            const float4 e = *reinterpret_cast<const float4*>(&sm.elast[cb][16 * t + 4 * lg]);
+            const float4 e = *reinterpret_cast<const float4*>(&sl.elast[16 * t + 4 * lg]);
             S[t][0] *= e.x; S[t][1] *= e.y; S[t][2] *= e.z; S[t][3] *= e.w;
-            const h4 kf = frag16(&sm.KHT[cb][16 * t][0], RP, ln, lg);
+            const h4 kf = frag16(&sl.KHT[16 * t][0], BT, ln, kg);
             S[t] = mfma16x16x16(kf, ph, S[t]);
             S[t] = mfma16x16x16(kf, pl, S[t]);
         }
     }
 };
 
+// Supersteps of NB blocks.  Before superstep s the producers have filled
+// slot set s % 2 with the blocks of superstep s; during it they fill the
+// other set with superstep s + 1 while the consumers run superstep s; one
+// workgroup barrier ends each superstep.  Every wave executes the same
+// barriers; every prefetch is issued unconditionally (block index clamped).
 template <int K, int NC, typename TQ>
-__global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda_fwd_args a) {
+__global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(const kda_fwd_args a) {
     using KN = Kern<K, NC, TQ>;
-    constexpr int NP = KN::NP, KT = KN::KT, VT = KN::VT;
+    constexpr int KT = KN::KT, VT = KN::VT;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
     __shared__ Smem<K> sm;
     KN kn(a, sm);
@@ -566,24 +662,25 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
     kn.T = a.T;
     kn.nch = static_cast<int>((a.T + BT - 1) / BT);
     kn.scale = a.scale;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    kn.lane = tid & 63;
+    // wave index as a scalar: block indices and buffer descriptors derived
+    // from it stay in SGPRs (no per-lane descriptor loops around the loads)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kn.lane = threadIdx.x & 63;
     kn.ln = kn.lane & 15;
     kn.lg = kn.lane >> 4;
     const int nch = kn.nch;
+    const int nss = (nch + NB - 1) / NB;
+    const int last = nch - 1;
 
     const bool consumer = wave < NC;
+    // producer wave q = wave - NC builds block q / PW, channel part q % PW
+    const int pq = consumer ? 0 : wave - NC;
+    kn.hh = pq % KN::PW;
     // consumer state: S[t][j] = S[16t + 4lg + j][col], col = col0 + ocol
     const int64_t col0 = static_cast<int64_t>(vt) * VT;
     const uint32_t ocol = static_cast<uint32_t>(16 * (consumer ? wave : 0) + kn.ln);
     const int64_t col = col0 + ocol;
     const int64_t sbase = (kn.b * H + kn.h) * static_cast<int64_t>(K) * V;
-    // producer lane: channel c, rows 8*hf .. 8*hf+7
-    const int pw = wave - NC;
-    const int pc = 32 * (consumer ? 0 : pw) + (kn.lane & 31);
-    const int phf = kn.lane >> 5;
-    const bool beta_lane = !consumer && pw == 0 && kn.lane < BT;
     {
         const uint32_t eq = static_cast<uint32_t>(sizeof(TQ));
         kn.rs_q = static_cast<uint32_t>(a.q_stride[1]) * eq;
@@ -591,81 +688,46 @@ __global__ __launch_bounds__(64 * (NC + K / 32)) void chunkwise_kernel(const kda
         kn.rs_v = static_cast<uint32_t>(a.v_stride[1]) * eq;
         kn.rs_g = static_cast<uint32_t>(a.g_stride[1]) * 4u;
         kn.rs_b = static_cast<uint32_t>(a.beta_stride[1]) * 4u;
-        // lane byte offsets inside a chunk; rows past T fall outside the
-        // chunk's descriptor and read as zero
-        const uint32_t pcol = static_cast<uint32_t>(pc);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t r = static_cast<uint32_t>(8 * phf + i);
-            kn.off_q[i] = r * kn.rs_q + pcol * eq;
-            kn.off_k[i] = r * kn.rs_k + pcol * eq;
-            kn.off_g[i] = r * kn.rs_g + pcol * 4u;
-        }
-        kn.off_b = static_cast<uint32_t>(kn.lane) * kn.rs_b;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            kn.off_v[j] = static_cast<uint32_t>(4 * kn.lg + j) * kn.rs_v + static_cast<uint32_t>(col) * eq;
+        const uint32_t c0 = static_cast<uint32_t>(kn.chan(0));
+        kn.vo_q = c0 * eq;
+        kn.vo_k = c0 * eq;
+        kn.vo_g = c0 * 4u;
+        kn.vo_b = static_cast<uint32_t>(4 * kn.lg) * kn.rs_b;
+        kn.vo_v = static_cast<uint32_t>(4 * kn.lg) * kn.rs_v + static_cast<uint32_t>(col) * eq;
     }
 
-    // step sp: producers build chunk sp, producer 0 inverts chunk sp-1,
-    // consumers run chunk sp-2.  Each role runs its own loop with the same
-    // two barriers per step; register sets alternate with sp's parity and
-    // every prefetch is issued unconditionally (chunk index clamped), so the
-    // compiler's load accounting stays exact and a wait covers only the chunk
-    // being consumed.
-    const int nsteps = nch + 2;
-    const int last = nch - 1;
     if (consumer) {
         f4 S[KT];
-        uint32_t vr0[4], vr1[4];
         load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
-        kn.v_load(vr0, 0);
-        kn.v_load(vr1, min(1, last));
-        f4 P = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
-        auto step = [&](int sp, uint32_t (&vr)[4]) {
-            const int cc = sp - 2;
-            if (cc >= 0) {
-                kn.consumer_a(cc, vr, S, P, O);
-                kn.v_load(vr, min(cc + 2, last));
+        uint32_t vr[NB][4];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) kn.v_load(vr[j], min(j, last));
+        for (int s = -1; s < nss; ++s) {
+            const Slot<K>* set = &sm.slot[(s & 1) * NB];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+#pragma unroll
+                for (int j = half * (NB / 2); j < (half + 1) * (NB / 2); ++j) {
+                    const int blk = NB * s + j;
+                    if (s >= 0 && blk < nch) kn.consume(set[j], blk, vr[j], min(blk + NB, last), S, col0, ocol);
+                }
+                __syncthreads();
             }
-            __syncthreads();
-            if (cc >= 0) kn.consumer_b(cc, S, P, O, col0, ocol);
-            __syncthreads();
-        };
-        for (int sp = 0; sp < nsteps; sp += 2) {
-            step(sp, vr0);
-            if (sp + 1 < nsteps) step(sp + 1, vr1);
         }
         store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
     } else {
-        PrepIn pin0, pin1;
-        kn.prep_load(pin0, 0, beta_lane);
-        kn.prep_load(pin1, min(1, last), beta_lane);
-        typename KN::PrepMid mid;
-        auto step = [&](int sp, PrepIn& pin) {
-            const int cp = sp, cs = sp - 1;
-            if (cp < nch) {
-                kn.prep_levels(pin, mid, cp, pc, phf, beta_lane);
-                kn.prep_load(pin, min(cp + 2, last), beta_lane);
-            }
+        const int p = pq / KN::PW;
+        typename KN::Raw raw;
+        typename KN::Work w;
+        f4 Lacc, Aacc;
+        kn.load_raw(raw, min(p, last));
+        for (int s = -1; s < nss; ++s) {
+            const int blk = NB * (s + 1) + p;
+            Slot<K>& sl = sm.slot[((s + 1) & 1) * NB + p];
+            if (blk < nch) kn.phase1(raw, w, Lacc, Aacc, p, sl, min(blk + NB, last));
             __syncthreads();
-            if (pw == 0 && cs >= 0 && cs < nch) kn.solve_m(cs);
-            if (cp < nch) {
-                if (NP == 1) {
-#pragma unroll
-                    for (int lev = 0; lev < NLEV; ++lev) kn.level_mfma(lev, cp);
-                } else {
-#pragma unroll
-                    for (int lev = 0; lev < NLEV; ++lev)
-                        if (1 + lev % (NP - 1) == pw) kn.level_mfma(lev, cp);
-                }
-                kn.prep_e(mid, cp, pc, phf);
-            }
+            if (blk < nch) kn.phase2(w, Lacc, Aacc, p, sl);
             __syncthreads();
-        };
-        for (int sp = 0; sp < nsteps; sp += 2) {
-            step(sp, pin0);
-            if (sp + 1 < nsteps) step(sp + 1, pin1);
         }
     }
 }
@@ -674,14 +736,18 @@ template <int K, int NC, typename TQ>
 int launch_knq(const kda_fwd_args& a, hipStream_t stream) {
     const int64_t blocks = a.B * a.H * (a.V / (16 * NC));
     hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(64 * (NC + K / 32)), 0, stream, a);
+                       dim3(64 * (NC + NB * kPW<K>)), 0, stream, a);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
+// Columns per workgroup: the widest tile (64, 32 or 16 columns) that still
+// gives at least one workgroup per CU; 16 when none does (few chains).
 template <int K, typename TQ>
 int launch_kq(const kda_fwd_args& a, hipStream_t stream) {
-    if (a.V % 64 == 0) return launch_knq<K, 4, TQ>(a, stream);
-    if (a.V % 32 == 0) return launch_knq<K, 2, TQ>(a, stream);
+    constexpr int64_t kCus = 256;
+    const int64_t heads = a.B * a.H;
+    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ>(a, stream);
+    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ>(a, stream);
     return launch_knq<K, 1, TQ>(a, stream);
 }
 

@@ -59,8 +59,18 @@ def _check_tensor(name, x):
 
 
 def _as_kernel_input(x: torch.Tensor) -> torch.Tensor:
-    """A view whose last dimension is contiguous (copying only if it is not)."""
-    if x.dim() > 0 and x.shape[-1] > 1 and x.stride(-1) != 1:
+    """A [B, T, H, D] view whose last dimension is contiguous and whose token
+    rows do not overlap (stride(1) >= D), copying only if it is not."""
+    if x.shape[-1] > 1 and x.stride(-1) != 1:
+        return x.contiguous()
+    if x.shape[1] > 1 and x.stride(1) < x.shape[-1]:
+        return x.contiguous()
+    return x
+
+
+def _beta_input(x: torch.Tensor) -> torch.Tensor:
+    """A [B, T, H] view with distinct token rows (stride(1) >= 1)."""
+    if x.shape[1] > 1 and x.stride(1) < 1:
         return x.contiguous()
     return x
 
@@ -133,7 +143,7 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
         g = g.float()
         beta = beta.float()
     g = _as_kernel_input(_float_or_f32(g))
-    beta = _float_or_f32(beta)
+    beta = _beta_input(_float_or_f32(beta))
     if state is not None:
         state = _float_or_f32(state)
         if not state.is_contiguous():

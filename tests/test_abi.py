@@ -98,6 +98,20 @@ def test_host_validation_codes(native, fn):
     assert call(ctypes.byref(_args(native, H=0)), None) == 0
 
 
+def test_chunkwise_row_stride_contract(native):
+    # chunkwise reads each chunk through a descriptor spanning its token rows,
+    # so a token stride shorter than a row is rejected before any launch
+    lib = native.load()
+    good = dict(q_stride=(ctypes.c_int64 * 3)(16 * 64, 64, 64), k_stride=(ctypes.c_int64 * 3)(16 * 64, 64, 64),
+                v_stride=(ctypes.c_int64 * 3)(16 * 64, 64, 64), g_stride=(ctypes.c_int64 * 3)(16 * 64, 64, 64),
+                beta_stride=(ctypes.c_int64 * 3)(16, 1, 1))
+    for name, bad in (("q_stride", (16 * 64, 0, 64)), ("g_stride", (16 * 64, 32, 64)),
+                      ("v_stride", (16 * 64, 63, 64)), ("beta_stride", (16, 0, 1))):
+        kw = dict(good)
+        kw[name] = (ctypes.c_int64 * 3)(*bad)
+        assert lib.kda_chunkwise_fwd(ctypes.byref(_args(native, **kw)), None) == 4, name
+
+
 def test_chunk_contract(native):
     lib = native.load()
     assert lib.kda_chunkwise_fwd(ctypes.byref(_args(native, T=20, chunk_size=16)), None) == 2

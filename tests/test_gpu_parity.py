@@ -254,6 +254,20 @@ def test_strided_body_slice_and_dtypes(kda_pkg, wl):
     assert max_abs(o2, o2_ref) <= O_TOL and rel(s2, s2_ref) <= 2e-3
 
 
+def test_broadcast_inputs(kda_pkg, wl):
+    # stride-0 (expanded) token dimensions: the wrapper copies them to
+    # distinct rows; results equal those of the materialised tensors
+    inp = to_dev(wl.make_inputs(1, 64, 2, 64, 64, seed=8, qkv_dtype=torch.float16, state_std=0.02))
+    ex = dict(inp)
+    ex["k"] = inp["k"][:, :1].expand(-1, 64, -1, -1)
+    ex["beta"] = inp["beta"][:, :1].expand(-1, 64, -1)
+    mat = dict(ex)
+    mat["k"], mat["beta"] = ex["k"].contiguous(), ex["beta"].contiguous()
+    o1, s1 = run_chunkwise(kda_pkg, ex, 16)
+    o2, s2 = run_chunkwise(kda_pkg, mat, 16)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
 @pytest.mark.parametrize("K,V", [(32, 32), (64, 16), (128, 64), (32, 128)])
 def test_head_dims(kda_pkg, wl, K, V):
     inp = wl.make_inputs(1, 48, 2, K, V, seed=7, qkv_dtype=torch.float16, state_std=0.02)
