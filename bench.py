@@ -126,8 +126,8 @@ def decode_bench(pkg, wl, torch, n_sets):
 def cpu_baselines(wl, torch, include_decode=True):
     from oracle import kda_chunkwise_ref, kda_recurrent_ref
     threads = torch.get_num_threads()
-    # chunkwise sample: two sequences of the same layer shape (all 16 heads), 8192 tokens each
-    Bs, Ts = 2, 8192
+    # chunkwise sample: four sequences of the same layer shape (all 16 heads), 12288 tokens each
+    Bs, Ts = 4, 12288
     s = wl.make_inputs(Bs, Ts, H1, D1, D1, device="cpu", seed=1, qkv_dtype=torch.float16)
     t0 = time.perf_counter()
     kda_chunkwise_ref(s["q"], s["k"], s["v"], s["g"], s["beta"], chunk_size=C1,
@@ -137,7 +137,7 @@ def cpu_baselines(wl, torch, include_decode=True):
            "sample": f"oracle kda_chunkwise_ref, B={Bs} T={Ts} H=16 dk=dv=128 C=64 (fp16 inputs "
                      f"upcast to fp32), one run, {tc:.1f} s"}
     if include_decode:
-        nst = 96
+        nst = 384
         d = wl.make_inputs(B2, nst, H2, D1, D1, device="cpu", seed=2, qkv_dtype=torch.float16,
                            gate_dtype=torch.float16, state_std=0.02)
         t0 = time.perf_counter()
