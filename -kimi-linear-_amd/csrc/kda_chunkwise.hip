@@ -154,16 +154,15 @@ __device__ __forceinline__ void to_h16(const float (&x)[BT], h8& lo, h8& hi) {
 // without any barrier; the compiler keeps the order of the possibly
 // aliasing LDS accesses.  The per-producer staging areas rely on this.
 
-// Operands of one block, as the consumers read them.  Matrices read through
-// LDS transpose loads are stored k-major ([K][16]: the 16 rows of a channel
-// contiguous); KHT holds channel rows read as A operands, with the two 8-byte
-// halves of each 16-byte group swapped on channels with bit 3 set, so the
-// 16 lanes of a read hit distinct banks without padding.
+// Operands of one block, as the consumers read them.  QET and KET are read
+// through LDS transpose loads, KHT as A-operand rows of channels; all three
+// are k-major ([K][16]: the 16 rows of a channel in one 32-byte line, halves
+// swizzled by channel bit 3, see kswz).
 template <int K>
 struct __align__(16) Slot {
     _Float16 QET[K][BT];                   // q * E
     _Float16 KET[K][BT];                   // k * E
-    _Float16 KHT[K][BT];                   // k * E15 / E (swizzled)
+    _Float16 KHT[K][BT];                   // k * E15 / E
     _Float16 AM[BT][RP];                   // scale * A
     _Float16 MH[BT][RP];                   // M hi
     _Float16 ML[BT][RP];                   // M lo
@@ -190,13 +189,29 @@ __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, 
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s4 lds_s4;
 
+// k-major [K][16] fp16 matrices (the 16 rows of a channel in one 32-byte
+// line) swap the two 16-byte halves of the line on channels with bit 3 set,
+// so the 16-byte writes of 16 consecutive channels (one per lane) cover all
+// 64 banks once.  Half h of channel c sits at 8 * (h ^ kswz(c)).
+__device__ __forceinline__ int kswz(int c) { return (c >> 3) & 1; }
+
+// Stores the 16 rows of channel c (rows 0-7, 8-15) into a k-major matrix.
+__device__ __forceinline__ void store_kmajor(_Float16* xt, int c, const h8& r0_7, const h8& r8_15) {
+    const int s = kswz(c) * 8;
+    *reinterpret_cast<h8*>(xt + c * BT + s) = r0_7;
+    *reinterpret_cast<h8*>(xt + c * BT + (8 - s)) = r8_15;
+}
+
 // MFMA row fragment from a k-major [K][16] fp16 matrix X^T through the LDS
 // transpose read (ds_read_b64_tr_b16): within each 16-lane group, lane 4j+q
 // supplies the four rows 4q..4q+3 of channel kbase+j, and lane i receives
 // X[i][kbase + 0..3] -- the A-operand fragment of row i, which is also the
-// B-operand fragment of column i of X^T.
-__device__ __forceinline__ h4 frag16_tr(const _Float16* xt, int kbase, int ln) {
-    const _Float16* p = xt + (kbase + (ln >> 2)) * BT + 4 * (ln & 3);
+// B-operand fragment of column i of X^T.  kbase is 4lg modulo 16, so the
+// channels kbase + j (j < 4) share bit 3 = lg >> 1 and the swizzled column of
+// rows 4q..4q+3 is 4 (q ^ 2 (lg >> 1)), a per-lane constant.
+__device__ __forceinline__ h4 frag16_tr(const _Float16* xt, int kbase, int ln, int lg) {
+    const int q = (ln & 3) ^ ((lg >> 1) * 2);
+    const _Float16* p = xt + (kbase + (ln >> 2)) * BT + 4 * q;
     return __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
 }
 
@@ -205,8 +220,8 @@ __device__ __forceinline__ h4 frag16_tr(const _Float16* xt, int kbase, int ln) {
 // product is the full 32-wide dot product whatever slot order the unit uses;
 // it also matches the two state tiles 2u, 2u+1 held by a consumer lane group.
 __device__ __forceinline__ h8 frag32_tr(const _Float16* xt, int lg, int ln, int u) {
-    const h4 lo = frag16_tr(xt, 32 * u + 4 * lg, ln);
-    const h4 hi = frag16_tr(xt, 32 * u + 16 + 4 * lg, ln);
+    const h4 lo = frag16_tr(xt, 32 * u + 4 * lg, ln, lg);
+    const h4 hi = frag16_tr(xt, 32 * u + 16 + 4 * lg, ln, lg);
     return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -406,16 +421,11 @@ struct Kern {
         }
     }
 
-    // One operand level of a block (producer p): stage X_b and Y_b k-major,
-    // read them back as MFMA fragments, form L_b = X_b X_b^T and
-    // A_b = Y_b X_b^T, and keep the level's pairs (accumulator layout: row
-    // 4lg + j, column ln).
+    // Operand level LEV of a block (this wave's channels): X_b = k * F_b and
+    // Y_b = q * F_b, stored k-major into a staging pair (xs, ys) whose row 0
+    // is this wave's first channel.
     template <int LEV>
-    __device__ void level(const Work& w, Slot<K>& sl, f4& Lacc, f4& Aacc) const {
-        // staged in this part's rows of the slot's QET / KET, which are
-        // written with their final values only after the last level
-        _Float16* xs = &sl.QET[0][0];
-        _Float16* ys = &sl.KET[0][0];
+    __device__ void stage(const Work& w, _Float16* xs, _Float16* ys) const {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             h8 x0 = w.kh[c][0], x1 = w.kh[c][1], y0 = w.qh[c][0], y1 = w.qh[c][1];
@@ -429,17 +439,22 @@ struct Kern {
                 y0 *= f0;
                 y1 *= f1;
             }
-            const int ch = chan(c);
-            *reinterpret_cast<h8*>(xs + ch * BT) = x0;
-            *reinterpret_cast<h8*>(xs + ch * BT + 8) = x1;
-            *reinterpret_cast<h8*>(ys + ch * BT) = y0;
-            *reinterpret_cast<h8*>(ys + ch * BT + 8) = y1;
+            const int lc = chan(c) - hh * KW;
+            store_kmajor(xs, lc, x0, x1);
+            store_kmajor(ys, lc, y0, y1);
         }
+    }
+
+    // Level LEV's products from its staging pair: L_b = X_b X_b^T and
+    // A_b = Y_b X_b^T over this wave's channels, keeping the level's pairs
+    // (accumulator layout: row 4lg + j, column ln).
+    template <int LEV>
+    __device__ void product(const Work& w, const _Float16* xs, const _Float16* ys, f4& Lacc, f4& Aacc) const {
         f4 accL = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < KUW; ++u) {
-            const h8 xf = frag32_tr(xs + hh * KW * BT, lg, ln, u);
-            const h8 yf = frag32_tr(ys + hh * KW * BT, lg, ln, u);
+            const h8 xf = frag32_tr(xs, lg, ln, u);
+            const h8 yf = frag32_tr(ys, lg, ln, u);
             if constexpr (LEV > 0) accL = mfma16x16x32(xf, xf, accL);
             accA = mfma16x16x32(yf, xf, accA);
         }
@@ -505,13 +520,9 @@ struct Kern {
             to_h16(pre, e0, e1);
             to_h16(suf, s0, s1);
             const int ch = chan(c);
-            *reinterpret_cast<h8*>(&sl.QET[ch][0]) = w.qh[c][0] * e0;
-            *reinterpret_cast<h8*>(&sl.QET[ch][8]) = w.qh[c][1] * e1;
-            *reinterpret_cast<h8*>(&sl.KET[ch][0]) = w.kh[c][0] * e0;
-            *reinterpret_cast<h8*>(&sl.KET[ch][8]) = w.kh[c][1] * e1;
-            const int sw = ((ch >> 3) & 1) * 8;          // 16-byte halves swapped on channel bit 3
-            *reinterpret_cast<h8*>(&sl.KHT[ch][sw]) = w.kh[c][0] * s0;
-            *reinterpret_cast<h8*>(&sl.KHT[ch][8 - sw]) = w.kh[c][1] * s1;
+            store_kmajor(&sl.QET[0][0], ch, w.qh[c][0] * e0, w.qh[c][1] * e1);
+            store_kmajor(&sl.KET[0][0], ch, w.kh[c][0] * e0, w.kh[c][1] * e1);
+            store_kmajor(&sl.KHT[0][0], ch, w.kh[c][0] * s0, w.kh[c][1] * s1);
             sl.elast[ch] = pre[BT - 1];
         }
     }
@@ -524,15 +535,24 @@ struct Kern {
         unpack(raw, w);
         Lacc = f4{0.f, 0.f, 0.f, 0.f};
         Aacc = f4{0.f, 0.f, 0.f, 0.f};
-        level<0>(w, sl, Lacc, Aacc);
+        // level operands are staged in this part's rows of the slot's QET /
+        // KET, which get their final values only after the last level
+        _Float16* xs = &sl.QET[hh * KW][0];
+        _Float16* ys = &sl.KET[hh * KW][0];
+        stage<0>(w, xs, ys);
+        product<0>(w, xs, ys, Lacc, Aacc);
         load_rows<0, 4>(raw, next);
-        level<1>(w, sl, Lacc, Aacc);
+        stage<1>(w, xs, ys);
+        product<1>(w, xs, ys, Lacc, Aacc);
         load_rows<4, 8>(raw, next);
-        level<2>(w, sl, Lacc, Aacc);
+        stage<2>(w, xs, ys);
+        product<2>(w, xs, ys, Lacc, Aacc);
         load_rows<8, 12>(raw, next);
-        level<3>(w, sl, Lacc, Aacc);
+        stage<3>(w, xs, ys);
+        product<3>(w, xs, ys, Lacc, Aacc);
         load_rows<12, BT>(raw, next);
-        level<4>(w, sl, Lacc, Aacc);
+        stage<4>(w, xs, ys);
+        product<4>(w, xs, ys, Lacc, Aacc);
         if (hh == 0) {
             escaled(w, sl);
         } else {
