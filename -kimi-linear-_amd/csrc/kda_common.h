@@ -36,6 +36,29 @@ __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) 
     }
 }
 
+// Branch-free element load for a runtime dtype: one 32-bit load of the
+// aligned word that holds element i (a 2-byte element sits in its low or high
+// half), issued the same way for every dtype so that several such loads are
+// in flight together; decode_elem converts it once the data is needed.
+struct RawElem {
+    uint32_t word;
+    uint32_t shift;   // 0 or 16 for 2-byte elements
+};
+__device__ __forceinline__ RawElem load_raw_elem(const void* p, int64_t i, int dtype) {
+    const int64_t es = dtype == KDA_DTYPE_F32 ? 4 : 2;
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(i * es);
+    RawElem r;
+    r.word = *reinterpret_cast<const uint32_t*>(addr & ~static_cast<uintptr_t>(3));
+    r.shift = static_cast<uint32_t>(addr & 2) * 8u;
+    return r;
+}
+__device__ __forceinline__ float decode_elem(const RawElem& r, int dtype) {
+    if (dtype == KDA_DTYPE_F32) return __uint_as_float(r.word);
+    const uint16_t half = static_cast<uint16_t>(r.word >> r.shift);
+    if (dtype == KDA_DTYPE_F16) return static_cast<float>(__builtin_bit_cast(_Float16, half));
+    return bf16_bits_to_f32(half);
+}
+
 __device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float x) {
     switch (dtype) {
         case KDA_DTYPE_F16: static_cast<_Float16*>(p)[i] = static_cast<_Float16>(x); break;

@@ -9,11 +9,14 @@
 //   S' = Diag(a) S,   u = S'^T k,   r = S'^T q~,   d = beta (v - u)
 //   S  = S' + k d^T,  o = r + (q~ . k) d            (== S^T q~ after the update)
 //
-// Work split: one 256-thread workgroup per (b, h, V-tile of VT columns).
-// Thread t owns 4 consecutive columns (t % (VT/4)) of rows rg, rg + RG, ...
-// with rg = t / (VT/4), so every state row segment is a coalesced 16-byte
-// access.  The two K-reductions (u, r) and q~.k go through wave shuffles and
-// one LDS exchange per token.
+// Work split: one workgroup of NW waves per (b, h, V-tile of 16 NW columns);
+// wave w owns columns [16w, 16w + 16) of the tile for all K rows, so both
+// K-reductions (u, r) and q~.k stay inside the wave.  Lane l holds the four
+// columns 4 (l & 3) .. +3 of the K/16 consecutive rows starting at
+// (K/16) (l >> 2): a row segment is one 16-byte access.  The reduction over
+// the 16 row groups is two DPP row rotations (lanes 4 and 8 apart) and the
+// two cross-row swaps (16 and 32 apart), all on the VALU.  q~, k and a of a
+// token are staged once per workgroup in LDS.
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -21,22 +24,32 @@ namespace kda {
 
 namespace {
 
-constexpr int kRecThreads = 256;
+// Sum of x over the 16 lanes that share l & 3 (all-reduce, every lane gets it).
+__device__ __forceinline__ float rowgroup_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));  // row_ror:4
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
+    // permlane16_swap(x, x) returns x of lane l & ~16 and of lane l | 16;
+    // permlane32_swap likewise for bit 5: the sum of both is the pair sum
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return x;
+}
 
-template <int K, int VT>
-__global__ __launch_bounds__(kRecThreads) void recurrent_kernel(const kda_fwd_args a) {
-    constexpr int CPR = VT / 4;                 // threads per state row
-    constexpr int RG = kRecThreads / CPR;       // row groups
-    constexpr int RPT = K / RG;                 // rows per thread
-    constexpr int NWAVE = kRecThreads / 64;
-    static_assert(VT % 4 == 0 && kRecThreads % CPR == 0, "bad V tile");
-    static_assert(RPT >= 1 && K % RG == 0, "K must be a multiple of the row-group count");
-    static_assert(CPR <= 64, "a state row segment must fit one wave");
+template <int K, int NW>
+__global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a) {
+    constexpr int RPL = K / 16;                 // rows per lane
+    constexpr int VT = 16 * NW;                 // columns per workgroup
+    static_assert(K % 16 == 0 && RPL >= 1, "K must be a multiple of 16");
 
     __shared__ float s_q[K], s_k[K], s_a[K];
-    __shared__ float s_v[VT];
-    __shared__ float s_beta;
-    __shared__ float s_red[NWAVE][2 * VT + 1];
 
     const int64_t H = a.H, T = a.T, V = a.V;
     const int nvt = static_cast<int>(V / VT);
@@ -48,110 +61,96 @@ __global__ __launch_bounds__(kRecThreads) void recurrent_kernel(const kda_fwd_ar
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int cg = tid % CPR, rg = tid / CPR;
-    const int64_t col0 = static_cast<int64_t>(vt) * VT + 4 * cg;
-
+    const int cg = lane & 3, rg = lane >> 2;
+    const int r0 = RPL * rg;
+    const int64_t col0 = static_cast<int64_t>(vt) * VT + 16 * wave + 4 * cg;
     const int64_t sbase = (b * H + h) * static_cast<int64_t>(K) * V;
 
-    float S[RPT][4];
+    // fp32 state rows go through one buffer descriptor per head: the lane
+    // offset is one register and the row offset a scalar
+    const uint32_t row_bytes = static_cast<uint32_t>(V) * 4u;
+    const uint32_t lane_off = static_cast<uint32_t>(r0) * row_bytes + static_cast<uint32_t>(col0) * 4u;
+    float S[RPL][4];
     const bool vec_in = a.state_in != nullptr && a.state_in_dtype == KDA_DTYPE_F32 &&
-                        (reinterpret_cast<uintptr_t>(a.state_in) & 15) == 0;
+                        (reinterpret_cast<uintptr_t>(a.state_in) & 15) == 0 && (V & 3) == 0;
     if (a.state_in == nullptr) {
 #pragma unroll
-        for (int j = 0; j < RPT; ++j)
+        for (int j = 0; j < RPL; ++j)
 #pragma unroll
             for (int c = 0; c < 4; ++c) S[j][c] = 0.f;
     } else if (vec_in) {
-        const float* sp = static_cast<const float*>(a.state_in);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(static_cast<const float*>(a.state_in) + sbase), static_cast<short>(0),
+            static_cast<int>(K * row_bytes), 0x00020000);
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int64_t r = rg + RG * j;
-            const float4 x = *reinterpret_cast<const float4*>(sp + sbase + r * V + col0);
-            S[j][0] = x.x; S[j][1] = x.y; S[j][2] = x.z; S[j][3] = x.w;
+        for (int j = 0; j < RPL; ++j) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(lane_off),
+                                                                  static_cast<int>(j * row_bytes), 0);
+            S[j][0] = __uint_as_float(x[0]); S[j][1] = __uint_as_float(x[1]);
+            S[j][2] = __uint_as_float(x[2]); S[j][3] = __uint_as_float(x[3]);
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int64_t r = rg + RG * j;
+        for (int j = 0; j < RPL; ++j)
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                S[j][c] = load_elem(a.state_in, sbase + r * V + col0 + c, a.state_in_dtype);
-        }
+                S[j][c] = load_elem(a.state_in, sbase + static_cast<int64_t>(r0 + j) * V + col0 + c,
+                                    a.state_in_dtype);
     }
 
     const float scale = a.scale;
     for (int64_t t = 0; t < T; ++t) {
-        // ---- stage token t: q~, k, exp(g) for all K rows; v for this tile; beta
-        if (tid < K) {
-            const int64_t iq = b * a.q_stride[0] + t * a.q_stride[1] + h * a.q_stride[2] + tid;
-            const int64_t ik = b * a.k_stride[0] + t * a.k_stride[1] + h * a.k_stride[2] + tid;
-            const int64_t ig = b * a.g_stride[0] + t * a.g_stride[1] + h * a.g_stride[2] + tid;
-            s_q[tid] = load_elem(a.q, iq, a.qkv_dtype) * scale;
-            s_k[tid] = load_elem(a.k, ik, a.qkv_dtype);
-            s_a[tid] = fast_exp(load_elem(a.g, ig, a.g_dtype));
+        // ---- stage token t: q~, k, exp(g) for all K rows; v, beta per lane.
+        // Every load is issued before any is decoded.
+        const int64_t tq = b * a.q_stride[0] + t * a.q_stride[1] + h * a.q_stride[2];
+        const int64_t tk = b * a.k_stride[0] + t * a.k_stride[1] + h * a.k_stride[2];
+        const int64_t tg = b * a.g_stride[0] + t * a.g_stride[1] + h * a.g_stride[2];
+        const int64_t tv = b * a.v_stride[0] + t * a.v_stride[1] + h * a.v_stride[2] + col0;
+        RawElem rv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rv[c] = load_raw_elem(a.v, tv + c, a.qkv_dtype);
+        const RawElem rb =
+            load_raw_elem(a.beta, b * a.beta_stride[0] + t * a.beta_stride[1] + h * a.beta_stride[2], a.beta_dtype);
+        for (int i = tid; i < K; i += 64 * NW) {
+            const RawElem rq = load_raw_elem(a.q, tq + i, a.qkv_dtype);
+            const RawElem rk = load_raw_elem(a.k, tk + i, a.qkv_dtype);
+            const RawElem rg = load_raw_elem(a.g, tg + i, a.g_dtype);
+            s_q[i] = decode_elem(rq, a.qkv_dtype) * scale;
+            s_k[i] = decode_elem(rk, a.qkv_dtype);
+            s_a[i] = fast_exp(decode_elem(rg, a.g_dtype));
         }
-        if (tid < VT) {
-            const int64_t iv = b * a.v_stride[0] + t * a.v_stride[1] + h * a.v_stride[2] +
-                               static_cast<int64_t>(vt) * VT + tid;
-            s_v[tid] = load_elem(a.v, iv, a.qkv_dtype);
-        }
-        if (tid == 0) {
-            const int64_t ib = b * a.beta_stride[0] + t * a.beta_stride[1] + h * a.beta_stride[2];
-            s_beta = load_elem(a.beta, ib, a.beta_dtype);
-        }
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = decode_elem(rv[c], a.qkv_dtype);
+        const float beta = decode_elem(rb, a.beta_dtype);
         __syncthreads();
 
-        // ---- decay, then partial K-reductions over this thread's rows
-        float pu[4] = {0.f, 0.f, 0.f, 0.f}, pr[4] = {0.f, 0.f, 0.f, 0.f}, pqk = 0.f;
+        // ---- decay, then the lane's partial K-reductions over its rows
+        float u[4] = {0.f, 0.f, 0.f, 0.f}, rr[4] = {0.f, 0.f, 0.f, 0.f}, qk = 0.f;
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int r = rg + RG * j;
-            const float al = s_a[r], kk = s_k[r], qq = s_q[r];
+        for (int j = 0; j < RPL; ++j) {
+            const float al = s_a[r0 + j], qq = s_q[r0 + j], kk = s_k[r0 + j];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 S[j][c] *= al;
-                pu[c] = fmaf(S[j][c], kk, pu[c]);
-                pr[c] = fmaf(S[j][c], qq, pr[c]);
+                u[c] = fmaf(S[j][c], kk, u[c]);
+                rr[c] = fmaf(S[j][c], qq, rr[c]);
             }
-            pqk = fmaf(qq, kk, pqk);
+            qk = fmaf(qq, kk, qk);
         }
-        // lanes that differ only in row group (bits >= log2(CPR)) share columns
 #pragma unroll
-        for (int off = CPR; off < 64; off <<= 1) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                pu[c] += __shfl_xor(pu[c], off);
-                pr[c] += __shfl_xor(pr[c], off);
-            }
-            pqk += __shfl_xor(pqk, off);
+        for (int c = 0; c < 4; ++c) {
+            u[c] = rowgroup_sum(u[c]);
+            rr[c] = rowgroup_sum(rr[c]);
         }
-        if (lane < CPR) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                s_red[wave][4 * cg + c] = pu[c];
-                s_red[wave][VT + 4 * cg + c] = pr[c];
-            }
-            if (cg == 0) s_red[wave][2 * VT] = pqk;
-        }
-        __syncthreads();
+        qk = rowgroup_sum(qk);
 
-        float u[4] = {0.f, 0.f, 0.f, 0.f}, rr[4] = {0.f, 0.f, 0.f, 0.f}, qk = 0.f;
-#pragma unroll
-        for (int w = 0; w < NWAVE; ++w) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                u[c] += s_red[w][4 * cg + c];
-                rr[c] += s_red[w][VT + 4 * cg + c];
-            }
-            qk += s_red[w][2 * VT];
-        }
-        const float beta = s_beta;
         float d[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) d[c] = beta * (s_v[4 * cg + c] - u[c]);
+        for (int c = 0; c < 4; ++c) d[c] = beta * (v[c] - u[c]);
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const float kk = s_k[rg + RG * j];
+        for (int j = 0; j < RPL; ++j) {
+            const float kk = s_k[r0 + j];
 #pragma unroll
             for (int c = 0; c < 4; ++c) S[j][c] = fmaf(kk, d[c], S[j][c]);
         }
@@ -164,64 +163,60 @@ __global__ __launch_bounds__(kRecThreads) void recurrent_kernel(const kda_fwd_ar
                 store_elem(a.o, io + c, a.qkv_dtype, o);
             }
         }
-        __syncthreads();   // the next token's staging overwrites s_* and s_red
+        if (t + 1 < T) __syncthreads();   // the next token's staging overwrites s_*
     }
 
     const bool vec_out = a.state_out_dtype == KDA_DTYPE_F32 &&
-                         (reinterpret_cast<uintptr_t>(a.state_out) & 15) == 0;
+                         (reinterpret_cast<uintptr_t>(a.state_out) & 15) == 0 && (V & 3) == 0;
     if (vec_out) {
-        float* sp = static_cast<float*>(a.state_out);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(static_cast<float*>(a.state_out) + sbase,
+                                                          static_cast<short>(0), static_cast<int>(K * row_bytes),
+                                                          0x00020000);
+        typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int64_t r = rg + RG * j;
-            *reinterpret_cast<float4*>(sp + sbase + r * V + col0) =
-                make_float4(S[j][0], S[j][1], S[j][2], S[j][3]);
-        }
+        for (int j = 0; j < RPL; ++j)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u4{__float_as_uint(S[j][0]), __float_as_uint(S[j][1]), __float_as_uint(S[j][2]),
+                   __float_as_uint(S[j][3])},
+                rs, static_cast<int>(lane_off), static_cast<int>(j * row_bytes), 0);
     } else {
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int64_t r = rg + RG * j;
+        for (int j = 0; j < RPL; ++j)
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                store_elem(a.state_out, sbase + r * V + col0 + c, a.state_out_dtype, S[j][c]);
-        }
+                store_elem(a.state_out, sbase + static_cast<int64_t>(r0 + j) * V + col0 + c, a.state_out_dtype,
+                           S[j][c]);
     }
 }
 
-template <int K, int VT>
-int launch_k_vt(const kda_fwd_args& a, hipStream_t stream) {
-    const int64_t blocks = a.B * a.H * (a.V / VT);
-    hipLaunchKernelGGL((recurrent_kernel<K, VT>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kRecThreads), 0, stream, a);
+template <int K, int NW>
+int launch_k_nw(const kda_fwd_args& a, hipStream_t stream) {
+    const int64_t blocks = a.B * a.H * (a.V / (16 * NW));
+    hipLaunchKernelGGL((recurrent_kernel<K, NW>), dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0, stream,
+                       a);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
 template <int K>
-int launch_k(const kda_fwd_args& a, hipStream_t stream, int vt) {
-    switch (vt) {
-        case 128: return launch_k_vt<K, 128>(a, stream);
-        case 64: return launch_k_vt<K, 64>(a, stream);
-        case 32: return launch_k_vt<K, 32>(a, stream);
-        default: return KDA_ERR_UNSUPPORTED;
-    }
+int launch_k(const kda_fwd_args& a, hipStream_t stream) {
+    if (a.V % 64 == 0) return launch_k_nw<K, 4>(a, stream);
+    if (a.V % 32 == 0) return launch_k_nw<K, 2>(a, stream);
+    return launch_k_nw<K, 1>(a, stream);
 }
 
 }  // namespace
 
 bool recurrent_supported(int64_t K, int64_t V) {
     if (!(K == 32 || K == 64 || K == 128 || K == 256)) return false;
-    return V % 32 == 0;
+    return V % 16 == 0;
 }
 
 int recurrent_launch(const kda_fwd_args& a, hipStream_t stream) {
-    // V tile: 64 columns where possible (two workgroups per head at V = 128
-    // gives 2048 workgroups at B = 64, H = 16), else 32.
-    const int vt = (a.V % 64 == 0) ? 64 : 32;
     switch (a.K) {
-        case 32: return launch_k<32>(a, stream, vt);
-        case 64: return launch_k<64>(a, stream, vt);
-        case 128: return launch_k<128>(a, stream, vt);
-        case 256: return launch_k<256>(a, stream, vt);
+        case 32: return launch_k<32>(a, stream);
+        case 64: return launch_k<64>(a, stream);
+        case 128: return launch_k<128>(a, stream);
+        case 256: return launch_k<256>(a, stream);
         default: return KDA_ERR_UNSUPPORTED;
     }
 }
