@@ -39,7 +39,8 @@ __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) 
 // Branch-free element load for a runtime dtype: one 32-bit load of the
 // aligned word that holds element i (a 2-byte element sits in its low or high
 // half), issued the same way for every dtype so that several such loads are
-// in flight together; decode_elem converts it once the data is needed.
+// in flight together; decode_elem converts it once the data is needed.  The
+// word never crosses a 4-byte boundary, so it lies in the element's page.
 struct RawElem {
     uint32_t word;
     uint32_t shift;   // 0 or 16 for 2-byte elements
