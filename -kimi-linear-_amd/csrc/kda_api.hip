@@ -16,8 +16,9 @@ bool dtype_ok(int32_t d) {
 
 int64_t elem_size(int32_t d) { return d == KDA_DTYPE_F32 ? 4 : 2; }
 
-// Checks shared by both entry points.
-int validate_common(const kda_fwd_args* a) {
+// Checks shared by both entry points.  `in_place_ok`: state_out may be
+// state_in itself (same address and dtype), the recurrence's in-place update.
+int validate_common(const kda_fwd_args* a, bool in_place_ok) {
     if (a == nullptr) return KDA_ERR_NULL_POINTER;
     if (a->B < 0 || a->T < 0 || a->H < 0 || a->K <= 0 || a->V <= 0) return KDA_ERR_BAD_SHAPE;
     if (!dtype_ok(a->qkv_dtype) || !dtype_ok(a->g_dtype) || !dtype_ok(a->beta_dtype) ||
@@ -34,7 +35,8 @@ int validate_common(const kda_fwd_args* a) {
         const auto in1 = in0 + static_cast<uintptr_t>(n * elem_size(a->state_in_dtype));
         const auto out0 = reinterpret_cast<uintptr_t>(a->state_out);
         const auto out1 = out0 + static_cast<uintptr_t>(n * elem_size(a->state_out_dtype));
-        if (in0 < out1 && out0 < in1) return KDA_ERR_ALIAS;
+        const bool same = in0 == out0 && a->state_in_dtype == a->state_out_dtype;
+        if (in0 < out1 && out0 < in1 && !(in_place_ok && same)) return KDA_ERR_ALIAS;
     }
     return KDA_OK;
 }
@@ -44,7 +46,9 @@ int validate_common(const kda_fwd_args* a) {
 extern "C" {
 
 int kda_recurrent_fwd(const kda_fwd_args* args, void* stream) {
-    const int st = validate_common(args);
+    // In place is safe: each workgroup loads its (b, h, column tile) slice of
+    // the state before any store to it, and no other workgroup touches it.
+    const int st = validate_common(args, true);
     if (st != KDA_OK) return st;
     if (args->B == 0 || args->H == 0) return KDA_OK;
     if (!kda::recurrent_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
@@ -53,7 +57,7 @@ int kda_recurrent_fwd(const kda_fwd_args* args, void* stream) {
 }
 
 int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) {
-    const int st = validate_common(args);
+    const int st = validate_common(args, false);
     if (st != KDA_OK) return st;
     if (args->chunk_size <= 0 || args->T % args->chunk_size != 0) return KDA_ERR_BAD_SHAPE;
     if (args->B == 0 || args->H == 0) return KDA_OK;

@@ -10,7 +10,8 @@ Same signatures and semantics as the reference kernels
   that dtype and computed in fp32.
 * Inputs are never modified; ``o`` is a new ``[B, T, H, V]`` tensor in
   ``v.dtype`` and the state a new ``[B, H, K, V]`` tensor in
-  ``state_dtype or v.dtype`` (``kda.py:185,219``).
+  ``state_dtype or v.dtype`` (``kda.py:185,219``).  The one opt-in exception
+  is ``kda_recurrent(..., state_out=state)``, an in-place state update.
 * ``kda_recurrent`` clamps an fp16 ``o`` to +-60000 (``kda.py:217-218``);
   ``kda_chunkwise`` does not.
 * ``kda_chunkwise`` requires ``T % chunk_size == 0`` (``kda.py:109``); the
@@ -83,11 +84,13 @@ def _strides3(x: torch.Tensor):
     return (ctypes.c_int64 * 3)(*x.stride()[:3])
 
 
-def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
+def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None):
     for name, x in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
         _check_tensor(name, x)
     if state is not None:
         _check_tensor("state", state)
+    if state_out is not None:
+        _check_tensor("state_out", state_out)
     if q.dim() != 4 or v.dim() != 4:
         raise KdaError(f"q and v must be [B, T, H, D]; got q {tuple(q.shape)}, v {tuple(v.shape)}")
     B, T, H, K = q.shape
@@ -111,7 +114,7 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
         raise KdaError(f"head dims must be positive, got K={K}, V={V}")
 
     dev = q.device
-    tensors = [q, k, v, g, beta] + ([state] if state is not None else [])
+    tensors = [q, k, v, g, beta] + [x for x in (state, state_out) if x is not None]
     if dev.type != "cuda" or any(x.device != dev for x in tensors):
         raise KdaError("the HIP KDA kernels need all inputs on one HIP device "
                        f"(got {', '.join(str(x.device) for x in tensors)}); there is no CPU path")
@@ -126,9 +129,18 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
     if not isinstance(s_dtype, torch.dtype) or not s_dtype.is_floating_point:
         raise KdaError(f"state_dtype must be a floating dtype, got {state_dtype!r}")
     kernel_s_dtype = s_dtype if s_dtype in _DTYPE_CODE else torch.float32
+    if state_out is not None:
+        if tuple(state_out.shape) != (B, H, K, V) or not state_out.is_contiguous():
+            raise KdaError(f"state_out must be a contiguous [B, H, K, V] = [{B}, {H}, {K}, {V}] tensor; "
+                           f"got {tuple(state_out.shape)} with strides {state_out.stride()}")
+        if state_out.dtype != s_dtype or s_dtype not in _DTYPE_CODE:
+            raise KdaError(f"state_out must have the state dtype {s_dtype} (float32, float16 or bfloat16); "
+                           f"got {state_out.dtype}")
+        if state_out.requires_grad and torch.is_grad_enabled():
+            raise KdaError("state_out is written in place: it must not require grad under grad mode")
 
     o = torch.empty(B, T, H, V, device=dev, dtype=out_dtype)
-    s_out = torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
+    s_out = state_out if state_out is not None else torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
     if B * H == 0:
         if state is not None:
             s_out.copy_(state)
@@ -148,6 +160,14 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype):
         state = _float_or_f32(state)
         if not state.is_contiguous():
             state = state.contiguous()
+        if state_out is not None and state.data_ptr() != s_out.data_ptr():
+            # the kernel reads a state slice before writing it: only an exact
+            # alias (in-place update) or disjoint memory is allowed
+            n_in = state.numel() * state.element_size()
+            n_out = s_out.numel() * s_out.element_size()
+            if state.data_ptr() < s_out.data_ptr() + n_out and s_out.data_ptr() < state.data_ptr() + n_in:
+                raise KdaError("state_out partially overlaps state: pass the same tensor (in place) "
+                               "or disjoint memory")
 
     args = _native.KdaFwdArgs()
     args.B, args.T, args.H, args.K, args.V = B, T, H, K, V
@@ -190,9 +210,16 @@ def kda_chunkwise(q, k, v, g, beta, initial_state=None, chunk_size=64, tile_size
     return _forward("chunkwise", q, k, v, g, beta, initial_state, int(chunk_size), state_dtype)
 
 
-def kda_recurrent(q, k, v, g, beta, state=None, state_dtype=None):
+def kda_recurrent(q, k, v, g, beta, state=None, state_dtype=None, *, state_out=None):
     """Token-by-token KDA recurrence on gfx950 (signature of kimi_linear/kda.py:188).
 
     Any ``T >= 0``; ``T == 1`` is the decode step.
+
+    ``state_out`` (keyword-only, no counterpart in the reference) receives the
+    new state instead of a fresh tensor: a contiguous ``[B, H, K, V]`` HIP
+    tensor of dtype ``state_dtype or v.dtype``.  It may be ``state`` itself --
+    an in-place update, which saves a decode loop with static state buffers
+    (a captured graph) the copy of the whole state back into its input
+    buffer.  It is returned as the second output.
     """
-    return _forward("recurrent", q, k, v, g, beta, state, 0, state_dtype)
+    return _forward("recurrent", q, k, v, g, beta, state, 0, state_dtype, state_out)

@@ -1,0 +1,265 @@
+"""KDA layer around the native core: the reference's ``KimiDeltaAttention``.
+
+Mirrors ``kimi_linear/kda.py:258-536`` -- same parameters (names and shapes, so a
+reference ``state_dict`` loads unchanged), same forward semantics and dispatch
+rules -- with the core recurrence running on the gfx950 kernels of
+:mod:`kimi_linear_amd.kda`.  Projections, the short convolutions and the
+norms are torch operations on the same device (library GEMMs and elementwise
+kernels).
+
+The core is forward-only (it raises on inputs that require grad under grad
+mode): run the layer under ``torch.no_grad()`` or ``torch.inference_mode()``.
+
+Semantics kept from the reference:
+
+* ``_projections`` (``kda.py:399-461``): q, k = l2norm(SiLU(ShortConv(W x)))
+  per head, v = SiLU(ShortConv(W_v x)); beta = sigmoid(W_beta x) in fp32;
+  g = -exp(A_log) * softplus(W_up W_down x + dt_bias) in fp32.  The T == 1
+  cached path updates the conv windows (``kda.py:295-307``); a cached
+  multi-token call continues from the cached conv inputs (chunked prefill).
+* dispatch (``kda.py:473-536``): ``use_cache`` with T == 1 goes to the
+  recurrence; otherwise the chunk size is ``chunk_size`` (or T when
+  0 < T < chunk_size), the body runs chunkwise and the remainder through the
+  recurrence, chained through the state.
+* state dtype (``kda.py:392-396``): an fp32 recurrent state when x is fp16 or
+  bf16, else the kernel default (v.dtype).
+* ``_output`` (``kda.py:464-470``): head-wise RMSNorm, sigmoid output gate in
+  fp32, output projection.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .kda import kda_chunkwise, kda_recurrent
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.float32 else t.float()
+
+
+class HeadwiseRMSNorm(nn.Module):
+    """Per-head RMSNorm with an fp32 weight ``[H, D]`` (``kda.py:258-279``)."""
+
+    def __init__(self, heads: int, dim: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(heads, dim))
+        self.eps = float(eps)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:       # x: [B, T, H, D]
+        dtype = x.dtype
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (xf * _f32(self.weight)).to(dtype)
+
+
+class ShortConv(nn.Module):
+    """Causal depthwise convolution, kernel ``conv_size`` (``kda.py:282-310``).
+
+    Parameters live in an ``nn.Conv1d`` named ``conv`` like the reference's, so
+    its ``state_dict`` keys (``conv.weight`` ``[D, 1, C]``, ``conv.bias``) match.
+    The batch path sums the ``conv_size`` shifted taps in fp32 and rounds once
+    to x's dtype (the reference's ``conv1d`` on a left-padded input,
+    ``kda.py:308-310``, computes the same sum): a depthwise filter of 4 taps is
+    a handful of elementwise passes, with no convolution library in the loop.
+    """
+
+    def __init__(self, dim: int, conv_size: int, bias: bool = True):
+        super().__init__()
+        self.dim = dim
+        self.conv_size = conv_size
+        self.conv = nn.Conv1d(dim, dim, conv_size, groups=dim, bias=bias)
+
+    def forward(self, x, conv_state=None, use_cache=False):
+        """x: [B, T, D].  With ``use_cache``, x is [B, 1, D] and ``conv_state`` the
+        last ``conv_size - 1`` inputs [B, conv_size - 1, D]; returns (out, state)."""
+        if use_cache:
+            window = torch.cat([conv_state, x], dim=1)                # [B, C, D]
+            w = _f32(self.conv.weight).squeeze(1).t()                 # [C, D]
+            out = (window.float() * w).sum(1)
+            if self.conv.bias is not None:
+                out = out + _f32(self.conv.bias)
+            out = out.to(x.dtype).unsqueeze(1)
+            new_state = window[:, 1 - self.conv_size:] if self.conv_size > 1 else window[:, :0]
+            return out, new_state
+        T = x.shape[1]
+        C = self.conv_size
+        w = _f32(self.conv.weight).squeeze(1)                         # [D, C]
+        xp = F.pad(x.float(), (0, 0, C - 1, 0))                       # left pad over time: causal
+        out = xp[:, C - 1:] * w[:, C - 1]
+        for c in range(C - 1):
+            out = out + xp[:, c:c + T] * w[:, c]
+        if self.conv.bias is not None:
+            out = out + _f32(self.conv.bias)
+        return out.to(x.dtype)
+
+
+def l2norm(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """Last-dimension L2 normalisation, reduced in fp32, returned in x's dtype
+    (``kda.py:313-325``): x * min(rsqrt(sum x^2), 1/eps)."""
+    src = x.dtype
+    xf = x.float()
+    rstd = (xf * xf).sum(-1, keepdim=True).rsqrt().clamp(max=1.0 / eps)
+    return (xf * rstd).to(src)
+
+
+def linear_attn_config(**kw) -> SimpleNamespace:
+    """A minimal config object with the fields ``KimiDeltaAttention`` reads
+    (``kda.py:332-386``); keyword overrides go into ``linear_attn_config``
+    except ``hidden_size``, ``l2norm_eps`` and ``rms_norm_eps``."""
+    la = dict(num_heads=16, head_dim=128, value_head_dim=128, conv_size=4, chunk_size=64,
+              tile_size=0, proj_bias=False, conv_bias=True, gate_low_rank=128,
+              output_gate_low_rank=128, a_log_init=0.0, dt_bias_init=0.0)
+    top = dict(hidden_size=2048, l2norm_eps=1e-6, rms_norm_eps=1e-6)
+    for k, v in kw.items():
+        (top if k in top else la)[k] = v
+    return SimpleNamespace(linear_attn_config=la, **top)
+
+
+class KimiDeltaAttention(nn.Module):
+    """The KDA layer (``kda.py:331-536``) with the native core."""
+
+    def __init__(self, config):
+        super().__init__()
+        la = config.linear_attn_config
+        d = config.hidden_size
+        self.num_heads = la["num_heads"]
+        self.head_dim = la["head_dim"]
+        self.value_head_dim = la["value_head_dim"]
+        self.conv_size = la["conv_size"]
+        self.chunk_size = la["chunk_size"]
+        self.tile_size = int(la.get("tile_size", 0))
+        self.l2norm_eps = config.l2norm_eps
+        H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+        bias = la["proj_bias"]
+        self.in_proj_q = nn.Linear(d, H * K, bias=bias)
+        self.in_proj_k = nn.Linear(d, H * K, bias=bias)
+        self.in_proj_v = nn.Linear(d, H * V, bias=bias)
+        conv_bias = la["conv_bias"]
+        self.conv_q = ShortConv(H * K, self.conv_size, bias=conv_bias)
+        self.conv_k = ShortConv(H * K, self.conv_size, bias=conv_bias)
+        self.conv_v = ShortConv(H * V, self.conv_size, bias=conv_bias)
+        self.gk_proj = nn.Sequential(nn.Linear(d, la["gate_low_rank"], bias=bias),
+                                     nn.Linear(la["gate_low_rank"], H * K, bias=bias))
+        self.A_log = nn.Parameter(torch.zeros(H, K) + float(la["a_log_init"]))
+        self.dt_bias = nn.Parameter(torch.zeros(H, K) + float(la["dt_bias_init"]))
+        self.beta_proj = nn.Linear(d, H, bias=bias)
+        self.og_proj = nn.Sequential(nn.Linear(d, la["output_gate_low_rank"], bias=bias),
+                                     nn.Linear(la["output_gate_low_rank"], H * V, bias=bias))
+        self.g_norm = HeadwiseRMSNorm(H, V, config.rms_norm_eps)
+        self.o_proj = nn.Linear(H * V, d, bias=bias)
+        self.fp32_recurrent_state = True
+
+    def _state_dtype(self, x):
+        if self.fp32_recurrent_state and x.dtype in (torch.float16, torch.bfloat16):
+            return torch.float32
+        return None
+
+    def init_state(self, batch: int, device=None, dtype=None) -> dict:
+        """An empty decode state (the shape ``forward`` creates for use_cache)."""
+        keep = max(self.conv_size - 1, 0)
+        H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+        z = lambda dim: torch.zeros(batch, keep, dim, device=device, dtype=dtype)  # noqa: E731
+        return {"conv": {"q": z(H * K), "k": z(H * K), "v": z(H * V)}, "recurrent": None}
+
+    def _projections(self, x, conv_cache=None, use_cache=False):
+        B, T, _ = x.shape
+        H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+        keep = max(self.conv_size - 1, 0)
+        new_conv = None
+        if use_cache and T == 1:
+            qc, cq = self.conv_q(self.in_proj_q(x), conv_cache["q"], use_cache=True)
+            kc, ck = self.conv_k(self.in_proj_k(x), conv_cache["k"], use_cache=True)
+            vc, cv = self.conv_v(self.in_proj_v(x), conv_cache["v"], use_cache=True)
+            new_conv = {"q": cq, "k": ck, "v": cv}
+        else:
+            q_in, k_in, v_in = self.in_proj_q(x), self.in_proj_k(x), self.in_proj_v(x)
+            history = use_cache and conv_cache is not None and keep > 0
+            if history:
+                q_full = torch.cat([conv_cache["q"], q_in], dim=1)
+                k_full = torch.cat([conv_cache["k"], k_in], dim=1)
+                v_full = torch.cat([conv_cache["v"], v_in], dim=1)
+                qc = self.conv_q(q_full)[:, keep:]
+                kc = self.conv_k(k_full)[:, keep:]
+                vc = self.conv_v(v_full)[:, keep:]
+            else:
+                qc, kc, vc = self.conv_q(q_in), self.conv_k(k_in), self.conv_v(v_in)
+            if use_cache:
+                if history:
+                    new_conv = {"q": q_full[:, -keep:], "k": k_full[:, -keep:], "v": v_full[:, -keep:]}
+                else:
+                    new_conv = {"q": q_in[:, -keep:] if keep else q_in[:, :0],
+                                "k": k_in[:, -keep:] if keep else k_in[:, :0],
+                                "v": v_in[:, -keep:] if keep else v_in[:, :0]}
+        q = l2norm(F.silu(qc).view(B, T, H, K), self.l2norm_eps)
+        k = l2norm(F.silu(kc).view(B, T, H, K), self.l2norm_eps)
+        v = F.silu(vc).view(B, T, H, V)
+        beta = torch.sigmoid(self.beta_proj(x).float())
+        gk = self.gk_proj(x).view(B, T, H, K)
+        g = -torch.exp(_f32(self.A_log)) * F.softplus(gk.float() + _f32(self.dt_bias))
+        return q, k, v, g, beta, new_conv
+
+    def _output(self, o_core, x):
+        B, T, H, V = o_core.shape
+        o = self.g_norm(o_core)
+        gate = torch.sigmoid(self.og_proj(x).view(B, T, H, V).float())
+        o = (o.float() * gate).to(o.dtype)
+        return self.o_proj(o.reshape(B, T, H * V))
+
+    def decode_step_(self, x, state):
+        """One cached decode token (x: [B, 1, d]) that updates ``state`` in
+        place and returns out [B, 1, d]: the result of
+        ``forward(x, state, use_cache=True)`` with the conv windows shifted by
+        copy and the recurrent state ([B, H, K, V], allocated) overwritten by
+        the kernel.  This is the static-state step a captured graph replays;
+        the reference instead copies each new state back into its static
+        buffers (``graph_decode.py:257-262``), a full extra read and write of
+        the state per layer and token."""
+        if x.shape[1] != 1:
+            raise ValueError(f"decode_step_ takes one token, got x of shape {tuple(x.shape)}")
+        q, k, v, g, beta, new_conv = self._projections(x, conv_cache=state["conv"], use_cache=True)
+        for n in ("q", "k", "v"):
+            state["conv"][n].copy_(new_conv[n])
+        rec = state["recurrent"]
+        if rec is None:
+            raise ValueError("decode_step_ needs an allocated recurrent state (run a prefill first)")
+        o_core, _ = kda_recurrent(q, k, v, g, beta, state=rec, state_dtype=rec.dtype, state_out=rec)
+        return self._output(o_core, x)
+
+    def forward(self, x, state=None, use_cache=False):
+        """x: [B, T, d]; ``state`` = {"conv": {"q", "k", "v"}, "recurrent"}.
+        Returns out, or (out, new_state) with ``use_cache``."""
+        if use_cache and state is None:
+            state = self.init_state(x.shape[0], device=x.device, dtype=x.dtype)
+        conv_cache = state["conv"] if state is not None else None
+        rec = state["recurrent"] if state is not None else None
+        q, k, v, g, beta, new_conv = self._projections(x, conv_cache=conv_cache, use_cache=use_cache)
+        B, T = x.shape[0], x.shape[1]
+        sdtype = self._state_dtype(x)
+        if use_cache and T == 1:
+            o_core, new_rec = kda_recurrent(q, k, v, g, beta, state=rec, state_dtype=sdtype)
+        else:
+            C = self.chunk_size
+            if 0 < T < C:
+                C = T
+            rem = T % C
+            body = T - rem
+            o_core = x.new_zeros(B, T, self.num_heads, self.value_head_dim)
+            if body > 0:
+                o_body, rec = kda_chunkwise(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
+                                            beta[:, :body], initial_state=rec, chunk_size=C,
+                                            state_dtype=sdtype, tile_size=self.tile_size)
+                o_core[:, :body] = o_body
+            if rem > 0:
+                o_tail, rec = kda_recurrent(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
+                                            beta[:, body:], state=rec, state_dtype=sdtype)
+                o_core[:, body:] = o_tail
+            new_rec = rec
+        out = self._output(o_core, x)
+        if use_cache:
+            return out, {"conv": new_conv, "recurrent": new_rec}
+        return out

@@ -23,7 +23,9 @@
  *  - The work is asynchronous and stream-ordered on `stream` (a hipStream_t,
  *    NULL = the legacy default stream).  The library never allocates, frees,
  *    synchronises or copies to the host, so a call may be captured in a
- *    hipGraph.  Inputs are never written; state_out may not alias state_in.
+ *    hipGraph.  Inputs are never written.  state_out may not overlap
+ *    state_in, except that kda_recurrent_fwd accepts state_out == state_in
+ *    (same address and dtype) as an in-place update.
  *  - Returns KDA_OK (0) or a kda_status code; kda_status_str() names it.
  *    Argument errors are detected on the host before any launch.
  */
@@ -51,7 +53,8 @@ typedef enum kda_status {
     KDA_ERR_BAD_SHAPE = 2,         /* negative/inconsistent sizes, T % chunk != 0 */
     KDA_ERR_BAD_DTYPE = 3,         /* dtype code outside kda_dtype / o != v dtype */
     KDA_ERR_UNSUPPORTED = 4,       /* head dims this build has no kernel for      */
-    KDA_ERR_ALIAS = 5,             /* state_out aliases state_in                  */
+    KDA_ERR_ALIAS = 5,             /* state_out overlaps state_in (other than an
+                                      exact in-place alias for the recurrence)   */
     KDA_ERR_LAUNCH = 6             /* hipGetLastError() after the launch          */
 } kda_status;
 
@@ -97,7 +100,10 @@ int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream);
 /*
  * Token-by-token recurrence; replaces the body of kda_recurrent
  * (kimi_linear/kda.py:188-219).  Any T >= 0; T == 1 is the decode step.
- * chunk_size is ignored.
+ * chunk_size is ignored.  state_out == state_in (same address and dtype)
+ * updates the state in place: a decode loop over static state buffers then
+ * needs no copy of the new state back into its input (the reference copies
+ * it back inside its captured graph, kimi_linear/graph_decode.py:257-262).
  */
 int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
 

@@ -98,6 +98,18 @@ def test_host_validation_codes(native, fn):
     assert call(ctypes.byref(_args(native, H=0)), None) == 0
 
 
+def test_in_place_state_contract(native):
+    lib = native.load()
+    same = _args(native, K=48)           # K=48 has no kernel: validation ends before any launch
+    same.state_in = same.state_out
+    # the recurrence accepts an exact alias (in-place update) and gets as far as the head-size check
+    assert lib.kda_recurrent_fwd(ctypes.byref(same), None) == 4
+    # the chunkwise pipeline does not, nor does an alias that changes dtype
+    assert lib.kda_chunkwise_fwd(ctypes.byref(same), None) == 5
+    same.state_in_dtype = native.DTYPE_F16
+    assert lib.kda_recurrent_fwd(ctypes.byref(same), None) == 5
+
+
 def test_chunkwise_row_stride_contract(native):
     # chunkwise reads each chunk through a descriptor spanning its token rows,
     # so a token stride shorter than a row is rejected before any launch

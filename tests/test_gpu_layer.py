@@ -1,0 +1,109 @@
+"""GPU parity of the KDA layer (native core + torch projections) against the
+layer oracle, and of its cache handling (chunked prefill, token-by-token decode).
+
+The module's own parameters (after any cast) are handed to the oracle, so the
+differences are compute precision only.  Tolerances on the layer output,
+relative L2 error: fp32 1e-3, fp16 5e-3, bf16 2e-2.  The chunkwise core feeds
+the MFMAs fp16 operands (hi + lo pairs for those that carry the state) with
+fp32 accumulation whatever the input dtype, so an fp32 layer sits at about
+3e-4; fp16/bf16 projections also round each activation to 11/8 bits.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.kda_layer_oracle import kda_layer_ref, make_layer_params
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL = {torch.float32: 1e-3, torch.float16: 5e-3, torch.bfloat16: 2e-2}
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def make_layer(pkg, dtype, seed=0, **kw):
+    cfg = pkg.linear_attn_config(**{"hidden_size": 256, "num_heads": 2, "gate_low_rank": 64,
+                                    "output_gate_low_rank": 64, **kw})
+    m = pkg.KimiDeltaAttention(cfg)
+    m.load_state_dict(make_layer_params(cfg, seed=seed))
+    m = m.to(device=DEV, dtype=dtype).eval()
+    params = {n: t.detach().float().cpu() for n, t in m.state_dict().items()}
+    return m, cfg, params
+
+
+def make_x(B, T, d, dtype, seed):
+    return torch.randn(B, T, d, generator=torch.Generator().manual_seed(seed)).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T", [150, 40, 64])
+def test_layer_prefill_vs_oracle(kda_pkg, dtype, T):
+    """T=150: chunkwise body of 128 + recurrent tail of 22; T=40: one chunk of
+    40 (T < chunk_size); T=64: exactly one chunk."""
+    m, cfg, p = make_layer(kda_pkg, dtype, seed=1)
+    x = make_x(2, T, 256, dtype, seed=2)
+    with torch.no_grad():
+        out = m(x.to(DEV))
+    ref = kda_layer_ref(p, cfg, x)
+    e = rel(out, ref)
+    print(f"[layer prefill {dtype} T={T}] rel {e:.3e}", flush=True)
+    assert out.dtype == dtype and out.shape == (2, T, 256)
+    assert e <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_layer_prefill_then_decode_vs_oracle(kda_pkg, dtype):
+    m, cfg, p = make_layer(kda_pkg, dtype, seed=3)
+    x = make_x(3, 76, 256, dtype, seed=4)
+    xd = x.to(DEV)
+    with torch.no_grad():
+        o, st = m(xd[:, :70], use_cache=True)
+        outs = [o]
+        for t in range(70, 76):
+            o, st = m(xd[:, t:t + 1], state=st, use_cache=True)
+            outs.append(o)
+    out = torch.cat(outs, 1)
+    ref, st_ref = kda_layer_ref(p, cfg, x, use_cache=True)
+    e = rel(out, ref)
+    es = rel(st["recurrent"], st_ref["recurrent"])
+    print(f"[layer decode {dtype}] out rel {e:.3e} state rel {es:.3e}", flush=True)
+    assert st["recurrent"].dtype == torch.float32            # fp32 state for fp16 activations
+    assert e <= TOL[dtype] and es <= TOL[dtype]
+    for n in ("q", "k", "v"):
+        assert rel(st["conv"][n], st_ref["conv"][n]) <= TOL[dtype]
+
+
+def test_layer_chunked_prefill_vs_one_pass(kda_pkg):
+    m, cfg, p = make_layer(kda_pkg, torch.float16, seed=5)
+    x = make_x(2, 228, 256, torch.float16, seed=6)
+    xd = x.to(DEV)
+    with torch.no_grad():
+        o1, st = m(xd[:, :100], use_cache=True)      # body 64 + tail 36
+        o2, st = m(xd[:, 100:], state=st, use_cache=True)
+        one = m(xd)
+    out = torch.cat([o1, o2], 1)
+    ref = kda_layer_ref(p, cfg, x)
+    e, e1 = rel(out, ref), rel(one, ref)
+    print(f"[layer chunked prefill] rel {e:.3e} one-pass rel {e1:.3e}", flush=True)
+    assert e <= TOL[torch.float16] and e1 <= TOL[torch.float16]
+
+
+def test_layer_model_width(kda_pkg):
+    """The Kimi-Linear attention width: hidden 2048, 16 heads of 128."""
+    cfg = kda_pkg.linear_attn_config(hidden_size=2048, num_heads=16)
+    m = kda_pkg.KimiDeltaAttention(cfg)
+    m.load_state_dict(make_layer_params(cfg, seed=7))
+    m = m.to(device=DEV, dtype=torch.float16).eval()
+    p = {n: t.detach().float().cpu() for n, t in m.state_dict().items()}
+    x = make_x(2, 192, 2048, torch.float16, seed=8)
+    with torch.no_grad():
+        out = m(x.to(DEV))
+    e = rel(out, kda_layer_ref(p, cfg, x))
+    print(f"[layer hidden 2048] rel {e:.3e}", flush=True)
+    assert e <= TOL[torch.float16]
