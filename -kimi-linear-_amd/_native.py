@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -44,7 +44,41 @@ class KdaFwdArgs(ctypes.Structure):
     ]
 
 
-EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_status_str", "kda_abi_version")
+_ptr3 = ctypes.c_void_p * 3
+
+
+class KdaPrepArgs(ctypes.Structure):
+    """Mirror of ``struct kda_prep_args`` (include/kda_hip.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int64), ("T", ctypes.c_int64), ("H", ctypes.c_int64),
+        ("K", ctypes.c_int64), ("V", ctypes.c_int64), ("conv_size", ctypes.c_int64),
+        ("x", _ptr3), ("x_stride", (ctypes.c_int64 * 2) * 3),
+        ("conv_w", _ptr3), ("conv_b", _ptr3), ("w_dtype", ctypes.c_int32),
+        ("hist_in", _ptr3), ("hist_out", _ptr3),
+        ("gk", ctypes.c_void_p), ("gk_stride", ctypes.c_int64 * 2),
+        ("a_log", ctypes.c_void_p), ("dt_bias", ctypes.c_void_p), ("p_dtype", ctypes.c_int32),
+        ("beta_logit", ctypes.c_void_p), ("beta_stride", ctypes.c_int64 * 2),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("g", ctypes.c_void_p), ("beta", ctypes.c_void_p),
+        ("l2_eps", ctypes.c_float), ("x_dtype", ctypes.c_int32),
+    ]
+
+
+class KdaOutputArgs(ctypes.Structure):
+    """Mirror of ``struct kda_output_args`` (include/kda_hip.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int64), ("T", ctypes.c_int64), ("H", ctypes.c_int64), ("V", ctypes.c_int64),
+        ("o", ctypes.c_void_p), ("o_stride", ctypes.c_int64 * 3),
+        ("gate", ctypes.c_void_p), ("gate_stride", ctypes.c_int64 * 2),
+        ("weight", ctypes.c_void_p), ("w_dtype", ctypes.c_int32),
+        ("y", ctypes.c_void_p), ("eps", ctypes.c_float), ("x_dtype", ctypes.c_int32),
+    ]
+
+
+EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_prep_fwd", "kda_output_fwd",
+                    "kda_status_str", "kda_abi_version")
 
 _lib = None
 _lock = threading.Lock()
@@ -77,6 +111,10 @@ def load() -> ctypes.CDLL:
         lib.kda_chunkwise_fwd.restype = ctypes.c_int
         lib.kda_recurrent_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_void_p]
         lib.kda_recurrent_fwd.restype = ctypes.c_int
+        lib.kda_prep_fwd.argtypes = [ctypes.POINTER(KdaPrepArgs), ctypes.c_void_p]
+        lib.kda_prep_fwd.restype = ctypes.c_int
+        lib.kda_output_fwd.argtypes = [ctypes.POINTER(KdaOutputArgs), ctypes.c_void_p]
+        lib.kda_output_fwd.restype = ctypes.c_int
         lib.kda_status_str.argtypes = [ctypes.c_int]
         lib.kda_status_str.restype = ctypes.c_char_p
         lib.kda_abi_version.argtypes = []

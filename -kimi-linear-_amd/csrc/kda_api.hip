@@ -79,7 +79,7 @@ const char* kda_status_str(int status) {
         case KDA_ERR_BAD_SHAPE: return "invalid shape (negative size, T not a multiple of chunk_size, or grid too large)";
         case KDA_ERR_BAD_DTYPE: return "unsupported dtype code";
         case KDA_ERR_UNSUPPORTED: return "no kernel for these head dimensions";
-        case KDA_ERR_ALIAS: return "state_out overlaps state_in";
+        case KDA_ERR_ALIAS: return "an output overlaps an input (state_out/state_in, or a conv cache written while still read)";
         case KDA_ERR_LAUNCH: return "kernel launch failed";
         default: return "unknown kda_status";
     }

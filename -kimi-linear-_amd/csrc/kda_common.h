@@ -104,6 +104,34 @@ __device__ __forceinline__ void split_h(float x, _Float16& hi, _Float16& lo) {
     lo = static_cast<_Float16>(x - static_cast<float>(hi));
 }
 
+// ---- cross-lane sums (VALU only: DPP and permlane swaps) -------------------
+// Sum of x over the 16 lanes that share l & 3 (all-reduce, every lane gets it).
+__device__ __forceinline__ float rowgroup_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));  // row_ror:4
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
+    // permlane16_swap(x, x) returns x of lane l & ~16 and of lane l | 16;
+    // permlane32_swap likewise for bit 5: the sum of both is the pair sum
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return x;
+}
+
+// Sum of x over the whole wave (every lane gets it): the four lanes of each
+// quad first (quad_perm xor 1, xor 2), then the 16 quads.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    return rowgroup_sum(x);
+}
+
 // ---- MFMA wrappers (gfx950) ----------------------------------------------
 // 16x16 output tile, f32 accumulate.  Lane l holds A row (l % 16) and B column
 // (l % 16); lane group g = l / 16 supplies the k slots; the accumulator holds

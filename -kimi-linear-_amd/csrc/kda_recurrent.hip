@@ -24,26 +24,11 @@ namespace kda {
 
 namespace {
 
-// Sum of x over the 16 lanes that share l & 3 (all-reduce, every lane gets it).
-__device__ __forceinline__ float rowgroup_sum(float x) {
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));  // row_ror:4
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
-    // permlane16_swap(x, x) returns x of lane l & ~16 and of lane l | 16;
-    // permlane32_swap likewise for bit 5: the sum of both is the pair sum
-    {
-        const unsigned u = __float_as_uint(x);
-        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    {
-        const unsigned u = __float_as_uint(x);
-        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    return x;
-}
-
-template <int K, int NW>
+// VEC: the state is read (unless absent) and written as 16-byte-aligned fp32
+// rows with buffer loads/stores; otherwise element by element in any dtype.
+// A separate instantiation keeps the generic path's registers out of the
+// fast one.
+template <int K, int NW, bool VEC>
 __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a) {
     constexpr int RPL = K / 16;                 // rows per lane
     constexpr int VT = 16 * NW;                 // columns per workgroup
@@ -71,14 +56,12 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
     const uint32_t row_bytes = static_cast<uint32_t>(V) * 4u;
     const uint32_t lane_off = static_cast<uint32_t>(r0) * row_bytes + static_cast<uint32_t>(col0) * 4u;
     float S[RPL][4];
-    const bool vec_in = a.state_in != nullptr && a.state_in_dtype == KDA_DTYPE_F32 &&
-                        (reinterpret_cast<uintptr_t>(a.state_in) & 15) == 0 && (V & 3) == 0;
     if (a.state_in == nullptr) {
 #pragma unroll
         for (int j = 0; j < RPL; ++j)
 #pragma unroll
             for (int c = 0; c < 4; ++c) S[j][c] = 0.f;
-    } else if (vec_in) {
+    } else if (VEC) {
         const auto rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(static_cast<const float*>(a.state_in) + sbase), static_cast<short>(0),
             static_cast<int>(K * row_bytes), 0x00020000);
@@ -166,9 +149,7 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
         if (t + 1 < T) __syncthreads();   // the next token's staging overwrites s_*
     }
 
-    const bool vec_out = a.state_out_dtype == KDA_DTYPE_F32 &&
-                         (reinterpret_cast<uintptr_t>(a.state_out) & 15) == 0 && (V & 3) == 0;
-    if (vec_out) {
+    if (VEC) {
         const auto rs = __builtin_amdgcn_make_buffer_rsrc(static_cast<float*>(a.state_out) + sbase,
                                                           static_cast<short>(0), static_cast<int>(K * row_bytes),
                                                           0x00020000);
@@ -189,11 +170,17 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
     }
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 template <int K, int NW>
 int launch_k_nw(const kda_fwd_args& a, hipStream_t stream) {
-    const int64_t blocks = a.B * a.H * (a.V / (16 * NW));
-    hipLaunchKernelGGL((recurrent_kernel<K, NW>), dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0, stream,
-                       a);
+    const dim3 grid(static_cast<unsigned>(a.B * a.H * (a.V / (16 * NW)))), block(64 * NW);
+    const bool vec = (a.V & 3) == 0 && a.state_out_dtype == KDA_DTYPE_F32 && aligned16(a.state_out) &&
+                     (a.state_in == nullptr || (a.state_in_dtype == KDA_DTYPE_F32 && aligned16(a.state_in)));
+    if (vec)
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, false>), grid, block, 0, stream, a);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 

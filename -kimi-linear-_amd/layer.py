@@ -3,9 +3,12 @@
 Mirrors ``kimi_linear/kda.py:258-536`` -- same parameters (names and shapes, so a
 reference ``state_dict`` loads unchanged), same forward semantics and dispatch
 rules -- with the core recurrence running on the gfx950 kernels of
-:mod:`kimi_linear_amd.kda`.  Projections, the short convolutions and the
-norms are torch operations on the same device (library GEMMs and elementwise
-kernels).
+:mod:`kimi_linear_amd.kda`.  The projections are library GEMMs; the
+elementwise work between them and the core (short convolutions with their
+cache, SiLU, L2 norms, gates; RMSNorm and output gate) runs in the two fused
+kernels of :mod:`kimi_linear_amd.layer_ops`.  The ``ShortConv``,
+``HeadwiseRMSNorm`` and ``l2norm`` pieces below are the reference's modules
+(parameter containers with their own torch forward), not the layer's path.
 
 The core is forward-only (it raises on inputs that require grad under grad
 mode): run the layer under ``torch.no_grad()`` or ``torch.inference_mode()``.
@@ -36,6 +39,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .kda import kda_chunkwise, kda_recurrent
+from .layer_ops import kda_output, kda_prep
 
 
 def _f32(t: torch.Tensor) -> torch.Tensor:
@@ -166,64 +170,46 @@ class KimiDeltaAttention(nn.Module):
         z = lambda dim: torch.zeros(batch, keep, dim, device=device, dtype=dtype)  # noqa: E731
         return {"conv": {"q": z(H * K), "k": z(H * K), "v": z(H * V)}, "recurrent": None}
 
-    def _projections(self, x, conv_cache=None, use_cache=False):
-        B, T, _ = x.shape
-        H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+    def _projections(self, x, conv_cache=None, use_cache=False, conv_out=None):
+        """q, k, v, g, beta and the new conv cache (``kda.py:399-461``).
+
+        The five projections are library GEMMs; everything after them -- the
+        three short convolutions with their cache, SiLU, the q/k L2 norms,
+        the forget gate and beta -- is one fused kernel (:func:`kda_prep`).
+        ``conv_out``: write the new conv cache into these tensors (may be
+        ``conv_cache`` itself for T <= 16) instead of returning new ones."""
         keep = max(self.conv_size - 1, 0)
-        new_conv = None
-        if use_cache and T == 1:
-            qc, cq = self.conv_q(self.in_proj_q(x), conv_cache["q"], use_cache=True)
-            kc, ck = self.conv_k(self.in_proj_k(x), conv_cache["k"], use_cache=True)
-            vc, cv = self.conv_v(self.in_proj_v(x), conv_cache["v"], use_cache=True)
-            new_conv = {"q": cq, "k": ck, "v": cv}
-        else:
-            q_in, k_in, v_in = self.in_proj_q(x), self.in_proj_k(x), self.in_proj_v(x)
-            history = use_cache and conv_cache is not None and keep > 0
-            if history:
-                q_full = torch.cat([conv_cache["q"], q_in], dim=1)
-                k_full = torch.cat([conv_cache["k"], k_in], dim=1)
-                v_full = torch.cat([conv_cache["v"], v_in], dim=1)
-                qc = self.conv_q(q_full)[:, keep:]
-                kc = self.conv_k(k_full)[:, keep:]
-                vc = self.conv_v(v_full)[:, keep:]
-            else:
-                qc, kc, vc = self.conv_q(q_in), self.conv_k(k_in), self.conv_v(v_in)
-            if use_cache:
-                if history:
-                    new_conv = {"q": q_full[:, -keep:], "k": k_full[:, -keep:], "v": v_full[:, -keep:]}
-                else:
-                    new_conv = {"q": q_in[:, -keep:] if keep else q_in[:, :0],
-                                "k": k_in[:, -keep:] if keep else k_in[:, :0],
-                                "v": v_in[:, -keep:] if keep else v_in[:, :0]}
-        q = l2norm(F.silu(qc).view(B, T, H, K), self.l2norm_eps)
-        k = l2norm(F.silu(kc).view(B, T, H, K), self.l2norm_eps)
-        v = F.silu(vc).view(B, T, H, V)
-        beta = torch.sigmoid(self.beta_proj(x).float())
-        gk = self.gk_proj(x).view(B, T, H, K)
-        g = -torch.exp(_f32(self.A_log)) * F.softplus(gk.float() + _f32(self.dt_bias))
+        hist = conv_cache if (use_cache and conv_cache is not None and keep > 0) else None
+        convs = (self.conv_q.conv, self.conv_k.conv, self.conv_v.conv)
+        q, k, v, g, beta, new_conv = kda_prep(
+            self.in_proj_q(x), self.in_proj_k(x), self.in_proj_v(x),
+            tuple(c.weight for c in convs), tuple(c.bias for c in convs),
+            self.gk_proj(x), self.A_log, self.dt_bias, self.beta_proj(x),
+            num_heads=self.num_heads, head_dim=self.head_dim, value_head_dim=self.value_head_dim,
+            l2_eps=self.l2norm_eps, hist=hist, hist_out=conv_out if use_cache else None,
+            want_hist=use_cache and conv_out is None)
         return q, k, v, g, beta, new_conv
 
     def _output(self, o_core, x):
-        B, T, H, V = o_core.shape
-        o = self.g_norm(o_core)
-        gate = torch.sigmoid(self.og_proj(x).view(B, T, H, V).float())
-        o = (o.float() * gate).to(o.dtype)
-        return self.o_proj(o.reshape(B, T, H * V))
+        """Head-wise RMSNorm, sigmoid output gate (one fused kernel,
+        :func:`kda_output`) and the output projection (``kda.py:464-470``)."""
+        gate = self.og_proj(x)
+        if gate.dtype != o_core.dtype:
+            gate = gate.to(o_core.dtype)
+        return self.o_proj(kda_output(o_core, gate, self.g_norm.weight, self.g_norm.eps))
 
     def decode_step_(self, x, state):
         """One cached decode token (x: [B, 1, d]) that updates ``state`` in
         place and returns out [B, 1, d]: the result of
-        ``forward(x, state, use_cache=True)`` with the conv windows shifted by
-        copy and the recurrent state ([B, H, K, V], allocated) overwritten by
-        the kernel.  This is the static-state step a captured graph replays;
+        ``forward(x, state, use_cache=True)`` with the conv cache and the
+        recurrent state ([B, H, K, V], allocated) overwritten by the kernels.  This is the static-state step a captured graph replays;
         the reference instead copies each new state back into its static
         buffers (``graph_decode.py:257-262``), a full extra read and write of
         the state per layer and token."""
         if x.shape[1] != 1:
             raise ValueError(f"decode_step_ takes one token, got x of shape {tuple(x.shape)}")
-        q, k, v, g, beta, new_conv = self._projections(x, conv_cache=state["conv"], use_cache=True)
-        for n in ("q", "k", "v"):
-            state["conv"][n].copy_(new_conv[n])
+        q, k, v, g, beta, _ = self._projections(x, conv_cache=state["conv"], use_cache=True,
+                                                conv_out=state["conv"])
         rec = state["recurrent"]
         if rec is None:
             raise ValueError("decode_step_ needs an allocated recurrent state (run a prefill first)")

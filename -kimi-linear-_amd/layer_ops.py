@@ -1,0 +1,202 @@
+"""Fused pre- and post-processing of the KDA layer on gfx950 (C ABI
+``kda_prep_fwd`` / ``kda_output_fwd`` in include/kda_hip.h).
+
+* :func:`kda_prep` -- projections to core inputs in one pass: causal short
+  convolution + SiLU (+ per-head L2 norm for q and k) of the three
+  projections, the forget gate ``g = -exp(A_log) * softplus(gk + dt_bias)``
+  and ``beta = sigmoid(beta_logit)`` (``kimi_linear/kda.py:399-461``, with
+  ``ShortConv`` ``kda.py:282-310`` and ``l2norm`` ``kda.py:313-325``).
+* :func:`kda_output` -- head-wise RMSNorm times the sigmoid output gate
+  (``kda.py:258-279, 464-470``), producing the input of ``o_proj``.
+
+HIP tensors only; a missing library or a CPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+from .kda import KdaError
+
+_DTYPE_CODE = {torch.float32: _native.DTYPE_F32, torch.float16: _native.DTYPE_F16,
+               torch.bfloat16: _native.DTYPE_BF16}
+_TILE = 16      # tokens per prep work unit; an in-place conv cache needs T <= this
+
+
+def _code(name, t):
+    if t.dtype not in _DTYPE_CODE:
+        raise KdaError(f"{name} must be float32, float16 or bfloat16, got {t.dtype}")
+    return _DTYPE_CODE[t.dtype]
+
+
+def _rows(name, t, shape):
+    """A [B, T, D] activation whose channel dimension is contiguous (copied if not)."""
+    if tuple(t.shape) != tuple(shape):
+        raise KdaError(f"{name} must be {list(shape)}, got {list(t.shape)}")
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def _device_check(tensors):
+    dev = tensors[0].device
+    if dev.type != "cuda" or any(t.device != dev for t in tensors):
+        raise KdaError("the fused KDA layer kernels need all tensors on one HIP device "
+                       f"(got {', '.join(str(t.device) for t in tensors)}); there is no CPU path")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        raise KdaError("the fused KDA layer kernels are forward-only: call under torch.no_grad()")
+    return dev
+
+
+def _call(fn, args, dev, what):
+    with torch.cuda.device(dev):
+        status = fn(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    if status != _native.STATUS_OK:
+        raise KdaError(f"{what} failed: {_native.status_str(status)}")
+
+
+def kda_prep(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *, num_heads, head_dim,
+             value_head_dim, l2_eps, hist=None, hist_out=None, want_hist=False):
+    """Core inputs from the layer's projections.
+
+    ``q_in, k_in: [B, T, H*K]``, ``v_in: [B, T, H*V]``, ``gk: [B, T, H*K]`` (the
+    gate's up-projection), ``beta_logit: [B, T, H]``, all in one activation
+    dtype; ``conv_w``/``conv_b``: the three ``nn.Conv1d`` weights
+    ``[D, 1, conv_size]`` and biases (or None); ``a_log``, ``dt_bias``: ``[H, K]``.
+    ``hist``: the conv cache ``{"q", "k", "v"}`` of ``[B, conv_size - 1, D]``
+    inputs preceding this call (None = zeros).  ``hist_out``: write the new
+    cache into these tensors (they may be ``hist`` itself when ``T <= 16``);
+    ``want_hist``: return a new cache instead.
+
+    Returns ``q, k [B, T, H, K]`` and ``v [B, T, H, V]`` in the activation
+    dtype, ``g [B, T, H, K]`` and ``beta [B, T, H]`` in fp32, and the new conv
+    cache dict (or None).
+    """
+    H, K, V = int(num_heads), int(head_dim), int(value_head_dim)
+    if q_in.dim() != 3:
+        raise KdaError(f"q_in must be [B, T, H*K], got {list(q_in.shape)}")
+    B, T = q_in.shape[0], q_in.shape[1]
+    Dk, Dv = H * K, H * V
+    q_in = _rows("q_in", q_in, (B, T, Dk))
+    k_in = _rows("k_in", k_in, (B, T, Dk))
+    v_in = _rows("v_in", v_in, (B, T, Dv))
+    gk = _rows("gk", gk, (B, T, Dk))
+    beta_logit = _rows("beta_logit", beta_logit, (B, T, H))
+    xs = (q_in, k_in, v_in)
+    dt = q_in.dtype
+    if any(t.dtype != dt for t in (k_in, v_in, gk, beta_logit)):
+        raise KdaError("q_in, k_in, v_in, gk and beta_logit must share one dtype")
+    cs = conv_w[0].shape[-1]
+    keep = cs - 1
+    ws = []
+    for n, w, D in zip("qkv", conv_w, (Dk, Dk, Dv)):
+        if tuple(w.shape) != (D, 1, cs):
+            raise KdaError(f"conv_{n} weight must be [{D}, 1, {cs}], got {list(w.shape)}")
+        ws.append(w.contiguous())
+    wdt = ws[0].dtype
+    bs = []
+    for n, b, D in zip("qkv", conv_b, (Dk, Dk, Dv)):
+        if b is not None:
+            if tuple(b.shape) != (D,) or b.dtype != wdt:
+                raise KdaError(f"conv_{n} bias must be [{D}] in {wdt}")
+            b = b.contiguous()
+        bs.append(b)
+    if any(w.dtype != wdt for w in ws):
+        raise KdaError("the three conv weights must share one dtype")
+    a_log = a_log.reshape(-1).contiguous()
+    dt_bias = dt_bias.reshape(-1).contiguous()
+    if a_log.numel() != Dk or dt_bias.numel() != Dk or a_log.dtype != dt_bias.dtype:
+        raise KdaError(f"A_log and dt_bias must be [H, K] = [{H}, {K}] of one dtype")
+    hs = [None, None, None]
+    if hist is not None:
+        for i, (n, D) in enumerate(zip("qkv", (Dk, Dk, Dv))):
+            h = hist[n]
+            if tuple(h.shape) != (B, keep, D) or h.dtype != dt:
+                raise KdaError(f"conv cache {n} must be [{B}, {keep}, {D}] in {dt}, got "
+                               f"{list(h.shape)} {h.dtype}")
+            hs[i] = h if h.is_contiguous() else h.contiguous()
+    if hist_out is not None and want_hist:
+        raise KdaError("pass hist_out or want_hist, not both")
+    dev = _device_check([*xs, gk, beta_logit, *ws, a_log, dt_bias] + [t for t in bs + hs if t is not None])
+
+    q = torch.empty(B, T, H, K, device=dev, dtype=dt)
+    k = torch.empty(B, T, H, K, device=dev, dtype=dt)
+    v = torch.empty(B, T, H, V, device=dev, dtype=dt)
+    g = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
+    beta = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    new_hist = None
+    if want_hist:
+        new_hist = {n: torch.empty(B, keep, D, device=dev, dtype=dt) for n, D in zip("qkv", (Dk, Dk, Dv))}
+    elif hist_out is not None:
+        for n, D in zip("qkv", (Dk, Dk, Dv)):
+            h = hist_out[n]
+            if tuple(h.shape) != (B, keep, D) or h.dtype != dt or not h.is_contiguous() or h.device != dev:
+                raise KdaError(f"hist_out {n} must be a contiguous [{B}, {keep}, {D}] {dt} tensor on {dev}")
+        new_hist = hist_out
+    if T == 0:
+        if new_hist is not None:
+            for i, n in enumerate("qkv"):
+                if hs[i] is None:
+                    new_hist[n].zero_()
+                elif new_hist[n].data_ptr() != hs[i].data_ptr():
+                    new_hist[n].copy_(hs[i])
+        return q, k, v, g, beta, new_hist
+
+    a = _native.KdaPrepArgs()
+    a.B, a.T, a.H, a.K, a.V, a.conv_size = B, T, H, K, V, cs
+    for i in range(3):
+        a.x[i] = xs[i].data_ptr()
+        a.x_stride[i][0], a.x_stride[i][1] = xs[i].stride(0), xs[i].stride(1)
+        a.conv_w[i] = ws[i].data_ptr()
+        a.conv_b[i] = bs[i].data_ptr() if bs[i] is not None else None
+        a.hist_in[i] = hs[i].data_ptr() if hs[i] is not None else None
+        a.hist_out[i] = new_hist["qkv"[i]].data_ptr() if new_hist is not None else None
+    a.w_dtype = _code("conv weight", ws[0])
+    a.gk = gk.data_ptr()
+    a.gk_stride[0], a.gk_stride[1] = gk.stride(0), gk.stride(1)
+    a.a_log, a.dt_bias = a_log.data_ptr(), dt_bias.data_ptr()
+    a.p_dtype = _code("A_log", a_log)
+    a.beta_logit = beta_logit.data_ptr()
+    a.beta_stride[0], a.beta_stride[1] = beta_logit.stride(0), beta_logit.stride(1)
+    a.q, a.k, a.v, a.g, a.beta = q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr()
+    a.l2_eps = float(l2_eps)
+    a.x_dtype = _code("activations", q_in)
+    _call(_native.load().kda_prep_fwd, a, dev, f"kda_prep_fwd (B={B}, T={T}, H={H}, K={K}, V={V}, conv {cs})")
+    return q, k, v, g, beta, new_hist
+
+
+def kda_output(o, gate, weight, eps):
+    """``o_proj`` input from the core output: ``rmsnorm(o) * weight`` per head,
+    rounded to o's dtype, times ``sigmoid(gate)``, rounded again.
+
+    ``o: [B, T, H, V]``, ``gate: [B, T, H*V]`` (same dtype), ``weight: [H, V]``.
+    Returns ``[B, T, H*V]``.
+    """
+    if o.dim() != 4:
+        raise KdaError(f"o must be [B, T, H, V], got {list(o.shape)}")
+    B, T, H, V = o.shape
+    if o.stride(-1) != 1:
+        o = o.contiguous()
+    gate = _rows("gate", gate, (B, T, H * V))
+    if gate.dtype != o.dtype:
+        raise KdaError("o and gate must share one dtype")
+    if tuple(weight.shape) != (H, V):
+        raise KdaError(f"weight must be [{H}, {V}], got {list(weight.shape)}")
+    weight = weight.contiguous()
+    dev = _device_check([o, gate, weight])
+    y = torch.empty(B, T, H * V, device=dev, dtype=o.dtype)
+    if y.numel() == 0:
+        return y
+    a = _native.KdaOutputArgs()
+    a.B, a.T, a.H, a.V = B, T, H, V
+    a.o = o.data_ptr()
+    a.o_stride[0], a.o_stride[1], a.o_stride[2] = o.stride(0), o.stride(1), o.stride(2)
+    a.gate = gate.data_ptr()
+    a.gate_stride[0], a.gate_stride[1] = gate.stride(0), gate.stride(1)
+    a.weight, a.w_dtype = weight.data_ptr(), _code("weight", weight)
+    a.y, a.eps, a.x_dtype = y.data_ptr(), float(eps), _code("o", o)
+    _call(_native.load().kda_output_fwd, a, dev, f"kda_output_fwd (B={B}, T={T}, H={H}, V={V})")
+    return y

@@ -10,7 +10,12 @@ Also reported on the same line:
 * ``decode``: the B=64 recurrent decode step (fp32 state N(0, 0.02), fp16
   q/k/v/g/beta) as 512 chained steps captured in one hipGraph, per-step time,
   plus a variant rotating 5 independent state sets (320 MiB working set) so
-  the state cannot stay resident in the 256 MB Infinity Cache;
+  the state cannot stay resident in the 256 MB Infinity Cache, each both with
+  a fresh state tensor per step (the reference API) and updated in place
+  (``state_out=state``, as the graph decoder runs it);
+* ``layer``: the whole KDA layer at hidden 2048 (projections, short
+  convolutions, norms and gates around the core): a B=4 T=2048 prefill and a
+  graph-replayed B=64 decode token;
 * ``cpu_baseline``: the CPU oracle (an op-for-op restatement of the
   reference's PyTorch algorithm) on a bounded sample of the same workload.
 
@@ -53,7 +58,9 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--only", choices=["chunkwise", "decode", "copy"], default=None,
+    p.add_argument("--decode-variant", choices=["all", "fresh", "in_place", "fresh_rot5", "in_place_rot5"],
+                   default="all", help="with --only decode: time one variant (for kernel traces)")
+    p.add_argument("--only", choices=["chunkwise", "decode", "layer", "copy"], default=None,
                    help="run one workload only (for profiling); 'copy' runs a plain 1 GiB "
                         "device copy used to calibrate the HBM byte counters")
     return p.parse_args()
@@ -85,8 +92,13 @@ def chunkwise_bench(pkg, wl, torch, steps, warmup):
     return wall, launch_ms
 
 
-def decode_bench(pkg, wl, torch, n_sets):
-    """512 chained decode steps in one hipGraph; returns (us_per_step, graph)."""
+def decode_bench(pkg, wl, torch, n_sets, in_place=False):
+    """512 chained decode steps in one hipGraph; returns us per step.
+
+    ``n_sets`` independent state sets are stepped in turn (5 sets = 320 MiB,
+    more than the Infinity Cache holds).  ``in_place``: each step overwrites
+    its state (``state_out=state``, the graph decoder's form); otherwise each
+    step returns a fresh state tensor, as the reference's API does."""
     inp = wl.make_inputs(B2, STEPS2, H2, D1, D1, device="cuda", seed=2,
                          qkv_dtype=torch.float16, gate_dtype=torch.float16, state_std=0.02)
     states = [inp["state"]] + [inp["state"].clone() for _ in range(n_sets - 1)]
@@ -97,7 +109,8 @@ def decode_bench(pkg, wl, torch, n_sets):
         for t in range(STEPS2):
             c = t % n_sets
             x = [a[:, t:t + 1] for a in xs]
-            _, cur[c] = pkg.kda_recurrent(*x, state=cur[c], state_dtype=torch.float32)
+            _, cur[c] = pkg.kda_recurrent(*x, state=cur[c], state_dtype=torch.float32,
+                                          state_out=cur[c] if in_place else None)
         return cur
 
     with torch.no_grad():
@@ -121,6 +134,52 @@ def decode_bench(pkg, wl, torch, n_sets):
     us = e0.elapsed_time(e1) * 1e3 / (reps * STEPS2)
     del graph
     return us
+
+
+def layer_bench(pkg, torch, reps=10):
+    """The whole KDA layer at hidden 2048 (16 heads of 128, fp16 weights N(0, 0.02),
+    fp32 state): a B=4 T=2048 prefill forward, and one graph-replayed decode
+    token at B=64 (the layer's static state updated in place)."""
+    from kimi_linear_amd.graph_decode import KdaGraphedDecoder
+
+    cfg = pkg.linear_attn_config(hidden_size=2048, num_heads=16)
+    torch.manual_seed(0)
+    layer = pkg.KimiDeltaAttention(cfg)
+    with torch.no_grad():
+        for name, prm in layer.named_parameters():
+            if name.endswith("weight") and prm.dim() >= 2:
+                prm.normal_(0.0, 0.02)
+    layer = layer.to(device="cuda", dtype=torch.float16).eval()
+    x = torch.randn(4, 2048, 2048, device="cuda", dtype=torch.float16)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.no_grad():
+        for _ in range(2):
+            layer(x)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            layer(x)
+        e1.record()
+        torch.cuda.synchronize()
+        prefill_ms = e0.elapsed_time(e1) / reps
+        dec = KdaGraphedDecoder([layer])
+        xd = torch.randn(64, 17, 2048, device="cuda", dtype=torch.float16)
+        dec.prefill(xd[:, :16])
+        tok = xd[:, 16:17]
+        for _ in range(3):
+            dec.step(tok)
+        torch.cuda.synchronize()
+        n = 100
+        e0.record()
+        for _ in range(n):
+            dec.step(tok)
+        e1.record()
+        torch.cuda.synchronize()
+        decode_us = e0.elapsed_time(e1) * 1e3 / n
+    return {"workload": "KimiDeltaAttention hidden 2048, 16 heads x 128, fp16 weights, fp32 state",
+            "prefill_B4_T2048_ms": prefill_ms,
+            "prefill_tokens_per_s": 4 * 2048 / (prefill_ms * 1e-3),
+            "decode_B64_graph_us_per_token": decode_us}
 
 
 def cpu_baselines(wl, torch, include_decode=True):
@@ -206,20 +265,36 @@ def main():
                          / FP16_PEAK_TFLOPS},
         })
     if args.only in (None, "decode"):
+        if args.decode_variant != "all":
+            sets = 5 if args.decode_variant.endswith("rot5") else 1
+            us = decode_bench(pkg, wl, torch, sets, in_place=args.decode_variant.startswith("in_place"))
+            print(json.dumps({"decode_variant": args.decode_variant, "us_per_step": us}), flush=True)
+            return
         us_mall = decode_bench(pkg, wl, torch, 1)
         us_hbm = decode_bench(pkg, wl, torch, 5)
+        us_ip = decode_bench(pkg, wl, torch, 1, in_place=True)
+        us_ip_hbm = decode_bench(pkg, wl, torch, 5, in_place=True)
         result["decode"] = {
             "workload": "kda_recurrent decode step, B=64 H=16 dk=dv=128, fp32 state, fp16 "
                         "q/k/v/g/beta; 512 chained steps in one hipGraph",
             "us_per_step": us_mall,
             "gbs": DECODE_BYTES / (us_mall * 1e-6) / 1e9,
+            "hbm_frac": DECODE_BYTES / (us_mall * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "us_per_step_rotating_320MiB": us_hbm,
             "gbs_rotating": DECODE_BYTES / (us_hbm * 1e-6) / 1e9,
             "hbm_frac_rotating": DECODE_BYTES / (us_hbm * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "us_per_step_in_place": us_ip,
+            "us_per_step_in_place_rotating_320MiB": us_ip_hbm,
+            "hbm_frac_in_place_rotating": DECODE_BYTES / (us_ip_hbm * 1e-6) / 1e9 / HBM_PEAK_GBS,
         }
         if "value" not in result:
             result.update({"value": us_mall, "unit": "us/step", "higher_is_better": False,
                            "ms_per_step": us_mall / 1e3})
+    if args.only in (None, "layer"):
+        result["layer"] = layer_bench(pkg, torch)
+        if "value" not in result:
+            result.update({"value": result["layer"]["prefill_tokens_per_s"], "unit": "tokens/s",
+                           "ms_per_step": result["layer"]["prefill_B4_T2048_ms"]})
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baselines(wl, torch, include_decode=args.only != "chunkwise")
     print(json.dumps(result), flush=True)

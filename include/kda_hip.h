@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 1
+#define KDA_ABI_VERSION 2
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -107,10 +107,78 @@ int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream);
  */
 int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Layer pre- and post-processing around the core (the KDA layer,
+ * kimi_linear/kda.py:399-470).  Same conventions: device pointers,
+ * asynchronous on `stream`, no allocation, KDA_OK or a kda_status code.
+ * "x dtype" is the activation dtype (kda_dtype) shared by every activation
+ * tensor of one call.
+ * ------------------------------------------------------------------------- */
+
+/* Projections -> core inputs, one pass (replaces ShortConv + SiLU + l2norm
+ * for q and k, ShortConv + SiLU for v, the forget gate and beta of
+ * _projections, kimi_linear/kda.py:399-461, 282-325).  Per token t, head h,
+ * channel c of q/k/v (tensor index i = 0, 1, 2):
+ *   u[t] = bias[c] + sum_j w[c, j] * x[t - (conv_size - 1) + j]     (causal)
+ *   s[t] = u / (1 + exp(-u))                                         (SiLU)
+ *   q, k: s * min(rsqrt(sum over the head's K channels of s^2), 1/l2_eps)
+ * where x[t < 0] comes from hist_in (the last conv_size - 1 inputs before
+ * this call) or is zero.  Gates: g = -exp(a_log) * softplus(gk + dt_bias)
+ * (softplus(z) = z for z > 20) and beta = sigmoid(beta_logit), in fp32.
+ * hist_out[i] (optional) receives the last conv_size - 1 inputs of
+ * [hist_in | x], the conv cache of the next call; it may be hist_in itself
+ * only when T <= 16. */
+typedef struct kda_prep_args {
+    int64_t B, T, H, K, V;         /* K, V in {64, 128, 256} */
+    int64_t conv_size;             /* 1..4 */
+    const void* x[3];              /* q, k, v projections [B, T, H*K] / [B, T, H*V], x dtype */
+    int64_t x_stride[3][2];        /* (batch, token) strides in elements; channels contiguous */
+    const void* conv_w[3];         /* [D, conv_size] contiguous (nn.Conv1d weight [D, 1, conv_size]) */
+    const void* conv_b[3];         /* [D] or NULL */
+    int32_t w_dtype;               /* kda_dtype of conv_w and conv_b */
+    const void* hist_in[3];        /* [B, conv_size - 1, D] contiguous, x dtype, or NULL (zeros) */
+    void* hist_out[3];             /* [B, conv_size - 1, D] contiguous, x dtype, or NULL */
+    const void* gk;                /* [B, T, H*K] gate up-projection output, x dtype */
+    int64_t gk_stride[2];
+    const void* a_log;             /* [H*K] */
+    const void* dt_bias;           /* [H*K] */
+    int32_t p_dtype;               /* kda_dtype of a_log and dt_bias */
+    const void* beta_logit;        /* [B, T, H], x dtype */
+    int64_t beta_stride[2];
+    void* q;                       /* [B, T, H, K] contiguous, x dtype */
+    void* k;                       /* [B, T, H, K] contiguous, x dtype */
+    void* v;                       /* [B, T, H, V] contiguous, x dtype */
+    void* g;                       /* [B, T, H, K] contiguous fp32 */
+    void* beta;                    /* [B, T, H] contiguous fp32 */
+    float l2_eps;
+    int32_t x_dtype;
+} kda_prep_args;
+
+int kda_prep_fwd(const kda_prep_args* args, void* stream);
+
+/* Core output -> o_proj input, one pass (replaces HeadwiseRMSNorm and the
+ * sigmoid output gate of _output, kimi_linear/kda.py:258-279, 464-470):
+ *   n = o * rsqrt(mean over V of o^2 + eps) * weight[h]   rounded to x dtype
+ *   y = n * sigmoid(gate)                                  rounded to x dtype */
+typedef struct kda_output_args {
+    int64_t B, T, H, V;            /* V in {64, 128, 256} */
+    const void* o;                 /* [B, T, H, V], x dtype */
+    int64_t o_stride[3];           /* (batch, token, head) strides; V contiguous */
+    const void* gate;              /* [B, T, H*V] output-gate up-projection, x dtype */
+    int64_t gate_stride[2];        /* (batch, token) strides */
+    const void* weight;            /* [H, V] contiguous */
+    int32_t w_dtype;
+    void* y;                       /* [B, T, H*V] contiguous, x dtype */
+    float eps;
+    int32_t x_dtype;
+} kda_output_args;
+
+int kda_output_fwd(const kda_output_args* args, void* stream);
+
 /* Human-readable name of a kda_status code (static storage). */
 const char* kda_status_str(int status);
 
-/* KDA_ABI_VERSION of the built library (layout of kda_fwd_args). */
+/* KDA_ABI_VERSION of the built library (layout of the argument structs). */
 int kda_abi_version(void);
 
 #ifdef __cplusplus
