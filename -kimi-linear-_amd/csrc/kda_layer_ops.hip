@@ -15,16 +15,19 @@
 // gate projection, one write of the o_proj input.
 //
 // Both are HBM-streaming kernels: one wave per unit of work (a 16-token tile
-// of one head of one tensor, or one (token, head) row), lanes across the
-// head's channels (K / 64 consecutive channels per lane, one vector access
-// per row), cross-lane sums on DPP and permlane swaps.
+// of one head of one tensor, or an 8-token tile of one output head), lanes
+// across the head's channels (K / 64 consecutive channels per lane, one
+// vector access per row), cross-lane sums on DPP and permlane swaps.  Every
+// load of a unit is issued unconditionally before its first use (rows past
+// the data re-read a valid row and are masked), so a wave keeps all of its
+// rows in flight at once instead of waiting on each.
 #include "kda_common.h"
 
 namespace kda {
 
 namespace {
 
-constexpr int kTile = 16;      // tokens per prep unit
+constexpr int kTile = 16;      // tokens per prep unit (a single-token call uses units of one token)
 constexpr int kMaxConv = 4;    // largest conv_size
 
 template <typename XT> __device__ __forceinline__ float to_f(XT x);
@@ -67,173 +70,217 @@ __device__ __forceinline__ float round_to(float x) {
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
 
 // softplus with torch's default threshold: z for z > 20
-__device__ __forceinline__ float softplus(float z) { return z > 20.f ? z : log1pf(__expf(z)); }
+__device__ __forceinline__ float softplus(float z) { return z > 20.f ? z : __logf(1.f + __expf(z)); }
+
+// A small parameter element of a runtime dtype: the load is unconditional
+// (a NULL or out-of-range element reads `fallback`'s first word instead and is
+// masked), so that every load of a unit is issued before any result is used.
+__device__ __forceinline__ RawElem param_load(const void* p, int64_t i, bool valid, const void* fallback,
+                                              int dtype) {
+    return valid ? load_raw_elem(p, i, dtype) : load_raw_elem(fallback, 0, dtype);
+}
 
 // ---- prep: one q, k or v head over a token tile ---------------------------
-template <typename XT, int CPL>
+template <typename XT, int CPL, int TILE>
 __device__ __forceinline__ void conv_unit(const kda_prep_args& a, int i, int64_t b, int64_t t0, int64_t h, int lane) {
+    constexpr int kRows = TILE + kMaxConv - 1;
     const int64_t Dh = 64 * CPL;
     const int64_t D = a.H * Dh;
     const int64_t ch0 = h * Dh + lane * CPL;
     const int cs = static_cast<int>(a.conv_size), cm = cs - 1;
     const int64_t T = a.T;
-    const int n = static_cast<int>((T - t0) < kTile ? (T - t0) : kTile);
+    const int n = static_cast<int>((T - t0) < TILE ? (T - t0) : TILE);
     const XT* x = static_cast<const XT*>(a.x[i]) + b * a.x_stride[i][0] + ch0;
     const XT* hist = static_cast<const XT*>(a.hist_in[i]);
+    const XT* hrow = hist != nullptr ? hist + b * cm * D + ch0 : x;
 
-    // window row r holds token t0 - cm + r; every load is issued first
-    float win[kTile + kMaxConv - 1][CPL];
+    // window row r holds token t0 - cm + r: a token of this call, a cached
+    // input (t < 0) or zero.  Every row is loaded unconditionally (rows with
+    // no data read token 0 and are masked) so that all loads are in flight
+    // together.
+    float win[kRows][CPL];
 #pragma unroll
-    for (int r = 0; r < kTile + kMaxConv - 1; ++r) {
+    for (int r = 0; r < kRows; ++r) {
         const int64_t tok = t0 - cm + r;
-        if (r < n + cm && tok >= 0) {
-            ld<XT, CPL>(x + tok * a.x_stride[i][1], win[r]);
-        } else if (r < n + cm && hist != nullptr) {
-            ld<XT, CPL>(hist + (b * cm + (cm + tok)) * D + ch0, win[r]);
-        } else {
+        const bool in_x = tok >= 0 && tok < T;
+        const bool in_h = tok < 0 && hist != nullptr;
+        const XT* src = in_x ? x + tok * a.x_stride[i][1] : (in_h ? hrow + (cm + tok) * D : x);
+        ld<XT, CPL>(src, win[r]);
+        if (!(in_x || in_h)) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c) win[r][c] = 0.f;
         }
     }
+    RawElem rw[kMaxConv][CPL], rb[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        rb[c] = param_load(a.conv_b[i], ch0 + c, a.conv_b[i] != nullptr, a.conv_w[i], a.w_dtype);
+#pragma unroll
+        for (int j = 0; j < kMaxConv; ++j)
+            rw[j][c] = param_load(a.conv_w[i], (ch0 + c) * cs + j, j < cs, a.conv_w[i], a.w_dtype);
+    }
     float w[kMaxConv][CPL], bias[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        bias[c] = a.conv_b[i] ? load_elem(a.conv_b[i], ch0 + c, a.w_dtype) : 0.f;
+        bias[c] = a.conv_b[i] != nullptr ? decode_elem(rb[c], a.w_dtype) : 0.f;
 #pragma unroll
-        for (int j = 0; j < kMaxConv; ++j)
-            w[j][c] = j < cs ? load_elem(a.conv_w[i], (ch0 + c) * cs + j, a.w_dtype) : 0.f;
+        for (int j = 0; j < kMaxConv; ++j) w[j][c] = j < cs ? decode_elem(rw[j][c], a.w_dtype) : 0.f;
     }
 
     XT* out = static_cast<XT*>(i == 0 ? a.q : (i == 1 ? a.k : a.v)) + (b * T + t0) * D + ch0;
     const float inv_eps = 1.f / a.l2_eps;
+    // tap j of tile token t reads window row t + j (token t0 + t - cm + j)
 #pragma unroll
-    for (int t = 0; t < kTile; ++t) {
-        if (t < n) {
-            float s[CPL];
-            float ss = 0.f;
+    for (int t = 0; t < TILE; ++t) {
+        float s[CPL];
+        float ss = 0.f;
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                float u = bias[c];
+        for (int c = 0; c < CPL; ++c) {
+            float u = bias[c];
 #pragma unroll
-                for (int j = 0; j < kMaxConv; ++j) u = fmaf(w[j][c], win[t + j][c], u);
-                s[c] = u * sigmoid(u);
-                ss = fmaf(s[c], s[c], ss);
-            }
-            if (i < 2) {
-                // l2 norm over the head: x * min(rsqrt(sum x^2), 1/eps)
-                const float rn = fminf(rsqrtf(wave_sum(ss)), inv_eps);
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) s[c] *= rn;
-            }
-            st<XT, CPL>(out + t * D, s);
+            for (int j = 0; j < kMaxConv; ++j)
+                if (j < cs) u = fmaf(w[j][c], win[t + j][c], u);
+            s[c] = u * sigmoid(u);
+            ss = fmaf(s[c], s[c], ss);
         }
+        if (i < 2) {
+            // l2 norm over the head: x * min(rsqrt(sum x^2), 1/eps)
+            const float rn = fminf(rsqrtf(wave_sum(ss)), inv_eps);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) s[c] *= rn;
+        }
+        if (t < n) st<XT, CPL>(out + t * D, s);
     }
 
-    // the next call's conv cache: inputs T - cm .. T - 1, window rows T - t0 + r
+    // the next call's conv cache: inputs T - cm .. T - 1 = window rows n + r
     if (a.hist_out[i] != nullptr && t0 + n == T) {
         XT* ho = static_cast<XT*>(a.hist_out[i]) + b * cm * D + ch0;
 #pragma unroll
         for (int r = 0; r < kMaxConv - 1; ++r) {
-            if (r < cm) {
+            float hv[CPL];
 #pragma unroll
-                for (int rr = 0; rr < kTile + kMaxConv - 1; ++rr)
-                    if (rr == n + r) st<XT, CPL>(ho + r * D, win[rr]);
-            }
+            for (int c = 0; c < CPL; ++c) hv[c] = 0.f;
+#pragma unroll
+            for (int rr = 0; rr < kRows; ++rr)
+                if (rr == n + r) {
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) hv[c] = win[rr][c];
+                }
+            if (r < cm) st<XT, CPL>(ho + r * D, hv);
         }
     }
 }
 
 // ---- prep: the forget gate of one head over a token tile, and its beta ----
-template <typename XT, int CPL>
+template <typename XT, int CPL, int TILE>
 __device__ __forceinline__ void gate_unit(const kda_prep_args& a, int64_t b, int64_t t0, int64_t h, int lane) {
     const int64_t Dh = 64 * CPL;
     const int64_t D = a.H * Dh;
     const int64_t ch0 = h * Dh + lane * CPL;
     const int64_t T = a.T;
-    const int n = static_cast<int>((T - t0) < kTile ? (T - t0) : kTile);
+    const int n = static_cast<int>((T - t0) < TILE ? (T - t0) : TILE);
     const XT* gk = static_cast<const XT*>(a.gk) + b * a.gk_stride[0] + ch0;
 
-    float z[kTile][CPL];
+    // every load first (rows past the end re-read the last token)
+    float z[TILE][CPL];
 #pragma unroll
-    for (int t = 0; t < kTile; ++t) {
-        if (t < n) {
-            ld<XT, CPL>(gk + (t0 + t) * a.gk_stride[1], z[t]);
-        } else {
+    for (int t = 0; t < TILE; ++t) ld<XT, CPL>(gk + (t0 + (t < n ? t : n - 1)) * a.gk_stride[1], z[t]);
+    const int tl = lane < n ? lane : n - 1;
+    const RawElem rlogit =
+        load_raw_elem(a.beta_logit, b * a.beta_stride[0] + (t0 + tl) * a.beta_stride[1] + h, a.x_dtype);
+    RawElem ra[CPL], rd[CPL];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) z[t][c] = 0.f;
-        }
+    for (int c = 0; c < CPL; ++c) {
+        ra[c] = load_raw_elem(a.a_log, ch0 + c, a.p_dtype);
+        rd[c] = load_raw_elem(a.dt_bias, ch0 + c, a.p_dtype);
     }
-    RawElem rlogit{0u, 0u};
-    if (lane < n)
-        rlogit = load_raw_elem(a.beta_logit, b * a.beta_stride[0] + (t0 + lane) * a.beta_stride[1] + h, a.x_dtype);
     float neg_a[CPL], dtb[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        neg_a[c] = -__expf(load_elem(a.a_log, ch0 + c, a.p_dtype));
-        dtb[c] = load_elem(a.dt_bias, ch0 + c, a.p_dtype);
+        neg_a[c] = -__expf(decode_elem(ra[c], a.p_dtype));
+        dtb[c] = decode_elem(rd[c], a.p_dtype);
     }
     float* g = static_cast<float*>(a.g) + (b * T + t0) * D + ch0;
 #pragma unroll
-    for (int t = 0; t < kTile; ++t) {
-        if (t < n) {
-            float o[CPL];
+    for (int t = 0; t < TILE; ++t) {
+        float o[CPL];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) o[c] = neg_a[c] * softplus(z[t][c] + dtb[c]);
-            st<float, CPL>(g + t * D, o);
-        }
+        for (int c = 0; c < CPL; ++c) o[c] = neg_a[c] * softplus(z[t][c] + dtb[c]);
+        if (t < n) st<float, CPL>(g + t * D, o);
     }
     if (lane < n)
         static_cast<float*>(a.beta)[(b * T + t0 + lane) * a.H + h] = sigmoid(decode_elem(rlogit, a.x_dtype));
 }
 
 // One wave per (batch, tile, part, head), part 0..2 = q, k, v, 3 = gate.
-template <typename XT, int CPLK, int CPLV>
-__global__ __launch_bounds__(256) void prep_kernel(const kda_prep_args a, int64_t ntiles) {
+// The host keeps the number of units below 2^31, so the unit index is split
+// with 32-bit arithmetic.
+template <typename XT, int CPLK, int CPLV, int TILE>
+__global__ __launch_bounds__(256) void prep_kernel(const kda_prep_args a, uint32_t ntiles, uint32_t units) {
     const int lane = threadIdx.x & 63;
-    const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (unit >= a.B * ntiles * 4 * a.H) return;
-    int64_t u = unit;
-    const int64_t h = u % a.H;
-    u /= a.H;
-    const int part = static_cast<int>(u % 4);
-    u /= 4;
-    const int64_t t0 = (u % ntiles) * kTile;
+    const uint32_t unit = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (unit >= units) return;
+    const uint32_t H = static_cast<uint32_t>(a.H);
+    uint32_t u = unit;
+    const int64_t h = u % H;
+    u /= H;
+    const int part = static_cast<int>(u & 3u);
+    u >>= 2;
+    const int64_t t0 = static_cast<int64_t>(u % ntiles) * TILE;
     const int64_t b = u / ntiles;
     if (part < 2)
-        conv_unit<XT, CPLK>(a, part, b, t0, h, lane);
+        conv_unit<XT, CPLK, TILE>(a, part, b, t0, h, lane);
     else if (part == 2)
-        conv_unit<XT, CPLV>(a, 2, b, t0, h, lane);
+        conv_unit<XT, CPLV, TILE>(a, 2, b, t0, h, lane);
     else
-        gate_unit<XT, CPLK>(a, b, t0, h, lane);
+        gate_unit<XT, CPLK, TILE>(a, b, t0, h, lane);
 }
 
-// ---- output: one wave per (batch, token, head) row -------------------------
+// ---- output: one wave per (batch, head, tile of kOutRows tokens) -----------
+constexpr int kOutRows = 8;
+
 template <typename XT, int CPL>
-__global__ __launch_bounds__(256) void output_kernel(const kda_output_args a) {
+__global__ __launch_bounds__(256) void output_kernel(const kda_output_args a, uint32_t ntiles, uint32_t units) {
     const int lane = threadIdx.x & 63;
-    const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (unit >= a.B * a.T * a.H) return;
-    const int64_t h = unit % a.H;
-    const int64_t bt = unit / a.H;
-    const int64_t t = bt % a.T, b = bt / a.T;
+    const uint32_t unit = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (unit >= units) return;
+    const uint32_t H = static_cast<uint32_t>(a.H);
+    const int64_t h = unit % H;
+    const uint32_t bt = unit / H;
+    const int64_t t0 = static_cast<int64_t>(bt % ntiles) * kOutRows, b = bt / ntiles;
+    const int n = static_cast<int>((a.T - t0) < kOutRows ? (a.T - t0) : kOutRows);
     const int64_t V = 64 * CPL;
     const int64_t c0 = lane * CPL;
 
-    float o[CPL], gt[CPL];
-    ld<XT, CPL>(static_cast<const XT*>(a.o) + b * a.o_stride[0] + t * a.o_stride[1] + h * a.o_stride[2] + c0, o);
-    ld<XT, CPL>(static_cast<const XT*>(a.gate) + b * a.gate_stride[0] + t * a.gate_stride[1] + h * V + c0, gt);
+    // every load first (rows past the end re-read the last token)
+    const XT* op = static_cast<const XT*>(a.o) + b * a.o_stride[0] + h * a.o_stride[2] + c0;
+    const XT* gp = static_cast<const XT*>(a.gate) + b * a.gate_stride[0] + h * V + c0;
+    float o[kOutRows][CPL], gt[kOutRows][CPL];
+#pragma unroll
+    for (int r = 0; r < kOutRows; ++r) {
+        const int64_t t = t0 + (r < n ? r : n - 1);
+        ld<XT, CPL>(op + t * a.o_stride[1], o[r]);
+        ld<XT, CPL>(gp + t * a.gate_stride[1], gt[r]);
+    }
+    RawElem rw[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) rw[c] = load_raw_elem(a.weight, h * V + c0 + c, a.w_dtype);
     float w[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) w[c] = load_elem(a.weight, h * V + c0 + c, a.w_dtype);
+    for (int c = 0; c < CPL; ++c) w[c] = decode_elem(rw[c], a.w_dtype);
 
-    float ss = 0.f;
+    XT* yp = static_cast<XT*>(a.y) + (b * a.T + t0) * a.H * V + h * V + c0;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) ss = fmaf(o[c], o[c], ss);
-    const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(V) + a.eps);
-    float y[CPL];
+    for (int r = 0; r < kOutRows; ++r) {
+        float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) y[c] = round_to<XT>((o[c] * rstd) * w[c]) * sigmoid(gt[c]);
-    st<XT, CPL>(static_cast<XT*>(a.y) + (b * a.T + t) * a.H * V + h * V + c0, y);
+        for (int c = 0; c < CPL; ++c) ss = fmaf(o[r][c], o[r][c], ss);
+        const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(V) + a.eps);
+        float y[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) y[c] = round_to<XT>((o[r][c] * rstd) * w[c]) * sigmoid(gt[r][c]);
+        if (r < n) st<XT, CPL>(yp + r * a.H * V, y);
+    }
 }
 
 // ---- host side --------------------------------------------------------------
@@ -256,10 +303,17 @@ bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
 
 template <typename XT, int CPLK, int CPLV>
 void launch_prep(const kda_prep_args& a, hipStream_t stream) {
+    // a single token (the decode step) gets units of one token
+    if (a.T == 1) {
+        const int64_t units = a.B * 4 * a.H;
+        hipLaunchKernelGGL((prep_kernel<XT, CPLK, CPLV, 1>), dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256),
+                           0, stream, a, 1u, static_cast<uint32_t>(units));
+        return;
+    }
     const int64_t ntiles = (a.T + kTile - 1) / kTile;
     const int64_t units = a.B * ntiles * 4 * a.H;
-    hipLaunchKernelGGL((prep_kernel<XT, CPLK, CPLV>), dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256), 0,
-                       stream, a, ntiles);
+    hipLaunchKernelGGL((prep_kernel<XT, CPLK, CPLV, kTile>), dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256),
+                       0, stream, a, static_cast<uint32_t>(ntiles), static_cast<uint32_t>(units));
 }
 
 template <typename XT>
@@ -282,11 +336,14 @@ int launch_prep_dims(const kda_prep_args& a, hipStream_t stream) {
 
 template <typename XT>
 int launch_output_dims(const kda_output_args& a, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((a.B * a.T * a.H + 3) / 4)), block(256);
+    const int64_t ntiles = (a.T + kOutRows - 1) / kOutRows;
+    const int64_t units = a.B * ntiles * a.H;
+    const dim3 grid(static_cast<unsigned>((units + 3) / 4)), block(256);
+    const uint32_t nt = static_cast<uint32_t>(ntiles), nu = static_cast<uint32_t>(units);
     switch (a.V) {
-        case 64: hipLaunchKernelGGL((output_kernel<XT, 1>), grid, block, 0, stream, a); break;
-        case 128: hipLaunchKernelGGL((output_kernel<XT, 2>), grid, block, 0, stream, a); break;
-        case 256: hipLaunchKernelGGL((output_kernel<XT, 4>), grid, block, 0, stream, a); break;
+        case 64: hipLaunchKernelGGL((output_kernel<XT, 1>), grid, block, 0, stream, a, nt, nu); break;
+        case 128: hipLaunchKernelGGL((output_kernel<XT, 2>), grid, block, 0, stream, a, nt, nu); break;
+        case 256: hipLaunchKernelGGL((output_kernel<XT, 4>), grid, block, 0, stream, a, nt, nu); break;
         default: return KDA_ERR_UNSUPPORTED;
     }
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
@@ -331,7 +388,7 @@ int validate_prep(const kda_prep_args* a) {
         !vec_ok(a->g, nullptr, 0, ck, KDA_DTYPE_F32))
         return KDA_ERR_BAD_SHAPE;
     const int64_t ntiles = (a->T + kTile - 1) / kTile;
-    if ((a->B * ntiles * 4 * a->H + 3) / 4 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    if (a->B * ntiles * 4 * a->H > INT32_MAX) return KDA_ERR_BAD_SHAPE;
     return KDA_OK;
 }
 
@@ -347,7 +404,7 @@ int validate_output(const kda_output_args* a) {
     if (!vec_ok(a->o, a->o_stride, 3, cpl, a->x_dtype) || !vec_ok(a->gate, a->gate_stride, 2, cpl, a->x_dtype) ||
         !vec_ok(a->y, nullptr, 0, cpl, a->x_dtype))
         return KDA_ERR_BAD_SHAPE;
-    if ((a->B * a->T * a->H + 3) / 4 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    if (a->B * ((a->T + kOutRows - 1) / kOutRows) * a->H > INT32_MAX) return KDA_ERR_BAD_SHAPE;
     return KDA_OK;
 }
 
