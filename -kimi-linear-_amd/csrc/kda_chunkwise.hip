@@ -1,51 +1,73 @@
 // Chunkwise KDA forward for gfx950: fp16 MFMA, fp32 accumulation, fp32 state.
 //
 // Replaces the body of kda_chunkwise (kimi_linear/kda.py:111-185).  The maths
-// is the reference's UT-transform form (paper Eq. 6-9) evaluated per block of
-// BT = 16 tokens; the recurrence is chunk-size invariant, so the caller's
-// chunk_size only fixes the T % chunk_size == 0 contract.
+// is the reference's UT-transform form (paper Eq. 6-9) with the state carried
+// across chunks of CT = 32 tokens, each made of two blocks of BT = 16 tokens.
+// The recurrence is chunk-size invariant, so the caller's chunk_size only
+// fixes the T % chunk_size == 0 contract.
 //
-// Per (b, h) and block (rows c, i in [0, 16)), with a_t = exp(g_t):
-//   E[r]   = prod_{t<=r} a_t              (= exp(gc_r), per channel)
-//   L[c,i] = beta_c <k_c, k_i * prod_{t=i+1..c} a_t>,  i < c
-//   A[c,i] = scale <q_c, k_i * prod_{t=i+1..c} a_t>,   i <= c
-//   M      = (I + L)^-1 Diag(beta)
-//   P      = M (V - (E * K) S)           (= U - W S with U = M V, W = M (E * K))
+// Per (b, h) and chunk, with a_t = exp(g_t) per channel, rows c, i of one
+// chunk, E[r] = prod_{t <= r} a_t from the chunk start and F = E[31] / E:
+//   G[c,i] = <k_c, k_i * prod_{t=i+1..c} a_t>,          i < c
+//   A[c,i] = scale <q_c, k_i * prod_{t=i+1..c} a_t>,    i <= c
+//   P      = (I + Diag(beta) G)^-1 Diag(beta) (V - (E * K) S)
 //   O      = scale (E * Q) S + A P
-//   S     <- Diag(E[15]) S + ((E[15]/E) * K)^T P
+//   S     <- Diag(E[31]) S + (F * K)^T P
+// With blocks 0 and 1 of the chunk, M_bb = (I + Diag(beta_b) G_bb)^-1
+// Diag(beta_b) and R_b = V_b - (E * K)_b S, the solve is two block steps:
+//   P_0 = M_00 R_0,   P_1 = M_11 (R_1 - G_10 P_0).
 //
-// Decay factoring without pairwise exponentials: every pair i < c of a block
-// has a unique highest differing bit b; c has it set, i clear, and both sit in
-// the aligned group of 2^(b+1) rows whose upper half starts at ref + 1.  Then
+// Decay factoring without pairwise exponentials.  Diagonal blocks: every
+// pair i < c of a block has a unique highest differing bit b; c has it set,
+// i clear, and both sit in the aligned group of 2^(b+1) rows whose upper half
+// starts at ref + 1.  Then
 //   prod_{t=i+1..c} a_t = (prod_{t=ref+1..c} a_t) * (prod_{t=i+1..ref} a_t),
-// both factors <= 1, so per level b one [16 x K] operand X_b (row r = k_r times
-// its factor) gives L_b = X_b X_b^T as a plain MFMA product, masked to level
-// b's pairs.  A factor only underflows when the true decay is smaller still.
-// Level "diag" (factor 1) gives A[c, c].
+// both factors <= 1, so per level b one [16 x K] operand X_b (row r = k_r
+// times its factor) gives G_b = X_b X_b^T as a plain MFMA product, masked to
+// level b's pairs.  Level "diag" (factor 1) gives A[c, c].  Off-diagonal
+// block G_10, A_10: the reference row is the last row of block 0, so the
+// factors are the block-local decay of row c of block 1 from its block start
+// and of row i of block 0 to its block end.  A factor only underflows when
+// the true decay is smaller still.
 //
-// (I + L)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8) for the nilpotent L: four
-// 16x16 products and three squarings on MFMA (fp16 hi/lo split operands),
-// entirely in registers.  An MFMA accumulator holds X[4g+j][n] in lane n+16g,
-// slot j -- the B-operand layout of X and the A-operand layout of X^T -- so a
-// chain that keeps X and X^T side by side needs no data movement.
+// (I + L)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8) for the nilpotent 16x16
+// L = Diag(beta) G_bb: four products and three squarings on MFMA (fp16 hi/lo
+// split operands), entirely in registers.  An MFMA accumulator holds
+// X[4g+j][n] in lane n+16g, slot j -- the B-operand layout of X and the
+// A-operand layout of X^T -- so a chain that keeps X and X^T side by side
+// needs no data movement.
 //
 // Pipeline, one workgroup per (b, h, 16*NC state columns), in supersteps of
-// NB = 4 blocks (64 tokens), each split in two halves by workgroup barriers:
+// NB = 4 blocks (two chunks), each split in two halves by workgroup barriers:
 //   NC consumer waves: wave w owns state columns [16w, 16w+16) for all K rows
-//     as MFMA accumulators and runs the sequential chain over blocks 0-1 of
-//     superstep s in the first half and blocks 2-3 in the second.
-//   NB * PW producer waves (PW = 2 for K = 128, else 1): the PW waves of
-//     block p build every operand of block NB*(s+1) + p, each over its own
-//     channels -- decays, level operands (staged k-major in the slot's own
-//     q*E / k*E rows before those receive their final values), partial L
-//     and A -- in the first half; in the second the first wave adds the
-//     partial sums, writes A and inverts (I + L), the other writes its
-//     E-scaled operands.  The next block's loads are issued between levels.
-// Operand slots alternate between two sets of NB, so the producers of
-// superstep s+1 and the consumers of superstep s never touch the same slot.
-// Operands that are not exact in fp16 and carry the state (S, P, M, L and
-// V - Z) are split into fp16 hi + lo; the others are single fp16 with fp32
-// accumulation.
+//     as MFMA accumulators and runs the chain over chunk 0 of superstep s in
+//     the first half and chunk 1 in the second.
+//   NB producer waves, one per block: wave p builds every operand of block
+//     NB*(s+1) + p.  Lane l holds K/32 adjacent channels of the block's rows
+//     8 (l / 32) .. +7, which one 8-byte (fp16) load per row brings in for
+//     all K channels of two rows.  First half: decays, the level operands
+//     and their products, the operands that need no other block's decay, the
+//     block-local operands of the chunk's off-diagonal products, the block
+//     decay E[15].  Second half, once the other block's decay is known: the
+//     chunk-relative operands, G_10 and A_10 (block 1's wave), A and the
+//     inverse of (I + L).  The next block's loads are issued in the first
+//     half and land during the rest of the superstep.
+// Operand slots alternate between two sets, so the producers of superstep
+// s+1 and the consumers of superstep s never touch the same slot.
+//
+// Operand layouts in LDS.  Row operands (q * E, k * E, the level operands,
+// the block-local k * F of block 0) are row-major [16 tokens][K + 8 pad],
+// channels permuted by chan_pos so that the eight channels one MFMA lane
+// needs (the ones paired with its state rows) are 16 contiguous bytes: a
+// producer lane writes a row's channels with one 8-byte store, an MFMA lane
+// reads its fragment with one 16-byte load, both free of bank conflicts.
+// k * F, which the state update reads by channel, is k-major: one 64-byte
+// line per channel holding the chunk's 32 tokens in the order of the
+// consumer's P fragments, its 16-byte pieces rotated by channel bits 2-3.
+//
+// Operands that are not exact in fp16 and carry the state (S, P, M, G_10
+// and V - Z) are split into fp16 hi + lo; the others are single fp16 with
+// fp32 accumulation.
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -54,19 +76,24 @@ namespace kda {
 namespace {
 
 constexpr int BT = 16;          // tokens per block
+constexpr int HR = 8;           // rows per producer lane (half a block)
+constexpr int CB = 2;           // blocks per chunk (the state advances per chunk)
 constexpr int NB = 4;           // blocks per superstep = producer waves
-constexpr int NSLOT = 2 * NB;   // operand slots (two supersteps)
+constexpr int NCH = NB / CB;    // chunks per superstep
 constexpr int RP = 24;          // padded row (halfs) of the [16][16] fp16 A-operand matrices
 constexpr int LP = 20;          // padded row (floats) of the 16x16 fp32 L
 constexpr int kXcds = 8;        // accelerator complex dies on MI355X
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-// Raw buffer loads.  A block's descriptor spans exactly its rows before T;
-// the range check covers the whole offset (lane offset + row offset), so
-// rows past T read as zero -- the neutral padding (k = q = v = g = beta = 0)
-// -- with no clamping or masking.  The row offset is wave-uniform and goes in
-// the scalar offset; the lane offset is one register per tensor.
+// Raw buffer loads.  A block's descriptor spans exactly its rows before T
+// (none for a block past T); the range check covers the whole offset (lane
+// offset + row offset), so rows past T read as zero -- the neutral padding
+// (k = q = v = g = beta = 0) -- with no clamping or masking.  The row offset
+// is wave-uniform and goes in the scalar offset; the lane offset is one
+// register per tensor.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                              static_cast<int>(nbytes), 0x00020000);
@@ -87,18 +114,29 @@ template <> struct BLoad<4> {
 template <> struct BLoad<8> {
     static constexpr int W = 2;
     static __device__ __forceinline__ void ld(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(vo), static_cast<int>(so), 0);
+        const u2 x = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(vo),
+                                                                                 static_cast<int>(so), 0));
         w[0] = x[0];
         w[1] = x[1];
     }
 };
+template <> struct BLoad<16> {
+    static constexpr int W = 4;
+    static __device__ __forceinline__ void ld(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+        const u4 x = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(vo),
+                                                                                  static_cast<int>(so), 0));
+        w[0] = x[0];
+        w[1] = x[1];
+        w[2] = x[2];
+        w[3] = x[3];
+    }
+};
 
 // Values are held raw, one load per register set, and converted only where
-// they are used.  Left alone, the compiler hoists a conversion (or the
-// packing of two fp16 loads into one register) up to the load, which puts a
-// wait for the whole prefetch right after it is issued.  An empty volatile
-// asm that "modifies" the registers at the point of use keeps every such
-// instruction, and the wait, there.
+// they are used.  Left alone, the compiler hoists a conversion up to the
+// load, which puts a wait for the whole prefetch right after it is issued.
+// An empty volatile asm that "modifies" the registers at the point of use
+// keeps every such instruction, and the wait, there.
 template <int N>
 __device__ __forceinline__ void use_here(uint32_t (&r)[N]) {
 #pragma unroll
@@ -110,119 +148,78 @@ __device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
     for (int i = 0; i < N; ++i) use_here(r[i]);
 }
 
-// Element type of q, k and v: CH adjacent channels of one token row.
-template <typename TQ, int CH>
-struct QRow {
-    static constexpr int BYTES = CH * static_cast<int>(sizeof(TQ));
-    static constexpr int W = BLoad<BYTES>::W;
-    // channel j of a raw row
-    static __device__ __forceinline__ float val(const uint32_t (&w)[W], int j) {
-        if constexpr (sizeof(TQ) == 4) {
-            return __uint_as_float(w[j]);
-        } else {
-            const uint32_t hbits = (w[0] >> (16 * j)) & 0xffffu;
-            if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
-                return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hbits)));
-            } else {
-                return __uint_as_float(hbits << 16);
-            }
-        }
-    }
-    // channel j of rows (r0, r1) as an fp16 pair (exact repacking for fp16)
-    static __device__ __forceinline__ h2 pair(const uint32_t (&w0)[W], const uint32_t (&w1)[W], int j) {
+// Element j of a raw row of TQ values, as fp16 (exact for fp16 inputs).
+template <typename TQ, int W>
+__device__ __forceinline__ _Float16 raw_h(const uint32_t (&w)[W], int j) {
+    if constexpr (sizeof(TQ) == 4) {
+        return static_cast<_Float16>(__uint_as_float(w[j]));
+    } else {
+        const uint16_t bits = static_cast<uint16_t>(w[j / 2] >> (16 * (j % 2)));
         if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
-            const uint32_t lo = (w0[0] >> (16 * j)) & 0xffffu;
-            const uint32_t hi = (w1[0] >> (16 * j)) << 16;
-            return __builtin_bit_cast(h2, lo | hi);
+            return __builtin_bit_cast(_Float16, bits);
         } else {
-            return h2{static_cast<_Float16>(val(w0, j)), static_cast<_Float16>(val(w1, j))};
+            return static_cast<_Float16>(__uint_as_float(static_cast<uint32_t>(bits) << 16));
         }
     }
-};
-
-// Sixteen fp32 values rounded to fp16, as two h8 (rows 0-7, 8-15).
-__device__ __forceinline__ void to_h16(const float (&x)[BT], h8& lo, h8& hi) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        lo[i] = static_cast<_Float16>(x[i]);
-        hi[i] = static_cast<_Float16>(x[8 + i]);
+}
+// One value of type TQ held raw in the low bits of a word, as fp32.
+template <typename TQ>
+__device__ __forceinline__ float raw_f(uint32_t w) {
+    if constexpr (sizeof(TQ) == 4) {
+        return __uint_as_float(w);
+    } else if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+    } else {
+        return __uint_as_float(w << 16);
     }
 }
 
-// Within one wave, LDS serves requests in issue order, so a wave reads back
-// what its own lanes wrote (and reads complete before later overwrites)
-// without any barrier; the compiler keeps the order of the possibly
-// aliasing LDS accesses.  The per-producer staging areas rely on this.
+__device__ __forceinline__ h8 cat(const h4& a, const h4& b) {
+    return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
-// Operands of one block, as the consumers read them.  QET and KET are read
-// through LDS transpose loads, KHT as A-operand rows of channels; all three
-// are k-major ([K][16]: the 16 rows of a channel in one 32-byte line, halves
-// swizzled by channel bit 3, see kswz).
+// Position of channel c inside a row-major operand row.  With c = 32u + 16hi
+// + 4g + j, the consumer lane of group g pairs channels 32u + 4g + j and
+// 32u + 16 + 4g + j with its state rows; they sit at 32u + 8g + (0..7).
+__device__ __forceinline__ int chan_pos(int c) {
+    return (c & ~31) | ((c & 12) << 1) | ((c & 16) >> 2) | (c & 3);
+}
+// 16-byte piece rotation of the k-major k * F lines (channel bits 2-3): the
+// 16 channel lines one consumer instruction reads land on 16 distinct bank
+// groups.
+__device__ __forceinline__ int kh_swz(int c) { return (c >> 2) & 3; }
+
+// Operands of one chunk, as the consumers read them.
 template <int K>
-struct __align__(16) Slot {
-    _Float16 QET[K][BT];                   // q * E
-    _Float16 KET[K][BT];                   // k * E
-    _Float16 KHT[K][BT];                   // k * E15 / E
-    _Float16 AM[BT][RP];                   // scale * A
-    _Float16 MH[BT][RP];                   // M hi
-    _Float16 ML[BT][RP];                   // M lo
-    float elast[K];                        // E[15]
+struct __align__(16) ChunkOps {
+    static constexpr int KR = K + 8;
+    _Float16 QE[CB][BT][KR];               // q * E (decay from the chunk start), row-major
+    _Float16 KE[CB][BT][KR];               // k * E
+    _Float16 KH[K][2 * BT];                // k * F (decay to the chunk end), k-major lines
+    _Float16 AM[CB][BT][RP];               // scale * A, diagonal blocks
+    _Float16 MH[CB][BT][RP];               // M hi
+    _Float16 ML[CB][BT][RP];               // M lo
+    _Float16 A10[BT][RP];                  // scale * A, rows of block 1, columns of block 0
+    _Float16 GH[BT][RP];                   // -G_10 hi
+    _Float16 GL[BT][RP];                   // -G_10 lo
+    float echunk[K];                       // decay over the chunk, E[31]
 };
-
-// Producer waves per block: for K = 128 two, each with half of the channels
-// (one channel per lane); one otherwise.
+// Producer-only exchange of one chunk within a superstep: written in the
+// first half, read in the second.
 template <int K>
-constexpr int kPW = K == 128 ? 2 : 1;
-
+struct __align__(16) Stage {
+    _Float16 KH0[BT][K + 8];               // block 0: k * (decay to the block end), row-major
+    float e15[CB][K];                      // per block: decay over the block
+};
 template <int K>
 struct __align__(16) Smem {
-    Slot<K> slot[NSLOT];
-    // per block: the second producer's partial L and A (lane-major), then
-    // the first producer's L for its transpose
-    float XCH[NB][2][64][4];
+    ChunkOps<K> set[2][NCH];
+    Stage<K> st[NCH];
+    float LT[NB][BT][LP];                  // per block: the transposition of L in the solve
 };
 
 __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, int lg) {
     return *reinterpret_cast<const h4*>(base + row * stride + 4 * lg);
-}
-
-typedef short s4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s4 lds_s4;
-
-// k-major [K][16] fp16 matrices (the 16 rows of a channel in one 32-byte
-// line) swap the two 16-byte halves of the line on channels with bit 3 set,
-// so the 16-byte writes of 16 consecutive channels (one per lane) cover all
-// 64 banks once.  Half h of channel c sits at 8 * (h ^ kswz(c)).
-__device__ __forceinline__ int kswz(int c) { return (c >> 3) & 1; }
-
-// Stores the 16 rows of channel c (rows 0-7, 8-15) into a k-major matrix.
-__device__ __forceinline__ void store_kmajor(_Float16* xt, int c, const h8& r0_7, const h8& r8_15) {
-    const int s = kswz(c) * 8;
-    *reinterpret_cast<h8*>(xt + c * BT + s) = r0_7;
-    *reinterpret_cast<h8*>(xt + c * BT + (8 - s)) = r8_15;
-}
-
-// MFMA row fragment from a k-major [K][16] fp16 matrix X^T through the LDS
-// transpose read (ds_read_b64_tr_b16): within each 16-lane group, lane 4j+q
-// supplies the four rows 4q..4q+3 of channel kbase+j, and lane i receives
-// X[i][kbase + 0..3] -- the A-operand fragment of row i, which is also the
-// B-operand fragment of column i of X^T.  kbase is 4lg modulo 16, so the
-// channels kbase + j (j < 4) share bit 3 = lg >> 1 and the swizzled column of
-// rows 4q..4q+3 is 4 (q ^ 2 (lg >> 1)), a per-lane constant.
-__device__ __forceinline__ h4 frag16_tr(const _Float16* xt, int kbase, int ln, int lg) {
-    const int q = (ln & 3) ^ ((lg >> 1) * 2);
-    const _Float16* p = xt + (kbase + (ln >> 2)) * BT + 4 * q;
-    return __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
-}
-
-// 16x16x32 fragment: slots 0-3 hold k = 32u + 4lg + j, slots 4-7 hold
-// k = 32u + 16 + 4lg + j.  A and B fragments use the same assignment, so the
-// product is the full 32-wide dot product whatever slot order the unit uses;
-// it also matches the two state tiles 2u, 2u+1 held by a consumer lane group.
-__device__ __forceinline__ h8 frag32_tr(const _Float16* xt, int lg, int ln, int u) {
-    const h4 lo = frag16_tr(xt, 32 * u + 4 * lg, ln, lg);
-    const h4 hi = frag16_tr(xt, 32 * u + 16 + 4 * lg, ln, lg);
-    return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 // Four fp32 values as fp16 hi + lo, x ~= hi + lo to ~2^-21 relative: hi is x
@@ -248,13 +245,18 @@ struct Split4 {
     __device__ explicit Split4(const f4& x) { split4(x, hi, lo); }
 };
 
-// acc(A_layout(a) * B_layout(b)) with both operands split: hi*hi + hi*lo + lo*hi.
-__device__ __forceinline__ f4 mm3(const Split4& a, const Split4& b) {
-    f4 d = {0.f, 0.f, 0.f, 0.f};
-    d = mfma16x16x16(a.hi, b.hi, d);
-    d = mfma16x16x16(a.hi, b.lo, d);
-    d = mfma16x16x16(a.lo, b.hi, d);
-    return d;
+// c + a b with both operands split: (hi + lo)(hi + lo) as two K = 32
+// products, [a_hi | a_lo] x [b_hi ; b_hi] + [a_hi | a_lo] x [b_lo ; b_lo]
+// (the lo*lo term is below the rounding of the rest and costs nothing).
+// cat(a0, a1) x cat(b0, b1) is a0 b0 + a1 b1 for any two pairs of 16x16x16
+// fragments: A and B map lane group g, slot s to the same k.
+__device__ __forceinline__ f4 mm4(const h4& ahi, const h4& alo, const h4& bhi, const h4& blo, f4 c) {
+    const h8 a = cat(ahi, alo);
+    c = mfma16x16x32(a, cat(bhi, bhi), c);
+    return mfma16x16x32(a, cat(blo, blo), c);
+}
+__device__ __forceinline__ f4 mm4(const Split4& a, const Split4& b, f4 c = f4{0.f, 0.f, 0.f, 0.f}) {
+    return mm4(a.hi, a.lo, b.hi, b.lo, c);
 }
 
 // Accumulator-layout state tiles: S[t][j] = state[16t + 4lg + j][col]; `off`
@@ -294,52 +296,54 @@ __device__ __forceinline__ void store_state(const f4 (&S)[KT], void* p, int dtyp
     else store_state_t<KT>(S, static_cast<bf16_t*>(p), off, V);
 }
 
+// Level of the pair (row c, column i) of a diagonal block: 0 on the diagonal,
+// 1 + the highest differing bit below it, -1 above.
+__device__ __forceinline__ int pair_level(int c, int i) {
+    if (c == i) return 0;
+    if (c < i) return -1;
+    return 32 - __builtin_clz(static_cast<unsigned>(c ^ i));
+}
+
 template <int K, int NC, typename TQ>
 struct Kern {
     static constexpr int KT = K / 16;                   // 16-row state tiles
     static constexpr int KU = K / 32;                   // 32-wide k blocks
-    static constexpr int PW = kPW<K>;                   // producer waves per block
-    static constexpr int KW = K / PW;                   // channels per producer wave
-    static constexpr int KUW = KW / 32;                 // 32-wide k blocks per producer wave
-    static constexpr int CH = 1;                        // channels per producer lane
+    static constexpr int CH = K / 32;                   // channels per producer lane
+    static constexpr int KR = K + 8;                    // padded row of a row-major operand
     static constexpr int VT = 16 * NC;
-    using QR = QRow<TQ, CH>;                            // producer rows of q / k
-    using VR = QRow<TQ, 1>;                             // consumer elements of v
-    static constexpr int QW = QR::W;
+    static constexpr int QB = CH * static_cast<int>(sizeof(TQ));   // bytes of a lane's q / k row
+    static constexpr int QW = BLoad<QB>::W;
+    static constexpr int GW = BLoad<4 * CH>::W;
 
-    // One block's raw inputs for a producer lane: channels chan(0..CH-1),
-    // rows 0..15, and beta of rows 4lg..4lg+3.
+    // One block's raw inputs for a producer lane: its CH channels of rows
+    // 8hf .. 8hf + 7, and beta of rows 4lg .. 4lg + 3 (for the solve).
     struct Raw {
-        uint32_t q[BT][QW], k[BT][QW];
-        uint32_t g[BT][CH];
+        uint32_t q[HR][QW], k[HR][QW], g[HR][GW];
         uint32_t beta[4];
     };
-    // The same block, converted: decays, fp16 q and k (rows 0-7 / 8-15), beta.
+    // The same block, converted: decays, fp16 q and k rows (channels in the
+    // low CH slots), beta.
     struct Work {
-        float al[CH][BT];
-        h8 qh[CH][2], kh[CH][2];
+        float al[CH][HR];
+        h4 q[HR], k[HR];
         float beta[4];
     };
 
     const kda_fwd_args& a;
     Smem<K>& sm;
     int64_t b, h, T;
-    int nch;
     float scale;
     int lane, ln, lg;
-    int hh;                                  // producer: channel part (0 .. PW-1)
+    int hf, cq;                              // producer: row half, channel group (channels CH*cq ..)
     uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;   // token-row strides in bytes
-    uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets (v, beta: from row 4lg)
+    uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets
 
     __device__ Kern(const kda_fwd_args& args, Smem<K>& s) : a(args), sm(s) {}
 
-    // Channel c of this producer lane (lanes 32-63 repeat lanes 0-31 when K = 32).
-    __device__ int chan(int c) const { return hh * KW + CH * (KW < 64 ? (lane % KW) : lane) + c; }
-
-    // Rows of block `blk` that lie before T (1..BT).
+    // Rows of block `blk` that lie before T (0..BT).
     __device__ int rows_in(int blk) const {
         const int64_t left = T - static_cast<int64_t>(blk) * BT;
-        return left < BT ? static_cast<int>(left) : BT;
+        return left <= 0 ? 0 : (left < BT ? static_cast<int>(left) : BT);
     }
 
     // Descriptor over the rows of one block of a [B, T, H, D] view (elements
@@ -351,27 +355,20 @@ struct Kern {
     }
 
     // ------------------------------------------------------------ producers
-    // Loads of rows [R0, R1) of one block (and beta with the last rows).
-    // The loads of the next block are issued in four parts between the
-    // levels of the current one, so they never queue up in one burst.
-    template <int R0, int R1>
-    __device__ void load_rows(Raw& r, int blk) const {
+    __device__ void load_raw(Raw& r, int blk) const {
         const auto rq = block_rsrc(a.q, a.q_stride, sizeof(TQ), rs_q, blk);
         const auto rk = block_rsrc(a.k, a.k_stride, sizeof(TQ), rs_k, blk);
         const auto rg = block_rsrc(a.g, a.g_stride, 4, rs_g, blk);
+        const auto rb = block_rsrc(a.beta, a.beta_stride, 4, rs_b, blk);
 #pragma unroll
-        for (int i = R0; i < R1; ++i) {
+        for (int i = 0; i < HR; ++i) {
             BLoad<4 * CH>::ld(r.g[i], rg, vo_g, i * rs_g);
-            BLoad<QR::BYTES>::ld(r.q[i], rq, vo_q, i * rs_q);
-            BLoad<QR::BYTES>::ld(r.k[i], rk, vo_k, i * rs_k);
+            BLoad<QB>::ld(r.q[i], rq, vo_q, i * rs_q);
+            BLoad<QB>::ld(r.k[i], rk, vo_k, i * rs_k);
         }
-        if constexpr (R1 == BT) {
-            const auto rb = block_rsrc(a.beta, a.beta_stride, 4, rs_b, blk);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) BLoad<4>::ld(&r.beta[j], rb, vo_b, j * rs_b);
-        }
+        for (int j = 0; j < 4; ++j) BLoad<4>::ld(&r.beta[j], rb, vo_b, j * rs_b);
     }
-    __device__ void load_raw(Raw& r, int blk) const { load_rows<0, BT>(r, blk); }
 
     __device__ void unpack(Raw& r, Work& w) const {
         use_here(r.q);
@@ -379,31 +376,69 @@ struct Kern {
         use_here(r.g);
         use_here(r.beta);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
+        for (int i = 0; i < HR; ++i) {
 #pragma unroll
-            for (int i = 0; i < BT; ++i) w.al[c][i] = fast_exp(__uint_as_float(r.g[i][c]));
+            for (int c = 0; c < CH; ++c) w.al[c][i] = fast_exp(__uint_as_float(r.g[i][c]));
+            h4 qv = {0, 0, 0, 0}, kv = {0, 0, 0, 0};
 #pragma unroll
-            for (int p = 0; p < BT / 2; ++p) {
-                const h2 qp = QR::pair(r.q[2 * p], r.q[2 * p + 1], c);
-                const h2 kp = QR::pair(r.k[2 * p], r.k[2 * p + 1], c);
-                w.qh[c][p / 4][2 * (p % 4)] = qp[0];
-                w.qh[c][p / 4][2 * (p % 4) + 1] = qp[1];
-                w.kh[c][p / 4][2 * (p % 4)] = kp[0];
-                w.kh[c][p / 4][2 * (p % 4) + 1] = kp[1];
+            for (int c = 0; c < CH; ++c) {
+                qv[c] = raw_h<TQ>(r.q[i], c);
+                kv[c] = raw_h<TQ>(r.k[i], c);
             }
+            w.q[i] = qv;
+            w.k[i] = kv;
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) w.beta[j] = __uint_as_float(r.beta[j]);
     }
 
-    // Level factors F_b(r), r = 0..15, of one channel: in each aligned group of
-    // 2^(b+1) rows, upper-half rows c get prod_{t=ref+1..c} a_t and lower-half
-    // rows i get prod_{t=i+1..ref} a_t, ref = the group's last lower row.
+    // Row r of per-channel values x[c][r], rounded to fp16, as a row vector
+    // (channels in the low CH slots).
+    static __device__ __forceinline__ h4 rowvec(const float (&x)[CH][HR], int r) {
+        h4 v = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = static_cast<_Float16>(x[c][r]);
+        return v;
+    }
+
+    // One row of a row-major operand: this lane's CH channels.
+    __device__ void put_row(_Float16* m, int row, const h4& v) const {
+        _Float16* p = m + row * KR + chan_pos(CH * cq);
+        if constexpr (CH == 4) {
+            *reinterpret_cast<h4*>(p) = v;
+        } else if constexpr (CH == 2) {
+            *reinterpret_cast<h2*>(p) = h2{v[0], v[1]};
+        } else {
+            *p = v[0];
+        }
+    }
+    // Rows 4part .. 4part + 3 of this lane's half of block bi into the
+    // k-major lines of its channels (one 8-byte piece per channel).
+    __device__ void put_kmajor(_Float16 (*kh)[2 * BT], int bi, int part, const h4 (&v)[4]) const {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int ch = CH * cq + c;
+            const h4 piece = {v[0][c], v[1][c], v[2][c], v[3][c]};
+            *reinterpret_cast<h4*>(&kh[ch][8 * ((2 * hf + part) ^ kh_swz(ch)) + 4 * bi]) = piece;
+        }
+    }
+    // Row r of x[c][r] * m[c], rounded to fp16, as a row vector.
+    static __device__ __forceinline__ h4 rowvec(const float (&x)[CH][HR], const float (&m)[CH], int r) {
+        h4 v = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = static_cast<_Float16>(x[c][r] * m[c]);
+        return v;
+    }
+
+    // Level factors of the half's 8 rows, level B in 0..2 (groups of 2^(B+1)
+    // rows inside the half): upper-half rows c get prod_{t=ref+1..c} a_t and
+    // lower-half rows i get prod_{t=i+1..ref} a_t, ref = the group's last
+    // lower row.
     template <int B>
-    static __device__ __forceinline__ void level_factors(const float (&al)[BT], float (&f)[BT]) {
+    static __device__ __forceinline__ void level_factors(const float (&al)[HR], float (&f)[HR]) {
         constexpr int S = 2 << B, HALF = 1 << B;
 #pragma unroll
-        for (int st = 0; st < BT; st += S) {
+        for (int st = 0; st < HR; st += S) {
             float run = al[st + HALF];
             f[st + HALF] = run;
 #pragma unroll
@@ -421,64 +456,63 @@ struct Kern {
         }
     }
 
-    // Operand level LEV of a block (this wave's channels): X_b = k * F_b and
-    // Y_b = q * F_b, stored k-major into a staging pair (xs, ys) whose row 0
-    // is this wave's first channel.
+    // Operand level LEV of a block: X_b = k * F_b and Y_b = q * F_b, written
+    // row-major into xs / ys.  Y_b is only read in rows that are the later
+    // row of a level-b pair; its other rows keep q.  Level 4 pairs the two
+    // halves: its factors are the decays from the upper half's start (pl)
+    // and to the lower half's end (sl).
     template <int LEV>
-    __device__ void stage(const Work& w, _Float16* xs, _Float16* ys) const {
+    __device__ void stage(const Work& w, const float (&pl)[CH][HR], const float (&sl)[CH][HR], _Float16* xs,
+                          _Float16* ys) const {
+        float f[CH][HR];
+        if constexpr (LEV >= 1 && LEV <= 3) {
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            h8 x0 = w.kh[c][0], x1 = w.kh[c][1], y0 = w.qh[c][0], y1 = w.qh[c][1];
+            for (int c = 0; c < CH; ++c) level_factors<LEV - 1>(w.al[c], f[c]);
+        } else if constexpr (LEV == 4) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int r = 0; r < HR; ++r) f[c][r] = hf ? pl[c][r] : sl[c][r];
+        }
+#pragma unroll
+        for (int r = 0; r < HR; ++r) {
+            h4 x = w.k[r], y = w.q[r];
             if constexpr (LEV > 0) {
-                float f[BT];
-                level_factors<LEV - 1>(w.al[c], f);
-                h8 f0, f1;
-                to_h16(f, f0, f1);
-                x0 *= f0;
-                x1 *= f1;
-                y0 *= f0;
-                y1 *= f1;
+                const h4 fr = rowvec(f, r);
+                x *= fr;
+                if (LEV == 4 || ((r >> (LEV - 1)) & 1)) y *= fr;
             }
-            const int lc = chan(c) - hh * KW;
-            store_kmajor(xs, lc, x0, x1);
-            store_kmajor(ys, lc, y0, y1);
+            put_row(xs, HR * hf + r, x);
+            put_row(ys, HR * hf + r, y);
         }
     }
 
-    // Level LEV's products from its staging pair: L_b = X_b X_b^T and
-    // A_b = Y_b X_b^T over this wave's channels, keeping the level's pairs
-    // (accumulator layout: row 4lg + j, column ln).
+    // Level LEV's products: G_b = X_b X_b^T and A_b = Y_b X_b^T over all K
+    // channels, keeping the level's pairs (accumulator layout: row 4lg + j,
+    // column ln).
     template <int LEV>
-    __device__ void product(const Work& w, const _Float16* xs, const _Float16* ys, f4& Lacc, f4& Aacc) const {
-        f4 accL = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
+    __device__ void product(const _Float16* xs, const _Float16* ys, f4& Gacc, f4& Aacc) const {
+        f4 accG = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < KUW; ++u) {
-            const h8 xf = frag32_tr(xs, lg, ln, u);
-            const h8 yf = frag32_tr(ys, lg, ln, u);
-            if constexpr (LEV > 0) accL = mfma16x16x32(xf, xf, accL);
+        for (int u = 0; u < KU; ++u) {
+            const h8 xf = *reinterpret_cast<const h8*>(xs + ln * KR + 32 * u + 8 * lg);
+            const h8 yf = *reinterpret_cast<const h8*>(ys + ln * KR + 32 * u + 8 * lg);
+            if constexpr (LEV > 0) accG = mfma16x16x32(xf, xf, accG);
             accA = mfma16x16x32(yf, xf, accA);
         }
-        const int i = ln;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int c = 4 * lg + j;
-            if constexpr (LEV == 0) {
-                if (i == c) Aacc[j] = accA[j];
-            } else {
-                constexpr int bb = LEV - 1;
-                const bool pair = ((c >> (bb + 1)) == (i >> (bb + 1))) && ((c >> bb) & 1) && !((i >> bb) & 1);
-                if (pair) {
-                    Lacc[j] = w.beta[j] * accL[j];
-                    Aacc[j] = accA[j];
-                }
+            if (pair_level(4 * lg + j, ln) == LEV) {
+                if constexpr (LEV > 0) Gacc[j] = accG[j];
+                Aacc[j] = accA[j];
             }
         }
     }
 
-    // M = (I + L)^-1 Diag(beta) of one block (producer p), stored as hi/lo
-    // A-operand fragments.
-    __device__ void solve(const f4& Lc, const float (&beta)[4], Slot<K>& sl, int p) const {
-        float* lt = &sm.XCH[p][0][0][0];
+    // M = (I + L)^-1 Diag(beta) of one block (wave p, L in accumulator
+    // layout), stored as hi/lo A-operand fragments.
+    __device__ void solve(const f4& Lc, const float (&beta)[4], _Float16 (*mh)[RP], _Float16 (*ml)[RP], int p) const {
+        float* lt = &sm.LT[p][0][0];
 #pragma unroll
         for (int j = 0; j < 4; ++j) lt[(4 * lg + j) * LP + ln] = Lc[j];
         f4 Lt;                                           // acc(L^T)
@@ -487,95 +521,166 @@ struct Kern {
             Lt[0] = r.x; Lt[1] = r.y; Lt[2] = r.z; Lt[3] = r.w;
         }
         const Split4 lc(Lc), ltt(Lt);
-        const Split4 l2(mm3(ltt, lc)), l2t(mm3(lc, ltt));  // L^2, (L^2)^T
-        const Split4 l4(mm3(l2t, l2)), l4t(mm3(l2, l2t));
-        const Split4 l8(mm3(l4t, l4));
+        const Split4 l2(mm4(ltt, lc)), l2t(mm4(lc, ltt));  // L^2, (L^2)^T
+        const Split4 l4(mm4(l2t, l2)), l4t(mm4(l2, l2t));
+        const Split4 l8(mm4(l4t, l4));
         f4 Q;                                            // acc(I - L^T)
 #pragma unroll
         for (int j = 0; j < 4; ++j) Q[j] = (4 * lg + j == ln ? 1.f : 0.f) - Lt[j];
-        Q += mm3(l2, Split4(Q));
-        Q += mm3(l4, Split4(Q));
-        Q += mm3(l8, Split4(Q));                         // acc(Minv^T) = A-layout of Minv
+        Q = mm4(l2, Split4(Q), Q);
+        Q = mm4(l4, Split4(Q), Q);
+        Q = mm4(l8, Split4(Q), Q);                       // acc(Minv^T) = A-layout of Minv
 #pragma unroll
         for (int j = 0; j < 4; ++j) Q[j] *= beta[j];
-        h4 mh, ml;
-        split4(Q, mh, ml);
-        *reinterpret_cast<h4*>(&sl.MH[ln][4 * lg]) = mh;
-        *reinterpret_cast<h4*>(&sl.ML[ln][4 * lg]) = ml;
+        h4 hi, lo;
+        split4(Q, hi, lo);
+        *reinterpret_cast<h4*>(&mh[ln][4 * lg]) = hi;
+        *reinterpret_cast<h4*>(&ml[ln][4 * lg]) = lo;
     }
 
-    // q * E, k * E, k * E15 / E and E15 of one block.
-    __device__ void escaled(const Work& w, Slot<K>& sl) const {
+    // First half of a superstep for block p (bi = p % 2 of chunk cj): the
+    // level products (the next block's loads go out after the first two),
+    // the decays of the block, and every operand that needs no other block's
+    // decay.  `keep` receives, for the second half, the decays to the block
+    // end (block 0) or from the block start (block 1).
+    __device__ void phase1(Raw& raw, Work& w, f4& Gacc, f4& Aacc, float (&keep)[CH][HR], int p,
+                           ChunkOps<K>& co, int next) const {
+        const int bi = p % CB, cj = p / CB;
+        Stage<K>& st = sm.st[cj];
+        unpack(raw, w);
+        Gacc = f4{0.f, 0.f, 0.f, 0.f};
+        Aacc = f4{0.f, 0.f, 0.f, 0.f};
+        // level operands are staged in the block's q * E / k * E rows, which
+        // get their final values after the last level
+        _Float16* xs = &co.QE[bi][0][0];
+        _Float16* ys = &co.KE[bi][0][0];
+        float pl[CH][HR], sl[CH][HR];                    // decays from the half's start / to its end
+        stage<0>(w, pl, sl, xs, ys);
+        product<0>(xs, ys, Gacc, Aacc);
+        stage<1>(w, pl, sl, xs, ys);
+        product<1>(xs, ys, Gacc, Aacc);
+        load_raw(raw, next);
+        stage<2>(w, pl, sl, xs, ys);
+        product<2>(xs, ys, Gacc, Aacc);
+        stage<3>(w, pl, sl, xs, ys);
+        product<3>(xs, ys, Gacc, Aacc);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const float (&al)[BT] = w.al[c];
-            float pre[BT], suf[BT];
-            pre[0] = al[0];
+            pl[c][0] = w.al[c][0];
 #pragma unroll
-            for (int i = 1; i < BT; ++i) pre[i] = pre[i - 1] * al[i];
-            suf[BT - 1] = 1.f;
+            for (int r = 1; r < HR; ++r) pl[c][r] = pl[c][r - 1] * w.al[c][r];
+            sl[c][HR - 1] = 1.f;
 #pragma unroll
-            for (int i = BT - 2; i >= 0; --i) suf[i] = suf[i + 1] * al[i + 1];
-            h8 e0, e1, s0, s1;
-            to_h16(pre, e0, e1);
-            to_h16(suf, s0, s1);
-            const int ch = chan(c);
-            store_kmajor(&sl.QET[0][0], ch, w.qh[c][0] * e0, w.qh[c][1] * e1);
-            store_kmajor(&sl.KET[0][0], ch, w.kh[c][0] * e0, w.kh[c][1] * e1);
-            store_kmajor(&sl.KHT[0][0], ch, w.kh[c][0] * s0, w.kh[c][1] * s1);
-            sl.elast[ch] = pre[BT - 1];
+            for (int r = HR - 2; r >= 0; --r) sl[c][r] = sl[c][r + 1] * w.al[c][r + 1];
         }
-    }
+        stage<4>(w, pl, sl, xs, ys);
+        product<4>(xs, ys, Gacc, Aacc);
 
-    // First half of a superstep: the level products of this wave's channels
-    // (partial L and A over them), with the next block's loads issued in
-    // between; the first part also writes its E-scaled operands, the second
-    // part hands its partial sums to the first.
-    __device__ void phase1(Raw& raw, Work& w, f4& Lacc, f4& Aacc, int p, Slot<K>& sl, int next) const {
-        unpack(raw, w);
-        Lacc = f4{0.f, 0.f, 0.f, 0.f};
-        Aacc = f4{0.f, 0.f, 0.f, 0.f};
-        // level operands are staged in this part's rows of the slot's QET /
-        // KET, which get their final values only after the last level
-        _Float16* xs = &sl.QET[hh * KW][0];
-        _Float16* ys = &sl.KET[hh * KW][0];
-        stage<0>(w, xs, ys);
-        product<0>(w, xs, ys, Lacc, Aacc);
-        load_rows<0, 4>(raw, next);
-        stage<1>(w, xs, ys);
-        product<1>(w, xs, ys, Lacc, Aacc);
-        load_rows<4, 8>(raw, next);
-        stage<2>(w, xs, ys);
-        product<2>(w, xs, ys, Lacc, Aacc);
-        load_rows<8, 12>(raw, next);
-        stage<3>(w, xs, ys);
-        product<3>(w, xs, ys, Lacc, Aacc);
-        load_rows<12, BT>(raw, next);
-        stage<4>(w, xs, ys);
-        product<4>(w, xs, ys, Lacc, Aacc);
-        if (hh == 0) {
-            escaled(w, sl);
+        // block decays: the upper half's prefix continues the lower half's,
+        // the lower half's suffix continues into the upper half
+        float mp[CH], ms[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            // the swap returns this lane's value in one slot and the other
+            // half's in the other
+            const unsigned u = __float_as_uint(pl[c][HR - 1]);
+            const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+            const float other = __uint_as_float(sw[0] != u ? sw[0] : sw[1]);
+            mp[c] = hf ? other : 1.f;
+            ms[c] = hf ? 1.f : other;
+            if (hf == 0) st.e15[bi][CH * cq + c] = pl[c][HR - 1] * other;
+        }
+        // rows are produced and stored one at a time (few registers live)
+        if (bi == 0) {
+            // block 0: decays from its start are decays from the chunk start
+#pragma unroll
+            for (int r = 0; r < HR; ++r) {
+                const h4 e = rowvec(pl, mp, r), f = rowvec(sl, ms, r);
+                put_row(&co.QE[0][0][0], HR * hf + r, w.q[r] * e);
+                put_row(&co.KE[0][0][0], HR * hf + r, w.k[r] * e);
+                put_row(&st.KH0[0][0], HR * hf + r, w.k[r] * f);
+#pragma unroll
+                for (int c = 0; c < CH; ++c) keep[c][r] = sl[c][r] * ms[c];
+            }
         } else {
-            *reinterpret_cast<f4*>(&sm.XCH[p][0][lane][0]) = Lacc;
-            *reinterpret_cast<f4*>(&sm.XCH[p][1][lane][0]) = Aacc;
+            // block 1: decays to its end are decays to the chunk end; its
+            // block-local q * E, k * E wait in place for G_10 and A_10
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                h4 fk[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * part + i;
+                    const h4 e = rowvec(pl, mp, r);
+                    fk[i] = w.k[r] * rowvec(sl, ms, r);
+                    put_row(&co.QE[1][0][0], HR * hf + r, w.q[r] * e);
+                    put_row(&co.KE[1][0][0], HR * hf + r, w.k[r] * e);
+#pragma unroll
+                    for (int c = 0; c < CH; ++c) keep[c][r] = pl[c][r] * mp[c];
+                }
+                put_kmajor(co.KH, 1, part, fk);
+            }
         }
     }
 
-    // Second half: the first part completes L and A, writes A and inverts
-    // (I + L); the second part writes its E-scaled operands.
-    __device__ void phase2(const Work& w, const f4& Lacc, const f4& Aacc, int p, Slot<K>& sl) const {
-        if (hh != 0) {
-            escaled(w, sl);
-            return;
-        }
-        f4 L = Lacc, A = Aacc;
-        if constexpr (PW == 2) {
-            L += *reinterpret_cast<const f4*>(&sm.XCH[p][0][lane][0]);
-            A += *reinterpret_cast<const f4*>(&sm.XCH[p][1][lane][0]);
-        }
+    // Second half: the operands that need the other block's decay (block 0:
+    // k * F; block 1: G_10 and A_10 from the block-local operands, then
+    // q * E and k * E from the chunk start, and the chunk decay), then A and
+    // the inverse of (I + L).
+    __device__ void phase2(const Work& w, const f4& Gacc, const f4& Aacc, const float (&keep)[CH][HR], int p,
+                           ChunkOps<K>& co) const {
+        const int bi = p % CB, cj = p / CB;
+        Stage<K>& st = sm.st[cj];
+        float d[CH];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sl.AM[4 * lg + j][ln] = static_cast<_Float16>(A[j] * scale);
-        solve(L, w.beta, sl, p);
+        for (int c = 0; c < CH; ++c) d[c] = st.e15[1 - bi][CH * cq + c];
+        if (bi == 0) {
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                h4 fk[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) fk[i] = w.k[4 * part + i] * rowvec(keep, d, 4 * part + i);
+                put_kmajor(co.KH, 0, part, fk);
+            }
+        } else {
+            // G_10^T and A_10^T over all K channels: the accumulator holds
+            // column ln of block 1 against rows 4lg + j of block 0, the
+            // A-operand layout of G_10 and A_10.
+            f4 accG = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < KU; ++u) {
+                const int o = ln * KR + 32 * u + 8 * lg;
+                const h8 hf0 = *reinterpret_cast<const h8*>(&st.KH0[0][0] + o);
+                accG = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o), accG);
+                accA = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o), accA);
+            }
+            h4 gh, gl;
+            split4(-accG, gh, gl);
+            *reinterpret_cast<h4*>(&co.GH[ln][4 * lg]) = gh;
+            *reinterpret_cast<h4*>(&co.GL[ln][4 * lg]) = gl;
+            const f4 as = accA * scale;
+            *reinterpret_cast<h4*>(&co.A10[ln][4 * lg]) =
+                h4{static_cast<_Float16>(as[0]), static_cast<_Float16>(as[1]), static_cast<_Float16>(as[2]),
+                   static_cast<_Float16>(as[3])};
+#pragma unroll
+            for (int r = 0; r < HR; ++r) {
+                const h4 e = rowvec(keep, d, r);
+                put_row(&co.QE[1][0][0], HR * hf + r, w.q[r] * e);
+                put_row(&co.KE[1][0][0], HR * hf + r, w.k[r] * e);
+            }
+            if (hf == 1) {
+                // row 15 of block 1 ends the chunk
+#pragma unroll
+                for (int c = 0; c < CH; ++c) co.echunk[CH * cq + c] = keep[c][HR - 1] * d[c];
+            }
+        }
+        f4 G = Gacc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(Aacc[j] * scale);
+            G[j] *= w.beta[j];
+        }
+        solve(G, w.beta, co.MH[bi], co.ML[bi], p);
     }
 
     // ------------------------------------------------------------ consumers
@@ -585,85 +690,109 @@ struct Kern {
         for (int j = 0; j < 4; ++j) BLoad<sizeof(TQ)>::ld(&vr[j], rv, vo_v, j * rs_v);
     }
 
-    // One block of the chain for this wave's 16 state columns.
-    __device__ void consume(const Slot<K>& sl, int blk, uint32_t (&vraw)[4], int next, f4 (&S)[KT],
-                            int64_t col0, uint32_t ocol) const {
-        use_here(vraw);
-        float vr[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t w1[1] = {vraw[j]};
-            vr[j] = VR::val(w1, 0);
-        }
-        v_load(vraw, next);
-        h8 shi[KU], slo[KU];
-#pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            h4 h0, l0, h1, l1;
-            split4(S[2 * u], h0, l0);
-            split4(S[2 * u + 1], h1, l1);
-            shi[u] = h8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-            slo[u] = h8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-        }
-        // Z = (k * E) S and O = (q * E) S over the K channels
-        f4 Z = {0.f, 0.f, 0.f, 0.f}, O = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            const h8 kf = frag32_tr(&sl.KET[0][0], lg, ln, u);
-            Z = mfma16x16x32(kf, shi[u], Z);
-            Z = mfma16x16x32(kf, slo[u], Z);
-            const h8 qf = frag32_tr(&sl.QET[0][0], lg, ln, u);
-            O = mfma16x16x32(qf, shi[u], O);
-            O = mfma16x16x32(qf, slo[u], O);
-        }
-        // P = U - W S = M (V - Z)
-        f4 R;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) R[j] = vr[j] - Z[j];
-        const Split4 r(R);
-        const h4 mh = frag16(&sl.MH[0][0], RP, ln, lg);
-        const h4 ml = frag16(&sl.ML[0][0], RP, ln, lg);
-        f4 P = {0.f, 0.f, 0.f, 0.f};
-        P = mfma16x16x16(mh, r.hi, P);
-        P = mfma16x16x16(mh, r.lo, P);
-        P = mfma16x16x16(ml, r.hi, P);
-        // O = scale (q * E) S + A P
-#pragma unroll
-        for (int j = 0; j < 4; ++j) O[j] *= scale;
-        h4 ph, pl;
-        split4(P, ph, pl);
-        const h4 af = frag16(&sl.AM[0][0], RP, ln, lg);
-        O = mfma16x16x16(af, ph, O);
-        O = mfma16x16x16(af, pl, O);
-        // o[b, t, h, col]: wave-uniform block base + 32-bit lane offset
+    // Output rows 4lg + j of block blk (rows past T are skipped).
+    __device__ void store_o(const f4& O, int blk, int64_t col0, uint32_t ocol) const {
         TQ* o = static_cast<TQ*>(a.o) + ((b * T + static_cast<int64_t>(blk) * BT) * a.H + h) * a.V + col0;
         const uint32_t orow = static_cast<uint32_t>(a.H * a.V);
         const int nrow = rows_in(blk);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (4 * lg + j < nrow) Elem<TQ>::st(o + (4 * lg + j) * orow + ocol, O[j]);
-        // S <- E15 S + Khat^T P
-        const int kg = lg ^ (((ln >> 3) & 1) * 2);       // KHT halves swapped on channel bit 3
+    }
+
+    // One chunk (blocks blk, blk + 1) of the chain for this wave's 16 state
+    // columns; the v loads of the same blocks one superstep later are issued
+    // into vraw0 / vraw1.
+    __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw0)[4], uint32_t (&vraw1)[4],
+                            f4 (&S)[KT], int64_t col0, uint32_t ocol) const {
+        use_here(vraw0);
+        use_here(vraw1);
+        f4 R0, R1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            R0[j] = raw_f<TQ>(vraw0[j]);
+            R1[j] = raw_f<TQ>(vraw1[j]);
+        }
+        v_load(vraw0, blk + NB);
+        v_load(vraw1, blk + 1 + NB);
+        h8 shi[KU], slo[KU];
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            h4 h0, l0, h1, l1;
+            split4(S[2 * u], h0, l0);
+            split4(S[2 * u + 1], h1, l1);
+            shi[u] = cat(h0, h1);
+            slo[u] = cat(l0, l1);
+        }
+        // Z_b = (k * E)_b S and O_b = (q * E)_b S over the K channels
+        f4 Z0 = {0.f, 0.f, 0.f, 0.f}, Z1 = Z0, O0 = Z0, O1 = Z0;
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            const int o = ln * KR + 32 * u + 8 * lg;
+            const h8 k0 = *reinterpret_cast<const h8*>(&co.KE[0][0][0] + o);
+            Z0 = mfma16x16x32(k0, shi[u], Z0);
+            Z0 = mfma16x16x32(k0, slo[u], Z0);
+            const h8 k1 = *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o);
+            Z1 = mfma16x16x32(k1, shi[u], Z1);
+            Z1 = mfma16x16x32(k1, slo[u], Z1);
+        }
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            const int o = ln * KR + 32 * u + 8 * lg;
+            const h8 q0 = *reinterpret_cast<const h8*>(&co.QE[0][0][0] + o);
+            O0 = mfma16x16x32(q0, shi[u], O0);
+            O0 = mfma16x16x32(q0, slo[u], O0);
+            const h8 q1 = *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o);
+            O1 = mfma16x16x32(q1, shi[u], O1);
+            O1 = mfma16x16x32(q1, slo[u], O1);
+        }
+        // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0)
+        R0 -= Z0;
+        R1 -= Z1;
+        const Split4 r0(R0);
+        const Split4 p0(mm4(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg), r0.hi,
+                            r0.lo, f4{0.f, 0.f, 0.f, 0.f}));
+        R1 = mm4(frag16(&co.GH[0][0], RP, ln, lg), frag16(&co.GL[0][0], RP, ln, lg), p0.hi, p0.lo, R1);
+        const Split4 r1(R1);
+        const Split4 p1(mm4(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg), r1.hi,
+                            r1.lo, f4{0.f, 0.f, 0.f, 0.f}));
+        // O = scale (q * E) S + A P
+        O0 *= scale;
+        O1 *= scale;
+        const h4 a00 = frag16(&co.AM[0][0][0], RP, ln, lg);
+        O0 = mfma16x16x32(cat(a00, a00), cat(p0.hi, p0.lo), O0);
+        const h8 a1 = cat(frag16(&co.A10[0][0], RP, ln, lg), frag16(&co.AM[1][0][0], RP, ln, lg));
+        O1 = mfma16x16x32(a1, cat(p0.hi, p1.hi), O1);
+        O1 = mfma16x16x32(a1, cat(p0.lo, p1.lo), O1);
+        store_o(O0, blk, col0, ocol);
+        store_o(O1, blk + 1, col0, ocol);
+        // S <- E[31] S + F^T P over both blocks: the k-major line of channel
+        // 16t + ln gives tokens 4lg..4lg+3 of block 0 then of block 1, the
+        // order of cat(P_0, P_1)
+        const h8 ph = cat(p0.hi, p1.hi), pl = cat(p0.lo, p1.lo);
+        const int piece = 8 * (lg ^ ((ln >> 2) & 3));
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
-            const float4 e = *reinterpret_cast<const float4*>(&sl.elast[16 * t + 4 * lg]);
+            const float4 e = *reinterpret_cast<const float4*>(&co.echunk[16 * t + 4 * lg]);
             S[t][0] *= e.x; S[t][1] *= e.y; S[t][2] *= e.z; S[t][3] *= e.w;
-            const h4 kf = frag16(&sl.KHT[16 * t][0], BT, ln, kg);
-            S[t] = mfma16x16x16(kf, ph, S[t]);
-            S[t] = mfma16x16x16(kf, pl, S[t]);
+            const h8 kf = *reinterpret_cast<const h8*>(&co.KH[16 * t + ln][piece]);
+            S[t] = mfma16x16x32(kf, ph, S[t]);
+            S[t] = mfma16x16x32(kf, pl, S[t]);
         }
     }
 };
 
-// Supersteps of NB blocks.  Before superstep s the producers have filled
-// slot set s % 2 with the blocks of superstep s; during it they fill the
-// other set with superstep s + 1 while the consumers run superstep s; one
-// workgroup barrier ends each superstep.  Every wave executes the same
-// barriers; every prefetch is issued unconditionally (block index clamped).
+// Supersteps of NB blocks (NCH chunks).  Before superstep s the producers
+// have filled slot set s % 2 with the chunks of superstep s; during it they
+// fill the other set with superstep s + 1 while the consumers run superstep
+// s; one workgroup barrier ends each half.  Every wave executes the same
+// barriers; every prefetch is issued unconditionally (a block past T loads
+// zeros).  The chunks cover T rounded up to whole chunks: a padded block
+// (all rows past T) is neutral and is built like any other.
 template <int K, int NC, typename TQ>
-__global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(const kda_fwd_args a) {
+__global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a) {
     using KN = Kern<K, NC, TQ>;
-    constexpr int KT = KN::KT, VT = KN::VT;
+    constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
     __shared__ Smem<K> sm;
     KN kn(a, sm);
@@ -680,7 +809,6 @@ __global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(cons
     kn.h = bid % H;
     kn.b = bid / H;
     kn.T = a.T;
-    kn.nch = static_cast<int>((a.T + BT - 1) / BT);
     kn.scale = a.scale;
     // wave index as a scalar: block indices and buffer descriptors derived
     // from it stay in SGPRs (no per-lane descriptor loops around the loads)
@@ -688,14 +816,14 @@ __global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(cons
     kn.lane = threadIdx.x & 63;
     kn.ln = kn.lane & 15;
     kn.lg = kn.lane >> 4;
-    const int nch = kn.nch;
-    const int nss = (nch + NB - 1) / NB;
-    const int last = nch - 1;
+    kn.hf = kn.lane >> 5;
+    kn.cq = kn.lane & 31;
+    const int nch = static_cast<int>((a.T + BT - 1) / BT);
+    const int ncc = (nch + CB - 1) / CB;                 // chunks
+    const int nblk = CB * ncc;                           // blocks, padded to whole chunks
+    const int nss = (ncc + NCH - 1) / NCH;               // supersteps
 
     const bool consumer = wave < NC;
-    // producer wave q = wave - NC builds block q / PW, channel part q % PW
-    const int pq = consumer ? 0 : wave - NC;
-    kn.hh = pq % KN::PW;
     // consumer state: S[t][j] = S[16t + 4lg + j][col], col = col0 + ocol
     const int64_t col0 = static_cast<int64_t>(vt) * VT;
     const uint32_t ocol = static_cast<uint32_t>(16 * (consumer ? wave : 0) + kn.ln);
@@ -708,10 +836,10 @@ __global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(cons
         kn.rs_v = static_cast<uint32_t>(a.v_stride[1]) * eq;
         kn.rs_g = static_cast<uint32_t>(a.g_stride[1]) * 4u;
         kn.rs_b = static_cast<uint32_t>(a.beta_stride[1]) * 4u;
-        const uint32_t c0 = static_cast<uint32_t>(kn.chan(0));
-        kn.vo_q = c0 * eq;
-        kn.vo_k = c0 * eq;
-        kn.vo_g = c0 * 4u;
+        const uint32_t c0 = static_cast<uint32_t>(CH * kn.cq), r0 = static_cast<uint32_t>(HR * kn.hf);
+        kn.vo_q = r0 * kn.rs_q + c0 * eq;
+        kn.vo_k = r0 * kn.rs_k + c0 * eq;
+        kn.vo_g = r0 * kn.rs_g + c0 * 4u;
         kn.vo_b = static_cast<uint32_t>(4 * kn.lg) * kn.rs_b;
         kn.vo_v = static_cast<uint32_t>(4 * kn.lg) * kn.rs_v + static_cast<uint32_t>(col) * eq;
     }
@@ -721,32 +849,30 @@ __global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(cons
         load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
         uint32_t vr[NB][4];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) kn.v_load(vr[j], min(j, last));
+        for (int j = 0; j < NB; ++j) kn.v_load(vr[j], j);
         for (int s = -1; s < nss; ++s) {
-            const Slot<K>* set = &sm.slot[(s & 1) * NB];
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-#pragma unroll
-                for (int j = half * (NB / 2); j < (half + 1) * (NB / 2); ++j) {
-                    const int blk = NB * s + j;
-                    if (s >= 0 && blk < nch) kn.consume(set[j], blk, vr[j], min(blk + NB, last), S, col0, ocol);
-                }
+            for (int cj = 0; cj < NCH; ++cj) {
+                const int cc = NCH * s + cj;
+                if (s >= 0 && cc < ncc)
+                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol);
                 __syncthreads();
             }
         }
         store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
     } else {
-        const int p = pq / KN::PW;
+        const int p = wave - NC;
         typename KN::Raw raw;
         typename KN::Work w;
-        f4 Lacc, Aacc;
-        kn.load_raw(raw, min(p, last));
+        f4 Gacc, Aacc;
+        float keep[CH][HR];
+        kn.load_raw(raw, p);
         for (int s = -1; s < nss; ++s) {
             const int blk = NB * (s + 1) + p;
-            Slot<K>& sl = sm.slot[((s + 1) & 1) * NB + p];
-            if (blk < nch) kn.phase1(raw, w, Lacc, Aacc, p, sl, min(blk + NB, last));
+            ChunkOps<K>& co = sm.set[(s + 1) & 1][p / CB];
+            if (blk < nblk) kn.phase1(raw, w, Gacc, Aacc, keep, p, co, blk + NB);
             __syncthreads();
-            if (blk < nch) kn.phase2(w, Lacc, Aacc, p, sl);
+            if (blk < nblk) kn.phase2(w, Gacc, Aacc, keep, p, co);
             __syncthreads();
         }
     }
@@ -755,8 +881,8 @@ __global__ __launch_bounds__(64 * (NC + NB * kPW<K>)) void chunkwise_kernel(cons
 template <int K, int NC, typename TQ>
 int launch_knq(const kda_fwd_args& a, hipStream_t stream) {
     const int64_t blocks = a.B * a.H * (a.V / (16 * NC));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(64 * (NC + NB * kPW<K>)), 0, stream, a);
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ>), dim3(static_cast<unsigned>(blocks)), dim3(64 * (NC + NB)), 0,
+                       stream, a);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
@@ -790,13 +916,13 @@ bool chunkwise_supported(int64_t K, int64_t V) {
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream) {
     // the pipeline reads gates in fp32 (the wrapper converts other dtypes)
     if (a.g_dtype != KDA_DTYPE_F32 || a.beta_dtype != KDA_DTYPE_F32) return KDA_ERR_BAD_DTYPE;
-    // in-chunk offsets are 32-bit byte offsets: 16 token strides + one row must fit
+    // in-block offsets are 32-bit byte offsets: 16 token strides + one row must fit
     const int64_t lim = int64_t(1) << 31;
     const int64_t ts[5] = {a.q_stride[1], a.k_stride[1], a.v_stride[1], a.g_stride[1], a.beta_stride[1]};
     for (int64_t st : ts)
         if (st < 0 || (BT + 1) * st * 4 + a.V * 4 >= lim) return KDA_ERR_UNSUPPORTED;
     if ((BT + 1) * a.H * a.V * 4 >= lim) return KDA_ERR_UNSUPPORTED;
-    // a chunk's buffer descriptor spans rows_in * token stride bytes, so every
+    // a block's buffer descriptor spans rows_in * token stride bytes, so every
     // token row must be disjoint from the next (stride >= row length)
     if (a.T > 1 && (a.q_stride[1] < a.K || a.k_stride[1] < a.K || a.g_stride[1] < a.K ||
                     a.v_stride[1] < a.V || a.beta_stride[1] < 1))
