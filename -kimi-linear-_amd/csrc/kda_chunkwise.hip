@@ -24,7 +24,9 @@
 //   prod_{t=i+1..c} a_t = (prod_{t=ref+1..c} a_t) * (prod_{t=i+1..ref} a_t),
 // both factors <= 1, so per level b one [16 x K] operand X_b (row r = k_r
 // times its factor) gives G_b = X_b X_b^T as a plain MFMA product, masked to
-// level b's pairs.  Level "diag" (factor 1) gives A[c, c].  Off-diagonal
+// level b's pairs.  The diagonal A[c, c] comes from the level whose
+// reference row c is (both of its factors are 1); row 15, no level's
+// reference row, is one dot product of its own.  Off-diagonal
 // block G_10, A_10: the reference row is the last row of block 0, so the
 // factors are the block-local decay of row c of block 1 from its block start
 // and of row i of block 0 to its block end.  A factor only underflows when
@@ -296,11 +298,15 @@ __device__ __forceinline__ void store_state(const f4 (&S)[KT], void* p, int dtyp
     else store_state_t<KT>(S, static_cast<bf16_t*>(p), off, V);
 }
 
-// Level of the pair (row c, column i) of a diagonal block: 0 on the diagonal,
-// 1 + the highest differing bit below it, -1 above.
+// Level whose product supplies entry (row c, column i) of a diagonal block:
+// below the diagonal 1 + the highest differing bit; on it the level whose
+// reference row c is (1 + the number of trailing ones of c: rows 0, 2, ..
+// from level 1, rows 1, 5, .. from level 2, 3 and 11 from level 3, 7 from
+// level 4, where both of row c's operands carry the factor 1); 5 for row 15,
+// which no level supplies; -1 above the diagonal.
 __device__ __forceinline__ int pair_level(int c, int i) {
-    if (c == i) return 0;
     if (c < i) return -1;
+    if (c == i) return 1 + __builtin_ctz(~static_cast<unsigned>(c));
     return 32 - __builtin_clz(static_cast<unsigned>(c ^ i));
 }
 
@@ -456,19 +462,23 @@ struct Kern {
         }
     }
 
-    // Operand level LEV of a block: X_b = k * F_b and Y_b = q * F_b, written
-    // row-major into xs / ys.  Y_b is only read in rows that are the later
-    // row of a level-b pair; its other rows keep q.  Level 4 pairs the two
-    // halves: its factors are the decays from the upper half's start (pl)
-    // and to the lower half's end (sl).
+    // Operand level LEV (1..4) of a block: X_b = k * F_b and Y_b = q * F_b,
+    // written row-major into xs / ys, b = LEV - 1.  Y_b is only read in the
+    // rows that are the later row of a level-b pair (bit b set, scaled) and
+    // in the level's reference rows (the last lower row of each group, factor
+    // 1: the diagonal of A); its other rows are not written.  Level 4 pairs
+    // the two halves: its factors are the decays from the upper half's start
+    // (pl) and to the lower half's end (sl, 1 in the reference row 7); all
+    // of its Y rows are written (a lane-dependent choice costs registers).
     template <int LEV>
     __device__ void stage(const Work& w, const float (&pl)[CH][HR], const float (&sl)[CH][HR], _Float16* xs,
                           _Float16* ys) const {
+        constexpr int bb = LEV - 1;
         float f[CH][HR];
-        if constexpr (LEV >= 1 && LEV <= 3) {
+        if constexpr (LEV <= 3) {
 #pragma unroll
-            for (int c = 0; c < CH; ++c) level_factors<LEV - 1>(w.al[c], f[c]);
-        } else if constexpr (LEV == 4) {
+            for (int c = 0; c < CH; ++c) level_factors<bb>(w.al[c], f[c]);
+        } else {
 #pragma unroll
             for (int c = 0; c < CH; ++c)
 #pragma unroll
@@ -476,34 +486,48 @@ struct Kern {
         }
 #pragma unroll
         for (int r = 0; r < HR; ++r) {
-            h4 x = w.k[r], y = w.q[r];
-            if constexpr (LEV > 0) {
-                const h4 fr = rowvec(f, r);
-                x *= fr;
-                if (LEV == 4 || ((r >> (LEV - 1)) & 1)) y *= fr;
+            const h4 fr = rowvec(f, r);
+            put_row(xs, HR * hf + r, w.k[r] * fr);
+            if constexpr (LEV <= 3) {
+                const bool upper = (r >> bb) & 1, ref = (r & ((2 << bb) - 1)) == (1 << bb) - 1;
+                if (upper) put_row(ys, HR * hf + r, w.q[r] * fr);
+                else if (ref) put_row(ys, HR * hf + r, w.q[r]);
+            } else {
+                put_row(ys, HR * hf + r, w.q[r] * fr);
             }
-            put_row(xs, HR * hf + r, x);
-            put_row(ys, HR * hf + r, y);
         }
     }
 
+    // A level's staged operands as MFMA fragments (row ln, the 8 channels of
+    // lane group lg in each 32-channel block).
+    struct Frags {
+        h8 x[KU], y[KU];
+    };
+    __device__ Frags read_frags(const _Float16* xs, const _Float16* ys) const {
+        Frags f;
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            f.x[u] = *reinterpret_cast<const h8*>(xs + ln * KR + 32 * u + 8 * lg);
+            f.y[u] = *reinterpret_cast<const h8*>(ys + ln * KR + 32 * u + 8 * lg);
+        }
+        return f;
+    }
+
     // Level LEV's products: G_b = X_b X_b^T and A_b = Y_b X_b^T over all K
-    // channels, keeping the level's pairs (accumulator layout: row 4lg + j,
-    // column ln).
+    // channels, keeping the entries the level supplies (accumulator layout:
+    // row 4lg + j, column ln).
     template <int LEV>
-    __device__ void product(const _Float16* xs, const _Float16* ys, f4& Gacc, f4& Aacc) const {
+    __device__ void product(const Frags& fr, f4& Gacc, f4& Aacc) const {
         f4 accG = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
-            const h8 xf = *reinterpret_cast<const h8*>(xs + ln * KR + 32 * u + 8 * lg);
-            const h8 yf = *reinterpret_cast<const h8*>(ys + ln * KR + 32 * u + 8 * lg);
-            if constexpr (LEV > 0) accG = mfma16x16x32(xf, xf, accG);
-            accA = mfma16x16x32(yf, xf, accA);
+            accG = mfma16x16x32(fr.x[u], fr.x[u], accG);
+            accA = mfma16x16x32(fr.y[u], fr.x[u], accA);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if (pair_level(4 * lg + j, ln) == LEV) {
-                if constexpr (LEV > 0) Gacc[j] = accG[j];
+                if (4 * lg + j != ln) Gacc[j] = accG[j];   // G (and L) is strictly lower
                 Aacc[j] = accA[j];
             }
         }
@@ -555,15 +579,19 @@ struct Kern {
         _Float16* xs = &co.QE[bi][0][0];
         _Float16* ys = &co.KE[bi][0][0];
         float pl[CH][HR], sl[CH][HR];                    // decays from the half's start / to its end
-        stage<0>(w, pl, sl, xs, ys);
-        product<0>(xs, ys, Gacc, Aacc);
+        // Levels are software-pipelined through the one staging pair: LDS
+        // serves a wave's requests in order, so level b+1's operands may be
+        // written as soon as level b's fragment reads are issued, and their
+        // VALU work covers those reads and level b's MFMAs.
         stage<1>(w, pl, sl, xs, ys);
-        product<1>(xs, ys, Gacc, Aacc);
-        load_raw(raw, next);
+        Frags fr = read_frags(xs, ys);
         stage<2>(w, pl, sl, xs, ys);
-        product<2>(xs, ys, Gacc, Aacc);
+        product<1>(fr, Gacc, Aacc);
+        load_raw(raw, next);
+        fr = read_frags(xs, ys);
         stage<3>(w, pl, sl, xs, ys);
-        product<3>(xs, ys, Gacc, Aacc);
+        product<2>(fr, Gacc, Aacc);
+        fr = read_frags(xs, ys);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             pl[c][0] = w.al[c][0];
@@ -574,7 +602,9 @@ struct Kern {
             for (int r = HR - 2; r >= 0; --r) sl[c][r] = sl[c][r + 1] * w.al[c][r + 1];
         }
         stage<4>(w, pl, sl, xs, ys);
-        product<4>(xs, ys, Gacc, Aacc);
+        product<3>(fr, Gacc, Aacc);
+        fr = read_frags(xs, ys);
+        product<4>(fr, Gacc, Aacc);
 
         // block decays: the upper half's prefix continues the lower half's,
         // the lower half's suffix continues into the upper half
@@ -674,10 +704,20 @@ struct Kern {
                 for (int c = 0; c < CH; ++c) co.echunk[CH * cq + c] = keep[c][HR - 1] * d[c];
             }
         }
+        // A[15][15] = <q_15, k_15>: row 15 is no level's reference row
+        f4 A = Aacc;
+        {
+            float dq = 0.f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+                dq += static_cast<float>(w.q[HR - 1][c]) * static_cast<float>(w.k[HR - 1][c]);
+            dq = wave_sum(hf ? dq : 0.f);
+            if (lane == 63) A[3] = dq;
+        }
         f4 G = Gacc;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(Aacc[j] * scale);
+            co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(A[j] * scale);
             G[j] *= w.beta[j];
         }
         solve(G, w.beta, co.MH[bi], co.ML[bi], p);

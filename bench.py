@@ -19,7 +19,7 @@ Also reported on the same line:
 * ``cpu_baseline``: the CPU oracle (an op-for-op restatement of the
   reference's PyTorch algorithm) on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 60] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -56,7 +56,8 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=60,
+                   help="untimed steps first; the GPU clock takes ~20 ms of load to settle")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--decode-variant", choices=["all", "fresh", "in_place", "fresh_rot5", "in_place_rot5"],
                    default="all", help="with --only decode: time one variant (for kernel traces)")
