@@ -224,26 +224,21 @@ __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, 
     return *reinterpret_cast<const h4*>(base + row * stride + 4 * lg);
 }
 
-// Two fp32 values as fp16 hi + lo, x ~= hi + lo to ~2^-22 relative: hi is x
-// rounded to fp16, x - hi is exact in fp32, and lo is x - hi rounded once.
-// The residual is one mixed-precision fma per value that reads hi as an fp16
-// operand and writes its fp16 half of lo (fma_mixlo / fma_mixhi).
-__device__ __forceinline__ void split2(float x0, float x1, h2& hi, h2& lo) {
-    hi = h2{static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
-    const uint32_t hb = __builtin_bit_cast(uint32_t, hi);
-    uint32_t lb;
-    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]\n\t"
-        "v_fma_mixhi_f16 %0, %3, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-        : "=&v"(lb)
-        : "v"(x0), "v"(hb), "v"(x1));
-    lo = __builtin_bit_cast(h2, lb);
-}
+// Four fp32 values as fp16 hi + lo, x ~= hi + lo to ~2^-21 relative: hi is x
+// truncated to fp16's 11 significant bits (exact in fp16 and in fp32), so
+// lo = x - hi is exact in fp32 and is rounded once.  Three VALU operations
+// per value, no conversion back from fp16.
 __device__ __forceinline__ void split4(const f4& x, h4& hi, h4& lo) {
-    h2 h01, h23, l01, l23;
-    split2(x[0], x[1], h01, l01);
-    split2(x[2], x[3], h23, l23);
-    hi = h4{h01[0], h01[1], h23[0], h23[1]};
-    lo = h4{l01[0], l01[1], l23[0], l23[1]};
+    float t[4], r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        t[i] = __uint_as_float(__float_as_uint(x[i]) & 0xffffe000u);
+        r[i] = x[i] - t[i];
+    }
+    hi = h4{static_cast<_Float16>(t[0]), static_cast<_Float16>(t[1]), static_cast<_Float16>(t[2]),
+            static_cast<_Float16>(t[3])};
+    lo = h4{static_cast<_Float16>(r[0]), static_cast<_Float16>(r[1]), static_cast<_Float16>(r[2]),
+            static_cast<_Float16>(r[3])};
 }
 
 // An fp32 accumulator tile split into fp16 hi + lo operands.
