@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -41,6 +41,21 @@ class KdaFwdArgs(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("clamp_fp16_out", ctypes.c_int32),
         ("chunk_size", ctypes.c_int64),
+    ]
+
+
+class KdaBwdArgs(ctypes.Structure):
+    """Mirror of ``struct kda_bwd_args`` (include/kda_hip.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int64), ("T", ctypes.c_int64), ("H", ctypes.c_int64),
+        ("K", ctypes.c_int64), ("V", ctypes.c_int64),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("g", ctypes.c_void_p), ("beta", ctypes.c_void_p), ("ckpt", ctypes.c_void_p),
+        ("d_o", ctypes.c_void_p), ("d_state_out", ctypes.c_void_p),
+        ("dq_part", ctypes.c_void_p), ("dk_part", ctypes.c_void_p), ("dg_part", ctypes.c_void_p),
+        ("dbeta_part", ctypes.c_void_p), ("dv", ctypes.c_void_p), ("d_state_in", ctypes.c_void_p),
+        ("scale", ctypes.c_float),
     ]
 
 
@@ -77,8 +92,8 @@ class KdaOutputArgs(ctypes.Structure):
     ]
 
 
-EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_prep_fwd", "kda_output_fwd",
-                    "kda_status_str", "kda_abi_version")
+EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_chunkwise_fwd_ckpt", "kda_chunkwise_bwd",
+                    "kda_prep_fwd", "kda_output_fwd", "kda_status_str", "kda_abi_version")
 
 _lib = None
 _lock = threading.Lock()
@@ -111,6 +126,10 @@ def load() -> ctypes.CDLL:
         lib.kda_chunkwise_fwd.restype = ctypes.c_int
         lib.kda_recurrent_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_void_p]
         lib.kda_recurrent_fwd.restype = ctypes.c_int
+        lib.kda_chunkwise_fwd_ckpt.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_void_p, ctypes.c_void_p]
+        lib.kda_chunkwise_fwd_ckpt.restype = ctypes.c_int
+        lib.kda_chunkwise_bwd.argtypes = [ctypes.POINTER(KdaBwdArgs), ctypes.c_void_p]
+        lib.kda_chunkwise_bwd.restype = ctypes.c_int
         lib.kda_prep_fwd.argtypes = [ctypes.POINTER(KdaPrepArgs), ctypes.c_void_p]
         lib.kda_prep_fwd.restype = ctypes.c_int
         lib.kda_output_fwd.argtypes = [ctypes.POINTER(KdaOutputArgs), ctypes.c_void_p]

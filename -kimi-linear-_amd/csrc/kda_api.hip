@@ -56,7 +56,9 @@ int kda_recurrent_fwd(const kda_fwd_args* args, void* stream) {
     return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream));
 }
 
-int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) {
+int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) { return kda_chunkwise_fwd_ckpt(args, nullptr, stream); }
+
+int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) {
     const int st = validate_common(args, false);
     if (st != KDA_OK) return st;
     if (args->chunk_size <= 0 || args->T % args->chunk_size != 0) return KDA_ERR_BAD_SHAPE;
@@ -69,7 +71,20 @@ int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) {
     }
     if (!kda::chunkwise_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
     if (args->B * args->H * args->V / 16 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
-    return kda::chunkwise_launch(*args, static_cast<hipStream_t>(stream));
+    return kda::chunkwise_launch(*args, static_cast<hipStream_t>(stream), ckpt);
+}
+
+int kda_chunkwise_bwd(const kda_bwd_args* a, void* stream) {
+    if (a == nullptr) return KDA_ERR_NULL_POINTER;
+    if (a->B < 0 || a->T < 0 || a->H < 0 || a->K <= 0 || a->V <= 0) return KDA_ERR_BAD_SHAPE;
+    if (a->B == 0 || a->H == 0) return KDA_OK;
+    if (!kda::chunkwise_bwd_supported(a->K, a->V)) return KDA_ERR_UNSUPPORTED;
+    if (a->T > 0 && (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->ckpt || !a->d_o || !a->dq_part ||
+                     !a->dk_part || !a->dg_part || !a->dbeta_part || !a->dv))
+        return KDA_ERR_NULL_POINTER;
+    if (a->B * a->H * (a->V / 32) > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    if (a->T == 0 && a->d_state_in == nullptr) return KDA_OK;
+    return kda::chunkwise_bwd_launch(*a, static_cast<hipStream_t>(stream));
 }
 
 const char* kda_status_str(int status) {

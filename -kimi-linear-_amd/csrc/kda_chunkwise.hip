@@ -830,7 +830,7 @@ struct Kern {
 // zeros).  The chunks cover T rounded up to whole chunks: a padded block
 // (all rows past T) is neutral and is built like any other.
 template <int K, int NC, typename TQ>
-__global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a) {
+__global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt) {
     using KN = Kern<K, NC, TQ>;
     constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
@@ -894,8 +894,12 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
 #pragma unroll
             for (int cj = 0; cj < NCH; ++cj) {
                 const int cc = NCH * s + cj;
-                if (s >= 0 && cc < ncc)
+                if (s >= 0 && cc < ncc) {
+                    // the state before chunk cc, for the backward
+                    if (ckpt) store_state_t<KT>(S, ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K) * V,
+                                                (4 * kn.lg) * V + col, V);
                     kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol);
+                }
                 __syncthreads();
             }
         }
@@ -919,30 +923,30 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
 }
 
 template <int K, int NC, typename TQ>
-int launch_knq(const kda_fwd_args& a, hipStream_t stream) {
+int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
     const int64_t blocks = a.B * a.H * (a.V / (16 * NC));
     hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ>), dim3(static_cast<unsigned>(blocks)), dim3(64 * (NC + NB)), 0,
-                       stream, a);
+                       stream, a, ckpt);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
 // Columns per workgroup: the widest tile (64, 32 or 16 columns) that still
 // gives at least one workgroup per CU; 16 when none does (few chains).
 template <int K, typename TQ>
-int launch_kq(const kda_fwd_args& a, hipStream_t stream) {
+int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
     constexpr int64_t kCus = 256;
     const int64_t heads = a.B * a.H;
-    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ>(a, stream);
-    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ>(a, stream);
-    return launch_knq<K, 1, TQ>(a, stream);
+    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ>(a, stream, ckpt);
+    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ>(a, stream, ckpt);
+    return launch_knq<K, 1, TQ>(a, stream, ckpt);
 }
 
 template <int K>
-int launch_k(const kda_fwd_args& a, hipStream_t stream) {
+int launch_k(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
     switch (a.qkv_dtype) {
-        case KDA_DTYPE_F16: return launch_kq<K, _Float16>(a, stream);
-        case KDA_DTYPE_BF16: return launch_kq<K, bf16_t>(a, stream);
-        case KDA_DTYPE_F32: return launch_kq<K, float>(a, stream);
+        case KDA_DTYPE_F16: return launch_kq<K, _Float16>(a, stream, ckpt);
+        case KDA_DTYPE_BF16: return launch_kq<K, bf16_t>(a, stream, ckpt);
+        case KDA_DTYPE_F32: return launch_kq<K, float>(a, stream, ckpt);
         default: return KDA_ERR_BAD_DTYPE;
     }
 }
@@ -953,7 +957,7 @@ bool chunkwise_supported(int64_t K, int64_t V) {
     return (K == 32 || K == 64 || K == 128) && V % 16 == 0;
 }
 
-int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream) {
+int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
     // the pipeline reads gates in fp32 (the wrapper converts other dtypes)
     if (a.g_dtype != KDA_DTYPE_F32 || a.beta_dtype != KDA_DTYPE_F32) return KDA_ERR_BAD_DTYPE;
     // in-block offsets are 32-bit byte offsets: 16 token strides + one row must fit
@@ -968,9 +972,9 @@ int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream) {
                     a.v_stride[1] < a.V || a.beta_stride[1] < 1))
         return KDA_ERR_UNSUPPORTED;
     switch (a.K) {
-        case 32: return launch_k<32>(a, stream);
-        case 64: return launch_k<64>(a, stream);
-        case 128: return launch_k<128>(a, stream);
+        case 32: return launch_k<32>(a, stream, ckpt);
+        case 64: return launch_k<64>(a, stream, ckpt);
+        case 128: return launch_k<128>(a, stream, ckpt);
         default: return KDA_ERR_UNSUPPORTED;
     }
 }

@@ -13,6 +13,11 @@ int recurrent_launch(const kda_fwd_args& a, hipStream_t stream);
 
 // Chunkwise forward (kda_chunkwise.hip).
 bool chunkwise_supported(int64_t K, int64_t V);
-int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream);
+// ckpt (nullable): fp32 [B, H, ceil(T/32), K, V], the state before each chunk
+int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr);
+
+// Chunkwise backward (kda_chunkwise_bwd.hip).
+bool chunkwise_bwd_supported(int64_t K, int64_t V);
+int chunkwise_bwd_launch(const kda_bwd_args& a, hipStream_t stream);
 
 }  // namespace kda

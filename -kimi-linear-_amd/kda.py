@@ -24,8 +24,12 @@ Differences that are deliberate:
 
 * HIP tensors only.  There is no CPU path and no fallback: CPU tensors, a
   missing ``libkda_hip.so`` or an unsupported head size raise.
-* Forward only: inputs that require grad under grad mode raise (the reference
-  is differentiable through autograd; a native backward is future work).
+* ``kda_chunkwise`` is differentiable: under grad mode, with any input that
+  requires grad, it runs as a ``torch.autograd.Function`` whose backward is
+  the native kernel ``kda_chunkwise_bwd`` (the reference is differentiated by
+  autograd through its torch ops).  Head dims K in {32, 64, 128} and V a
+  multiple of 32.  ``kda_recurrent`` is forward-only: inputs that require
+  grad under grad mode raise.
 
 Every call is asynchronous on the current stream, allocates only through the
 torch caching allocator and never synchronises, so it can be captured in a
@@ -84,7 +88,9 @@ def _strides3(x: torch.Tensor):
     return (ctypes.c_int64 * 3)(*x.stride()[:3])
 
 
-def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None):
+def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None, ckpt=False):
+    """Shared forward.  ``ckpt=True`` (chunkwise, inside the autograd
+    function) also returns the fp32 state before every 32-token chunk."""
     for name, x in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
         _check_tensor(name, x)
     if state is not None:
@@ -141,10 +147,12 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
 
     o = torch.empty(B, T, H, V, device=dev, dtype=out_dtype)
     s_out = state_out if state_out is not None else torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
+    ck = torch.empty(B, H, (T + CKPT_SPACING - 1) // CKPT_SPACING, K, V, device=dev,
+                     dtype=torch.float32) if ckpt else None
     if B * H == 0:
         if state is not None:
             s_out.copy_(state)
-        return o, s_out.to(s_dtype)
+        return (o, s_out.to(s_dtype), ck) if ckpt else (o, s_out.to(s_dtype))
 
     qk_dtype = out_dtype
     q = _as_kernel_input(q if q.dtype == qk_dtype else q.to(qk_dtype))
@@ -188,16 +196,85 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
     args.chunk_size = chunk_size if kind == "chunkwise" else 1
 
     lib = _native.load()
-    fn = lib.kda_chunkwise_fwd if kind == "chunkwise" else lib.kda_recurrent_fwd
     with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        status = fn(ctypes.byref(args), ctypes.c_void_p(stream))
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        if ckpt:
+            status = lib.kda_chunkwise_fwd_ckpt(ctypes.byref(args), ctypes.c_void_p(ck.data_ptr()), stream)
+        elif kind == "chunkwise":
+            status = lib.kda_chunkwise_fwd(ctypes.byref(args), stream)
+        else:
+            status = lib.kda_recurrent_fwd(ctypes.byref(args), stream)
     if status != _native.STATUS_OK:
         raise KdaError(f"kda_{kind}_fwd failed: {_native.status_str(status)} "
                        f"(B={B}, T={T}, H={H}, K={K}, V={V})")
     if kernel_s_dtype != s_dtype:
         s_out = s_out.to(s_dtype)
-    return o, s_out
+    return (o, s_out, ck) if ckpt else (o, s_out)
+
+
+CKPT_SPACING = 32   # tokens between the forward's state checkpoints (kda_chunkwise_fwd_ckpt)
+BWD_TILE = 32       # state columns per backward workgroup (partial-gradient tiles)
+
+
+def _f32c(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.float32).contiguous()
+
+
+def _chunkwise_backward(q, k, v, g, beta, ckpt, d_o, d_state, need_d_state_in):
+    """dq, dk, dv, dg, dbeta (and dS_0) in fp32 from the native backward."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dev = q.device
+    nvt = V // BWD_TILE
+    q, k, v, g, beta, d_o = (_f32c(x) for x in (q, k, v, g, beta, d_o))
+    d_state = _f32c(d_state) if d_state is not None else None
+    dq = torch.empty(nvt, B, T, H, K, device=dev, dtype=torch.float32)
+    dk = torch.empty_like(dq)
+    dg = torch.empty_like(dq)
+    dbeta = torch.empty(nvt, B, T, H, device=dev, dtype=torch.float32)
+    dv = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
+    ds0 = torch.empty(B, H, K, V, device=dev, dtype=torch.float32) if need_d_state_in else None
+    args = _native.KdaBwdArgs()
+    args.B, args.T, args.H, args.K, args.V = B, T, H, K, V
+    args.q, args.k, args.v, args.g, args.beta = (x.data_ptr() for x in (q, k, v, g, beta))
+    args.ckpt, args.d_o = ckpt.data_ptr(), d_o.data_ptr()
+    args.d_state_out = d_state.data_ptr() if d_state is not None else None
+    args.dq_part, args.dk_part, args.dg_part = dq.data_ptr(), dk.data_ptr(), dg.data_ptr()
+    args.dbeta_part, args.dv = dbeta.data_ptr(), dv.data_ptr()
+    args.d_state_in = ds0.data_ptr() if ds0 is not None else None
+    args.scale = float(K) ** -0.5
+    lib = _native.load()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        status = lib.kda_chunkwise_bwd(ctypes.byref(args), ctypes.c_void_p(stream))
+    if status != _native.STATUS_OK:
+        raise KdaError(f"kda_chunkwise_bwd failed: {_native.status_str(status)} "
+                       f"(B={B}, T={T}, H={H}, K={K}, V={V})")
+    return dq.sum(0), dk.sum(0), dv, dg.sum(0), dbeta.sum(0), ds0
+
+
+class _ChunkwiseFn(torch.autograd.Function):
+    """kda_chunkwise with the native backward (state checkpoints every 32 tokens)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, chunk_size, state_dtype):
+        o, s, ckpt = _forward("chunkwise", q, k, v, g, beta, initial_state, chunk_size, state_dtype, ckpt=True)
+        # the kernel read q and k in v's dtype and the gates in fp32: differentiate that function
+        ctx.save_for_backward(q.to(v.dtype), k.to(v.dtype), v, g.float(), beta.float(), ckpt)
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, g.dtype, beta.dtype,
+                      initial_state.dtype if initial_state is not None else None)
+        return o, s
+
+    @staticmethod
+    def backward(ctx, d_o, d_state):
+        q, k, v, g, beta, ckpt = ctx.saved_tensors
+        if d_o is None:
+            d_o = torch.zeros(v.shape, device=v.device, dtype=torch.float32)
+        need_ds0 = ctx.needs_input_grad[5]
+        dq, dk, dv, dg, dbeta, ds0 = _chunkwise_backward(q, k, v, g, beta, ckpt, d_o, d_state, need_ds0)
+        tq, tk, tv, tg, tb, ts = ctx.dtypes
+        return (dq.to(tq), dk.to(tk), dv.to(tv), dg.to(tg), dbeta.to(tb),
+                ds0.to(ts) if need_ds0 else None, None, None)
 
 
 def kda_chunkwise(q, k, v, g, beta, initial_state=None, chunk_size=64, tile_size=0,
@@ -207,6 +284,13 @@ def kda_chunkwise(q, k, v, g, beta, initial_state=None, chunk_size=64, tile_size
     Returns ``(o [B, T, H, V] in v.dtype, state [B, H, K, V] in state_dtype or v.dtype)``.
     """
     del tile_size
+    inputs = [x for x in (q, k, v, g, beta, initial_state) if isinstance(x, torch.Tensor)]
+    if torch.is_grad_enabled() and any(x.requires_grad for x in inputs):
+        K, V = q.shape[-1], v.shape[-1]
+        if K not in (32, 64, 128) or V % BWD_TILE != 0:
+            raise KdaError(f"the native chunkwise backward supports K in (32, 64, 128) and V a multiple "
+                           f"of {BWD_TILE}; got K={K}, V={V} (call under torch.no_grad() for the forward)")
+        return _ChunkwiseFn.apply(q, k, v, g, beta, initial_state, int(chunk_size), state_dtype)
     return _forward("chunkwise", q, k, v, g, beta, initial_state, int(chunk_size), state_dtype)
 
 

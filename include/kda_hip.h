@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 2
+#define KDA_ABI_VERSION 3
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -106,6 +106,45 @@ int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream);
  * it back inside its captured graph, kimi_linear/graph_decode.py:257-262).
  */
 int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Backward of the chunkwise forward.  The reference differentiates
+ * kda_chunkwise (kimi_linear/kda.py:58-185) with autograd and trains through
+ * it (scripts/train_musicgpt_fp16.py:519-523); these two calls are what a
+ * torch.autograd.Function around the HIP forward binds instead.
+ * ------------------------------------------------------------------------- */
+
+/* kda_chunkwise_fwd, plus the fp32 state before every 32-token chunk:
+ * ckpt is [B, H, ceil(T/32), K, V] contiguous fp32 (the input of
+ * kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
+int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
+
+/* Every tensor is contiguous fp32 in the forward layout: q, k, g, dq, dk, dg
+ * [B, T, H, K]; v, d_o, dv [B, T, H, V]; beta [B, T, H]; states [B, H, K, V].
+ * dq, dk, dg and dbeta are sums over the state columns: the call writes one
+ * share per 32-column tile, [V/32, B, T, H, K] (dbeta [V/32, B, T, H]), and
+ * the gradient is the sum over the first axis.  dv and d_state_in are
+ * complete.  K in {32, 64, 128}, V a multiple of 32, any T >= 0. */
+typedef struct kda_bwd_args {
+    int64_t B, T, H, K, V;
+    const float* q;                /* the forward's inputs (q unscaled)        */
+    const float* k;
+    const float* v;
+    const float* g;
+    const float* beta;
+    const float* ckpt;             /* from kda_chunkwise_fwd_ckpt on the same inputs */
+    const float* d_o;              /* dL/do                                      */
+    const float* d_state_out;      /* dL/d(final state), or NULL for zeros       */
+    float* dq_part;                /* [V/32, B, T, H, K] */
+    float* dk_part;
+    float* dg_part;
+    float* dbeta_part;             /* [V/32, B, T, H]    */
+    float* dv;                     /* [B, T, H, V]       */
+    float* d_state_in;             /* dL/d(initial state) [B, H, K, V], or NULL   */
+    float scale;                   /* the forward's q multiplier                  */
+} kda_bwd_args;
+
+int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Layer pre- and post-processing around the core (the KDA layer,

@@ -28,11 +28,17 @@ explicit matrix products in float64 numpy -- a different formulation of the
 same recurrence, used by the tests to pin the fp32 oracle together with the
 closed-form special cases in ``tests/test_oracle.py``.
 
+Both compute in fp64 instead when ``v`` is fp64: the tests differentiate them
+with autograd (in fp64) as the reference for the native backward.
+
 Pinning status (which independent checks fix each function):
 * ``kda_recurrent_ref`` -- fp64 matrix form, closed forms (beta=0 pure decay,
   alpha=1/beta=1 delta-rule write, alpha=0 reset, orthogonal keys), linearity.
 * ``kda_chunkwise_ref`` -- equality with the recurrence (a different
   algorithm), chunk-size invariance, split-T chaining, prefix invariance.
+* autograd of ``kda_chunkwise_ref`` (the backward reference) -- finite
+  differences (``torch.autograd.gradcheck`` in fp64) and equality with
+  autograd of ``kda_recurrent_ref``.
 No golden vectors ship with the reference for this path (it has no tests), so
 no reference-held vector pins either function; see ``tests/test_oracle.py``.
 """
@@ -45,9 +51,15 @@ import torch
 FP16_MAX_SAFE = 60000.0     # kimi_linear/fp16.py:97
 
 
-def _blocks(x: torch.Tensor, B: int, NT: int, C: int, H: int) -> torch.Tensor:
+def _compute_dtype(x: torch.Tensor) -> torch.dtype:
+    """fp32, as the reference computes; fp64 when the caller passes fp64 (the
+    tests differentiate the oracle in fp64 to check the native backward)."""
+    return torch.float64 if x.dtype == torch.float64 else torch.float32
+
+
+def _blocks(x: torch.Tensor, B: int, NT: int, C: int, H: int, cd=torch.float32) -> torch.Tensor:
     """[B, T, H, D] -> [B, H, NT, C, D] in fp32 (kda.py:123-127)."""
-    return x.float().reshape(B, NT, C, H, x.shape[-1]).permute(0, 3, 1, 2, 4)
+    return x.to(cd).reshape(B, NT, C, H, x.shape[-1]).permute(0, 3, 1, 2, 4)
 
 
 def kda_chunkwise_ref(q, k, v, g, beta, initial_state=None, chunk_size=64,
@@ -65,20 +77,21 @@ def kda_chunkwise_ref(q, k, v, g, beta, initial_state=None, chunk_size=64,
         raise ValueError(f"T={T} must be a multiple of chunk_size={C}")
     NT = T // C
     out_dtype = v.dtype
+    cd = _compute_dtype(v)
 
-    Q = _blocks(q, B, NT, C, H) * (K ** -0.5)
-    Kb = _blocks(k, B, NT, C, H)
-    Vb = _blocks(v, B, NT, C, H)
-    G = _blocks(g, B, NT, C, H).cumsum(-2)          # in-chunk cumulative log decay
-    Bt = beta.float().reshape(B, NT, C, H).permute(0, 3, 1, 2)
+    Q = _blocks(q, B, NT, C, H, cd) * (K ** -0.5)
+    Kb = _blocks(k, B, NT, C, H, cd)
+    Vb = _blocks(v, B, NT, C, H, cd)
+    G = _blocks(g, B, NT, C, H, cd).cumsum(-2)      # in-chunk cumulative log decay
+    Bt = beta.to(cd).reshape(B, NT, C, H).permute(0, 3, 1, 2)
 
     if initial_state is None:
-        S = torch.zeros(B, H, K, V, dtype=torch.float32)
+        S = torch.zeros(B, H, K, V, dtype=cd)
     else:
-        S = initial_state.float().clone()
-    o = torch.empty(B, H, NT, C, V, dtype=torch.float32)
+        S = initial_state.to(cd).clone()
+    o = torch.empty(B, H, NT, C, V, dtype=cd)
 
-    eye = torch.eye(C, dtype=torch.float32)
+    eye = torch.eye(C, dtype=cd)
     keep = torch.ones(C, C, dtype=torch.bool).tril()          # i <= c
     strict = torch.ones(C, C, dtype=torch.bool).tril(-1)      # i <  c
     for n in range(NT):
@@ -113,11 +126,12 @@ def kda_recurrent_ref(q, k, v, g, beta, state=None, state_dtype=None):
     B, T, H, K = q.shape
     V = v.shape[-1]
     out_dtype = v.dtype
-    qf = q.float() * (K ** -0.5)
-    kf, vf, gf, bf = k.float(), v.float(), g.float(), beta.float()
-    S = torch.zeros(B, H, K, V, dtype=torch.float32) if state is None \
-        else state.float().clone()
-    o = torch.zeros(B, T, H, V, dtype=torch.float32)
+    cd = _compute_dtype(v)
+    qf = q.to(cd) * (K ** -0.5)
+    kf, vf, gf, bf = k.to(cd), v.to(cd), g.to(cd), beta.to(cd)
+    S = torch.zeros(B, H, K, V, dtype=cd) if state is None \
+        else state.to(cd).clone()
+    o = torch.zeros(B, T, H, V, dtype=cd)
     for t in range(T):
         S = S * gf[:, t].exp().unsqueeze(-1)                 # Diag(alpha_t) S
         kt = kf[:, t]

@@ -1,0 +1,139 @@
+"""GPU parity of the native chunkwise backward (kda_chunkwise under autograd).
+
+Reference: autograd of the oracle ``kda_chunkwise_ref`` in fp64 on the CPU
+(pinned by finite differences and by the recurrence in
+tests/test_oracle_backward.py).  The loss is <o, W_o> + <S_T, W_S> for fixed
+random weights, so every gradient path -- through the outputs, the final
+state and the initial state -- is exercised.
+
+Tolerance: relative L2 error <= 2e-3 per gradient for fp32 inputs (the
+forward's state checkpoints come from the fp16-MFMA forward kernel, relative
+error ~1e-4), 2e-2 for fp16 inputs (gradients rounded to fp16).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import kda_chunkwise_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+NAMES = ("q", "k", "v", "g", "beta", "s0")
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+@pytest.fixture(scope="module")
+def wl(kda_pkg):
+    import importlib
+    return importlib.import_module("kimi_linear_amd.workloads")
+
+
+def _case(wl, B, T, H, K, V, seed, dtype, state):
+    inp = wl.make_inputs(B, T, H, K, V, seed=seed, qkv_dtype=dtype,
+                         state_std=0.02 if state else None)
+    gen = torch.Generator().manual_seed(seed + 7)
+    wo = torch.randn(B, T, H, V, generator=gen, dtype=torch.float64)
+    ws = torch.randn(B, H, K, V, generator=gen, dtype=torch.float64)
+    return [inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"]], wo, ws
+
+
+def _ref_grads(xs, wo, ws, chunk):
+    leaves = [x.double().clone().requires_grad_(True) if x is not None else None for x in xs]
+    T = xs[0].shape[1]
+    # the oracle needs T % chunk == 0 like the reference; any chunk dividing T gives the same function
+    o, s = kda_chunkwise_ref(*leaves[:5], initial_state=leaves[5], chunk_size=chunk, state_dtype=torch.float64)
+    ((o * wo).sum() + (s * ws).sum()).backward()
+    assert T % chunk == 0
+    return [x.grad if x is not None else None for x in leaves]
+
+
+def _native_grads(pkg, xs, wo, ws, chunk):
+    leaves = [x.to(DEV).clone().requires_grad_(True) if x is not None else None for x in xs]
+    o, s = pkg.kda_chunkwise(*leaves[:5], initial_state=leaves[5], chunk_size=chunk,
+                             state_dtype=torch.float32)
+    ((o.float() * wo.to(DEV, torch.float32)).sum() + (s * ws.to(DEV, torch.float32)).sum()).backward()
+    torch.cuda.synchronize()
+    return [x.grad if x is not None else None for x in leaves]
+
+
+@pytest.mark.parametrize("B,T,H,K,V,chunk,state", [
+    (1, 64, 2, 32, 32, 32, False),
+    (2, 80, 2, 64, 64, 16, True),      # 2.5 checkpoint chunks: a ragged last chunk
+    (1, 128, 1, 128, 128, 64, True),
+    (1, 16, 3, 128, 64, 16, True),     # a single partial chunk
+])
+def test_backward_fp32(kda_pkg, wl, B, T, H, K, V, chunk, state):
+    print(f"backward fp32 B={B} T={T} H={H} K={K} V={V} chunk={chunk} state={state}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=100 + K + T, dtype=torch.float32, state=state)
+    ref = _ref_grads(xs, wo, ws, chunk)
+    got = _native_grads(kda_pkg, xs, wo, ws, chunk)
+    for name, a, r in zip(NAMES, got, ref):
+        if r is None:
+            assert a is None
+            continue
+        assert a.dtype == xs[NAMES.index(name)].dtype and a.shape == r.shape
+        err = _rel(a, r)
+        print(f"  d{name}: rel {err:.2e}", flush=True)
+        assert err <= 2e-3, (name, err)
+
+
+def test_backward_fp16(kda_pkg, wl):
+    B, T, H, K, V = 1, 96, 2, 64, 64
+    print(f"backward fp16 B={B} T={T} H={H} K={K} V={V}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=5, dtype=torch.float16, state=True)
+    ref = _ref_grads(xs, wo, ws, 32)
+    got = _native_grads(kda_pkg, xs, wo, ws, 32)
+    for name, a, r in zip(NAMES, got, ref):
+        err = _rel(a, r)
+        print(f"  d{name}: rel {err:.2e}", flush=True)
+        assert err <= 2e-2, (name, err)
+
+
+def test_backward_state_only_loss(kda_pkg, wl):
+    """Only the final state enters the loss: the output gradient is zero."""
+    xs, _, ws = _case(wl, 1, 64, 2, 64, 64, seed=9, dtype=torch.float32, state=True)
+    leaves = [x.double().clone().requires_grad_(True) for x in xs]
+    _, s = kda_chunkwise_ref(*leaves[:5], initial_state=leaves[5], chunk_size=32, state_dtype=torch.float64)
+    (s * ws).sum().backward()
+    dev = [x.to(DEV).clone().requires_grad_(True) for x in xs]
+    _, s2 = kda_pkg.kda_chunkwise(*dev[:5], initial_state=dev[5], chunk_size=32, state_dtype=torch.float32)
+    (s2 * ws.to(DEV, torch.float32)).sum().backward()
+    for name, a, r in zip(NAMES, dev, leaves):
+        if r.grad is None:
+            # q only reaches the outputs: its gradient is zero
+            assert a.grad is None or not a.grad.any(), name
+            continue
+        err = _rel(a.grad, r.grad)
+        assert err <= 2e-3, (name, err)
+
+
+def test_backward_matches_eager_chaining(kda_pkg, wl):
+    """Gradients through two chained calls (state handed over) equal one call's."""
+    xs, wo, ws = _case(wl, 1, 128, 2, 64, 64, seed=21, dtype=torch.float32, state=True)
+    one = _native_grads(kda_pkg, xs, wo, ws, 32)
+    leaves = [x.to(DEV).clone().requires_grad_(True) for x in xs]
+    q, k, v, g, beta, s0 = leaves
+    o1, s1 = kda_pkg.kda_chunkwise(q[:, :64], k[:, :64], v[:, :64], g[:, :64], beta[:, :64],
+                                   initial_state=s0, chunk_size=32, state_dtype=torch.float32)
+    o2, s2 = kda_pkg.kda_chunkwise(q[:, 64:], k[:, 64:], v[:, 64:], g[:, 64:], beta[:, 64:],
+                                   initial_state=s1, chunk_size=32, state_dtype=torch.float32)
+    o = torch.cat([o1, o2], dim=1)
+    ((o * wo.to(DEV, torch.float32)).sum() + (s2 * ws.to(DEV, torch.float32)).sum()).backward()
+    for name, a, b in zip(NAMES, [x.grad for x in leaves], one):
+        err = _rel(a, b)
+        assert err <= 1e-4, (name, err)
+
+
+def test_backward_unsupported_head_dims_raise(kda_pkg, wl):
+    inp = wl.make_inputs(1, 16, 1, 16, 32, seed=3)
+    q = inp["q"].to(DEV).requires_grad_(True)
+    with pytest.raises(kda_pkg.KdaError, match="backward supports"):
+        kda_pkg.kda_chunkwise(q, inp["k"].to(DEV), inp["v"].to(DEV), inp["g"].to(DEV), inp["beta"].to(DEV),
+                              chunk_size=16)

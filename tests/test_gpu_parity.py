@@ -326,7 +326,8 @@ def test_chunkwise_graph_replays(kda_pkg, wl):
 
 
 def test_grad_inputs_rejected(kda_pkg, wl):
+    """The recurrence is forward-only (the chunkwise kernel has a native backward)."""
     inp = to_dev(wl.make_inputs(1, 16, 1, 64, 64, seed=11, qkv_dtype=torch.float32))
     q = inp["q"].clone().requires_grad_(True)
     with pytest.raises(kda_pkg.KdaError, match="forward-only"):
-        kda_pkg.kda_chunkwise(q, inp["k"], inp["v"], inp["g"], inp["beta"], chunk_size=16)
+        kda_pkg.kda_recurrent(q, inp["k"], inp["v"], inp["g"], inp["beta"])
