@@ -25,9 +25,10 @@
 // and the pairwise-decay products of dA and dL give dq~, dk and dG, which
 // the reverse in-chunk cumulative sum turns into dg.
 //
-// Work decomposition: one workgroup of 256 threads per (b, h, VT = 32 state
-// columns); the chunk's q, k, G, E, the state tile S, the gradient tile dS and
-// every CT x CT matrix live in LDS.  dq, dk, dg and dbeta are sums over the
+// Work decomposition: one workgroup of 1024 threads (four waves per SIMD, to
+// overlap the LDS latency of the loops) per (b, h, VT = 32 state columns);
+// the chunk's q, k, G, E, the state tile S, the gradient tile dS and every
+// CT x CT matrix live in LDS.  dq, dk, dg and dbeta are sums over the
 // state columns, so each workgroup writes its column tile's share to a
 // partial buffer (the caller adds the V / VT shares); dv and dS_0 are exact
 // per tile.  Rows past T read as zero inputs, which leave the state and
@@ -41,34 +42,39 @@ namespace {
 
 constexpr int CT = 32;          // tokens per chunk = the forward's checkpoint spacing
 constexpr int VT = 32;          // state columns per workgroup
-constexpr int NT = 256;         // threads per workgroup
+constexpr int NT = 1024;        // threads per workgroup: one per CT x VT and CT x CT entry
+static_assert(CT * VT == NT && CT * CT == NT, "one output per thread for the chunk-sized products");
 
+// Rows padded to a multiple of 4 floats plus 4: 16-byte vector reads along a
+// row, and consecutive rows 4 banks apart.
 template <int K>
-struct BwdSmem {
-    float q[CT][K + 1];         // scale * q
-    float k[CT][K + 1];
-    float gc[CT][K + 1];        // in-chunk cumulative log decay G
-    float e[CT][K + 1];         // exp(G); then, per element, dG
-    float S[K][VT + 1];         // state at the chunk start (checkpoint)
-    float dS[K][VT + 1];        // gradient of the state at the chunk end, then at its start
-    float v[CT][VT + 1];
-    float dO[CT][VT + 1];
-    float R[CT][VT + 1];
-    float P[CT][VT + 1];
-    float dP[CT][VT + 1];
-    float dR[CT][VT + 1];
+struct __align__(16) BwdSmem {
+    static constexpr int KP = K + 4, VP = VT + 4;
+    float q[CT][KP];            // scale * q
+    float k[CT][KP];
+    float gc[CT][KP];           // in-chunk cumulative log decay G
+    float e[CT][KP];            // exp(G); then, per element, dG
+    float S[K][VP];             // state at the chunk start (checkpoint)
+    float dS[K][VP];            // gradient of the state at the chunk end, then at its start
+    float v[CT][VP];
+    float dO[CT][VP];
+    float R[CT][VP];
+    float P[CT][VP];
+    float dP[CT][VP];
+    float dR[CT][VP];
     float A[CT][CT + 1];        // A (i <= c)
     float L[CT][CT + 1];        // L (i < c)
     float N[CT][CT + 1];        // (I + Diag(beta) L)^-1
     float dA[CT][CT + 1];       // dA (i <= c)
-    float dM[CT][CT + 1];       // dM, then dN
-    float Y[CT][CT + 1];        // dN N^T, then dX
+    float dM[CT][CT + 1];       // dM, then dN, then dX
+    float Y[CT][CT + 1];        // dN N^T; then, per thread, its rows' share of
+                                // sum_c d(k*F)[c] k[c] F[c] (NT floats)
     float beta[CT];
     float dbeta[CT];
     float eps[K];               // exp(G_last)
     float deps[K];              // rowsum(dS * S)
-    float last[NT / K][K];      // per thread: its rows' share of sum_c d(k*F)[c] k[c] F[c]
 };
+static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
 
 template <int K>
 __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a) {
@@ -91,9 +97,10 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
     const int kk = t % K;
     const int r0 = t / K;
     constexpr int RSTEP = NT / K;
-    // state-tile element j: row t / (VT / SPT) ... as (k row, v column)
-    auto st_row = [&](int j) { return (t + NT * j) / VT; };
-    auto st_col = [&](int j) { return (t + NT * j) % VT; };
+    // state-tile elements of this thread: SPT adjacent columns of one row
+    constexpr int TPR = VT / SPT;           // threads per state row
+    auto st_row = [&](int j) { return t / TPR + 0 * j; };
+    auto st_col = [&](int j) { return SPT * (t % TPR) + j; };
 
     // dS <- dL/dS_T
     for (int j = 0; j < SPT; ++j) {
@@ -152,15 +159,26 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
         }
         __syncthreads();
 
+        // Entry (pc, pv) of the CT x VT products and (pc, pv) = (c, i) of the
+        // CT x CT ones: thread t.
+        const int pc = t / VT, pv = t % VT;
+
         // ----------------------------------------------------------- A and L
-        for (int j = 0; j < CT * CT / NT; ++j) {
-            const int e = t + NT * j, c = e / CT, i = e % CT;
+        {
+            const int c = pc, i = pv;
             float av = 0.f, lv = 0.f;
             if (i <= c) {
-                for (int x = 0; x < K; ++x) {
-                    const float d = __expf(sm.gc[c][x] - sm.gc[i][x]) * sm.k[i][x];
-                    av += sm.q[c][x] * d;
-                    lv += sm.k[c][x] * d;
+#pragma unroll 2
+                for (int x = 0; x < K; x += 4) {
+                    const float4 gcv = *reinterpret_cast<const float4*>(&sm.gc[c][x]);
+                    const float4 giv = *reinterpret_cast<const float4*>(&sm.gc[i][x]);
+                    const float4 kiv = *reinterpret_cast<const float4*>(&sm.k[i][x]);
+                    const float4 qcv = *reinterpret_cast<const float4*>(&sm.q[c][x]);
+                    const float4 kcv = *reinterpret_cast<const float4*>(&sm.k[c][x]);
+                    const float d0 = __expf(gcv.x - giv.x) * kiv.x, d1 = __expf(gcv.y - giv.y) * kiv.y;
+                    const float d2 = __expf(gcv.z - giv.z) * kiv.z, d3 = __expf(gcv.w - giv.w) * kiv.w;
+                    av += qcv.x * d0 + qcv.y * d1 + qcv.z * d2 + qcv.w * d3;
+                    lv += kcv.x * d0 + kcv.y * d1 + kcv.z * d2 + kcv.w * d3;
                 }
                 if (i == c) lv = 0.f;
             }
@@ -182,67 +200,52 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
         }
         __syncthreads();
 
-        // Outputs (c, 4 columns) of the CT x VT products: thread t -> row t / 8.
-        const int pc = t / (VT / 4), pv = 4 * (t % (VT / 4));
-
         // --------------------------------------- R = V - (k*E) S, dP = (k*F) dS + A^T dO
         {
-            float rr[4], dp[4];
-            for (int u = 0; u < 4; ++u) {
-                rr[u] = sm.v[pc][pv + u];
-                dp[u] = 0.f;
+            float rr = sm.v[pc][pv], dp = 0.f;
+#pragma unroll 2
+            for (int x = 0; x < K; x += 4) {
+                const float4 kx = *reinterpret_cast<const float4*>(&sm.k[pc][x]);
+                const float4 ex = *reinterpret_cast<const float4*>(&sm.e[pc][x]);
+                const float4 gl = *reinterpret_cast<const float4*>(&sm.gc[CT - 1][x]);
+                const float4 gx = *reinterpret_cast<const float4*>(&sm.gc[pc][x]);
+                rr -= kx.x * ex.x * sm.S[x][pv] + kx.y * ex.y * sm.S[x + 1][pv] + kx.z * ex.z * sm.S[x + 2][pv] +
+                      kx.w * ex.w * sm.S[x + 3][pv];
+                dp += kx.x * __expf(gl.x - gx.x) * sm.dS[x][pv] + kx.y * __expf(gl.y - gx.y) * sm.dS[x + 1][pv] +
+                      kx.z * __expf(gl.z - gx.z) * sm.dS[x + 2][pv] + kx.w * __expf(gl.w - gx.w) * sm.dS[x + 3][pv];
             }
-            for (int x = 0; x < K; ++x) {
-                const float ke = sm.k[pc][x] * sm.e[pc][x];
-                const float kf = sm.k[pc][x] * __expf(sm.gc[CT - 1][x] - sm.gc[pc][x]);
-                for (int u = 0; u < 4; ++u) {
-                    rr[u] -= ke * sm.S[x][pv + u];
-                    dp[u] += kf * sm.dS[x][pv + u];
-                }
-            }
-            for (int c2 = pc; c2 < CT; ++c2) {
-                const float w = sm.A[c2][pc];
-                for (int u = 0; u < 4; ++u) dp[u] += w * sm.dO[c2][pv + u];
-            }
-            for (int u = 0; u < 4; ++u) {
-                sm.R[pc][pv + u] = rr[u];
-                sm.dP[pc][pv + u] = dp[u];
-            }
+            for (int c2 = pc; c2 < CT; ++c2) dp += sm.A[c2][pc] * sm.dO[c2][pv];
+            sm.R[pc][pv] = rr;
+            sm.dP[pc][pv] = dp;
         }
         __syncthreads();
 
         // ------------------------------------------ P = M R, dR = M^T dP = dV
         {
-            float pp[4] = {0.f, 0.f, 0.f, 0.f}, dr[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int i = 0; i <= pc; ++i) {
-                const float w = sm.N[pc][i] * sm.beta[i];
-                for (int u = 0; u < 4; ++u) pp[u] += w * sm.R[i][pv + u];
-            }
-            for (int c2 = pc; c2 < CT; ++c2) {
-                const float w = sm.N[c2][pc];
-                for (int u = 0; u < 4; ++u) dr[u] += w * sm.dP[c2][pv + u];
-            }
+            float pp = 0.f, dr = 0.f;
+            for (int i = 0; i <= pc; ++i) pp += sm.N[pc][i] * sm.beta[i] * sm.R[i][pv];
+            for (int c2 = pc; c2 < CT; ++c2) dr += sm.N[c2][pc] * sm.dP[c2][pv];
+            dr *= sm.beta[pc];
+            sm.P[pc][pv] = pp;
+            sm.dR[pc][pv] = dr;
             const int64_t row = static_cast<int64_t>(n) * CT + pc;
-            for (int u = 0; u < 4; ++u) {
-                dr[u] *= sm.beta[pc];
-                sm.P[pc][pv + u] = pp[u];
-                sm.dR[pc][pv + u] = dr[u];
-            }
-            if (row < T) {
-                float* dv = a.dv + ((b * T + row) * H + h) * V + v0 + pv;
-                for (int u = 0; u < 4; ++u) dv[u] = dr[u];
-            }
+            if (row < T) a.dv[((b * T + row) * H + h) * V + v0 + pv] = dr;
         }
         __syncthreads();
 
         // ------------------------------------------ dA = dO P^T, dM = dP R^T
-        for (int j = 0; j < CT * CT / NT; ++j) {
-            const int e = t + NT * j, c = e / CT, i = e % CT;
+        {
+            const int c = pc, i = pv;
             float da = 0.f, dm = 0.f;
             if (i <= c) {
-                for (int vv = 0; vv < VT; ++vv) {
-                    da += sm.dO[c][vv] * sm.P[i][vv];
-                    dm += sm.dP[c][vv] * sm.R[i][vv];
+#pragma unroll 2
+                for (int vv = 0; vv < VT; vv += 4) {
+                    const float4 a0 = *reinterpret_cast<const float4*>(&sm.dO[c][vv]);
+                    const float4 b0 = *reinterpret_cast<const float4*>(&sm.P[i][vv]);
+                    const float4 a1 = *reinterpret_cast<const float4*>(&sm.dP[c][vv]);
+                    const float4 b1 = *reinterpret_cast<const float4*>(&sm.R[i][vv]);
+                    da += a0.x * b0.x + a0.y * b0.y + a0.z * b0.z + a0.w * b0.w;
+                    dm += a1.x * b1.x + a1.y * b1.y + a1.z * b1.z + a1.w * b1.w;
                 }
             }
             sm.dA[c][i] = da;
@@ -257,23 +260,19 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
             sm.dbeta[t] = s;
         }
         __syncthreads();
-        for (int j = 0; j < CT * CT / NT; ++j) {
-            const int e = t + NT * j, c = e / CT, i = e % CT;
-            sm.dM[c][i] *= sm.beta[i];
-        }
+        sm.dM[pc][pv] *= sm.beta[pv];
         __syncthreads();
         // Y = dN N^T (lower: Y[c,i] = sum_{m <= min(c,i)} dN[c,m] N[i,m])
-        for (int j = 0; j < CT * CT / NT; ++j) {
-            const int e = t + NT * j, c = e / CT, i = e % CT;
-            const int mmax = c < i ? c : i;
+        {
+            const int c = pc, i = pv, mmax = c < i ? c : i;
             float s = 0.f;
             for (int m = 0; m <= mmax; ++m) s += sm.dM[c][m] * sm.N[i][m];
             sm.Y[c][i] = s;
         }
         __syncthreads();
         // dX[c,i] = -sum_{m >= c} N[m,c] Y[m,i] for i < c (kept in dM)
-        for (int j = 0; j < CT * CT / NT; ++j) {
-            const int e = t + NT * j, c = e / CT, i = e % CT;
+        {
+            const int c = pc, i = pv;
             float s = 0.f;
             if (i < c)
                 for (int m = c; m < CT; ++m) s += sm.N[m][c] * sm.Y[m][i];
@@ -293,52 +292,59 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
 
         // ------------------- dS_start = Diag(eps) dS + (q~*E)^T dO - (k*E)^T dR
         float dsn[SPT];
-        for (int j = 0; j < SPT; ++j) {
-            const int r = st_row(j), c = st_col(j);
-            float s = sm.eps[r] * sm.dS[r][c];
-            for (int c2 = 0; c2 < CT; ++c2)
-                s += sm.e[c2][r] * (sm.q[c2][r] * sm.dO[c2][c] - sm.k[c2][r] * sm.dR[c2][c]);
-            dsn[j] = s;
+        {
+            const int r = st_row(0), c0 = st_col(0);
+            for (int j = 0; j < SPT; ++j) dsn[j] = sm.eps[r] * sm.dS[r][c0 + j];
+#pragma unroll 4
+            for (int c2 = 0; c2 < CT; ++c2) {
+                const float qe = sm.e[c2][r] * sm.q[c2][r], ke = sm.e[c2][r] * sm.k[c2][r];
+                for (int j = 0; j < SPT; ++j) dsn[j] += qe * sm.dO[c2][c0 + j] - ke * sm.dR[c2][c0 + j];
+            }
         }
         __syncthreads();
 
         // ---------------------------- per (row, channel): dq, dk and dG
         {
-            float gcol[CT], kcol[CT], qcol[CT];
-            for (int c = 0; c < CT; ++c) {
-                gcol[c] = sm.gc[c][kk];
-                kcol[c] = sm.k[c][kk];
-                qcol[c] = sm.q[c][kk];
-            }
+            // column kk of G, k and q~ (each thread keeps its channel)
+            auto gcol = [&](int c) { return sm.gc[c][kk]; };
+            auto kcol = [&](int c) { return sm.k[c][kk]; };
+            auto qcol = [&](int c) { return sm.q[c][kk]; };
             float last = 0.f;
+#pragma unroll 1
             for (int j = 0; j < EPT; ++j) {
                 const int c = r0 + RSTEP * j;
                 float dqe = 0.f, dke = 0.f, dkf = 0.f;
-                for (int vv = 0; vv < VT; ++vv) {
-                    const float s = sm.S[kk][vv];
-                    dqe += sm.dO[c][vv] * s;
-                    dke -= sm.dR[c][vv] * s;
-                    dkf += sm.P[c][vv] * sm.dS[kk][vv];
+#pragma unroll 2
+                for (int vv = 0; vv < VT; vv += 4) {
+                    const float4 s4 = *reinterpret_cast<const float4*>(&sm.S[kk][vv]);
+                    const float4 d4 = *reinterpret_cast<const float4*>(&sm.dS[kk][vv]);
+                    const float4 o4 = *reinterpret_cast<const float4*>(&sm.dO[c][vv]);
+                    const float4 r4 = *reinterpret_cast<const float4*>(&sm.dR[c][vv]);
+                    const float4 p4 = *reinterpret_cast<const float4*>(&sm.P[c][vv]);
+                    dqe += o4.x * s4.x + o4.y * s4.y + o4.z * s4.z + o4.w * s4.w;
+                    dke -= r4.x * s4.x + r4.y * s4.y + r4.z * s4.z + r4.w * s4.w;
+                    dkf += p4.x * d4.x + p4.y * d4.y + p4.z * d4.z + p4.w * d4.w;
                 }
                 float t1 = 0.f, t2 = 0.f, t3 = 0.f, t4 = 0.f;
                 const float bc = sm.beta[c];
+                const float gcc = gcol(c);
                 for (int i = 0; i <= c; ++i) {
-                    const float d = __expf(gcol[c] - gcol[i]) * kcol[i];
+                    const float d = __expf(gcc - gcol(i)) * kcol(i);
                     t1 += sm.dA[c][i] * d;
                     if (i < c) t3 += bc * sm.dM[c][i] * d;
                 }
                 for (int c2 = c; c2 < CT; ++c2) {
-                    const float d = __expf(gcol[c2] - gcol[c]);
-                    t2 += sm.dA[c2][c] * qcol[c2] * d;
-                    if (c2 > c) t4 += sm.beta[c2] * sm.dM[c2][c] * kcol[c2] * d;
+                    const float d = __expf(gcol(c2) - gcc);
+                    t2 += sm.dA[c2][c] * qcol(c2) * d;
+                    if (c2 > c) t4 += sm.beta[c2] * sm.dM[c2][c] * kcol(c2) * d;
                 }
                 const float E = sm.e[c][kk];
-                const float F = __expf(gcol[CT - 1] - gcol[c]);
+                const float F = __expf(gcol(CT - 1) - gcc);
                 const float dqt = t1 + dqe * E;
                 const float dk = t2 + t3 + t4 + dke * E + dkf * F;
-                const float dgv = qcol[c] * t1 + kcol[c] * (t3 - t2 - t4) + dqe * qcol[c] * E +
-                                  dke * kcol[c] * E - dkf * kcol[c] * F;
-                last += dkf * kcol[c] * F;
+                const float qc = qcol(c), kc = kcol(c);
+                const float dgv = qc * t1 + kc * (t3 - t2 - t4) + dqe * qc * E + dke * kc * E - dkf * kc * F;
+                last += dkf * kc * F;
                 sm.e[c][kk] = dgv;   // only this thread reads e[c][kk] from here on
                 const int64_t row = static_cast<int64_t>(n) * CT + c;
                 if (row < T) {
@@ -347,7 +353,7 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
                     a.dk_part[o] = dk;
                 }
             }
-            sm.last[r0][kk] = last;
+            (&sm.Y[0][0])[t] = last;
         }
         __syncthreads();
 
@@ -355,7 +361,7 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
         for (int j = 0; j < SPT; ++j) sm.dS[st_row(j)][st_col(j)] = dsn[j];
         if (t < K) {
             float run = sm.deps[t] * sm.eps[t];
-            for (int x = 0; x < NT / K; ++x) run += sm.last[x][t];
+            for (int x = 0; x < NT / K; ++x) run += (&sm.Y[0][0])[x * K + t];
             for (int c = CT - 1; c >= 0; --c) {
                 run += sm.e[c][t];
                 const int64_t row = static_cast<int64_t>(n) * CT + c;
