@@ -61,7 +61,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--decode-variant", choices=["all", "fresh", "in_place", "fresh_rot5", "in_place_rot5"],
                    default="all", help="with --only decode: time one variant (for kernel traces)")
-    p.add_argument("--only", choices=["chunkwise", "decode", "layer", "copy"], default=None,
+    p.add_argument("--only", choices=["chunkwise", "decode", "layer", "backward", "copy"], default=None,
                    help="run one workload only (for profiling); 'copy' runs a plain 1 GiB "
                         "device copy used to calibrate the HBM byte counters")
     return p.parse_args()
@@ -183,6 +183,33 @@ def layer_bench(pkg, torch, reps=10):
             "decode_B64_graph_us_per_token": decode_us}
 
 
+def backward_bench(pkg, wl, torch, reps=3):
+    """kda_chunkwise forward + native backward under autograd at the chunkwise
+    benchmark shape (fp16 q/k/v, fp32 g/beta, fp32 state from zeros)."""
+    inp = wl.make_inputs(B1, T1, H1, D1, D1, device="cuda", seed=1, qkv_dtype=torch.float16)
+    xs = [inp[n].clone().requires_grad_(True) for n in ("q", "k", "v", "g", "beta")]
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    d_o = torch.randn(B1, T1, H1, D1, device="cuda", dtype=torch.float16, generator=gen)
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    fwd = bwd = 0.0
+    for i in range(reps + 2):
+        for x in xs:
+            x.grad = None
+        e0.record()
+        o, _ = pkg.kda_chunkwise(*xs, chunk_size=C1, state_dtype=torch.float32)
+        e1.record()
+        o.backward(d_o)
+        e2.record()
+        torch.cuda.synchronize()
+        if i >= 2:
+            fwd += e0.elapsed_time(e1) / reps
+            bwd += e1.elapsed_time(e2) / reps
+    return {"workload": "kda_chunkwise forward (with 32-token state checkpoints) + native backward under "
+                        "autograd, B=8 T=4096 H=16 dk=dv=128; fp16 q/k/v, fp32 g/beta",
+            "forward_ckpt_ms": fwd, "backward_ms": bwd,
+            "train_tokens_per_s": B1 * T1 / ((fwd + bwd) * 1e-3)}
+
+
 def cpu_baselines(wl, torch, include_decode=True):
     from oracle import kda_chunkwise_ref, kda_recurrent_ref
     threads = torch.get_num_threads()
@@ -291,6 +318,11 @@ def main():
         if "value" not in result:
             result.update({"value": us_mall, "unit": "us/step", "higher_is_better": False,
                            "ms_per_step": us_mall / 1e3})
+    if args.only in (None, "backward"):
+        result["backward"] = backward_bench(pkg, wl, torch)
+        if "value" not in result:
+            result.update({"value": result["backward"]["train_tokens_per_s"], "unit": "tokens/s",
+                           "ms_per_step": result["backward"]["forward_ckpt_ms"] + result["backward"]["backward_ms"]})
     if args.only in (None, "layer"):
         result["layer"] = layer_bench(pkg, torch)
         if "value" not in result:
