@@ -189,14 +189,19 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
 
         // ------------------------------- N = (I + Diag(beta) L)^-1, by columns
         if (t < CT) {
+            // column jc in registers: the substitution only reads L (LDS,
+            // the same address in every lane) and the column itself
             const int jc = t;
-            for (int c = 0; c < jc; ++c) sm.N[c][jc] = 0.f;
-            sm.N[jc][jc] = 1.f;
-            for (int c = jc + 1; c < CT; ++c) {
+            float col[CT];
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
                 float s = 0.f;
-                for (int m = jc; m < c; ++m) s += sm.L[c][m] * sm.N[m][jc];
-                sm.N[c][jc] = -sm.beta[c] * s;
+#pragma unroll
+                for (int m = 0; m < c; ++m) s += sm.L[c][m] * col[m];
+                col[c] = c < jc ? 0.f : (c == jc ? 1.f : -sm.beta[c] * s);
             }
+#pragma unroll
+            for (int c = 0; c < CT; ++c) sm.N[c][jc] = col[c];
         }
         __syncthreads();
 
