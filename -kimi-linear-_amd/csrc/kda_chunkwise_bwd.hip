@@ -76,6 +76,17 @@ struct __align__(16) BwdSmem {
 };
 static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
 
+// D += A B for one 16 x 16 tile on the fp32 matrix cores (16x16x4 steps):
+// A(r, k) and B(k, c) give the operands; lane (ln, lg) supplies A(ln, 4u + lg)
+// and B(4u + lg, ln) and holds D[4 lg + j][ln] in slot j.
+template <int KS, typename FA, typename FB>
+__device__ __forceinline__ f4 tile_mm(FA fa, FB fb, int ln, int lg, f4 acc) {
+#pragma unroll 4
+    for (int u = 0; u < KS / 4; ++u)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa(ln, 4 * u + lg), fb(4 * u + lg, ln), acc, 0, 0, 0);
+    return acc;
+}
+
 template <int K>
 __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a) {
     static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
@@ -205,56 +216,76 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
         }
         __syncthreads();
 
+        // The products below run on the fp32 matrix cores, one 16 x 16 output
+        // tile per wave: lane (ln, lg) receives rows 4 lg + j, column ln.
+        const int w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
+
         // --------------------------------------- R = V - (k*E) S, dP = (k*F) dS + A^T dO
-        {
-            float rr = sm.v[pc][pv], dp = 0.f;
-#pragma unroll 2
-            for (int x = 0; x < K; x += 4) {
-                const float4 kx = *reinterpret_cast<const float4*>(&sm.k[pc][x]);
-                const float4 ex = *reinterpret_cast<const float4*>(&sm.e[pc][x]);
-                const float4 gl = *reinterpret_cast<const float4*>(&sm.gc[CT - 1][x]);
-                const float4 gx = *reinterpret_cast<const float4*>(&sm.gc[pc][x]);
-                rr -= kx.x * ex.x * sm.S[x][pv] + kx.y * ex.y * sm.S[x + 1][pv] + kx.z * ex.z * sm.S[x + 2][pv] +
-                      kx.w * ex.w * sm.S[x + 3][pv];
-                dp += kx.x * __expf(gl.x - gx.x) * sm.dS[x][pv] + kx.y * __expf(gl.y - gx.y) * sm.dS[x + 1][pv] +
-                      kx.z * __expf(gl.z - gx.z) * sm.dS[x + 2][pv] + kx.w * __expf(gl.w - gx.w) * sm.dS[x + 3][pv];
+        if (w < 8) {
+            const int rt = (w >> 1) & 1, ct = w & 1, r0t = 16 * rt, c0t = 16 * ct;
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (w < 4) {
+                acc = tile_mm<K>([&](int r, int x) { return sm.k[r0t + r][x] * sm.e[r0t + r][x]; },
+                                 [&](int x, int v) { return sm.S[x][c0t + v]; }, ln, lg, acc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int c = r0t + 4 * lg + j;
+                    sm.R[c][c0t + ln] = sm.v[c][c0t + ln] - acc[j];
+                }
+            } else {
+                acc = tile_mm<K>([&](int r, int x) {
+                                     return sm.k[r0t + r][x] * __expf(sm.gc[CT - 1][x] - sm.gc[r0t + r][x]);
+                                 },
+                                 [&](int x, int v) { return sm.dS[x][c0t + v]; }, ln, lg, acc);
+                acc = tile_mm<CT>([&](int r, int c2) { return sm.A[c2][r0t + r]; },
+                                  [&](int c2, int v) { return sm.dO[c2][c0t + v]; }, ln, lg, acc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sm.dP[r0t + 4 * lg + j][c0t + ln] = acc[j];
             }
-            for (int c2 = pc; c2 < CT; ++c2) dp += sm.A[c2][pc] * sm.dO[c2][pv];
-            sm.R[pc][pv] = rr;
-            sm.dP[pc][pv] = dp;
         }
         __syncthreads();
 
         // ------------------------------------------ P = M R, dR = M^T dP = dV
-        {
-            float pp = 0.f, dr = 0.f;
-            for (int i = 0; i <= pc; ++i) pp += sm.N[pc][i] * sm.beta[i] * sm.R[i][pv];
-            for (int c2 = pc; c2 < CT; ++c2) dr += sm.N[c2][pc] * sm.dP[c2][pv];
-            dr *= sm.beta[pc];
-            sm.P[pc][pv] = pp;
-            sm.dR[pc][pv] = dr;
-            const int64_t row = static_cast<int64_t>(n) * CT + pc;
-            if (row < T) a.dv[((b * T + row) * H + h) * V + v0 + pv] = dr;
+        if (w < 8) {
+            const int rt = (w >> 1) & 1, ct = w & 1, r0t = 16 * rt, c0t = 16 * ct;
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (w < 4) {
+                acc = tile_mm<CT>([&](int r, int i) { return sm.N[r0t + r][i] * sm.beta[i]; },
+                                  [&](int i, int v) { return sm.R[i][c0t + v]; }, ln, lg, acc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sm.P[r0t + 4 * lg + j][c0t + ln] = acc[j];
+            } else {
+                acc = tile_mm<CT>([&](int r, int c2) { return sm.N[c2][r0t + r]; },
+                                  [&](int c2, int v) { return sm.dP[c2][c0t + v]; }, ln, lg, acc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int c = r0t + 4 * lg + j;
+                    const float dr = acc[j] * sm.beta[c];
+                    sm.dR[c][c0t + ln] = dr;
+                    const int64_t row = static_cast<int64_t>(n) * CT + c;
+                    if (row < T) a.dv[((b * T + row) * H + h) * V + v0 + c0t + ln] = dr;
+                }
+            }
         }
         __syncthreads();
 
-        // ------------------------------------------ dA = dO P^T, dM = dP R^T
-        {
-            const int c = pc, i = pv;
-            float da = 0.f, dm = 0.f;
-            if (i <= c) {
-#pragma unroll 2
-                for (int vv = 0; vv < VT; vv += 4) {
-                    const float4 a0 = *reinterpret_cast<const float4*>(&sm.dO[c][vv]);
-                    const float4 b0 = *reinterpret_cast<const float4*>(&sm.P[i][vv]);
-                    const float4 a1 = *reinterpret_cast<const float4*>(&sm.dP[c][vv]);
-                    const float4 b1 = *reinterpret_cast<const float4*>(&sm.R[i][vv]);
-                    da += a0.x * b0.x + a0.y * b0.y + a0.z * b0.z + a0.w * b0.w;
-                    dm += a1.x * b1.x + a1.y * b1.y + a1.z * b1.z + a1.w * b1.w;
-                }
+        // ------------------------------------------ dA = dO P^T, dM = dP R^T (i <= c)
+        if (w < 8) {
+            const int rt = (w >> 1) & 1, ct = w & 1, r0t = 16 * rt, c0t = 16 * ct;
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (w < 4)
+                acc = tile_mm<VT>([&](int r, int v) { return sm.dO[r0t + r][v]; },
+                                  [&](int v, int i) { return sm.P[c0t + i][v]; }, ln, lg, acc);
+            else
+                acc = tile_mm<VT>([&](int r, int v) { return sm.dP[r0t + r][v]; },
+                                  [&](int v, int i) { return sm.R[c0t + i][v]; }, ln, lg, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = r0t + 4 * lg + j, i = c0t + ln;
+                const float x = i <= c ? acc[j] : 0.f;
+                if (w < 4) sm.dA[c][i] = x;
+                else sm.dM[c][i] = x;
             }
-            sm.dA[c][i] = da;
-            sm.dM[c][i] = dm;
         }
         __syncthreads();
 
@@ -265,23 +296,29 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
             sm.dbeta[t] = s;
         }
         __syncthreads();
-        sm.dM[pc][pv] *= sm.beta[pv];
+        sm.dM[t / CT][t % CT] *= sm.beta[t % CT];
         __syncthreads();
-        // Y = dN N^T (lower: Y[c,i] = sum_{m <= min(c,i)} dN[c,m] N[i,m])
-        {
-            const int c = pc, i = pv, mmax = c < i ? c : i;
-            float s = 0.f;
-            for (int m = 0; m <= mmax; ++m) s += sm.dM[c][m] * sm.N[i][m];
-            sm.Y[c][i] = s;
+        // Y = dN N^T
+        if (w < 4) {
+            const int r0t = 16 * (w >> 1), c0t = 16 * (w & 1);
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = tile_mm<CT>([&](int r, int m) { return sm.dM[r0t + r][m]; },
+                              [&](int m, int i) { return sm.N[c0t + i][m]; }, ln, lg, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.Y[r0t + 4 * lg + j][c0t + ln] = acc[j];
         }
         __syncthreads();
-        // dX[c,i] = -sum_{m >= c} N[m,c] Y[m,i] for i < c (kept in dM)
-        {
-            const int c = pc, i = pv;
-            float s = 0.f;
-            if (i < c)
-                for (int m = c; m < CT; ++m) s += sm.N[m][c] * sm.Y[m][i];
-            sm.dM[c][i] = -s;
+        // dX = -N^T Y, strictly lower (kept in dM)
+        if (w < 4) {
+            const int r0t = 16 * (w >> 1), c0t = 16 * (w & 1);
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = tile_mm<CT>([&](int r, int m) { return sm.N[m][r0t + r]; },
+                              [&](int m, int i) { return sm.Y[m][c0t + i]; }, ln, lg, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = r0t + 4 * lg + j, i = c0t + ln;
+                sm.dM[c][i] = i < c ? -acc[j] : 0.f;
+            }
         }
         __syncthreads();
         if (t < CT) {
@@ -295,41 +332,51 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
             sm.deps[t] = s;
         }
 
+        // Per wave, one 16 x 16 tile of the K x VT state gradient and one of
+        // the CT x K (row, channel) elements.
+        constexpr int KTL = K / 16;
+        const bool tw = w < 2 * KTL;
         // ------------------- dS_start = Diag(eps) dS + (q~*E)^T dO - (k*E)^T dR
-        float dsn[SPT];
-        {
-            const int r = st_row(0), c0 = st_col(0);
-            for (int j = 0; j < SPT; ++j) dsn[j] = sm.eps[r] * sm.dS[r][c0 + j];
-#pragma unroll 4
-            for (int c2 = 0; c2 < CT; ++c2) {
-                const float qe = sm.e[c2][r] * sm.q[c2][r], ke = sm.e[c2][r] * sm.k[c2][r];
-                for (int j = 0; j < SPT; ++j) dsn[j] += qe * sm.dO[c2][c0 + j] - ke * sm.dR[c2][c0 + j];
+        f4 dsn = {0.f, 0.f, 0.f, 0.f};
+        const int srt = 16 * (w >> 1), sct = 16 * (w & 1);
+        // element tile: rows 16 (w / KTL) + 4 lg + j, channel 16 (w % KTL) + ln
+        const int ert = 16 * (w / KTL), ekk = 16 * (w % KTL) + ln;
+        f4 dqe = {0.f, 0.f, 0.f, 0.f}, dke = dqe, dkf = dqe;
+        if (tw) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int x = srt + 4 * lg + j;
+                dsn[j] = sm.eps[x] * sm.dS[x][sct + ln];
             }
+            dsn = tile_mm<CT>([&](int r, int c) { return sm.q[c][srt + r] * sm.e[c][srt + r]; },
+                              [&](int c, int v) { return sm.dO[c][sct + v]; }, ln, lg, dsn);
+            dsn = tile_mm<CT>([&](int r, int c) { return -sm.k[c][srt + r] * sm.e[c][srt + r]; },
+                              [&](int c, int v) { return sm.dR[c][sct + v]; }, ln, lg, dsn);
+            // d(q~*E) = dO S^T, d(k*E) = -dR S^T, d(k*F) = P dS^T
+            dqe = tile_mm<VT>([&](int r, int v) { return sm.dO[ert + r][v]; },
+                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dqe);
+            dke = tile_mm<VT>([&](int r, int v) { return -sm.dR[ert + r][v]; },
+                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dke);
+            dkf = tile_mm<VT>([&](int r, int v) { return sm.P[ert + r][v]; },
+                              [&](int v, int kc) { return sm.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
         }
+        // every read of exp(G) and of the end-of-chunk dS is done: dS takes
+        // its new value, and each (row, channel) element's exp(G) becomes dG
         __syncthreads();
+        if (tw) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.dS[srt + 4 * lg + j][sct + ln] = dsn[j];
+        }
 
         // ---------------------------- per (row, channel): dq, dk and dG
-        {
-            // column kk of G, k and q~ (each thread keeps its channel)
-            auto gcol = [&](int c) { return sm.gc[c][kk]; };
-            auto kcol = [&](int c) { return sm.k[c][kk]; };
-            auto qcol = [&](int c) { return sm.q[c][kk]; };
+        if (tw) {
+            auto gcol = [&](int c) { return sm.gc[c][ekk]; };
+            auto kcol = [&](int c) { return sm.k[c][ekk]; };
+            auto qcol = [&](int c) { return sm.q[c][ekk]; };
             float last = 0.f;
 #pragma unroll 1
-            for (int j = 0; j < EPT; ++j) {
-                const int c = r0 + RSTEP * j;
-                float dqe = 0.f, dke = 0.f, dkf = 0.f;
-#pragma unroll 2
-                for (int vv = 0; vv < VT; vv += 4) {
-                    const float4 s4 = *reinterpret_cast<const float4*>(&sm.S[kk][vv]);
-                    const float4 d4 = *reinterpret_cast<const float4*>(&sm.dS[kk][vv]);
-                    const float4 o4 = *reinterpret_cast<const float4*>(&sm.dO[c][vv]);
-                    const float4 r4 = *reinterpret_cast<const float4*>(&sm.dR[c][vv]);
-                    const float4 p4 = *reinterpret_cast<const float4*>(&sm.P[c][vv]);
-                    dqe += o4.x * s4.x + o4.y * s4.y + o4.z * s4.z + o4.w * s4.w;
-                    dke -= r4.x * s4.x + r4.y * s4.y + r4.z * s4.z + r4.w * s4.w;
-                    dkf += p4.x * d4.x + p4.y * d4.y + p4.z * d4.z + p4.w * d4.w;
-                }
+            for (int j = 0; j < 4; ++j) {
+                const int c = ert + 4 * lg + j;
                 float t1 = 0.f, t2 = 0.f, t3 = 0.f, t4 = 0.f;
                 const float bc = sm.beta[c];
                 const float gcc = gcol(c);
@@ -343,30 +390,29 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
                     t2 += sm.dA[c2][c] * qcol(c2) * d;
                     if (c2 > c) t4 += sm.beta[c2] * sm.dM[c2][c] * kcol(c2) * d;
                 }
-                const float E = sm.e[c][kk];
+                const float E = sm.e[c][ekk];
                 const float F = __expf(gcol(CT - 1) - gcc);
-                const float dqt = t1 + dqe * E;
-                const float dk = t2 + t3 + t4 + dke * E + dkf * F;
+                const float dqt = t1 + dqe[j] * E;
+                const float dk = t2 + t3 + t4 + dke[j] * E + dkf[j] * F;
                 const float qc = qcol(c), kc = kcol(c);
-                const float dgv = qc * t1 + kc * (t3 - t2 - t4) + dqe * qc * E + dke * kc * E - dkf * kc * F;
-                last += dkf * kc * F;
-                sm.e[c][kk] = dgv;   // only this thread reads e[c][kk] from here on
+                const float dgv = qc * t1 + kc * (t3 - t2 - t4) + dqe[j] * qc * E + dke[j] * kc * E - dkf[j] * kc * F;
+                last += dkf[j] * kc * F;
+                sm.e[c][ekk] = dgv;   // exp(G) is no longer read: it holds dG from here on
                 const int64_t row = static_cast<int64_t>(n) * CT + c;
                 if (row < T) {
-                    const int64_t o = ((static_cast<int64_t>(vt) * a.B + b) * T + row) * H * K + h * K + kk;
+                    const int64_t o = ((static_cast<int64_t>(vt) * a.B + b) * T + row) * H * K + h * K + ekk;
                     a.dq_part[o] = dqt * scale;
                     a.dk_part[o] = dk;
                 }
             }
-            (&sm.Y[0][0])[t] = last;
+            (&sm.Y[0][0])[((w / KTL) * 4 + lg) * K + ekk] = last;
         }
         __syncthreads();
 
-        // ------------------------- carry, dg (reverse in-chunk cumsum), dbeta
-        for (int j = 0; j < SPT; ++j) sm.dS[st_row(j)][st_col(j)] = dsn[j];
+        // ------------------------------- dg (reverse in-chunk cumsum), dbeta
         if (t < K) {
             float run = sm.deps[t] * sm.eps[t];
-            for (int x = 0; x < NT / K; ++x) run += (&sm.Y[0][0])[x * K + t];
+            for (int x = 0; x < 8; ++x) run += (&sm.Y[0][0])[x * K + t];
             for (int c = CT - 1; c >= 0; --c) {
                 run += sm.e[c][t];
                 const int64_t row = static_cast<int64_t>(n) * CT + c;
