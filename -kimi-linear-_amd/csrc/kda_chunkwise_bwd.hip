@@ -100,26 +100,31 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
     const int64_t bh = blockIdx.x / nvt;
     const int64_t b = bh / H, h = bh % H;
     const int64_t v0 = static_cast<int64_t>(vt) * VT;
-    const int t = threadIdx.x;
+    const int t0 = threadIdx.x;
     const int nck = static_cast<int>((T + CT - 1) / CT);
     const float scale = a.scale;
 
-    // (row, channel) element j of this thread: row t / K + j * (NT / K), channel t % K
-    const int kk = t % K;
-    const int r0 = t / K;
     constexpr int RSTEP = NT / K;
     // state-tile elements of this thread: SPT adjacent columns of one row
     constexpr int TPR = VT / SPT;           // threads per state row
-    auto st_row = [&](int j) { return t / TPR + 0 * j; };
-    auto st_col = [&](int j) { return SPT * (t % TPR) + j; };
 
     // dS <- dL/dS_T
     for (int j = 0; j < SPT; ++j) {
-        const int r = st_row(j), c = st_col(j);
+        const int r = t0 / TPR, c = SPT * (t0 % TPR) + j;
         sm.dS[r][c] = a.d_state_out ? a.d_state_out[(bh * K + r) * V + v0 + c] : 0.f;
     }
 
     for (int n = nck - 1; n >= 0; --n) {
+        // The thread index, read afresh per chunk: the many lane-derived LDS
+        // addresses are recomputed here instead of being held across the loop.
+        int t;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"(t0));
+        const int w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;   // wave, MFMA lane
+        // (row, channel) element j of this thread: row t / K + j * (NT / K), channel t % K
+        const int kk = t % K;
+        const int r0 = t / K;
+        auto st_row = [&](int j) { return t / TPR + 0 * j; };
+        auto st_col = [&](int j) { return SPT * (t % TPR) + j; };
         // ---------------------------------------------------------------- loads
         for (int j = 0; j < EPT; ++j) {
             const int c = r0 + RSTEP * j;
@@ -199,26 +204,46 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
         __syncthreads();
 
         // ------------------------------- N = (I + Diag(beta) L)^-1, by columns
+        // Blocked: the two 16 x 16 diagonal blocks by forward substitution
+        // (lane t of wave 0: column t % 16 of block t / 16, in registers),
+        // then N10 = -N11 X10 N00 on the matrix cores, all in wave 0.
         if (t < CT) {
-            // column jc in registers: the substitution only reads L (LDS,
-            // the same address in every lane) and the column itself
-            const int jc = t;
-            float col[CT];
+            const int bo = 16 * (t >> 4), jc = t & 15;
+            float col[16];
 #pragma unroll
-            for (int c = 0; c < CT; ++c) {
+            for (int c = 0; c < 16; ++c) {
                 float s = 0.f;
 #pragma unroll
-                for (int m = 0; m < c; ++m) s += sm.L[c][m] * col[m];
-                col[c] = c < jc ? 0.f : (c == jc ? 1.f : -sm.beta[c] * s);
+                for (int m = 0; m < c; ++m) s += sm.L[bo + c][bo + m] * col[m];
+                col[c] = c < jc ? 0.f : (c == jc ? 1.f : -sm.beta[bo + c] * s);
             }
 #pragma unroll
-            for (int c = 0; c < CT; ++c) sm.N[c][jc] = col[c];
+            for (int c = 0; c < 16; ++c) {
+                sm.N[bo + c][bo + jc] = col[c];
+                if (bo == 0) sm.N[c][16 + jc] = 0.f;
+            }
+        }
+        if (t < 64) {
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            // Y (free here) <- X10 N00, X10 = Diag(beta_1) L10
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = tile_mm<16>([&](int r, int m) { return sm.beta[16 + r] * sm.L[16 + r][m]; },
+                              [&](int m, int i) { return sm.N[m][i]; }, ln, lg, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.Y[4 * lg + j][ln] = acc[j];
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+            acc = tile_mm<16>([&](int r, int m) { return sm.N[16 + r][16 + m]; },
+                              [&](int m, int i) { return sm.Y[m][i]; }, ln, lg, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.N[16 + 4 * lg + j][ln] = -acc[j];
         }
         __syncthreads();
 
         // The products below run on the fp32 matrix cores, one 16 x 16 output
         // tile per wave: lane (ln, lg) receives rows 4 lg + j, column ln.
-        const int w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
 
         // --------------------------------------- R = V - (k*E) S, dP = (k*F) dS + A^T dO
         if (w < 8) {
@@ -369,33 +394,66 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
         }
 
         // ---------------------------- per (row, channel): dq, dk and dG
+        // The lane's rows c0 .. c0 + 3 share the decay products through a
+        // reference row: for i <= c0, exp(G_c - G_i) = exp(G_c - G_c0) exp(G_c0 - G_i),
+        // and for c2 >= c3 = c0 + 3, exp(G_c2 - G_c) = exp(G_c2 - G_c3) exp(G_c3 - G_c),
+        // every factor <= 1; the few pairs between the lane's own rows are direct.
         if (tw) {
             auto gcol = [&](int c) { return sm.gc[c][ekk]; };
             auto kcol = [&](int c) { return sm.k[c][ekk]; };
             auto qcol = [&](int c) { return sm.q[c][ekk]; };
+            const int c0 = ert + 4 * lg, c3 = c0 + 3;
+            const float g0 = gcol(c0), g3 = gcol(c3);
+            float t1[4] = {0.f, 0.f, 0.f, 0.f}, t2[4] = {0.f, 0.f, 0.f, 0.f};
+            float t3[4] = {0.f, 0.f, 0.f, 0.f}, t4[4] = {0.f, 0.f, 0.f, 0.f};
+            // row side, i <= c0 (dA and dM vanish above the diagonal)
+            for (int i = 0; i <= c0; ++i) {
+                const float kh = kcol(i) * __expf(g0 - gcol(i));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    t1[j] += sm.dA[c0 + j][i] * kh;
+                    t3[j] += sm.dM[c0 + j][i] * kh;
+                }
+            }
+            // column side, c2 >= c3
+            for (int c2 = c3; c2 < CT; ++c2) {
+                const float h = __expf(gcol(c2) - g3);
+                const float qh = qcol(c2) * h, kh = sm.beta[c2] * kcol(c2) * h;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    t2[j] += sm.dA[c2][c0 + j] * qh;
+                    t4[j] += sm.dM[c2][c0 + j] * kh;
+                }
+            }
             float last = 0.f;
-#pragma unroll 1
+#pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int c = ert + 4 * lg + j;
-                float t1 = 0.f, t2 = 0.f, t3 = 0.f, t4 = 0.f;
-                const float bc = sm.beta[c];
+                const int c = c0 + j;
                 const float gcc = gcol(c);
-                for (int i = 0; i <= c; ++i) {
-                    const float d = __expf(gcc - gcol(i)) * kcol(i);
-                    t1 += sm.dA[c][i] * d;
-                    if (i < c) t3 += bc * sm.dM[c][i] * d;
+                const float f0 = __expf(gcc - g0), f3 = __expf(g3 - gcc);
+                float T1 = f0 * t1[j], T3 = f0 * t3[j], T2 = f3 * t2[j], T4 = f3 * t4[j];
+                // the lane's own rows: c0 < i <= c (row side), c <= c2 < c3 (column side)
+#pragma unroll
+                for (int x = 1; x < 4; ++x) {
+                    if (x <= j) {
+                        const float d = __expf(gcc - gcol(c0 + x)) * kcol(c0 + x);
+                        T1 += sm.dA[c][c0 + x] * d;
+                        T3 += sm.dM[c][c0 + x] * d;
+                    }
+                    if (x - 1 >= j) {
+                        const int c2 = c0 + x - 1;
+                        const float d = __expf(gcol(c2) - gcc);
+                        T2 += sm.dA[c2][c] * qcol(c2) * d;
+                        T4 += sm.beta[c2] * sm.dM[c2][c] * kcol(c2) * d;
+                    }
                 }
-                for (int c2 = c; c2 < CT; ++c2) {
-                    const float d = __expf(gcol(c2) - gcc);
-                    t2 += sm.dA[c2][c] * qcol(c2) * d;
-                    if (c2 > c) t4 += sm.beta[c2] * sm.dM[c2][c] * kcol(c2) * d;
-                }
+                T3 *= sm.beta[c];
                 const float E = sm.e[c][ekk];
                 const float F = __expf(gcol(CT - 1) - gcc);
-                const float dqt = t1 + dqe[j] * E;
-                const float dk = t2 + t3 + t4 + dke[j] * E + dkf[j] * F;
+                const float dqt = T1 + dqe[j] * E;
+                const float dk = T2 + T3 + T4 + dke[j] * E + dkf[j] * F;
                 const float qc = qcol(c), kc = kcol(c);
-                const float dgv = qc * t1 + kc * (t3 - t2 - t4) + dqe[j] * qc * E + dke[j] * kc * E - dkf[j] * kc * F;
+                const float dgv = qc * T1 + kc * (T3 - T2 - T4) + dqe[j] * qc * E + dke[j] * kc * E - dkf[j] * kc * F;
                 last += dkf[j] * kc * F;
                 sm.e[c][ekk] = dgv;   // exp(G) is no longer read: it holds dG from here on
                 const int64_t row = static_cast<int64_t>(n) * CT + c;
@@ -429,7 +487,7 @@ __global__ __launch_bounds__(NT) void chunkwise_bwd_kernel(const kda_bwd_args a)
 
     if (a.d_state_in) {
         for (int j = 0; j < SPT; ++j) {
-            const int r = st_row(j), c = st_col(j);
+            const int r = t0 / TPR, c = SPT * (t0 % TPR) + j;
             a.d_state_in[(bh * K + r) * V + v0 + c] = sm.dS[r][c];
         }
     }
