@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -53,9 +53,9 @@ class KdaBwdArgs(ctypes.Structure):
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
         ("g", ctypes.c_void_p), ("beta", ctypes.c_void_p), ("ckpt", ctypes.c_void_p),
         ("d_o", ctypes.c_void_p), ("d_state_out", ctypes.c_void_p),
-        ("dq_part", ctypes.c_void_p), ("dk_part", ctypes.c_void_p), ("dg_part", ctypes.c_void_p),
-        ("dbeta_part", ctypes.c_void_p), ("dv", ctypes.c_void_p), ("d_state_in", ctypes.c_void_p),
-        ("scale", ctypes.c_float),
+        ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dg", ctypes.c_void_p),
+        ("dbeta", ctypes.c_void_p), ("dv", ctypes.c_void_p), ("d_state_in", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("scale", ctypes.c_float),
     ]
 
 
@@ -93,6 +93,7 @@ class KdaOutputArgs(ctypes.Structure):
 
 
 EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_chunkwise_fwd_ckpt", "kda_chunkwise_bwd",
+                    "kda_chunkwise_bwd_workspace_size",
                     "kda_prep_fwd", "kda_output_fwd", "kda_status_str", "kda_abi_version")
 
 _lib = None
@@ -130,6 +131,8 @@ def load() -> ctypes.CDLL:
         lib.kda_chunkwise_fwd_ckpt.restype = ctypes.c_int
         lib.kda_chunkwise_bwd.argtypes = [ctypes.POINTER(KdaBwdArgs), ctypes.c_void_p]
         lib.kda_chunkwise_bwd.restype = ctypes.c_int
+        lib.kda_chunkwise_bwd_workspace_size.argtypes = [ctypes.c_int64] * 5
+        lib.kda_chunkwise_bwd_workspace_size.restype = ctypes.c_size_t
         lib.kda_prep_fwd.argtypes = [ctypes.POINTER(KdaPrepArgs), ctypes.c_void_p]
         lib.kda_prep_fwd.restype = ctypes.c_int
         lib.kda_output_fwd.argtypes = [ctypes.POINTER(KdaOutputArgs), ctypes.c_void_p]

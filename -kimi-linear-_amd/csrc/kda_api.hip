@@ -74,15 +74,23 @@ int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) 
     return kda::chunkwise_launch(*args, static_cast<hipStream_t>(stream), ckpt);
 }
 
+size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
+    if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0) return 0;
+    if (T > (int64_t{1} << 40) || B * H > (int64_t{1} << 31) || K > 4096 || V > 4096) return 0;
+    return static_cast<size_t>(kda::chunkwise_bwd_workspace_bytes(B, T, H, K, V));
+}
+
 int kda_chunkwise_bwd(const kda_bwd_args* a, void* stream) {
     if (a == nullptr) return KDA_ERR_NULL_POINTER;
     if (a->B < 0 || a->T < 0 || a->H < 0 || a->K <= 0 || a->V <= 0) return KDA_ERR_BAD_SHAPE;
     if (a->B == 0 || a->H == 0) return KDA_OK;
     if (!kda::chunkwise_bwd_supported(a->K, a->V)) return KDA_ERR_UNSUPPORTED;
-    if (a->T > 0 && (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->ckpt || !a->d_o || !a->dq_part ||
-                     !a->dk_part || !a->dg_part || !a->dbeta_part || !a->dv))
+    if (a->T > 0 && (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->ckpt || !a->d_o || !a->dq ||
+                     !a->dk || !a->dg || !a->dbeta || !a->dv || !a->workspace))
         return KDA_ERR_NULL_POINTER;
-    if (a->B * a->H * (a->V / 32) > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    // grids: B H ceil(T / 32) and B H V / 32 workgroups
+    if (a->B * a->H * ((a->T + 31) / 32) > INT32_MAX || a->B * a->H * (a->V / 32) > INT32_MAX)
+        return KDA_ERR_BAD_SHAPE;
     if (a->T == 0 && a->d_state_in == nullptr) return KDA_OK;
     return kda::chunkwise_bwd_launch(*a, static_cast<hipStream_t>(stream));
 }

@@ -18,6 +18,7 @@ int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nu
 
 // Chunkwise backward (kda_chunkwise_bwd.hip).
 bool chunkwise_bwd_supported(int64_t K, int64_t V);
+int64_t chunkwise_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 int chunkwise_bwd_launch(const kda_bwd_args& a, hipStream_t stream);
 
 }  // namespace kda

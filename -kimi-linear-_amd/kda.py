@@ -213,7 +213,7 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
 
 
 CKPT_SPACING = 32   # tokens between the forward's state checkpoints (kda_chunkwise_fwd_ckpt)
-BWD_TILE = 32       # state columns per backward workgroup (partial-gradient tiles)
+BWD_TILE = 32       # the native backward takes V in multiples of this
 
 
 def _f32c(x: torch.Tensor) -> torch.Tensor:
@@ -225,32 +225,34 @@ def _chunkwise_backward(q, k, v, g, beta, ckpt, d_o, d_state, need_d_state_in):
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device
-    nvt = V // BWD_TILE
     q, k, v, g, beta, d_o = (_f32c(x) for x in (q, k, v, g, beta, d_o))
     d_state = _f32c(d_state) if d_state is not None else None
-    dq = torch.empty(nvt, B, T, H, K, device=dev, dtype=torch.float32)
+    dq = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
     dk = torch.empty_like(dq)
     dg = torch.empty_like(dq)
-    dbeta = torch.empty(nvt, B, T, H, device=dev, dtype=torch.float32)
+    dbeta = torch.empty(B, T, H, device=dev, dtype=torch.float32)
     dv = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
     ds0 = torch.empty(B, H, K, V, device=dev, dtype=torch.float32) if need_d_state_in else None
+    lib = _native.load()
+    ws = torch.empty(max(int(lib.kda_chunkwise_bwd_workspace_size(B, T, H, K, V)), 1),
+                     device=dev, dtype=torch.uint8)
     args = _native.KdaBwdArgs()
     args.B, args.T, args.H, args.K, args.V = B, T, H, K, V
     args.q, args.k, args.v, args.g, args.beta = (x.data_ptr() for x in (q, k, v, g, beta))
     args.ckpt, args.d_o = ckpt.data_ptr(), d_o.data_ptr()
     args.d_state_out = d_state.data_ptr() if d_state is not None else None
-    args.dq_part, args.dk_part, args.dg_part = dq.data_ptr(), dk.data_ptr(), dg.data_ptr()
-    args.dbeta_part, args.dv = dbeta.data_ptr(), dv.data_ptr()
+    args.dq, args.dk, args.dg = dq.data_ptr(), dk.data_ptr(), dg.data_ptr()
+    args.dbeta, args.dv = dbeta.data_ptr(), dv.data_ptr()
     args.d_state_in = ds0.data_ptr() if ds0 is not None else None
+    args.workspace = ws.data_ptr()
     args.scale = float(K) ** -0.5
-    lib = _native.load()
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
         status = lib.kda_chunkwise_bwd(ctypes.byref(args), ctypes.c_void_p(stream))
     if status != _native.STATUS_OK:
         raise KdaError(f"kda_chunkwise_bwd failed: {_native.status_str(status)} "
                        f"(B={B}, T={T}, H={H}, K={K}, V={V})")
-    return dq.sum(0), dk.sum(0), dv, dg.sum(0), dbeta.sum(0), ds0
+    return dq, dk, dv, dg, dbeta, ds0
 
 
 class _ChunkwiseFn(torch.autograd.Function):

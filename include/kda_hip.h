@@ -32,13 +32,14 @@
 #ifndef KDA_HIP_H
 #define KDA_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 3
+#define KDA_ABI_VERSION 4
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -120,11 +121,11 @@ int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 
 /* Every tensor is contiguous fp32 in the forward layout: q, k, g, dq, dk, dg
- * [B, T, H, K]; v, d_o, dv [B, T, H, V]; beta [B, T, H]; states [B, H, K, V].
- * dq, dk, dg and dbeta are sums over the state columns: the call writes one
- * share per 32-column tile, [V/32, B, T, H, K] (dbeta [V/32, B, T, H]), and
- * the gradient is the sum over the first axis.  dv and d_state_in are
- * complete.  K in {32, 64, 128}, V a multiple of 32, any T >= 0. */
+ * [B, T, H, K]; v, d_o, dv [B, T, H, V]; beta, dbeta [B, T, H]; states
+ * [B, H, K, V].  workspace: device memory of at least
+ * kda_chunkwise_bwd_workspace_size(B, T, H, K, V) bytes, 16-byte aligned (its
+ * contents on entry do not matter; calls that share one workspace must not
+ * overlap).  K in {32, 64, 128}, V a multiple of 32, any T >= 0. */
 typedef struct kda_bwd_args {
     int64_t B, T, H, K, V;
     const float* q;                /* the forward's inputs (q unscaled)        */
@@ -135,14 +136,19 @@ typedef struct kda_bwd_args {
     const float* ckpt;             /* from kda_chunkwise_fwd_ckpt on the same inputs */
     const float* d_o;              /* dL/do                                      */
     const float* d_state_out;      /* dL/d(final state), or NULL for zeros       */
-    float* dq_part;                /* [V/32, B, T, H, K] */
-    float* dk_part;
-    float* dg_part;
-    float* dbeta_part;             /* [V/32, B, T, H]    */
-    float* dv;                     /* [B, T, H, V]       */
+    float* dq;                     /* [B, T, H, K] */
+    float* dk;
+    float* dg;
+    float* dbeta;                  /* [B, T, H]    */
+    float* dv;                     /* [B, T, H, V] */
     float* d_state_in;             /* dL/d(initial state) [B, H, K, V], or NULL   */
+    void* workspace;
     float scale;                   /* the forward's q multiplier                  */
 } kda_bwd_args;
+
+/* Bytes of workspace kda_chunkwise_bwd needs: per (b, h) and 32-token chunk,
+ * (3 * 32 * 32 + K * V + 32 * V) floats.  0 for a bad or empty shape. */
+size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 
 int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
 

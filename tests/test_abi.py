@@ -29,7 +29,7 @@ def native(kda_pkg):
 
 def header_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(kda_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(kda_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol(native):
