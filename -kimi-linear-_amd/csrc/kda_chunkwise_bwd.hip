@@ -93,11 +93,22 @@ struct __align__(16) PairSmem {
     float q[CT][KP];            // scale * q
     float k[CT][KP];
     float gc[CT][KP];           // in-chunk cumulative log decay G
+    float A[CT][CT + 1];
     float L[CT][CT + 1];
     float N[CT][CT + 1];
     float Y[CT][CT + 1];
     float beta[CT];
 };
+
+// Sum over the 16 lanes of a DPP row (every lane gets it): quad_perm xor 1,
+// xor 2, then row_ror 4 and 8.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+    return x;
+}
 
 template <int K>
 __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, const BwdWs ws) {
@@ -109,7 +120,7 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
     const int64_t bh = blockIdx.x / nck, b = bh / H, h = bh % H;
     const int n = static_cast<int>(blockIdx.x % nck);
     const int64_t cb = bh * nck + n;
-    const int t = threadIdx.x, lane = t & 63, ln = lane & 15, lg = lane >> 4;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
     const int kk = t % K, r0 = t / K;
 
     for (int j = 0; j < EPT; ++j) {
@@ -140,28 +151,89 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
     }
     __syncthreads();
 
-    // A and L, one (c, i) entry per thread
-    {
-        const int c = t / CT, i = t % CT;
-        float av = 0.f, lv = 0.f;
-        if (i <= c) {
-#pragma unroll 2
-            for (int x = 0; x < K; x += 4) {
-                const float4 gcv = *reinterpret_cast<const float4*>(&sm.gc[c][x]);
-                const float4 giv = *reinterpret_cast<const float4*>(&sm.gc[i][x]);
-                const float4 kiv = *reinterpret_cast<const float4*>(&sm.k[i][x]);
-                const float4 qcv = *reinterpret_cast<const float4*>(&sm.q[c][x]);
-                const float4 kcv = *reinterpret_cast<const float4*>(&sm.k[c][x]);
-                const float d0 = __expf(gcv.x - giv.x) * kiv.x, d1 = __expf(gcv.y - giv.y) * kiv.y;
-                const float d2 = __expf(gcv.z - giv.z) * kiv.z, d3 = __expf(gcv.w - giv.w) * kiv.w;
-                av += qcv.x * d0 + qcv.y * d1 + qcv.z * d2 + qcv.w * d3;
-                lv += kcv.x * d0 + kcv.y * d1 + kcv.z * d2 + kcv.w * d3;
-            }
-            if (i == c) lv = 0.f;
+    // A and L on 4 x 4 blocks of entries (c, i), i <= c: the 16 lanes of a
+    // DPP row take one block, lane cg the channels cg + 16 m, and the row adds
+    // its partial sums at the end.  Waves 0-1: the 8 diagonal blocks (direct
+    // decays); waves 2-8: the 28 blocks below them, whose decays factor
+    // through the block's first row b: exp(G_c - G_i) = exp(G_c - G_b)
+    // exp(G_b - G_i) for i < b <= c, both factors <= 1.
+    if (w < 9) {
+        const int blk = t >> 4, cg = t & 15;
+        int bc, bi;
+        if (blk < 8) {
+            bc = bi = blk;
+        } else {
+            const int o = blk - 8;
+            bc = 1;
+            while ((bc + 1) * bc / 2 <= o) ++bc;
+            bi = o - bc * (bc - 1) / 2;
         }
-        sm.L[c][i] = lv;
-        ws.A[cb * CT * CT + t] = av;
-        ws.L[cb * CT * CT + t] = lv;
+        const int c0 = 4 * bc, i0 = 4 * bi;
+        float av[16], lv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) av[e] = lv[e] = 0.f;
+        if (w < 2) {
+            for (int x = cg; x < K; x += 16) {
+                float gv[4], qv[4], kv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    gv[j] = sm.gc[c0 + j][x];
+                    qv[j] = sm.q[c0 + j][x];
+                    kv[j] = sm.k[c0 + j][x];
+                }
+#pragma unroll
+                for (int jc = 0; jc < 4; ++jc) {
+                    av[jc * 4 + jc] += qv[jc] * kv[jc];
+#pragma unroll
+                    for (int ji = 0; ji < jc; ++ji) {
+                        const float d = __expf(gv[jc] - gv[ji]) * kv[ji];
+                        av[jc * 4 + ji] += qv[jc] * d;
+                        lv[jc * 4 + ji] += kv[jc] * d;
+                    }
+                }
+            }
+        } else {
+            for (int x = cg; x < K; x += 16) {
+                const float gb = sm.gc[c0][x];
+                float qu[4], ku[4], kw[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float uc = __expf(sm.gc[c0 + j][x] - gb);
+                    qu[j] = sm.q[c0 + j][x] * uc;
+                    ku[j] = sm.k[c0 + j][x] * uc;
+                    kw[j] = sm.k[i0 + j][x] * __expf(gb - sm.gc[i0 + j][x]);
+                }
+#pragma unroll
+                for (int jc = 0; jc < 4; ++jc)
+#pragma unroll
+                    for (int ji = 0; ji < 4; ++ji) {
+                        av[jc * 4 + ji] += qu[jc] * kw[ji];
+                        lv[jc * 4 + ji] += ku[jc] * kw[ji];
+                    }
+            }
+        }
+        float ao = 0.f, lo = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float as = row16_sum(av[e]), ls = row16_sum(lv[e]);
+            ao = cg == e ? as : ao;
+            lo = cg == e ? ls : lo;
+        }
+        const int jc = cg >> 2, ji = cg & 3;
+        const bool keep = w >= 2 || ji <= jc;
+        sm.A[c0 + jc][i0 + ji] = keep ? ao : 0.f;
+        sm.L[c0 + jc][i0 + ji] = keep ? lo : 0.f;
+    } else {
+        // the 28 blocks above the diagonal are zero
+        const int o = t - 9 * 64;
+        if (o < 28 * 16) {
+            const int blk = o >> 4, e = o & 15;
+            int bi = 1;
+            while ((bi + 1) * bi / 2 <= blk) ++bi;
+            const int bc = blk - bi * (bi - 1) / 2;
+            sm.A[4 * bc + (e >> 2)][4 * bi + (e & 3)] = 0.f;
+            sm.L[4 * bc + (e >> 2)][4 * bi + (e & 3)] = 0.f;
+        }
     }
     __syncthreads();
 
@@ -202,6 +274,8 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
         for (int j = 0; j < 4; ++j) sm.N[16 + 4 * lg + j][ln] = -acc[j];
     }
     __syncthreads();
+    ws.A[cb * CT * CT + t] = sm.A[t / CT][t % CT];
+    ws.L[cb * CT * CT + t] = sm.L[t / CT][t % CT];
     ws.N[cb * CT * CT + t] = sm.N[t / CT][t % CT];
 }
 
@@ -436,10 +510,10 @@ static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
 template <int K>
 __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, const BwdWs ws) {
     static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
-    constexpr int EPT = CT * K / NT;        // (row, channel) elements per thread
-    constexpr int RSTEP = NT / K;
+    constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
     constexpr int SPT = K * VT / NT;        // state tile elements per thread
     constexpr int TPR = VT / SPT;           // threads per state row
+    static_assert(NT / K * K <= CT * (CT + 1), "the row-group sums fit Y");
     __shared__ ChunkSmem<K> sm;
 
     const int64_t H = a.H, T = a.T, V = a.V;
@@ -450,11 +524,15 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     const int nvt = static_cast<int>(V / VT);
     const float scale = a.scale;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
-    const int kk = t % K, r0 = t / K;
+    const int kk = t % K, rg = t / K;
 
     // ---------------------------------------------------------------- loads
-    for (int j = 0; j < EPT; ++j) {
-        const int c = r0 + RSTEP * j;
+    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk
+    float gl[RPT];
+    float run = 0.f;
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+        const int c = RPT * rg + j;
         const int64_t row = static_cast<int64_t>(n) * CT + c;
         float qv = 0.f, kv = 0.f, gv = 0.f;
         if (row < T) {
@@ -465,8 +543,11 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         }
         sm.q[c][kk] = qv;
         sm.k[c][kk] = kv;
-        sm.gc[c][kk] = gv;
+        run += gv;
+        gl[j] = run;
     }
+    float* tot = &sm.Y[0][0];               // [NT / K][K]: per row group, the sum of its g
+    tot[rg * K + kk] = run;
     if (t < CT) {
         const int64_t row = static_cast<int64_t>(n) * CT + t;
         sm.beta[t] = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
@@ -477,14 +558,21 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     __syncthreads();
 
     // ------------------------------------------- cumulative decays, eps
-    if (t < K) {
-        float run = 0.f;
-        for (int c = 0; c < CT; ++c) {
-            run += sm.gc[c][t];
-            sm.gc[c][t] = run;
-            sm.e[c][t] = __expf(run);
+    {
+        float pre = 0.f, last = 0.f;
+#pragma unroll
+        for (int r = 0; r < NT / K; ++r) {
+            const float x = tot[r * K + kk];
+            pre += r < rg ? x : 0.f;
+            last += x;
         }
-        sm.eps[t] = __expf(run);
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+            const int c = RPT * rg + j;
+            sm.gc[c][kk] = pre + gl[j];
+            sm.e[c][kk] = __expf(pre + gl[j]);
+        }
+        if (rg == 0) sm.eps[kk] = __expf(last);
     }
 
     // ------------------------------------- sums over the state columns
@@ -537,6 +625,7 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         if (vt + 1 < nvt) fetch(vt + 1);
         __syncthreads();
 
+        // waves 0-3: R; the other element waves: their d(q~E), d(kE)
         if (w < 4) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
             acc = tile_mm<K>([&](int r, int x) { return sm.k[r0t + r][x] * sm.e[r0t + r][x]; },
@@ -546,36 +635,43 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
                 const int c = r0t + 4 * lg + j;
                 sm.R[c][c0t + ln] = sm.v[c][c0t + ln] - acc[j];
             }
+        } else if (tw) {
+            dqe = tile_mm<VT>([&](int r, int v) { return sm.dO[ert + r][v]; },
+                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dqe);
+            dke = tile_mm<VT>([&](int r, int v) { return -sm.dR[ert + r][v]; },
+                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dke);
         }
         __syncthreads();
 
+        // waves 0-3: P = M R; waves 4-7: dM += dP R^T; waves 8-: deps
         if (w < 4) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
             acc = tile_mm<CT>([&](int r, int i) { return sm.N[r0t + r][i] * sm.beta[i]; },
                               [&](int i, int v) { return sm.R[i][c0t + v]; }, ln, lg, acc);
 #pragma unroll
             for (int j = 0; j < 4; ++j) sm.P[r0t + 4 * lg + j][c0t + ln] = acc[j];
+        } else if (w < 8) {
+            accm = tile_mm<VT>([&](int r, int v) { return sm.dP[r0t + r][v]; },
+                               [&](int v, int i) { return sm.R[c0t + i][v]; }, ln, lg, accm);
+        } else if (t - 512 < K) {
+            const int x = t - 512;
+#pragma unroll 8
+            for (int vv = 0; vv < VT; ++vv) deps += sm.dS[x][vv] * sm.S[x][vv];
         }
         __syncthreads();
 
-        if (w < 4)
+        // waves 0-3: dA += dO P^T and their d(q~E), d(kE); every element wave: d(kF) += P dS^T
+        if (w < 4) {
             accm = tile_mm<VT>([&](int r, int v) { return sm.dO[r0t + r][v]; },
                                [&](int v, int i) { return sm.P[c0t + i][v]; }, ln, lg, accm);
-        else if (w < 8)
-            accm = tile_mm<VT>([&](int r, int v) { return sm.dP[r0t + r][v]; },
-                               [&](int v, int i) { return sm.R[c0t + i][v]; }, ln, lg, accm);
-        if (tw) {
             dqe = tile_mm<VT>([&](int r, int v) { return sm.dO[ert + r][v]; },
                               [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dqe);
             dke = tile_mm<VT>([&](int r, int v) { return -sm.dR[ert + r][v]; },
                               [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dke);
+        }
+        if (tw)
             dkf = tile_mm<VT>([&](int r, int v) { return sm.P[ert + r][v]; },
                               [&](int v, int kc) { return sm.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
-        }
-        if (t < K) {
-#pragma unroll 8
-            for (int vv = 0; vv < VT; ++vv) deps += sm.dS[t][vv] * sm.S[t][vv];
-        }
         __syncthreads();
     }
     if (w < 8) {
@@ -587,17 +683,20 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             else sm.dM[c][i] = x;
         }
     }
-    if (t < K) sm.deps[t] = deps;
+    if (t >= 512 && t - 512 < K) sm.deps[t - 512] = deps;
     __syncthreads();
 
     // ------------------------------- dbeta (M = N Diag(beta)), dN in place
-    if (t < CT) {
-        float s = 0.f;
-        for (int c = t; c < CT; ++c) s += sm.dM[c][t] * sm.N[c][t];
-        sm.dbeta[t] = s;
+    // column sums of dM * N: over the two rows of each wave, then over the waves
+    float* red = &sm.S[0][0];               // [NT / 64][CT]; S is no longer read
+    {
+        const int c = t / CT, i = t % CT;
+        const float dm = sm.dM[c][i];
+        float p = dm * sm.N[c][i];
+        p += __shfl_xor(p, 32);
+        if (lane < 32) red[w * CT + i] = p;
+        sm.dM[c][i] = dm * sm.beta[i];
     }
-    __syncthreads();
-    sm.dM[t / CT][t % CT] *= sm.beta[t % CT];
     __syncthreads();
     // Y = dN N^T
     if (w < 4) {
@@ -620,10 +719,18 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         }
     }
     __syncthreads();
-    if (t < CT) {
-        float s = 0.f;
-        for (int i = 0; i < t; ++i) s += sm.dM[t][i] * sm.L[t][i];
-        sm.dbeta[t] += s;
+    // row sums of dX * L (over the 32 lanes of a row), plus the column sums above
+    {
+        const int c = t / CT, i = t % CT;
+        float p = sm.dM[c][i] * sm.L[c][i];
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) p += __shfl_xor(p, m);
+        if (i == 0) {
+            float s = p;
+#pragma unroll
+            for (int x = 0; x < NT / 64; ++x) s += red[x * CT + c];
+            sm.dbeta[c] = s;
+        }
     }
 
     // ---------------------------- per (row, channel): dq, dk and dG
@@ -701,13 +808,27 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     __syncthreads();
 
     // ------------------------------- dg (reverse in-chunk cumsum), dbeta
-    if (t < K) {
-        float run = sm.deps[t] * sm.eps[t];
-        for (int x = 0; x < 8; ++x) run += (&sm.Y[0][0])[x * K + t];
-        for (int c = CT - 1; c >= 0; --c) {
-            run += sm.e[c][t];
-            const int64_t row = static_cast<int64_t>(n) * CT + c;
-            if (row < T) a.dg[((b * T + row) * H + h) * K + t] = run;
+    // thread (rg, kk): suffix sums over its rows, then over the later row groups
+    {
+        float* gtot = &sm.dS[0][0];         // [NT / K][K]; dS is no longer read
+        float sfx[RPT];
+        float acc = 0.f;
+#pragma unroll
+        for (int j = RPT - 1; j >= 0; --j) {
+            acc += sm.e[RPT * rg + j][kk];
+            sfx[j] = acc;
+        }
+        gtot[rg * K + kk] = acc;
+        __syncthreads();
+        float post = sm.deps[kk] * sm.eps[kk];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) post += (&sm.Y[0][0])[x * K + kk];
+#pragma unroll
+        for (int r = 0; r < NT / K; ++r) post += r > rg ? gtot[r * K + kk] : 0.f;
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+            const int64_t row = static_cast<int64_t>(n) * CT + RPT * rg + j;
+            if (row < T) a.dg[((b * T + row) * H + h) * K + kk] = post + sfx[j];
         }
     }
     if (t < CT) {
