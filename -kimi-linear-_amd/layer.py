@@ -157,6 +157,24 @@ class KimiDeltaAttention(nn.Module):
         self.g_norm = HeadwiseRMSNorm(H, V, config.rms_norm_eps)
         self.o_proj = nn.Linear(H * V, d, bias=bias)
         self.fp32_recurrent_state = True
+        self._wcat = None          # (key, weight, bias) of the fused input projection
+
+    def _input_weight(self):
+        """The six projections of x -- q, k, v, beta and the down-projections
+        of the forget gate and the output gate -- as one ``[N, d]`` weight (and
+        bias), so that a step runs one GEMM over x instead of six small ones.
+        The module keeps its own parameters (checkpoints load unchanged); the
+        concatenation is cached and rebuilt when any of them is replaced or
+        updated in place."""
+        mods = (self.in_proj_q, self.in_proj_k, self.in_proj_v, self.beta_proj,
+                self.gk_proj[0], self.og_proj[0])
+        key = tuple((m.weight.data_ptr(), m.weight._version, m.weight.dtype, m.weight.device) for m in mods)
+        if self._wcat is None or self._wcat[0] != key:
+            with torch.no_grad():
+                w = torch.cat([m.weight for m in mods], 0)
+                b = torch.cat([m.bias for m in mods]) if mods[0].bias is not None else None
+            self._wcat = (key, w, b)
+        return self._wcat[1], self._wcat[2]
 
     def _state_dtype(self, x):
         if self.fp32_recurrent_state and x.dtype in (torch.float16, torch.bfloat16):
@@ -171,9 +189,11 @@ class KimiDeltaAttention(nn.Module):
         return {"conv": {"q": z(H * K), "k": z(H * K), "v": z(H * V)}, "recurrent": None}
 
     def _projections(self, x, conv_cache=None, use_cache=False, conv_out=None):
-        """q, k, v, g, beta and the new conv cache (``kda.py:399-461``).
+        """q, k, v, g, beta, the new conv cache and the output gate's
+        down-projection of x (``kda.py:399-461``).
 
-        The five projections are library GEMMs; everything after them -- the
+        The projections of x are one library GEMM (:meth:`_input_weight`) and
+        the gate's up-projection a second; everything after them -- the
         three short convolutions with their cache, SiLU, the q/k L2 norms,
         the forget gate and beta -- is one fused kernel (:func:`kda_prep`).
         ``conv_out``: write the new conv cache into these tensors (may be
@@ -181,19 +201,25 @@ class KimiDeltaAttention(nn.Module):
         keep = max(self.conv_size - 1, 0)
         hist = conv_cache if (use_cache and conv_cache is not None and keep > 0) else None
         convs = (self.conv_q.conv, self.conv_k.conv, self.conv_v.conv)
+        H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+        w, b = self._input_weight()
+        y = torch.nn.functional.linear(x, w, b)
+        q_in, k_in, v_in, beta_logit, gk_low, og_low = torch.split(
+            y, (H * K, H * K, H * V, H, self.gk_proj[0].out_features, self.og_proj[0].out_features), dim=-1)
         q, k, v, g, beta, new_conv = kda_prep(
-            self.in_proj_q(x), self.in_proj_k(x), self.in_proj_v(x),
+            q_in, k_in, v_in,
             tuple(c.weight for c in convs), tuple(c.bias for c in convs),
-            self.gk_proj(x), self.A_log, self.dt_bias, self.beta_proj(x),
+            self.gk_proj[1](gk_low), self.A_log, self.dt_bias, beta_logit,
             num_heads=self.num_heads, head_dim=self.head_dim, value_head_dim=self.value_head_dim,
             l2_eps=self.l2norm_eps, hist=hist, hist_out=conv_out if use_cache else None,
             want_hist=use_cache and conv_out is None)
-        return q, k, v, g, beta, new_conv
+        return q, k, v, g, beta, new_conv, og_low
 
-    def _output(self, o_core, x):
+    def _output(self, o_core, og_low):
         """Head-wise RMSNorm, sigmoid output gate (one fused kernel,
-        :func:`kda_output`) and the output projection (``kda.py:464-470``)."""
-        gate = self.og_proj(x)
+        :func:`kda_output`) and the output projection (``kda.py:464-470``);
+        ``og_low`` is the output gate's down-projection of x."""
+        gate = self.og_proj[1](og_low)
         if gate.dtype != o_core.dtype:
             gate = gate.to(o_core.dtype)
         return self.o_proj(kda_output(o_core, gate, self.g_norm.weight, self.g_norm.eps))
@@ -208,13 +234,13 @@ class KimiDeltaAttention(nn.Module):
         the state per layer and token."""
         if x.shape[1] != 1:
             raise ValueError(f"decode_step_ takes one token, got x of shape {tuple(x.shape)}")
-        q, k, v, g, beta, _ = self._projections(x, conv_cache=state["conv"], use_cache=True,
+        q, k, v, g, beta, _, og_low = self._projections(x, conv_cache=state["conv"], use_cache=True,
                                                 conv_out=state["conv"])
         rec = state["recurrent"]
         if rec is None:
             raise ValueError("decode_step_ needs an allocated recurrent state (run a prefill first)")
         o_core, _ = kda_recurrent(q, k, v, g, beta, state=rec, state_dtype=rec.dtype, state_out=rec)
-        return self._output(o_core, x)
+        return self._output(o_core, og_low)
 
     def forward(self, x, state=None, use_cache=False):
         """x: [B, T, d]; ``state`` = {"conv": {"q", "k", "v"}, "recurrent"}.
@@ -223,7 +249,7 @@ class KimiDeltaAttention(nn.Module):
             state = self.init_state(x.shape[0], device=x.device, dtype=x.dtype)
         conv_cache = state["conv"] if state is not None else None
         rec = state["recurrent"] if state is not None else None
-        q, k, v, g, beta, new_conv = self._projections(x, conv_cache=conv_cache, use_cache=use_cache)
+        q, k, v, g, beta, new_conv, og_low = self._projections(x, conv_cache=conv_cache, use_cache=use_cache)
         B, T = x.shape[0], x.shape[1]
         sdtype = self._state_dtype(x)
         if use_cache and T == 1:
@@ -245,7 +271,7 @@ class KimiDeltaAttention(nn.Module):
                                             beta[:, body:], state=rec, state_dtype=sdtype)
                 o_core[:, body:] = o_tail
             new_rec = rec
-        out = self._output(o_core, x)
+        out = self._output(o_core, og_low)
         if use_cache:
             return out, {"conv": new_conv, "recurrent": new_rec}
         return out
