@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -55,7 +55,7 @@ class KdaBwdArgs(ctypes.Structure):
         ("d_o", ctypes.c_void_p), ("d_state_out", ctypes.c_void_p),
         ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dg", ctypes.c_void_p),
         ("dbeta", ctypes.c_void_p), ("dv", ctypes.c_void_p), ("d_state_in", ctypes.c_void_p),
-        ("workspace", ctypes.c_void_p), ("scale", ctypes.c_float),
+        ("workspace", ctypes.c_void_p), ("scale", ctypes.c_float), ("io_dtype", ctypes.c_int32),
     ]
 
 

@@ -85,6 +85,8 @@ int kda_chunkwise_bwd(const kda_bwd_args* a, void* stream) {
     if (a->B < 0 || a->T < 0 || a->H < 0 || a->K <= 0 || a->V <= 0) return KDA_ERR_BAD_SHAPE;
     if (a->B == 0 || a->H == 0) return KDA_OK;
     if (!kda::chunkwise_bwd_supported(a->K, a->V)) return KDA_ERR_UNSUPPORTED;
+    if (a->io_dtype != KDA_DTYPE_F32 && a->io_dtype != KDA_DTYPE_F16 && a->io_dtype != KDA_DTYPE_BF16)
+        return KDA_ERR_BAD_DTYPE;
     if (a->T > 0 && (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->ckpt || !a->d_o || !a->dq ||
                      !a->dk || !a->dg || !a->dbeta || !a->dv || !a->workspace))
         return KDA_ERR_NULL_POINTER;

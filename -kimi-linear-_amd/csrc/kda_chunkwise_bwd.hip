@@ -29,16 +29,18 @@
 //   1. bwd_pairs_kernel, one workgroup per (b, h, chunk): A, L and N of every
 //      chunk (functions of q, k, g and beta only).
 //   2. bwd_state_kernel, one workgroup per (b, h, VA state columns), the chunks
-//      in reverse: the chain above; it stores each chunk's dS_end and dP, dv
-//      and dS_0.  The next chunk's inputs are fetched into registers while
+//      in reverse: the chain above; it stores each chunk's dS_end, dP and dR
+//      (fp32) and dS_0.  The next chunk's inputs are fetched into registers while
 //      the current one is computed.
-//   3. bwd_chunk_kernel, one workgroup per (b, h, chunk): from S (checkpoint),
-//      dS_end, dP and dR the sums over all state columns (VT at a time) of
+//   3. bwd_chunk_kernel, one workgroup per (b, h, chunk): writes dv = dR; from
+//      S (checkpoint), dS_end, dP and dR the sums over all state columns (VT at a time) of
 //      dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain through the
 //      inverse, the pairwise-decay products and the reverse cumulative sum:
 //      complete dq, dk, dg and dbeta.
 // Rows past T read as zero inputs, which leave the state and every gradient
-// of the rows before T unchanged.  The chunk-sized products run on the fp32
+// of the rows before T unchanged.  q, k, v, dO and dq, dk, dv are in the
+// caller's activation dtype (fp32, fp16 or bf16; every product in fp32); g,
+// beta, the checkpoints, dg, dbeta and the state gradients are fp32.  The chunk-sized products run on the fp32
 // matrix cores (v_mfma_f32_16x16x4f32, no precision loss).
 #include "kda_common.h"
 #include "kda_launch.h"
@@ -53,13 +55,14 @@ constexpr int NT = 1024;        // threads per workgroup
 static_assert(CT * VT == NT && CT * CT == NT, "one output per thread for the chunk-sized products");
 
 // Workspace, per (b, h) and chunk (index cb = (b H + h) nck + n):
-// A, L, N [CT][CT], dS_end [K][V] and dP [CT][V], fp32.
+// A, L, N [CT][CT], dS_end [K][V], dP and dR [CT][V], fp32.
 struct BwdWs {
     float* A;
     float* L;
     float* N;
     float* dS;
     float* dP;
+    float* dR;
 };
 
 BwdWs ws_layout(void* base, int64_t BH, int64_t nck, int64_t K, int64_t V) {
@@ -71,6 +74,7 @@ BwdWs ws_layout(void* base, int64_t BH, int64_t nck, int64_t K, int64_t V) {
     w.N = p + 2 * mat;
     w.dS = p + 3 * mat;
     w.dP = w.dS + BH * nck * K * V;
+    w.dR = w.dP + BH * nck * CT * V;
     return w;
 }
 
@@ -110,11 +114,13 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
-template <int K>
+template <int K, typename TI>
 __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, const BwdWs ws) {
     static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
     constexpr int EPT = CT * K / NT, RSTEP = NT / K;
     __shared__ PairSmem<K> sm;
+    const TI* qp = static_cast<const TI*>(a.q);
+    const TI* kp = static_cast<const TI*>(a.k);
     const int64_t H = a.H, T = a.T;
     const int nck = static_cast<int>((T + CT - 1) / CT);
     const int64_t bh = blockIdx.x / nck, b = bh / H, h = bh % H;
@@ -129,8 +135,8 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
         float qv = 0.f, kv = 0.f, gv = 0.f;
         if (row < T) {
             const int64_t o = ((b * T + row) * H + h) * K + kk;
-            qv = a.q[o] * a.scale;
-            kv = a.k[o];
+            qv = Elem<TI>::ld(qp + o) * a.scale;
+            kv = Elem<TI>::ld(kp + o);
             gv = a.g[o];
         }
         sm.q[c][kk] = qv;
@@ -298,7 +304,7 @@ struct __align__(16) StateSmem {
     float eps[K];
 };
 
-template <int K, int VA>
+template <int K, int VA, typename TI>
 __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, const BwdWs ws) {
     constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
     constexpr int DPT = CT * VA / NT;       // dO elements per thread
@@ -309,6 +315,9 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
     constexpr int TPW = (NTS + 15) / 16;    // dS tiles per wave
     static_assert(RPT >= 1 && DPT >= 1 && SPT >= 1 && NDP <= 16, "thread mapping");
     __shared__ StateSmem<K, VA> sm;
+    const TI* qp = static_cast<const TI*>(a.q);
+    const TI* kp = static_cast<const TI*>(a.k);
+    const TI* dop = static_cast<const TI*>(a.d_o);
 
     const int64_t H = a.H, T = a.T, V = a.V;
     const int nva = static_cast<int>(V / VA);
@@ -323,16 +332,20 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         sm.dS[r][c] = a.d_state_out ? a.d_state_out[(bh * K + r) * V + v0 + c] : 0.f;
     }
 
-    float pq[RPT], pk[RPT], pg[RPT], pdo[DPT], pa = 0.f, pn = 0.f, pb = 0.f;
+    // fetched elements stay in the input dtype until they are staged: a
+    // conversion next to its load would wait for it
+    TI pq[RPT], pk[RPT], pdo[DPT];
+    float pg[RPT], pa = 0.f, pn = 0.f, pb = 0.f;
     auto fetch = [&](int n) {
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
             const int64_t row = static_cast<int64_t>(n) * CT + RPT * rg + j;
-            pq[j] = pk[j] = pg[j] = 0.f;
+            pq[j] = pk[j] = TI{};
+            pg[j] = 0.f;
             if (row < T) {
                 const int64_t o = ((b * T + row) * H + h) * K + x;
-                pq[j] = a.q[o];
-                pk[j] = a.k[o];
+                pq[j] = qp[o];
+                pk[j] = kp[o];
                 pg[j] = a.g[o];
             }
         }
@@ -340,7 +353,7 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         for (int j = 0; j < DPT; ++j) {
             const int e = t + NT * j;
             const int64_t row = static_cast<int64_t>(n) * CT + e / VA;
-            pdo[j] = row < T ? a.d_o[((b * T + row) * H + h) * V + v0 + e % VA] : 0.f;
+            pdo[j] = row < T ? dop[((b * T + row) * H + h) * V + v0 + e % VA] : TI{};
         }
         const int64_t cb = bh * nck + n;
         pa = ws.A[cb * CT * CT + t];
@@ -362,14 +375,14 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         for (int j = 0; j < RPT; ++j) {
             run += pg[j];
             cg[j] = run;
-            cq[j] = pq[j];
-            ck[j] = pk[j];
+            cq[j] = Elem<TI>::ld(&pq[j]);
+            ck[j] = Elem<TI>::ld(&pk[j]);
         }
         sm.tot[rg][x] = run;
 #pragma unroll
         for (int j = 0; j < DPT; ++j) {
             const int e = t + NT * j;
-            sm.dO[e / VA][e % VA] = pdo[j];
+            sm.dO[e / VA][e % VA] = Elem<TI>::ld(&pdo[j]);
         }
         sm.A[t / CT][t % CT] = pa;
         sm.N[t / CT][t % CT] = pn;
@@ -434,7 +447,7 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         }
         __syncthreads();
 
-        // dR = M^T dP = Diag(beta) N^T dP = dV
+        // dR = M^T dP = Diag(beta) N^T dP (= dV, which bwd_chunk_kernel writes out)
         if (w < NDP) {
             const int r0t = 16 * (w / VTL), c0t = 16 * (w % VTL);
             f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -445,8 +458,7 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
                 const int c = r0t + 4 * lg + j;
                 const float dr = acc[j] * sm.beta[c];
                 sm.dR[c][c0t + ln] = dr;
-                const int64_t row = static_cast<int64_t>(n) * CT + c;
-                if (row < T) a.dv[((b * T + row) * H + h) * V + v0 + c0t + ln] = dr;
+                ws.dR[(cb * CT + c) * V + v0 + c0t + ln] = dr;
             }
         }
         __syncthreads();
@@ -507,7 +519,7 @@ struct __align__(16) ChunkSmem {
 };
 static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
 
-template <int K>
+template <int K, typename TI>
 __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, const BwdWs ws) {
     static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
     constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
@@ -515,6 +527,13 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     constexpr int TPR = VT / SPT;           // threads per state row
     static_assert(NT / K * K <= CT * (CT + 1), "the row-group sums fit Y");
     __shared__ ChunkSmem<K> sm;
+    const TI* qp = static_cast<const TI*>(a.q);
+    const TI* kp = static_cast<const TI*>(a.k);
+    const TI* vp = static_cast<const TI*>(a.v);
+    const TI* dop = static_cast<const TI*>(a.d_o);
+    TI* dqp = static_cast<TI*>(a.dq);
+    TI* dkp = static_cast<TI*>(a.dk);
+    TI* dvp = static_cast<TI*>(a.dv);
 
     const int64_t H = a.H, T = a.T, V = a.V;
     const int nck = static_cast<int>((T + CT - 1) / CT);
@@ -537,8 +556,8 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         float qv = 0.f, kv = 0.f, gv = 0.f;
         if (row < T) {
             const int64_t o = ((b * T + row) * H + h) * K + kk;
-            qv = a.q[o] * scale;
-            kv = a.k[o];
+            qv = Elem<TI>::ld(qp + o) * scale;
+            kv = Elem<TI>::ld(kp + o);
             gv = a.g[o];
         }
         sm.q[c][kk] = qv;
@@ -580,7 +599,8 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     // dA += dO P^T, dM += dP R^T, d(q~*E) += dO S^T, d(k*E) -= dR S^T,
     // d(k*F) += P dS^T, deps += rowsum(dS * S).  The next step's tiles are
     // fetched into registers while the current one is computed.
-    float ps[SPT], pds[SPT], pv = 0.f, pdo = 0.f, pdp = 0.f, pdr = 0.f;
+    float ps[SPT], pds[SPT], pdp = 0.f, pdr = 0.f;
+    TI pv{}, pdo{};                         // converted when staged
     const int st_row = t / TPR, st_col = SPT * (t % TPR);
     const int tc = t / VT, tv = t % VT;
     auto fetch = [&](int vt) {
@@ -592,13 +612,13 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             pds[j] = ws.dS[o];
         }
         pdp = ws.dP[(cb * CT + tc) * V + v0 + tv];
+        pdr = ws.dR[(cb * CT + tc) * V + v0 + tv];
         const int64_t row = static_cast<int64_t>(n) * CT + tc;
-        pv = pdo = pdr = 0.f;
+        pv = pdo = TI{};
         if (row < T) {
             const int64_t o = ((b * T + row) * H + h) * V + v0 + tv;
-            pv = a.v[o];
-            pdo = a.d_o[o];
-            pdr = a.dv[o];
+            pv = vp[o];
+            pdo = dop[o];
         }
     };
     fetch(0);
@@ -618,10 +638,14 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             sm.S[st_row][st_col + j] = ps[j];
             sm.dS[st_row][st_col + j] = pds[j];
         }
-        sm.v[tc][tv] = pv;
-        sm.dO[tc][tv] = pdo;
+        sm.v[tc][tv] = Elem<TI>::ld(&pv);
+        sm.dO[tc][tv] = Elem<TI>::ld(&pdo);
         sm.dP[tc][tv] = pdp;
         sm.dR[tc][tv] = pdr;
+        {
+            const int64_t row = static_cast<int64_t>(n) * CT + tc;
+            if (row < T) Elem<TI>::st(dvp + ((b * T + row) * H + h) * V + static_cast<int64_t>(vt) * VT + tv, pdr);
+        }
         if (vt + 1 < nvt) fetch(vt + 1);
         __syncthreads();
 
@@ -799,8 +823,8 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             const int64_t row = static_cast<int64_t>(n) * CT + c;
             if (row < T) {
                 const int64_t o = ((b * T + row) * H + h) * K + ekk;
-                a.dq[o] = dqt * scale;
-                a.dk[o] = dk;
+                Elem<TI>::st(dqp + o, dqt * scale);
+                Elem<TI>::st(dkp + o, dk);
             }
         }
         (&sm.Y[0][0])[((w / KTL) * 4 + lg) * K + ekk] = last;
@@ -837,27 +861,39 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     }
 }
 
-template <int K>
+template <int K, typename TI>
 int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
     const int64_t BH = a.B * a.H;
     const int64_t nck = (a.T + CT - 1) / CT;
     const BwdWs ws = ws_layout(a.workspace, BH, nck, a.K, a.V);
     if (nck > 0) {
-        hipLaunchKernelGGL((bwd_pairs_kernel<K>), dim3(static_cast<unsigned>(BH * nck)), dim3(NT), 0, stream, a, ws);
+        hipLaunchKernelGGL((bwd_pairs_kernel<K, TI>), dim3(static_cast<unsigned>(BH * nck)), dim3(NT), 0, stream,
+                           a, ws);
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
     if (a.V % 64 == 0)
-        hipLaunchKernelGGL((bwd_state_kernel<K, 64>), dim3(static_cast<unsigned>(BH * (a.V / 64))), dim3(NT), 0,
+        hipLaunchKernelGGL((bwd_state_kernel<K, 64, TI>), dim3(static_cast<unsigned>(BH * (a.V / 64))), dim3(NT), 0,
                            stream, a, ws);
     else
-        hipLaunchKernelGGL((bwd_state_kernel<K, 32>), dim3(static_cast<unsigned>(BH * (a.V / 32))), dim3(NT), 0,
+        hipLaunchKernelGGL((bwd_state_kernel<K, 32, TI>), dim3(static_cast<unsigned>(BH * (a.V / 32))), dim3(NT), 0,
                            stream, a, ws);
     if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     if (nck > 0) {
-        hipLaunchKernelGGL((bwd_chunk_kernel<K>), dim3(static_cast<unsigned>(BH * nck)), dim3(NT), 0, stream, a, ws);
+        hipLaunchKernelGGL((bwd_chunk_kernel<K, TI>), dim3(static_cast<unsigned>(BH * nck)), dim3(NT), 0, stream,
+                           a, ws);
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
     return KDA_OK;
+}
+
+template <int K>
+int launch_bwd_typed(const kda_bwd_args& a, hipStream_t stream) {
+    switch (a.io_dtype) {
+        case KDA_DTYPE_F32: return launch_bwd<K, float>(a, stream);
+        case KDA_DTYPE_F16: return launch_bwd<K, _Float16>(a, stream);
+        case KDA_DTYPE_BF16: return launch_bwd<K, bf16_t>(a, stream);
+        default: return KDA_ERR_BAD_DTYPE;
+    }
 }
 
 }  // namespace
@@ -868,14 +904,14 @@ bool chunkwise_bwd_supported(int64_t K, int64_t V) {
 
 int64_t chunkwise_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
     const int64_t nck = (T + CT - 1) / CT;
-    return B * H * nck * (3 * CT * CT + K * V + CT * V) * static_cast<int64_t>(sizeof(float));
+    return B * H * nck * (3 * CT * CT + K * V + 2 * CT * V) * static_cast<int64_t>(sizeof(float));
 }
 
 int chunkwise_bwd_launch(const kda_bwd_args& a, hipStream_t stream) {
     switch (a.K) {
-        case 32: return launch_bwd<32>(a, stream);
-        case 64: return launch_bwd<64>(a, stream);
-        case 128: return launch_bwd<128>(a, stream);
+        case 32: return launch_bwd_typed<32>(a, stream);
+        case 64: return launch_bwd_typed<64>(a, stream);
+        case 128: return launch_bwd_typed<128>(a, stream);
         default: return KDA_ERR_UNSUPPORTED;
     }
 }

@@ -221,17 +221,23 @@ def _f32c(x: torch.Tensor) -> torch.Tensor:
 
 
 def _chunkwise_backward(q, k, v, g, beta, ckpt, d_o, d_state, need_d_state_in):
-    """dq, dk, dv, dg, dbeta (and dS_0) in fp32 from the native backward."""
+    """dq, dk, dv (in v's dtype), dg, dbeta (fp32) and dS_0 from the native backward.
+
+    q, k and v share v's dtype (the forward read them so); the kernels read
+    them, and ``d_o`` in the same dtype, as they are and write dq, dk, dv in it."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device
-    q, k, v, g, beta, d_o = (_f32c(x) for x in (q, k, v, g, beta, d_o))
+    io = v.dtype if v.dtype in _DTYPE_CODE else torch.float32
+    q, k, v = (x.to(io).contiguous() for x in (q, k, v))
+    d_o = d_o.to(io).contiguous()
+    g, beta = _f32c(g), _f32c(beta)
     d_state = _f32c(d_state) if d_state is not None else None
-    dq = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
+    dq = torch.empty(B, T, H, K, device=dev, dtype=io)
     dk = torch.empty_like(dq)
-    dg = torch.empty_like(dq)
+    dv = torch.empty(B, T, H, V, device=dev, dtype=io)
+    dg = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
     dbeta = torch.empty(B, T, H, device=dev, dtype=torch.float32)
-    dv = torch.empty(B, T, H, V, device=dev, dtype=torch.float32)
     ds0 = torch.empty(B, H, K, V, device=dev, dtype=torch.float32) if need_d_state_in else None
     lib = _native.load()
     ws = torch.empty(max(int(lib.kda_chunkwise_bwd_workspace_size(B, T, H, K, V)), 1),
@@ -246,6 +252,7 @@ def _chunkwise_backward(q, k, v, g, beta, ckpt, d_o, d_state, need_d_state_in):
     args.d_state_in = ds0.data_ptr() if ds0 is not None else None
     args.workspace = ws.data_ptr()
     args.scale = float(K) ** -0.5
+    args.io_dtype = _DTYPE_CODE[io]
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
         status = lib.kda_chunkwise_bwd(ctypes.byref(args), ctypes.c_void_p(stream))

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 4
+#define KDA_ABI_VERSION 5
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -120,34 +120,36 @@ int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
  * kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 
-/* Every tensor is contiguous fp32 in the forward layout: q, k, g, dq, dk, dg
+/* Every tensor is contiguous in the forward layout: q, k, g, dq, dk, dg
  * [B, T, H, K]; v, d_o, dv [B, T, H, V]; beta, dbeta [B, T, H]; states
- * [B, H, K, V].  workspace: device memory of at least
+ * [B, H, K, V].  q, k, v, d_o, dq, dk and dv are in io_dtype (a kda_dtype);
+ * g, beta, ckpt, dg, dbeta and the state gradients are fp32.  workspace: device memory of at least
  * kda_chunkwise_bwd_workspace_size(B, T, H, K, V) bytes, 16-byte aligned (its
  * contents on entry do not matter; calls that share one workspace must not
  * overlap).  K in {32, 64, 128}, V a multiple of 32, any T >= 0. */
 typedef struct kda_bwd_args {
     int64_t B, T, H, K, V;
-    const float* q;                /* the forward's inputs (q unscaled)        */
-    const float* k;
-    const float* v;
+    const void* q;                 /* the forward's inputs (q unscaled)        */
+    const void* k;
+    const void* v;
     const float* g;
     const float* beta;
     const float* ckpt;             /* from kda_chunkwise_fwd_ckpt on the same inputs */
-    const float* d_o;              /* dL/do                                      */
+    const void* d_o;               /* dL/do                                      */
     const float* d_state_out;      /* dL/d(final state), or NULL for zeros       */
-    float* dq;                     /* [B, T, H, K] */
-    float* dk;
+    void* dq;                      /* [B, T, H, K] */
+    void* dk;
     float* dg;
     float* dbeta;                  /* [B, T, H]    */
-    float* dv;                     /* [B, T, H, V] */
+    void* dv;                      /* [B, T, H, V] */
     float* d_state_in;             /* dL/d(initial state) [B, H, K, V], or NULL   */
     void* workspace;
     float scale;                   /* the forward's q multiplier                  */
+    int32_t io_dtype;              /* kda_dtype of q, k, v, d_o, dq, dk, dv       */
 } kda_bwd_args;
 
 /* Bytes of workspace kda_chunkwise_bwd needs: per (b, h) and 32-token chunk,
- * (3 * 32 * 32 + K * V + 32 * V) floats.  0 for a bad or empty shape. */
+ * (3 * 32 * 32 + K * V + 2 * 32 * V) floats.  0 for a bad or empty shape. */
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 
 int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);

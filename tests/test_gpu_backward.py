@@ -8,7 +8,7 @@ state and the initial state -- is exercised.
 
 Tolerance: relative L2 error <= 2e-3 per gradient for fp32 inputs (the
 forward's state checkpoints come from the fp16-MFMA forward kernel, relative
-error ~1e-4), 2e-2 for fp16 inputs (gradients rounded to fp16).
+error ~1e-4), 2e-2 for fp16 and bf16 inputs (gradients rounded to that dtype).
 """
 
 from __future__ import annotations
@@ -84,10 +84,12 @@ def test_backward_fp32(kda_pkg, wl, B, T, H, K, V, chunk, state):
         assert err <= 2e-3, (name, err)
 
 
-def test_backward_fp16(kda_pkg, wl):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_backward_half(kda_pkg, wl, dtype):
+    """q, k, v, d_o and dq, dk, dv in the activation dtype, read and written as such."""
     B, T, H, K, V = 1, 96, 2, 64, 64
-    print(f"backward fp16 B={B} T={T} H={H} K={K} V={V}", flush=True)
-    xs, wo, ws = _case(wl, B, T, H, K, V, seed=5, dtype=torch.float16, state=True)
+    print(f"backward {dtype} B={B} T={T} H={H} K={K} V={V}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=5, dtype=dtype, state=True)
     ref = _ref_grads(xs, wo, ws, 32)
     got = _native_grads(kda_pkg, xs, wo, ws, 32)
     for name, a, r in zip(NAMES, got, ref):
