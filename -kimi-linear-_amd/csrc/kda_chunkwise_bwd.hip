@@ -546,34 +546,66 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     const int kk = t % K, rg = t / K;
 
     // ---------------------------------------------------------------- loads
-    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk
-    float gl[RPT];
+    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk.  The
+    // first column step's tiles are fetched right behind these loads.
+    float ql[RPT], kl[RPT], gl[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+        const int64_t row = static_cast<int64_t>(n) * CT + RPT * rg + j;
+        ql[j] = kl[j] = gl[j] = 0.f;
+        if (row < T) {
+            const int64_t o = ((b * T + row) * H + h) * K + kk;
+            ql[j] = Elem<TI>::ld(qp + o) * scale;
+            kl[j] = Elem<TI>::ld(kp + o);
+            gl[j] = a.g[o];
+        }
+    }
+    const float al = ws.A[cb * CT * CT + t], ll = ws.L[cb * CT * CT + t], nl = ws.N[cb * CT * CT + t];
+    float bl = 0.f;
+    if (t < CT) {
+        const int64_t row = static_cast<int64_t>(n) * CT + t;
+        bl = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
+    }
+
+    float ps[SPT], pds[SPT], pdp = 0.f, pdr = 0.f;
+    TI pv{}, pdo{};                         // converted when staged
+    const int st_row = t / TPR, st_col = SPT * (t % TPR);
+    const int tc = t / VT, tv = t % VT;
+    auto fetch = [&](int vt) {
+        const int64_t v0 = static_cast<int64_t>(vt) * VT;
+#pragma unroll
+        for (int j = 0; j < SPT; ++j) {
+            const int64_t o = (cb * K + st_row) * V + v0 + st_col + j;
+            ps[j] = a.ckpt[o];
+            pds[j] = ws.dS[o];
+        }
+        pdp = ws.dP[(cb * CT + tc) * V + v0 + tv];
+        pdr = ws.dR[(cb * CT + tc) * V + v0 + tv];
+        const int64_t row = static_cast<int64_t>(n) * CT + tc;
+        pv = pdo = TI{};
+        if (row < T) {
+            const int64_t o = ((b * T + row) * H + h) * V + v0 + tv;
+            pv = vp[o];
+            pdo = dop[o];
+        }
+    };
+    fetch(0);
+
     float run = 0.f;
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
         const int c = RPT * rg + j;
-        const int64_t row = static_cast<int64_t>(n) * CT + c;
-        float qv = 0.f, kv = 0.f, gv = 0.f;
-        if (row < T) {
-            const int64_t o = ((b * T + row) * H + h) * K + kk;
-            qv = Elem<TI>::ld(qp + o) * scale;
-            kv = Elem<TI>::ld(kp + o);
-            gv = a.g[o];
-        }
-        sm.q[c][kk] = qv;
-        sm.k[c][kk] = kv;
-        run += gv;
+        sm.q[c][kk] = ql[j];
+        sm.k[c][kk] = kl[j];
+        run += gl[j];
         gl[j] = run;
     }
     float* tot = &sm.Y[0][0];               // [NT / K][K]: per row group, the sum of its g
     tot[rg * K + kk] = run;
-    if (t < CT) {
-        const int64_t row = static_cast<int64_t>(n) * CT + t;
-        sm.beta[t] = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
-    }
-    sm.A[t / CT][t % CT] = ws.A[cb * CT * CT + t];
-    sm.L[t / CT][t % CT] = ws.L[cb * CT * CT + t];
-    sm.N[t / CT][t % CT] = ws.N[cb * CT * CT + t];
+    if (t < CT) sm.beta[t] = bl;
+    sm.A[t / CT][t % CT] = al;
+    sm.L[t / CT][t % CT] = ll;
+    sm.N[t / CT][t % CT] = nl;
     __syncthreads();
 
     // ------------------------------------------- cumulative decays, eps
@@ -599,29 +631,6 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     // dA += dO P^T, dM += dP R^T, d(q~*E) += dO S^T, d(k*E) -= dR S^T,
     // d(k*F) += P dS^T, deps += rowsum(dS * S).  The next step's tiles are
     // fetched into registers while the current one is computed.
-    float ps[SPT], pds[SPT], pdp = 0.f, pdr = 0.f;
-    TI pv{}, pdo{};                         // converted when staged
-    const int st_row = t / TPR, st_col = SPT * (t % TPR);
-    const int tc = t / VT, tv = t % VT;
-    auto fetch = [&](int vt) {
-        const int64_t v0 = static_cast<int64_t>(vt) * VT;
-#pragma unroll
-        for (int j = 0; j < SPT; ++j) {
-            const int64_t o = (cb * K + st_row) * V + v0 + st_col + j;
-            ps[j] = a.ckpt[o];
-            pds[j] = ws.dS[o];
-        }
-        pdp = ws.dP[(cb * CT + tc) * V + v0 + tv];
-        pdr = ws.dR[(cb * CT + tc) * V + v0 + tv];
-        const int64_t row = static_cast<int64_t>(n) * CT + tc;
-        pv = pdo = TI{};
-        if (row < T) {
-            const int64_t o = ((b * T + row) * H + h) * V + v0 + tv;
-            pv = vp[o];
-            pdo = dop[o];
-        }
-    };
-    fetch(0);
 
     constexpr int KTL = K / 16;
     const bool tw = w < 2 * KTL;

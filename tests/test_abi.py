@@ -50,11 +50,13 @@ def test_abi_version_and_status_strings(native):
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
-def test_struct_layout_matches_header(native, tmp_path):
-    fields = [name for name, _ in native.KdaFwdArgs._fields_]
+@pytest.mark.parametrize("struct,cname", [("KdaFwdArgs", "kda_fwd_args"), ("KdaBwdArgs", "kda_bwd_args")])
+def test_struct_layout_matches_header(native, tmp_path, struct, cname):
+    cls = getattr(native, struct)
+    fields = [name for name, _ in cls._fields_]
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "kda_hip.h"',
-             "int main(void) {", '  printf("size %zu\\n", sizeof(kda_fwd_args));']
-    lines += [f'  printf("{f} %zu\\n", offsetof(kda_fwd_args, {f}));' for f in fields]
+             "int main(void) {", f'  printf("size %zu\\n", sizeof({cname}));']
+    lines += [f'  printf("{f} %zu\\n", offsetof({cname}, {f}));' for f in fields]
     lines += ["  return 0;", "}"]
     src = tmp_path / "layout.c"
     src.write_text("\n".join(lines))
@@ -62,9 +64,45 @@ def test_struct_layout_matches_header(native, tmp_path):
     subprocess.run(["gcc", f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     got = dict(line.split() for line in out if line)
-    assert int(got["size"]) == ctypes.sizeof(native.KdaFwdArgs)
+    assert int(got["size"]) == ctypes.sizeof(cls)
     for f in fields:
-        assert int(got[f]) == getattr(native.KdaFwdArgs, f).offset, f
+        assert int(got[f]) == getattr(cls, f).offset, f
+
+
+def test_backward_workspace_size(native):
+    """(3 * 32 * 32 + K * V + 2 * 32 * V) floats per (b, h) and 32-token chunk; 0 for bad shapes."""
+    size = native.load().kda_chunkwise_bwd_workspace_size
+    assert size(8, 4096, 16, 128, 128) == 8 * 16 * 128 * (3 * 1024 + 128 * 128 + 64 * 128) * 4
+    assert size(2, 80, 3, 64, 32) == 2 * 3 * 3 * (3 * 1024 + 64 * 32 + 64 * 32) * 4    # ragged: 3 chunks
+    assert size(1, 0, 1, 64, 64) == 0
+    assert size(-1, 16, 1, 64, 64) == 0 and size(1, 16, 1, 0, 64) == 0
+
+
+def test_backward_host_validation_codes(native):
+    lib = native.load()
+
+    def bargs(**kw):
+        a = native.KdaBwdArgs()
+        a.B, a.T, a.H, a.K, a.V = 1, 64, 1, 64, 64
+        fake = 0x100000   # never dereferenced: every case here fails validation first
+        for f in ("q", "k", "v", "g", "beta", "ckpt", "d_o", "dq", "dk", "dg", "dbeta", "dv", "workspace"):
+            setattr(a, f, fake)
+        a.scale, a.io_dtype = 0.125, native.DTYPE_F32
+        for name, val in kw.items():
+            setattr(a, name, val)
+        return ctypes.byref(a)
+
+    call = lib.kda_chunkwise_bwd
+    assert call(None, None) == 1
+    assert call(bargs(T=-1), None) == 2
+    assert call(bargs(io_dtype=9), None) == 3
+    assert call(bargs(K=48), None) == 4
+    assert call(bargs(V=48), None) == 4
+    assert call(bargs(workspace=None), None) == 1
+    assert call(bargs(dq=None), None) == 1
+    assert call(bargs(ckpt=None), None) == 1
+    assert call(bargs(B=0), None) == 0                                   # empty: no launch
+    assert call(bargs(T=0), None) == 0                                   # no d_state_in: nothing to do
 
 
 def _args(native, **kw):
