@@ -28,11 +28,33 @@ namespace {
 // rows with buffer loads/stores; otherwise element by element in any dtype.
 // A separate instantiation keeps the generic path's registers out of the
 // fast one.
-template <int K, int NW, bool VEC>
+// Sum of x over the 8 lanes that share l & 7 (all-reduce): row_ror:8, then
+// the permlane swaps of bits 4 and 5.
+__device__ __forceinline__ float lanegroup8_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return x;
+}
+
+// Lane l of a wave holds 4 adjacent state columns (column group l % CPL) of
+// RPL = K CPL / 64 adjacent rows (row group l / CPL); the K-reductions are
+// sums over the lanes of one column group.
+template <int K, int NW, int CPL, bool VEC>
 __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a) {
-    constexpr int RPL = K / 16;                 // rows per lane
-    constexpr int VT = 16 * NW;                 // columns per workgroup
-    static_assert(K % 16 == 0 && RPL >= 1, "K must be a multiple of 16");
+    static_assert(CPL == 4 || CPL == 8, "column groups per wave");
+    constexpr int RPL = K * CPL / 64;           // rows per lane
+    constexpr int VT = 4 * CPL * NW;            // columns per workgroup
+    static_assert(K % (64 / CPL) == 0 && RPL >= 1, "K must be a multiple of the row groups");
+    auto ksum = [](float x) { return CPL == 4 ? rowgroup_sum(x) : lanegroup8_sum(x); };
 
     __shared__ float s_q[K], s_k[K], s_a[K];
 
@@ -46,9 +68,9 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int cg = lane & 3, rg = lane >> 2;
+    const int cg = lane % CPL, rg = lane / CPL;
     const int r0 = RPL * rg;
-    const int64_t col0 = static_cast<int64_t>(vt) * VT + 16 * wave + 4 * cg;
+    const int64_t col0 = static_cast<int64_t>(vt) * VT + 4 * CPL * wave + 4 * cg;
     const int64_t sbase = (b * H + h) * static_cast<int64_t>(K) * V;
 
     // fp32 state rows go through one buffer descriptor per head: the lane
@@ -123,10 +145,10 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            u[c] = rowgroup_sum(u[c]);
-            rr[c] = rowgroup_sum(rr[c]);
+            u[c] = ksum(u[c]);
+            rr[c] = ksum(rr[c]);
         }
-        qk = rowgroup_sum(qk);
+        qk = ksum(qk);
 
         float d[4];
 #pragma unroll
@@ -172,23 +194,29 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-template <int K, int NW>
+template <int K, int NW, int CPL>
 int launch_k_nw(const kda_fwd_args& a, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(a.B * a.H * (a.V / (16 * NW)))), block(64 * NW);
+    const dim3 grid(static_cast<unsigned>(a.B * a.H * (a.V / (4 * CPL * NW)))), block(64 * NW);
     const bool vec = (a.V & 3) == 0 && a.state_out_dtype == KDA_DTYPE_F32 && aligned16(a.state_out) &&
                      (a.state_in == nullptr || (a.state_in_dtype == KDA_DTYPE_F32 && aligned16(a.state_in)));
     if (vec)
-        hipLaunchKernelGGL((recurrent_kernel<K, NW, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, true>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((recurrent_kernel<K, NW, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, false>), grid, block, 0, stream, a);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
 template <int K>
 int launch_k(const kda_fwd_args& a, hipStream_t stream) {
-    if (a.V % 64 == 0) return launch_k_nw<K, 4>(a, stream);
-    if (a.V % 32 == 0) return launch_k_nw<K, 2>(a, stream);
-    return launch_k_nw<K, 1>(a, stream);
+    // K <= 128: 32 columns per one-wave workgroup, K / 8 x 4 state elements
+    // per lane (at K 128, 128 VGPRs: a B=64 H=16 V=128 step's 4096 waves all
+    // resident at once); K 256: 16 columns a wave, K / 16 x 4 per lane.
+    if constexpr (K <= 128) {
+        if (a.V % 32 == 0) return launch_k_nw<K, 1, 8>(a, stream);
+    }
+    if (a.V % 64 == 0) return launch_k_nw<K, 4, 4>(a, stream);
+    if (a.V % 32 == 0) return launch_k_nw<K, 2, 4>(a, stream);
+    return launch_k_nw<K, 1, 4>(a, stream);
 }
 
 }  // namespace
