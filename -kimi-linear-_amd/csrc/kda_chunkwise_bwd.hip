@@ -767,7 +767,12 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     }
 
     // ---------------------------- per (row, channel): dq, dk and dG
-    // The lane's rows c0 .. c0 + 3 share the decay products through a
+    // Pairs of rows in different 16-row blocks (i < 16 <= c) factor their
+    // decay through row 16, exp(G_c - G_i) = exp(G_c - G_16) exp(G_16 - G_i),
+    // both <= 1: plain products on the matrix cores whose 16 x 16 output tile
+    // is the wave's own element tile (block 1's waves: the row-side sums over
+    // block 0; block 0's waves: the column-side sums over block 1).  Within a
+    // block, the lane's rows c0 .. c0 + 3 share the decay products through a
     // reference row: for i <= c0, exp(G_c - G_i) = exp(G_c - G_c0) exp(G_c0 - G_i),
     // and for c2 >= c3 = c0 + 3, exp(G_c2 - G_c) = exp(G_c2 - G_c3) exp(G_c3 - G_c),
     // every factor <= 1; the few pairs between the lane's own rows are direct.
@@ -779,8 +784,32 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         const float g0 = gcol(c0), g3 = gcol(c3);
         float t1[4] = {0.f, 0.f, 0.f, 0.f}, t2[4] = {0.f, 0.f, 0.f, 0.f};
         float t3[4] = {0.f, 0.f, 0.f, 0.f}, t4[4] = {0.f, 0.f, 0.f, 0.f};
-        // row side, i <= c0 (dA and dM vanish above the diagonal)
-        for (int i = 0; i <= c0; ++i) {
+        // across the blocks, through row 16 (x0: the tile's first channel)
+        const int x0 = ekk - ln;
+        const float g16 = gcol(16);
+        f4 oa = {0.f, 0.f, 0.f, 0.f}, om = oa;
+        if (ert == 16) {
+            oa = tile_mm<16>([&](int r, int i) { return sm.dA[16 + r][i]; },
+                             [&](int i, int x) { return sm.k[i][x0 + x] * __expf(sm.gc[16][x0 + x] - sm.gc[i][x0 + x]); },
+                             ln, lg, oa);
+            om = tile_mm<16>([&](int r, int i) { return sm.dM[16 + r][i]; },
+                             [&](int i, int x) { return sm.k[i][x0 + x] * __expf(sm.gc[16][x0 + x] - sm.gc[i][x0 + x]); },
+                             ln, lg, om);
+        } else {
+            oa = tile_mm<16>([&](int r, int c2) { return sm.dA[16 + c2][r]; },
+                             [&](int c2, int x) {
+                                 return sm.q[16 + c2][x0 + x] * __expf(sm.gc[16 + c2][x0 + x] - sm.gc[16][x0 + x]);
+                             },
+                             ln, lg, oa);
+            om = tile_mm<16>([&](int r, int c2) { return sm.dM[16 + c2][r]; },
+                             [&](int c2, int x) {
+                                 return sm.beta[16 + c2] * sm.k[16 + c2][x0 + x] *
+                                        __expf(sm.gc[16 + c2][x0 + x] - sm.gc[16][x0 + x]);
+                             },
+                             ln, lg, om);
+        }
+        // row side within the block, ert <= i <= c0 (dA and dM vanish above the diagonal)
+        for (int i = ert; i <= c0; ++i) {
             const float kh = kcol(i) * __expf(g0 - gcol(i));
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -788,8 +817,8 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
                 t3[j] += sm.dM[c0 + j][i] * kh;
             }
         }
-        // column side, c2 >= c3
-        for (int c2 = c3; c2 < CT; ++c2) {
+        // column side within the block, c3 <= c2 < ert + 16
+        for (int c2 = c3; c2 < ert + 16; ++c2) {
             const float hh = __expf(gcol(c2) - g3);
             const float qh = qcol(c2) * hh, kh = sm.beta[c2] * kcol(c2) * hh;
 #pragma unroll
@@ -805,6 +834,15 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             const float gcc = gcol(c);
             const float f0 = __expf(gcc - g0), f3 = __expf(g3 - gcc);
             float T1 = f0 * t1[j], T3 = f0 * t3[j], T2 = f3 * t2[j], T4 = f3 * t4[j];
+            if (ert == 16) {
+                const float e = __expf(gcc - g16);
+                T1 += e * oa[j];
+                T3 += e * om[j];
+            } else {
+                const float e = __expf(g16 - gcc);
+                T2 += e * oa[j];
+                T4 += e * om[j];
+            }
             // the lane's own rows: c0 < i <= c (row side), c <= c2 < c3 (column side)
 #pragma unroll
             for (int x = 1; x < 4; ++x) {
