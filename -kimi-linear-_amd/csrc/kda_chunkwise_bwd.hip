@@ -117,7 +117,8 @@ __device__ __forceinline__ float row16_sum(float x) {
 template <int K, typename TI>
 __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, const BwdWs ws) {
     static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
-    constexpr int EPT = CT * K / NT, RSTEP = NT / K;
+    constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
+    static_assert(NT / K * K <= CT * (CT + 1), "the row-group sums fit Y");
     __shared__ PairSmem<K> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
@@ -127,10 +128,15 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
     const int n = static_cast<int>(blockIdx.x % nck);
     const int64_t cb = bh * nck + n;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
-    const int kk = t % K, r0 = t / K;
+    const int kk = t % K, rg = t / K;
 
-    for (int j = 0; j < EPT; ++j) {
-        const int c = r0 + RSTEP * j;
+    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk; G from
+    // per-thread partial sums and the row-group totals (in Y, free here)
+    float gl[RPT];
+    float run = 0.f;
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+        const int c = RPT * rg + j;
         const int64_t row = static_cast<int64_t>(n) * CT + c;
         float qv = 0.f, kv = 0.f, gv = 0.f;
         if (row < T) {
@@ -141,19 +147,22 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
         }
         sm.q[c][kk] = qv;
         sm.k[c][kk] = kv;
-        sm.gc[c][kk] = gv;
+        run += gv;
+        gl[j] = run;
     }
+    float* tot = &sm.Y[0][0];
+    tot[rg * K + kk] = run;
     if (t < CT) {
         const int64_t row = static_cast<int64_t>(n) * CT + t;
         sm.beta[t] = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
     }
     __syncthreads();
-    if (t < K) {
-        float run = 0.f;
-        for (int c = 0; c < CT; ++c) {
-            run += sm.gc[c][t];
-            sm.gc[c][t] = run;
-        }
+    {
+        float pre = 0.f;
+#pragma unroll
+        for (int r = 0; r < NT / K; ++r) pre += r < rg ? tot[r * K + kk] : 0.f;
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) sm.gc[RPT * rg + j][kk] = pre + gl[j];
     }
     __syncthreads();
 
