@@ -742,9 +742,10 @@ struct Kern {
 
     // One chunk (blocks blk, blk + 1) of the chain for this wave's 16 state
     // columns; the v loads of the same blocks one superstep later are issued
-    // into vraw0 / vraw1.
+    // into vraw0 / vraw1.  rp (or null): rows [0, 32) of the chunk's
+    // R = V - (k * E) S and rows [32, 64) of P, in fp32, for the backward.
     __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw0)[4], uint32_t (&vraw1)[4],
-                            f4 (&S)[KT], int64_t col0, uint32_t ocol) const {
+                            f4 (&S)[KT], int64_t col0, uint32_t ocol, float* rp) const {
         use_here(vraw0);
         use_here(vraw1);
         f4 R0, R1;
@@ -789,13 +790,30 @@ struct Kern {
         // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0)
         R0 -= Z0;
         R1 -= Z1;
+        const int64_t V = a.V, rc = col0 + ocol;
+        if (rp) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                rp[(4 * lg + j) * V + rc] = R0[j];
+                rp[(16 + 4 * lg + j) * V + rc] = R1[j];
+            }
+        }
         const Split4 r0(R0);
-        const Split4 p0(mm4(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg), r0.hi,
-                            r0.lo, f4{0.f, 0.f, 0.f, 0.f}));
+        const f4 P0 = mm4(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg), r0.hi, r0.lo,
+                          f4{0.f, 0.f, 0.f, 0.f});
+        const Split4 p0(P0);
         R1 = mm4(frag16(&co.GH[0][0], RP, ln, lg), frag16(&co.GL[0][0], RP, ln, lg), p0.hi, p0.lo, R1);
         const Split4 r1(R1);
-        const Split4 p1(mm4(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg), r1.hi,
-                            r1.lo, f4{0.f, 0.f, 0.f, 0.f}));
+        const f4 P1 = mm4(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg), r1.hi, r1.lo,
+                          f4{0.f, 0.f, 0.f, 0.f});
+        const Split4 p1(P1);
+        if (rp) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                rp[(32 + 4 * lg + j) * V + rc] = P0[j];
+                rp[(48 + 4 * lg + j) * V + rc] = P1[j];
+            }
+        }
         // O = scale (q * E) S + A P
         O0 *= scale;
         O1 *= scale;
@@ -895,10 +913,12 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             for (int cj = 0; cj < NCH; ++cj) {
                 const int cc = NCH * s + cj;
                 if (s >= 0 && cc < ncc) {
-                    // the state before chunk cc, for the backward
-                    if (ckpt) store_state_t<KT>(S, ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K) * V,
-                                                (4 * kn.lg) * V + col, V);
-                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol);
+                    // for the backward: the state before chunk cc, then its R and P
+                    float* ck = ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K + 2 * CB * BT) * V
+                                     : nullptr;
+                    if (ck) store_state_t<KT>(S, ck, (4 * kn.lg) * V + col, V);
+                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol,
+                               ck ? ck + static_cast<int64_t>(K) * V : nullptr);
                 }
                 __syncthreads();
             }

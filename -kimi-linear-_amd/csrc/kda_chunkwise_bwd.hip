@@ -2,8 +2,9 @@
 //
 // Gradient of kda_chunkwise (kimi_linear/kda.py:58-185), whose reference is
 // differentiated by autograd (training: scripts/train_musicgpt_fp16.py:519-523).
-// The forward is re-evaluated chunk by chunk from the state checkpoints that
-// kda_chunkwise_fwd_ckpt writes (the state before every CT = 32-token chunk).
+// The forward is re-evaluated chunk by chunk from the checkpoints that
+// kda_chunkwise_fwd_ckpt writes: per CT = 32-token chunk, the state before it
+// and the chunk's R and P (below), which the forward computes anyway.
 //
 // Per (b, h) and chunk, rows c, i in [0, CT), channels k, state columns v:
 //   G = in-chunk cumulative sum of g,  E = exp(G),  F = exp(G_last - G),
@@ -33,7 +34,8 @@
 //      (fp32) and dS_0.  The next chunk's inputs are fetched into registers while
 //      the current one is computed.
 //   3. bwd_chunk_kernel, one workgroup per (b, h, chunk): writes dv = dR; from
-//      S (checkpoint), dS_end, dP and dR the sums over all state columns (VT at a time) of
+//      S, R, P (checkpoint), dS_end, dP and dR the sums over all state columns
+//      (VT at a time) of
 //      dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain through the
 //      inverse, the pairwise-decay products and the reverse cumulative sum:
 //      complete dq, dk, dg and dbeta.
@@ -508,7 +510,6 @@ struct __align__(16) ChunkSmem {
     float e[CT][KP];            // exp(G); then, per element, dG
     float S[K][VP];             // state at the chunk start (checkpoint), VT columns
     float dS[K][VP];            // gradient of the state at the chunk end, VT columns
-    float v[CT][VP];
     float dO[CT][VP];
     float R[CT][VP];
     float P[CT][VP];
@@ -538,7 +539,6 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     __shared__ ChunkSmem<K> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
-    const TI* vp = static_cast<const TI*>(a.v);
     const TI* dop = static_cast<const TI*>(a.d_o);
     TI* dqp = static_cast<TI*>(a.dq);
     TI* dkp = static_cast<TI*>(a.dk);
@@ -576,27 +576,27 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         bl = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
     }
 
-    float ps[SPT], pds[SPT], pdp = 0.f, pdr = 0.f;
-    TI pv{}, pdo{};                         // converted when staged
+    // the checkpoint of chunk cb: the state before it (K rows), then its R
+    // and P (CT rows each), V columns
+    const float* ck = a.ckpt + cb * static_cast<int64_t>(K + 2 * CT) * V;
+    float ps[SPT], pds[SPT], pr = 0.f, pp = 0.f, pdp = 0.f, pdr = 0.f;
+    TI pdo{};                               // converted when staged
     const int st_row = t / TPR, st_col = SPT * (t % TPR);
     const int tc = t / VT, tv = t % VT;
     auto fetch = [&](int vt) {
         const int64_t v0 = static_cast<int64_t>(vt) * VT;
 #pragma unroll
         for (int j = 0; j < SPT; ++j) {
-            const int64_t o = (cb * K + st_row) * V + v0 + st_col + j;
-            ps[j] = a.ckpt[o];
-            pds[j] = ws.dS[o];
+            ps[j] = ck[st_row * V + v0 + st_col + j];
+            pds[j] = ws.dS[(cb * K + st_row) * V + v0 + st_col + j];
         }
+        pr = ck[(K + tc) * V + v0 + tv];
+        pp = ck[(K + CT + tc) * V + v0 + tv];
         pdp = ws.dP[(cb * CT + tc) * V + v0 + tv];
         pdr = ws.dR[(cb * CT + tc) * V + v0 + tv];
         const int64_t row = static_cast<int64_t>(n) * CT + tc;
-        pv = pdo = TI{};
-        if (row < T) {
-            const int64_t o = ((b * T + row) * H + h) * V + v0 + tv;
-            pv = vp[o];
-            pdo = dop[o];
-        }
+        pdo = TI{};
+        if (row < T) pdo = dop[((b * T + row) * H + h) * V + v0 + tv];
     };
     fetch(0);
 
@@ -636,7 +636,7 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     }
 
     // ------------------------------------- sums over the state columns
-    // per VT-column step: R = V - (k*E) S, P = M R, then
+    // per VT-column step (R and P from the forward's checkpoint):
     // dA += dO P^T, dM += dP R^T, d(q~*E) += dO S^T, d(k*E) -= dR S^T,
     // d(k*F) += P dS^T, deps += rowsum(dS * S).  The next step's tiles are
     // fetched into registers while the current one is computed.
@@ -656,7 +656,8 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             sm.S[st_row][st_col + j] = ps[j];
             sm.dS[st_row][st_col + j] = pds[j];
         }
-        sm.v[tc][tv] = Elem<TI>::ld(&pv);
+        sm.R[tc][tv] = pr;
+        sm.P[tc][tv] = pp;
         sm.dO[tc][tv] = Elem<TI>::ld(&pdo);
         sm.dP[tc][tv] = pdp;
         sm.dR[tc][tv] = pdr;
@@ -667,53 +668,27 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         if (vt + 1 < nvt) fetch(vt + 1);
         __syncthreads();
 
-        // waves 0-3: R; the other element waves: their d(q~E), d(kE)
-        if (w < 4) {
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = tile_mm<K>([&](int r, int x) { return sm.k[r0t + r][x] * sm.e[r0t + r][x]; },
-                             [&](int x, int v) { return sm.S[x][c0t + v]; }, ln, lg, acc);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = r0t + 4 * lg + j;
-                sm.R[c][c0t + ln] = sm.v[c][c0t + ln] - acc[j];
-            }
-        } else if (tw) {
+        // waves 0-3: dA += dO P^T; waves 4-7: dM += dP R^T; every element wave:
+        // d(q~E) += dO S^T, d(kE) -= dR S^T, d(kF) += P dS^T; deps
+        if (w < 4)
+            accm = tile_mm<VT>([&](int r, int v) { return sm.dO[r0t + r][v]; },
+                               [&](int v, int i) { return sm.P[c0t + i][v]; }, ln, lg, accm);
+        else if (w < 8)
+            accm = tile_mm<VT>([&](int r, int v) { return sm.dP[r0t + r][v]; },
+                               [&](int v, int i) { return sm.R[c0t + i][v]; }, ln, lg, accm);
+        if (tw) {
             dqe = tile_mm<VT>([&](int r, int v) { return sm.dO[ert + r][v]; },
                               [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dqe);
             dke = tile_mm<VT>([&](int r, int v) { return -sm.dR[ert + r][v]; },
                               [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dke);
+            dkf = tile_mm<VT>([&](int r, int v) { return sm.P[ert + r][v]; },
+                              [&](int v, int kc) { return sm.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
         }
-        __syncthreads();
-
-        // waves 0-3: P = M R; waves 4-7: dM += dP R^T; waves 8-: deps
-        if (w < 4) {
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = tile_mm<CT>([&](int r, int i) { return sm.N[r0t + r][i] * sm.beta[i]; },
-                              [&](int i, int v) { return sm.R[i][c0t + v]; }, ln, lg, acc);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sm.P[r0t + 4 * lg + j][c0t + ln] = acc[j];
-        } else if (w < 8) {
-            accm = tile_mm<VT>([&](int r, int v) { return sm.dP[r0t + r][v]; },
-                               [&](int v, int i) { return sm.R[c0t + i][v]; }, ln, lg, accm);
-        } else if (t - 512 < K) {
+        if (t >= 512 && t - 512 < K) {
             const int x = t - 512;
 #pragma unroll 8
             for (int vv = 0; vv < VT; ++vv) deps += sm.dS[x][vv] * sm.S[x][vv];
         }
-        __syncthreads();
-
-        // waves 0-3: dA += dO P^T and their d(q~E), d(kE); every element wave: d(kF) += P dS^T
-        if (w < 4) {
-            accm = tile_mm<VT>([&](int r, int v) { return sm.dO[r0t + r][v]; },
-                               [&](int v, int i) { return sm.P[c0t + i][v]; }, ln, lg, accm);
-            dqe = tile_mm<VT>([&](int r, int v) { return sm.dO[ert + r][v]; },
-                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dqe);
-            dke = tile_mm<VT>([&](int r, int v) { return -sm.dR[ert + r][v]; },
-                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dke);
-        }
-        if (tw)
-            dkf = tile_mm<VT>([&](int r, int v) { return sm.P[ert + r][v]; },
-                              [&](int v, int kc) { return sm.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
         __syncthreads();
     }
     if (w < 8) {

@@ -147,7 +147,8 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
 
     o = torch.empty(B, T, H, V, device=dev, dtype=out_dtype)
     s_out = state_out if state_out is not None else torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
-    ck = torch.empty(B, H, (T + CKPT_SPACING - 1) // CKPT_SPACING, K, V, device=dev,
+    # per 32-token chunk: the state before it (K rows), then the chunk's R and P (32 rows each)
+    ck = torch.empty(B, H, (T + CKPT_SPACING - 1) // CKPT_SPACING, K + 2 * CKPT_SPACING, V, device=dev,
                      dtype=torch.float32) if ckpt else None
     if B * H == 0:
         if state is not None:

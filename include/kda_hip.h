@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 5
+#define KDA_ABI_VERSION 6
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -115,9 +115,11 @@ int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
  * torch.autograd.Function around the HIP forward binds instead.
  * ------------------------------------------------------------------------- */
 
-/* kda_chunkwise_fwd, plus the fp32 state before every 32-token chunk:
- * ckpt is [B, H, ceil(T/32), K, V] contiguous fp32 (the input of
- * kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
+/* kda_chunkwise_fwd, plus per 32-token chunk, in fp32: the state before the
+ * chunk and the chunk's R = V - (k * E) S and P = (I + Diag(beta) L)^-1
+ * Diag(beta) R (the solve's result): ckpt is [B, H, ceil(T/32), K + 64, V]
+ * contiguous, rows [0, K) the state, [K, K + 32) R, [K + 32, K + 64) P (the
+ * input of kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 
 /* Every tensor is contiguous in the forward layout: q, k, g, dq, dk, dg
@@ -131,7 +133,7 @@ typedef struct kda_bwd_args {
     int64_t B, T, H, K, V;
     const void* q;                 /* the forward's inputs (q unscaled)        */
     const void* k;
-    const void* v;
+    const void* v;                 /* not read: R comes from the checkpoint     */
     const float* g;
     const float* beta;
     const float* ckpt;             /* from kda_chunkwise_fwd_ckpt on the same inputs */
