@@ -742,10 +742,12 @@ struct Kern {
 
     // One chunk (blocks blk, blk + 1) of the chain for this wave's 16 state
     // columns; the v loads of the same blocks one superstep later are issued
-    // into vraw0 / vraw1.  rp (or null): rows [0, 32) of the chunk's
-    // R = V - (k * E) S and rows [32, 64) of P, in fp32, for the backward.
+    // into vraw0 / vraw1.  ck (or null): the chunk's checkpoint for the
+    // backward, in fp32: rows [0, K) the state before it, [K, K + 32) its
+    // R = V - (k * E) S, [K + 32, K + 64) its P.  The stores go out after the
+    // v loads, so that waiting for those loads never waits for them.
     __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw0)[4], uint32_t (&vraw1)[4],
-                            f4 (&S)[KT], int64_t col0, uint32_t ocol, float* rp) const {
+                            f4 (&S)[KT], int64_t col0, uint32_t ocol, float* ck) const {
         use_here(vraw0);
         use_here(vraw1);
         f4 R0, R1;
@@ -756,6 +758,9 @@ struct Kern {
         }
         v_load(vraw0, blk + NB);
         v_load(vraw1, blk + 1 + NB);
+        const int64_t V = a.V, rc = col0 + ocol;
+        if (ck) store_state_t<KT>(S, ck, (4 * lg) * V + rc, V);
+        float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
         h8 shi[KU], slo[KU];
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
@@ -790,7 +795,6 @@ struct Kern {
         // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0)
         R0 -= Z0;
         R1 -= Z1;
-        const int64_t V = a.V, rc = col0 + ocol;
         if (rp) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -913,12 +917,10 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             for (int cj = 0; cj < NCH; ++cj) {
                 const int cc = NCH * s + cj;
                 if (s >= 0 && cc < ncc) {
-                    // for the backward: the state before chunk cc, then its R and P
+                    // the checkpoint of chunk cc, for the backward
                     float* ck = ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K + 2 * CB * BT) * V
                                      : nullptr;
-                    if (ck) store_state_t<KT>(S, ck, (4 * kn.lg) * V + col, V);
-                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol,
-                               ck ? ck + static_cast<int64_t>(K) * V : nullptr);
+                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol, ck);
                 }
                 __syncthreads();
             }
