@@ -526,6 +526,11 @@ struct __align__(16) ChunkSmem {
     float dbeta[CT];
     float eps[K];               // exp(G_last)
     float deps[K];              // rowsum(dS * S)
+    // the element step's copies of dA and dX live in the dS area when it is
+    // large enough (K = 128), here otherwise
+    static constexpr int CPY = 4 * CT * (CT + 4);
+    static constexpr bool CPY_IN_DS = K * VP >= CPY;
+    float cpy[CPY_IN_DS ? 4 : CPY];
 };
 static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
 
@@ -691,13 +696,26 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         }
         __syncthreads();
     }
+    // 16-byte-aligned copies for the element step (in the dS area, no longer
+    // read, when it is large enough): dA by rows and by columns, dX (the
+    // final dM) by rows and by columns
+    float* cpy = ChunkSmem<K>::CPY_IN_DS ? &sm.dS[0][0] : &sm.cpy[0];
+    float (*dAr)[CT + 4] = reinterpret_cast<float (*)[CT + 4]>(cpy);
+    float (*dAc)[CT + 4] = dAr + CT;
+    float (*dXr)[CT + 4] = dAr + 2 * CT;
+    float (*dXc)[CT + 4] = dAr + 3 * CT;
     if (w < 8) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
             const float x = i <= c ? accm[j] : 0.f;
-            if (w < 4) sm.dA[c][i] = x;
-            else sm.dM[c][i] = x;
+            if (w < 4) {
+                sm.dA[c][i] = x;
+                dAr[c][i] = x;
+                dAc[i][c] = x;
+            } else {
+                sm.dM[c][i] = x;
+            }
         }
     }
     if (t >= 512 && t - 512 < K) sm.deps[t - 512] = deps;
@@ -732,7 +750,10 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
-            sm.dM[c][i] = i < c ? -acc[j] : 0.f;
+            const float x = i < c ? -acc[j] : 0.f;
+            sm.dM[c][i] = x;
+            dXr[c][i] = x;
+            dXc[i][c] = x;
         }
     }
     __syncthreads();
@@ -795,21 +816,19 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         // row side within the block, ert <= i <= c0 (dA and dM vanish above the diagonal)
         for (int i = ert; i <= c0; ++i) {
             const float kh = kcol(i) * __expf(g0 - gcol(i));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                t1[j] += sm.dA[c0 + j][i] * kh;
-                t3[j] += sm.dM[c0 + j][i] * kh;
-            }
+            const float4 a4 = *reinterpret_cast<const float4*>(&dAc[i][c0]);
+            const float4 m4 = *reinterpret_cast<const float4*>(&dXc[i][c0]);
+            t1[0] += a4.x * kh; t1[1] += a4.y * kh; t1[2] += a4.z * kh; t1[3] += a4.w * kh;
+            t3[0] += m4.x * kh; t3[1] += m4.y * kh; t3[2] += m4.z * kh; t3[3] += m4.w * kh;
         }
         // column side within the block, c3 <= c2 < ert + 16
         for (int c2 = c3; c2 < ert + 16; ++c2) {
             const float hh = __expf(gcol(c2) - g3);
             const float qh = qcol(c2) * hh, kh = sm.beta[c2] * kcol(c2) * hh;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                t2[j] += sm.dA[c2][c0 + j] * qh;
-                t4[j] += sm.dM[c2][c0 + j] * kh;
-            }
+            const float4 a4 = *reinterpret_cast<const float4*>(&dAr[c2][c0]);
+            const float4 m4 = *reinterpret_cast<const float4*>(&dXr[c2][c0]);
+            t2[0] += a4.x * qh; t2[1] += a4.y * qh; t2[2] += a4.z * qh; t2[3] += a4.w * qh;
+            t4[0] += m4.x * kh; t4[1] += m4.y * kh; t4[2] += m4.z * kh; t4[3] += m4.w * kh;
         }
         float last = 0.f;
 #pragma unroll
