@@ -204,7 +204,7 @@ def backward_bench(pkg, wl, torch, reps=3):
         if i >= 2:
             fwd += e0.elapsed_time(e1) / reps
             bwd += e1.elapsed_time(e2) / reps
-    return {"workload": "kda_chunkwise forward (with 32-token state checkpoints) + native backward under "
+    return {"workload": "kda_chunkwise forward (with 32-token checkpoints: state, R, P) + native backward under "
                         "autograd, B=8 T=4096 H=16 dk=dv=128; fp16 q/k/v, fp32 g/beta",
             "forward_ckpt_ms": fwd, "backward_ms": bwd,
             "train_tokens_per_s": B1 * T1 / ((fwd + bwd) * 1e-3)}
