@@ -107,3 +107,20 @@ def test_layer_model_width(kda_pkg):
     e = rel(out, kda_layer_ref(p, cfg, x))
     print(f"[layer hidden 2048] rel {e:.3e}", flush=True)
     assert e <= TOL[torch.float16]
+
+
+def test_fused_projection_weight_follows_updates(kda_pkg):
+    """The six projections of x run as one GEMM over a cached concatenation of
+    their weights: an in-place update or a replaced parameter must reach it."""
+    m, cfg, _ = make_layer(kda_pkg, torch.float16, seed=3)
+    x = make_x(2, 48, cfg.hidden_size, torch.float16, seed=4).to(DEV)
+    with torch.no_grad():
+        m(x)                                                  # builds the cache
+        m.in_proj_k.weight.mul_(0.5)                          # in place
+        m.gk_proj[0].weight = torch.nn.Parameter(m.gk_proj[0].weight * 2.0)   # replaced
+        m.load_state_dict({k: v for k, v in m.state_dict().items()})          # copy_ into params
+        out = m(x)
+        fresh, _, _ = make_layer(kda_pkg, torch.float16, seed=3)
+        fresh.load_state_dict(m.state_dict())
+        ref = fresh(x)
+    assert torch.equal(out, ref)
