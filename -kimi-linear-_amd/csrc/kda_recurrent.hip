@@ -45,16 +45,34 @@ __device__ __forceinline__ float lanegroup8_sum(float x) {
     return x;
 }
 
+// Sum of x over the 4 lanes that share l & 15 (all-reduce): the permlane
+// swaps of bits 4 and 5.
+__device__ __forceinline__ float lanegroup4_sum(float x) {
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return x;
+}
+
 // Lane l of a wave holds 4 adjacent state columns (column group l % CPL) of
 // RPL = K CPL / 64 adjacent rows (row group l / CPL); the K-reductions are
 // sums over the lanes of one column group.
 template <int K, int NW, int CPL, bool VEC>
 __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a) {
-    static_assert(CPL == 4 || CPL == 8, "column groups per wave");
+    static_assert(CPL == 4 || CPL == 8 || CPL == 16, "column groups per wave");
     constexpr int RPL = K * CPL / 64;           // rows per lane
     constexpr int VT = 4 * CPL * NW;            // columns per workgroup
     static_assert(K % (64 / CPL) == 0 && RPL >= 1, "K must be a multiple of the row groups");
-    auto ksum = [](float x) { return CPL == 4 ? rowgroup_sum(x) : lanegroup8_sum(x); };
+    auto ksum = [](float x) {
+        return CPL == 4 ? rowgroup_sum(x) : (CPL == 8 ? lanegroup8_sum(x) : lanegroup4_sum(x));
+    };
 
     __shared__ float s_q[K], s_k[K], s_a[K];
 
@@ -211,6 +229,9 @@ int launch_k(const kda_fwd_args& a, hipStream_t stream) {
     // K <= 128: 32 columns per one-wave workgroup, K / 8 x 4 state elements
     // per lane (at K 128, 128 VGPRs: a B=64 H=16 V=128 step's 4096 waves all
     // resident at once); K 256: 16 columns a wave, K / 16 x 4 per lane.
+    if constexpr (K == 128) {
+        if (a.V % 64 == 0) return launch_k_nw<K, 1, 16>(a, stream);
+    }
     if constexpr (K <= 128) {
         if (a.V % 32 == 0) return launch_k_nw<K, 1, 8>(a, stream);
     }
