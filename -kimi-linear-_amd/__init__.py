@@ -7,7 +7,7 @@ HIP kernels behind the C ABI in ``include/kda_hip.h``, and the reference's
 """
 
 from .kda import FP16_MAX_SAFE, KdaError, kda_chunkwise, kda_recurrent  # noqa: F401
-from .layer import HeadwiseRMSNorm, KimiDeltaAttention, ShortConv, l2norm, linear_attn_config  # noqa: F401
+from .layer import HeadwiseRMSNorm, KimiDeltaAttention, ShortConv, linear_attn_config  # noqa: F401
 
 __all__ = ["kda_chunkwise", "kda_recurrent", "KdaError", "FP16_MAX_SAFE", "KimiDeltaAttention", "ShortConv",
-           "HeadwiseRMSNorm", "l2norm", "linear_attn_config"]
+           "HeadwiseRMSNorm", "linear_attn_config"]

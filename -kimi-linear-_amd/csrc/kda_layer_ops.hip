@@ -69,8 +69,12 @@ __device__ __forceinline__ float round_to(float x) {
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// softplus with torch's default threshold: z for z > 20
-__device__ __forceinline__ float softplus(float z) { return z > 20.f ? z : __logf(1.f + __expf(z)); }
+// softplus with torch's default threshold: z for z > 20, else
+// log(1 + e^z) = max(z, 0) + log1p(e^-|z|), which keeps its e^z behaviour for
+// z << 0 (log(1 + e^z) in fp32 rounds to 0 below z ~ -17)
+__device__ __forceinline__ float softplus(float z) {
+    return z > 20.f ? z : fmaxf(z, 0.f) + log1pf(__expf(-fabsf(z)));
+}
 
 // A small parameter element of a runtime dtype: the load is unconditional
 // (a NULL or out-of-range element reads `fallback`'s first word instead and is

@@ -48,6 +48,13 @@ class KdaGraphedDecoder:
     ``step`` returns a view of the static output buffer: read or clone it
     before the next call.  Weights are read, never written, so one capture
     serves any number of prompts of the same batch size.
+
+    The captured GEMMs read each layer's concatenated input-projection weight
+    (``KimiDeltaAttention._input_weight``) and the parameters themselves.
+    ``prefill`` refills that concatenation from the parameters (in place, so
+    the graph keeps reading valid memory) and recaptures if a buffer had to be
+    reallocated (new dtype or shape).  After updating weights between two
+    ``step`` calls of one generation, call :meth:`refresh_weights`.
     """
 
     def __init__(self, layers: Sequence[KimiDeltaAttention], residual: bool = True, warmup_iters: int = 3):
@@ -60,6 +67,26 @@ class KdaGraphedDecoder:
         self.graph: torch.cuda.CUDAGraph | None = None
         self.static_states: list[dict] | None = None
         self._B = None
+        self._wbufs = None          # addresses of the fused weights the graph reads
+
+    def _weight_buffers(self):
+        bufs = []
+        for layer in self.layers:
+            w, b = layer._input_weight()
+            bufs.append((w.data_ptr(), b.data_ptr() if b is not None else 0))
+        return bufs
+
+    @torch.no_grad()
+    def refresh_weights(self) -> None:
+        """Bring the captured step up to date with the layers' parameters:
+        refill the fused input-projection weights (in place) and recapture if
+        one of them moved.  Needed only when weights change mid-generation."""
+        if self.graph is None:
+            return
+        for layer in self.layers:
+            layer.refresh_fused_weight()
+        if self._weight_buffers() != self._wbufs:
+            self._capture()
 
     # ------------------------------------------------------------ the stack
     def _run_stack(self, x, states, use_cache):
@@ -114,6 +141,7 @@ class KdaGraphedDecoder:
             self._step()
         self._restore(snap)
         torch.cuda.synchronize()
+        self._wbufs = self._weight_buffers()
 
     # ------------------------------------------------------------ public API
     @torch.no_grad()
@@ -133,6 +161,8 @@ class KdaGraphedDecoder:
                 st["recurrent"].dtype != new["recurrent"].dtype for st, new in zip(self.static_states, states)):
             self.graph = None
             self.static_states = None
+        if self.graph is not None and self._weight_buffers() != self._wbufs:
+            self.graph = None           # a fused weight was reallocated: the graph would read freed memory
         self._fill_static(states)
         if self.graph is None:
             self._B = B

@@ -6,9 +6,8 @@ rules -- with the core recurrence running on the gfx950 kernels of
 :mod:`kimi_linear_amd.kda`.  The projections are library GEMMs; the
 elementwise work between them and the core (short convolutions with their
 cache, SiLU, L2 norms, gates; RMSNorm and output gate) runs in the two fused
-kernels of :mod:`kimi_linear_amd.layer_ops`.  The ``ShortConv``,
-``HeadwiseRMSNorm`` and ``l2norm`` pieces below are the reference's modules
-(parameter containers with their own torch forward), not the layer's path.
+kernels of :mod:`kimi_linear_amd.layer_ops`.  ``ShortConv`` and
+``HeadwiseRMSNorm`` below only hold parameters under the reference's names.
 
 The core is forward-only (it raises on inputs that require grad under grad
 mode): run the layer under ``torch.no_grad()`` or ``torch.inference_mode()``.
@@ -36,79 +35,35 @@ from types import SimpleNamespace
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from .kda import kda_chunkwise, kda_recurrent
 from .layer_ops import kda_output, kda_prep
 
 
-def _f32(t: torch.Tensor) -> torch.Tensor:
-    return t if t.dtype == torch.float32 else t.float()
-
-
 class HeadwiseRMSNorm(nn.Module):
-    """Per-head RMSNorm with an fp32 weight ``[H, D]`` (``kda.py:258-279``)."""
+    """Holder of the per-head RMSNorm weight ``[H, D]`` and eps
+    (``kda.py:258-279``).  The layer applies the norm inside the fused output
+    kernel (:func:`kimi_linear_amd.layer_ops.kda_output`), so this module has
+    no forward of its own; it keeps the reference's ``g_norm.weight`` key."""
 
     def __init__(self, heads: int, dim: int, eps: float):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(heads, dim))
         self.eps = float(eps)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:       # x: [B, T, H, D]
-        dtype = x.dtype
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return (xf * _f32(self.weight)).to(dtype)
-
 
 class ShortConv(nn.Module):
-    """Causal depthwise convolution, kernel ``conv_size`` (``kda.py:282-310``).
-
-    Parameters live in an ``nn.Conv1d`` named ``conv`` like the reference's, so
-    its ``state_dict`` keys (``conv.weight`` ``[D, 1, C]``, ``conv.bias``) match.
-    The batch path sums the ``conv_size`` shifted taps in fp32 and rounds once
-    to x's dtype (the reference's ``conv1d`` on a left-padded input,
-    ``kda.py:308-310``, computes the same sum): a depthwise filter of 4 taps is
-    a handful of elementwise passes, with no convolution library in the loop.
-    """
+    """Holder of one causal depthwise convolution's parameters
+    (``kda.py:282-310``): an ``nn.Conv1d`` named ``conv``, so the
+    ``state_dict`` keys (``conv.weight`` ``[D, 1, C]``, ``conv.bias``) match the
+    reference's.  The convolution itself, with its cache, runs inside the fused
+    pre-processing kernel (:func:`kimi_linear_amd.layer_ops.kda_prep`)."""
 
     def __init__(self, dim: int, conv_size: int, bias: bool = True):
         super().__init__()
         self.dim = dim
         self.conv_size = conv_size
         self.conv = nn.Conv1d(dim, dim, conv_size, groups=dim, bias=bias)
-
-    def forward(self, x, conv_state=None, use_cache=False):
-        """x: [B, T, D].  With ``use_cache``, x is [B, 1, D] and ``conv_state`` the
-        last ``conv_size - 1`` inputs [B, conv_size - 1, D]; returns (out, state)."""
-        if use_cache:
-            window = torch.cat([conv_state, x], dim=1)                # [B, C, D]
-            w = _f32(self.conv.weight).squeeze(1).t()                 # [C, D]
-            out = (window.float() * w).sum(1)
-            if self.conv.bias is not None:
-                out = out + _f32(self.conv.bias)
-            out = out.to(x.dtype).unsqueeze(1)
-            new_state = window[:, 1 - self.conv_size:] if self.conv_size > 1 else window[:, :0]
-            return out, new_state
-        T = x.shape[1]
-        C = self.conv_size
-        w = _f32(self.conv.weight).squeeze(1)                         # [D, C]
-        xp = F.pad(x.float(), (0, 0, C - 1, 0))                       # left pad over time: causal
-        out = xp[:, C - 1:] * w[:, C - 1]
-        for c in range(C - 1):
-            out = out + xp[:, c:c + T] * w[:, c]
-        if self.conv.bias is not None:
-            out = out + _f32(self.conv.bias)
-        return out.to(x.dtype)
-
-
-def l2norm(x: torch.Tensor, eps: float) -> torch.Tensor:
-    """Last-dimension L2 normalisation, reduced in fp32, returned in x's dtype
-    (``kda.py:313-325``): x * min(rsqrt(sum x^2), 1/eps)."""
-    src = x.dtype
-    xf = x.float()
-    rstd = (xf * xf).sum(-1, keepdim=True).rsqrt().clamp(max=1.0 / eps)
-    return (xf * rstd).to(src)
 
 
 def linear_attn_config(**kw) -> SimpleNamespace:
@@ -159,22 +114,53 @@ class KimiDeltaAttention(nn.Module):
         self.fp32_recurrent_state = True
         self._wcat = None          # (key, weight, bias) of the fused input projection
 
+    def _input_mods(self):
+        return (self.in_proj_q, self.in_proj_k, self.in_proj_v, self.beta_proj, self.gk_proj[0], self.og_proj[0])
+
     def _input_weight(self):
         """The six projections of x -- q, k, v, beta and the down-projections
         of the forget gate and the output gate -- as one ``[N, d]`` weight (and
         bias), so that a step runs one GEMM over x instead of six small ones.
+
         The module keeps its own parameters (checkpoints load unchanged); the
-        concatenation is cached and rebuilt when any of them is replaced or
-        updated in place."""
-        mods = (self.in_proj_q, self.in_proj_k, self.in_proj_v, self.beta_proj,
-                self.gk_proj[0], self.og_proj[0])
-        key = tuple((m.weight.data_ptr(), m.weight._version, m.weight.dtype, m.weight.device) for m in mods)
-        if self._wcat is None or self._wcat[0] != key:
-            with torch.no_grad():
-                w = torch.cat([m.weight for m in mods], 0)
-                b = torch.cat([m.bias for m in mods]) if mods[0].bias is not None else None
-            self._wcat = (key, w, b)
-        return self._wcat[1], self._wcat[2]
+        concatenation is a cache keyed on every weight's and bias's
+        (data_ptr, _version, dtype, device).  Replacing a parameter, or
+        updating it in place through autograd-visible ops (``copy_``,
+        ``load_state_dict``, an optimizer step), changes the key and refills
+        the cache.  A refill of the same shape, dtype and device writes into
+        the existing buffers, so a captured decode graph that reads them sees
+        the new weights.  Writes through ``.data`` do not bump ``_version``:
+        call :meth:`refresh_fused_weight` after them."""
+        mods = self._input_mods()
+        params = [m.weight for m in mods] + [m.bias for m in mods if m.bias is not None]
+        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
+        if self._wcat is not None and self._wcat[0] == key:
+            return self._wcat[1], self._wcat[2]
+        with torch.no_grad():
+            w_parts = [m.weight for m in mods]
+            b_parts = [m.bias for m in mods] if mods[0].bias is not None else None
+            n = sum(p.shape[0] for p in w_parts)
+            old = self._wcat
+            w0 = w_parts[0]
+            if (old is not None and old[1].shape == (n, w0.shape[1]) and old[1].dtype == w0.dtype
+                    and old[1].device == w0.device and (old[2] is None) == (b_parts is None)):
+                w, b = old[1], old[2]
+                torch.cat(w_parts, 0, out=w)
+                if b is not None:
+                    torch.cat(b_parts, out=b)
+            else:
+                w = torch.cat(w_parts, 0)
+                b = torch.cat(b_parts) if b_parts is not None else None
+        self._wcat = (key, w, b)
+        return w, b
+
+    def refresh_fused_weight(self) -> None:
+        """Refill the concatenated input-projection weight from the parameters
+        (in place when the layout is unchanged).  Needed only after writes that
+        bypass autograd's version counter, such as ``p.data.copy_(...)``."""
+        if self._wcat is not None:
+            self._wcat = (None, self._wcat[1], self._wcat[2])
+        self._input_weight()
 
     def _state_dtype(self, x):
         if self.fp32_recurrent_state and x.dtype in (torch.float16, torch.bfloat16):

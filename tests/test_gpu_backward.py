@@ -139,3 +139,26 @@ def test_backward_unsupported_head_dims_raise(kda_pkg, wl):
     with pytest.raises(kda_pkg.KdaError, match="backward supports"):
         kda_pkg.kda_chunkwise(q, inp["k"].to(DEV), inp["v"].to(DEV), inp["g"].to(DEV), inp["beta"].to(DEV),
                               chunk_size=16)
+
+
+def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl):
+    """256 (batch, head) chains of 64 columns: the checkpointing forward runs its
+    widest instantiation (four 16-column consumer waves a workgroup) and the
+    gradients come from its checkpoints.  They must equal the gradients of the
+    same sequences run one at a time (16 chains: one-wave instantiation), and
+    sequence 0 must match the fp64 oracle."""
+    B, T, H, K, V = 16, 64, 16, 64, 64
+    print(f"backward wide launch B={B} T={T} H={H} K={K} V={V}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=31, dtype=torch.float32, state=True)
+    wide = _native_grads(kda_pkg, xs, wo, ws, 32)
+    for b in (0, 7, 15):
+        sub = [x[b:b + 1] for x in xs]
+        one = _native_grads(kda_pkg, sub, wo[b:b + 1], ws[b:b + 1], 32)
+        for name, a, r in zip(NAMES, wide, one):
+            err = _rel(a[b:b + 1], r)
+            assert err <= 1e-6, (b, name, err)
+    ref = _ref_grads([x[:1] for x in xs], wo[:1], ws[:1], 32)
+    for name, a, r in zip(NAMES, wide, ref):
+        err = _rel(a[:1], r)
+        print(f"  d{name}: rel {err:.2e}", flush=True)
+        assert err <= 2e-3, (name, err)

@@ -195,3 +195,40 @@ def test_graphed_decoder_reprefill_reuses_graph(kda_pkg):
         e = rel(torch.stack(ys, 1), full[:, prompt_len:])
         print(f"[graph decode re-prefill {prompt_len}] rel vs oracle {e:.3e}", flush=True)
         assert e <= 1e-2
+
+
+def test_graphed_decoder_follows_weight_updates(kda_pkg):
+    """Weights loaded in place after capture (load_state_dict) reach the replayed
+    step: the next prefill refills the fused projection weight in its own buffer
+    (the captured GEMM keeps reading valid memory, no recapture), and
+    refresh_weights() does the same between two steps of one generation."""
+    from kimi_linear_amd.graph_decode import KdaGraphedDecoder
+
+    B = 2
+    cfg, layers, _ = make_stack(kda_pkg, 1, torch.float16, seed=50)
+    dec = KdaGraphedDecoder(layers)
+    g = torch.Generator().manual_seed(51)
+    x = torch.randn(B, 30, 256, generator=g).half().to(DEV)
+    new_params = make_layer_params(cfg, seed=52)
+    with torch.no_grad():
+        dec.prefill(x[:, :24])
+        graph = dec.graph
+        dec.step(x[:, 24:25])
+        layers[0].load_state_dict(new_params)                  # copy_ into the live parameters
+        dec.prefill(x[:, :24])
+        assert dec.graph is graph                              # the fused weight stayed in place
+        ys = [dec.step(x[:, t:t + 1]).clone() for t in range(24, 27)]
+        fresh_cfg, fresh, fresh_params = make_stack(kda_pkg, 1, torch.float16, seed=52)
+        ref_dec = KdaGraphedDecoder(fresh)
+        ref_dec.prefill(x[:, :24])
+        want = [ref_dec.step(x[:, t:t + 1]).clone() for t in range(24, 27)]
+        for a, b in zip(ys, want):
+            assert torch.equal(a, b)
+        # an update between two steps of one generation, then refresh_weights()
+        layers[0].load_state_dict(make_layer_params(cfg, seed=50))
+        fresh[0].load_state_dict(make_layer_params(cfg, seed=50))
+        dec.refresh_weights()
+        ref_dec.refresh_weights()
+        a = dec.step(x[:, 27:28]).clone()
+        b = ref_dec.step(x[:, 27:28]).clone()
+        assert torch.equal(a, b)

@@ -109,18 +109,51 @@ def test_layer_model_width(kda_pkg):
     assert e <= TOL[torch.float16]
 
 
-def test_fused_projection_weight_follows_updates(kda_pkg):
+@pytest.mark.parametrize("proj_bias", [False, True])
+def test_fused_projection_weight_follows_updates(kda_pkg, proj_bias):
     """The six projections of x run as one GEMM over a cached concatenation of
-    their weights: an in-place update or a replaced parameter must reach it."""
-    m, cfg, _ = make_layer(kda_pkg, torch.float16, seed=3)
+    their weights and biases: an in-place update or a replaced parameter must
+    reach it; a write through ``.data`` reaches it after refresh_fused_weight()."""
+    m, cfg, _ = make_layer(kda_pkg, torch.float16, seed=3, proj_bias=proj_bias)
     x = make_x(2, 48, cfg.hidden_size, torch.float16, seed=4).to(DEV)
     with torch.no_grad():
         m(x)                                                  # builds the cache
+        w_buf = m._wcat[1].data_ptr()
         m.in_proj_k.weight.mul_(0.5)                          # in place
+        if proj_bias:
+            m.beta_proj.bias.add_(0.25)                       # a bias alone changes
         m.gk_proj[0].weight = torch.nn.Parameter(m.gk_proj[0].weight * 2.0)   # replaced
         m.load_state_dict({k: v for k, v in m.state_dict().items()})          # copy_ into params
         out = m(x)
-        fresh, _, _ = make_layer(kda_pkg, torch.float16, seed=3)
+        assert m._wcat[1].data_ptr() == w_buf                 # refilled in place
+        fresh, _, _ = make_layer(kda_pkg, torch.float16, seed=3, proj_bias=proj_bias)
         fresh.load_state_dict(m.state_dict())
-        ref = fresh(x)
-    assert torch.equal(out, ref)
+        assert torch.equal(out, fresh(x))
+        m.in_proj_v.weight.data.mul_(0.5)                     # invisible to the version counter
+        m.refresh_fused_weight()
+        fresh.load_state_dict(m.state_dict())
+        assert torch.equal(m(x), fresh(x))
+
+
+def test_layer_config4_full_shape(kda_pkg):
+    """The whole layer at its benchmark shape: B=4, T=2048, hidden 2048 (16 heads
+    of 128), fp16 weights N(0, 0.02), fp32 recurrent state.  All four sequences
+    run on the GPU in one call (the chunkwise kernel's instantiation for 64
+    heads); sequences 0 and 3 are checked against the fp32 oracle."""
+    cfg = kda_pkg.linear_attn_config(hidden_size=2048, num_heads=16)
+    m = kda_pkg.KimiDeltaAttention(cfg)
+    m.load_state_dict(make_layer_params(cfg, seed=11))
+    m = m.to(device=DEV, dtype=torch.float16).eval()
+    p = {n: t.detach().float().cpu() for n, t in m.state_dict().items()}
+    x = make_x(4, 2048, 2048, torch.float16, seed=12)
+    print("[layer config 4] B=4 T=2048 hidden 2048 fp16", flush=True)
+    with torch.no_grad():
+        out, st = m(x.to(DEV), use_cache=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    sel = [0, 3]
+    ref, st_ref = kda_layer_ref(p, cfg, x[sel], use_cache=True)
+    e = rel(out[sel], ref)
+    es = rel(st["recurrent"][sel], st_ref["recurrent"])
+    print(f"[layer config 4] out rel {e:.3e} state rel {es:.3e}", flush=True)
+    assert e <= TOL[torch.float16] and es <= TOL[torch.float16]

@@ -162,3 +162,22 @@ def test_output_strided_core_view(ops):
         y1 = ops.kda_output(full[:, :32], gate, w, 1e-6)
         y2 = ops.kda_output(full[:, :32].contiguous(), gate, w, 1e-6)
     assert torch.equal(y1, y2)
+
+
+def test_prep_gate_softplus_tails(ops):
+    """The forget gate over the whole softplus range: for z = gk + dt_bias far
+    below 0, softplus(z) ~ e^z (not 0), and above the threshold 20 it is z
+    (torch's rule).  Relative error per element <= 1e-5 against log1p(exp(z))."""
+    B, T, H, K, V, cs = 1, 16, 2, 128, 128, 4
+    xs, ws, bs, _, a_log, dt_bias, beta_logit = make_prep_inputs(B, T, H, K, V, cs, torch.float32, seed=77)
+    z = torch.linspace(-60.0, 40.0, B * T * H * K, dtype=torch.float64).view(B, T, H * K)
+    gk = (z - dt_bias.double().cpu().reshape(-1)).float().to(DEV)
+    with torch.no_grad():
+        got = ops.kda_prep(*xs, ws, bs, gk, a_log, dt_bias, beta_logit, num_heads=H, head_dim=K,
+                           value_head_dim=V, l2_eps=1e-6)
+    zf = gk.double().cpu() + dt_bias.double().cpu().reshape(-1)
+    sp = torch.where(zf > 20, zf, torch.log1p(torch.exp(torch.clamp(zf, max=20))))
+    ref = (-torch.exp(a_log.double().cpu().reshape(-1)) * sp).view(B, T, H, K)
+    err = ((got[3].double().cpu() - ref).abs() / ref.abs()).max().item()
+    print(f"[prep softplus tails] max rel err {err:.2e}", flush=True)
+    assert (got[3] < 0).all() and err <= 1e-5

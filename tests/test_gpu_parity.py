@@ -142,6 +142,33 @@ def test_config1_chunk_size_invariance(kda_pkg, cfg1):
 
 
 # ----------------------------------------------------------------- configuration 2
+@pytest.mark.parametrize("B,H,T", [(4, 16, 512), (2, 8, 128)])
+def test_chunkwise_mid_head_counts(kda_pkg, wl, B, H, T):
+    """64 and 16 (batch, head) chains: the launch picks a narrower column tile
+    than at the benchmark shape (32 columns a workgroup at 64 chains, 16 at 16
+    chains), a different kernel instantiation that must agree with the oracle
+    on every head."""
+    print(f"chunkwise B={B} H={H} T={T} K=V=128 fp16", flush=True)
+    inp = wl.make_inputs(B, T, H, 128, 128, seed=B * 100 + H, qkv_dtype=torch.float16, state_std=0.02)
+    o, s = run_chunkwise(kda_pkg, to_dev(inp), 64)
+    o_ref, s_ref = ref_chunkwise(inp, 64)
+    eo, es = max_abs(o, o_ref), rel(s, s_ref)
+    report(f"mid heads B={B} H={H}", eo, es)
+    assert eo <= O_TOL and es <= S_TOL
+
+
+@pytest.mark.parametrize("V", [128, 256])
+def test_recurrent_k256(kda_pkg, wl, V):
+    """Head dim K = 256 (16 state columns a wave): fp32 recurrence vs the oracle."""
+    print(f"recurrent K=256 V={V}", flush=True)
+    inp = wl.make_inputs(2, 12, 3, 256, V, seed=V, qkv_dtype=torch.float32, state_std=0.02)
+    o, s = run_recurrent(kda_pkg, to_dev(inp))
+    o_ref, s_ref = ref_recurrent(inp)
+    eo, es = max_abs(o, o_ref), rel(s, s_ref)
+    report(f"recurrent K=256 V={V}", eo, es)
+    assert eo <= 1e-5 and es <= 1e-5
+
+
 def test_config2_decode_graph(kda_pkg, wl):
     B, H, K, V, steps = 64, 16, 128, 128, 512
     gen_inp = wl.make_inputs(B, steps, H, K, V, device=DEV, seed=2, qkv_dtype=torch.float16,
