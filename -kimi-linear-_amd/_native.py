@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -20,6 +20,9 @@ DTYPE_BF16 = 2
 STATUS_OK = 0
 STATUS_BAD_SHAPE = 2
 STATUS_UNSUPPORTED = 4
+STATUS_TOO_LARGE = 7
+
+BWD_SCRATCH_BYTES = 64 << 20    # KDA_BWD_SCRATCH_BYTES: the static buffer of kda_chunkwise_bwd_noalloc
 
 _i64x3 = ctypes.c_int64 * 3
 
@@ -93,7 +96,7 @@ class KdaOutputArgs(ctypes.Structure):
 
 
 EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_chunkwise_fwd_ckpt", "kda_chunkwise_bwd",
-                    "kda_chunkwise_bwd_workspace_size",
+                    "kda_chunkwise_bwd_workspace_size", "kda_chunkwise_bwd_noalloc",
                     "kda_prep_fwd", "kda_output_fwd", "kda_status_str", "kda_abi_version")
 
 _lib = None
@@ -131,6 +134,8 @@ def load() -> ctypes.CDLL:
         lib.kda_chunkwise_fwd_ckpt.restype = ctypes.c_int
         lib.kda_chunkwise_bwd.argtypes = [ctypes.POINTER(KdaBwdArgs), ctypes.c_void_p]
         lib.kda_chunkwise_bwd.restype = ctypes.c_int
+        lib.kda_chunkwise_bwd_noalloc.argtypes = [ctypes.POINTER(KdaBwdArgs), ctypes.c_void_p]
+        lib.kda_chunkwise_bwd_noalloc.restype = ctypes.c_int
         lib.kda_chunkwise_bwd_workspace_size.argtypes = [ctypes.c_int64] * 5
         lib.kda_chunkwise_bwd_workspace_size.restype = ctypes.c_size_t
         lib.kda_prep_fwd.argtypes = [ctypes.POINTER(KdaPrepArgs), ctypes.c_void_p]

@@ -80,21 +80,57 @@ size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t
     return static_cast<size_t>(kda::chunkwise_bwd_workspace_bytes(B, T, H, K, V));
 }
 
-int kda_chunkwise_bwd(const kda_bwd_args* a, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks shared by both backward entry points; `need_workspace`: the caller
+// must supply args->workspace.  KDA_OK with *empty set when nothing is to be
+// launched.
+int validate_bwd(const kda_bwd_args* a, bool need_workspace, bool* empty) {
+    *empty = false;
     if (a == nullptr) return KDA_ERR_NULL_POINTER;
     if (a->B < 0 || a->T < 0 || a->H < 0 || a->K <= 0 || a->V <= 0) return KDA_ERR_BAD_SHAPE;
-    if (a->B == 0 || a->H == 0) return KDA_OK;
+    if (a->B == 0 || a->H == 0) {
+        *empty = true;
+        return KDA_OK;
+    }
     if (!kda::chunkwise_bwd_supported(a->K, a->V)) return KDA_ERR_UNSUPPORTED;
     if (a->io_dtype != KDA_DTYPE_F32 && a->io_dtype != KDA_DTYPE_F16 && a->io_dtype != KDA_DTYPE_BF16)
         return KDA_ERR_BAD_DTYPE;
     if (a->T > 0 && (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->ckpt || !a->d_o || !a->dq ||
-                     !a->dk || !a->dg || !a->dbeta || !a->dv || !a->workspace))
+                     !a->dk || !a->dg || !a->dbeta || !a->dv || (need_workspace && !a->workspace)))
         return KDA_ERR_NULL_POINTER;
     // grids: B H ceil(T / 32) and B H V / 32 workgroups
     if (a->B * a->H * ((a->T + 31) / 32) > INT32_MAX || a->B * a->H * (a->V / 32) > INT32_MAX)
         return KDA_ERR_BAD_SHAPE;
-    if (a->T == 0 && a->d_state_in == nullptr) return KDA_OK;
+    if (a->T == 0 && a->d_state_in == nullptr) *empty = true;
+    return KDA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kda_chunkwise_bwd(const kda_bwd_args* a, void* stream) {
+    bool empty = false;
+    const int st = validate_bwd(a, true, &empty);
+    if (st != KDA_OK || empty) return st;
     return kda::chunkwise_bwd_launch(*a, static_cast<hipStream_t>(stream));
+}
+
+int kda_chunkwise_bwd_noalloc(const kda_bwd_args* a, void* stream) {
+    bool empty = false;
+    const int st = validate_bwd(a, false, &empty);
+    if (st != KDA_OK || empty) return st;
+    if (kda::chunkwise_bwd_workspace_bytes(a->B, a->T, a->H, a->K, a->V) > static_cast<int64_t>(KDA_BWD_SCRATCH_BYTES))
+        return KDA_ERR_TOO_LARGE;
+    void* scratch = nullptr;
+    const int sst = kda::chunkwise_bwd_scratch(&scratch);
+    if (sst != KDA_OK) return sst;
+    kda_bwd_args b = *a;
+    b.workspace = scratch;
+    return kda::chunkwise_bwd_launch(b, static_cast<hipStream_t>(stream));
 }
 
 const char* kda_status_str(int status) {
@@ -105,7 +141,8 @@ const char* kda_status_str(int status) {
         case KDA_ERR_BAD_DTYPE: return "unsupported dtype code";
         case KDA_ERR_UNSUPPORTED: return "no kernel for these head dimensions";
         case KDA_ERR_ALIAS: return "an output overlaps an input (state_out/state_in, or a conv cache written while still read)";
-        case KDA_ERR_LAUNCH: return "kernel launch failed";
+        case KDA_ERR_LAUNCH: return "kernel launch failed (or no current HIP device)";
+        case KDA_ERR_TOO_LARGE: return "shape needs more scratch than the static buffer holds (KDA_BWD_SCRATCH_BYTES)";
         default: return "unknown kda_status";
     }
 }

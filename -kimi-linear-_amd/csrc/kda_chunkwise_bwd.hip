@@ -44,6 +44,9 @@
 // caller's activation dtype (fp32, fp16 or bf16; every product in fp32); g,
 // beta, the checkpoints, dg, dbeta and the state gradients are fp32.  The chunk-sized products run on the fp32
 // matrix cores (v_mfma_f32_16x16x4f32, no precision loss).
+#include <atomic>
+#include <mutex>
+
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -955,6 +958,34 @@ bool chunkwise_bwd_supported(int64_t K, int64_t V) {
 int64_t chunkwise_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
     const int64_t nck = (T + CT - 1) / CT;
     return B * H * nck * (3 * CT * CT + K * V + 2 * CT * V) * static_cast<int64_t>(sizeof(float));
+}
+
+// Static scratch of kda_chunkwise_bwd_noalloc: the workspace of the three
+// kernels (A, L, N, dS_end, dP, dR) for shapes that fit.  The array's name is
+// a host-side stand-in; kernels get the device address hipGetSymbolAddress
+// returns for the current device, kept per device.
+static __device__ __align__(256) unsigned char scratch[KDA_BWD_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+}  // namespace
+
+int chunkwise_bwd_scratch(void** ptr) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return KDA_ERR_LAUNCH;
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return KDA_ERR_LAUNCH;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *ptr = p;
+    return KDA_OK;
 }
 
 int chunkwise_bwd_launch(const kda_bwd_args& a, hipStream_t stream) {

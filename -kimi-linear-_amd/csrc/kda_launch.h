@@ -20,5 +20,8 @@ int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nu
 bool chunkwise_bwd_supported(int64_t K, int64_t V);
 int64_t chunkwise_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 int chunkwise_bwd_launch(const kda_bwd_args& a, hipStream_t stream);
+// Device address of the static backward scratch buffer (KDA_BWD_SCRATCH_BYTES)
+// on the current device; resolved once per device.  KDA_OK or KDA_ERR_LAUNCH.
+int chunkwise_bwd_scratch(void** ptr);
 
 }  // namespace kda

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 6
+#define KDA_ABI_VERSION 7
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -56,7 +56,10 @@ typedef enum kda_status {
     KDA_ERR_UNSUPPORTED = 4,       /* head dims this build has no kernel for      */
     KDA_ERR_ALIAS = 5,             /* state_out overlaps state_in (other than an
                                       exact in-place alias for the recurrence)   */
-    KDA_ERR_LAUNCH = 6             /* hipGetLastError() after the launch          */
+    KDA_ERR_LAUNCH = 6,            /* hipGetLastError() after the launch, or no
+                                      current HIP device                         */
+    KDA_ERR_TOO_LARGE = 7          /* the shape needs more scratch memory than the
+                                      library's static buffer holds               */
 } kda_status;
 
 /* One call's arguments.  Plain data: pointers, sizes, strides, codes. */
@@ -155,6 +158,26 @@ typedef struct kda_bwd_args {
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 
 int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
+
+/* Bytes of the static device buffer behind kda_chunkwise_bwd_noalloc. */
+#define KDA_BWD_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * kda_chunkwise_bwd without a caller workspace and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory -- code under hipGraph capture, tight serving or training
+ * loops, harnesses that forbid hipMalloc.  args->workspace is ignored; the
+ * three kernels use instead a static device buffer of KDA_BWD_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends
+ * (resolved once per device, on the first call with that device current;
+ * `stream` must belong to the current device).  Shapes whose
+ * kda_chunkwise_bwd_workspace_size() exceeds KDA_BWD_SCRATCH_BYTES return
+ * KDA_ERR_TOO_LARGE before any launch.  Every call on one GPU shares that
+ * GPU's buffer: calls that overlap on one GPU (two streams, two threads) race
+ * and must be serialised by the caller.  Results are identical to
+ * kda_chunkwise_bwd's (the same kernels).
+ */
+int kda_chunkwise_bwd_noalloc(const kda_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Layer pre- and post-processing around the core (the KDA layer,

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(native):
 def test_abi_version_and_status_strings(native):
     lib = native.load()
     assert lib.kda_abi_version() == native.ABI_VERSION
-    for code in range(7):
+    for code in range(8):
         assert native.status_str(code)
     assert native.status_str(0) == "ok"
     assert "unknown" in native.status_str(99)
@@ -192,3 +192,25 @@ def test_wrapper_shape_and_chunk_errors(kda_pkg):
         kda_pkg.kda_recurrent(q, q, v, q, torch.zeros(1, 20, 2))
     with pytest.raises(kda_pkg.KdaError, match="state must be"):
         kda_pkg.kda_recurrent(q, q, v, q, beta, state=torch.zeros(1, 1, 64, 32))
+
+
+def test_noalloc_backward_rejects_shapes_beyond_its_buffer(native):
+    """kda_chunkwise_bwd_noalloc refuses, on the host and before touching the
+    device, a shape whose workspace exceeds KDA_BWD_SCRATCH_BYTES."""
+    lib = native.load()
+    header = HEADER.read_text()
+    assert re.search(r"#define KDA_BWD_SCRATCH_BYTES \(\(size_t\)64 << 20\)", header)
+    assert native.BWD_SCRATCH_BYTES == 64 << 20
+    a = native.KdaBwdArgs()
+    a.B, a.T, a.H, a.K, a.V = 8, 4096, 16, 128, 128
+    assert lib.kda_chunkwise_bwd_workspace_size(8, 4096, 16, 128, 128) > native.BWD_SCRATCH_BYTES
+    fake = 0x1000                       # never dereferenced: the call is rejected first
+    for f in ("q", "k", "v", "g", "beta", "ckpt", "d_o", "dq", "dk", "dg", "dbeta", "dv"):
+        setattr(a, f, fake)
+    a.io_dtype = native.DTYPE_F16
+    a.workspace = None                  # ignored by the no-allocation entry point
+    assert lib.kda_chunkwise_bwd_noalloc(ctypes.byref(a), None) == native.STATUS_TOO_LARGE
+    a.q = None
+    assert lib.kda_chunkwise_bwd_noalloc(ctypes.byref(a), None) == 1     # NULL input first
+    a.B = 0
+    assert lib.kda_chunkwise_bwd_noalloc(ctypes.byref(a), None) == 0     # empty: nothing to do
