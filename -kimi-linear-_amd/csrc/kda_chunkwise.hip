@@ -67,9 +67,11 @@
 // line per channel holding the chunk's 32 tokens in the order of the
 // consumer's P fragments, its 16-byte pieces rotated by channel bits 2-3.
 //
-// Operands that are not exact in fp16 and carry the state (S, P, M, G_10
-// and V - Z) are split into fp16 hi + lo; the others are single fp16 with
-// fp32 accumulation.
+// Precision: fp32 accumulation everywhere; the state is carried in fp32.
+// The solve's results P, M and G_10, which the state update and the chunk's
+// outputs take as operands, are split into fp16 hi + lo; S (in Z and O) and
+// R = V - Z enter their products as single fp16 operands (rounded once per
+// chunk), like q * E, k * E and A.
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -83,7 +85,6 @@ constexpr int CB = 2;           // blocks per chunk (the state advances per chun
 constexpr int NB = 4;           // blocks per superstep = producer waves
 constexpr int NCH = NB / CB;    // chunks per superstep
 constexpr int RP = 24;          // padded row (halfs) of the [16][16] fp16 A-operand matrices
-constexpr int LP = 20;          // padded row (floats) of the 16x16 fp32 L
 constexpr int kXcds = 8;        // accelerator complex dies on MI355X
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -180,6 +181,12 @@ __device__ __forceinline__ h8 cat(const h4& a, const h4& b) {
     return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// Four fp32 values rounded to fp16 (round to nearest even).
+__device__ __forceinline__ h4 to_h4(const f4& x) {
+    return h4{static_cast<_Float16>(x[0]), static_cast<_Float16>(x[1]), static_cast<_Float16>(x[2]),
+              static_cast<_Float16>(x[3])};
+}
+
 // Position of channel c inside a row-major operand row.  With c = 32u + 16hi
 // + 4g + j, the consumer lane of group g pairs channels 32u + 4g + j and
 // 32u + 16 + 4g + j with its state rows; they sit at 32u + 8g + (0..7).
@@ -213,11 +220,12 @@ struct __align__(16) Stage {
     _Float16 KH0[BT][K + 8];               // block 0: k * (decay to the block end), row-major
     float e15[CB][K];                      // per block: decay over the block
 };
+constexpr int MAX_NC = 4;        // consumer waves per workgroup (at most)
 template <int K>
 struct __align__(16) Smem {
     ChunkOps<K> set[2][NCH];
     Stage<K> st[NCH];
-    float LT[NB][BT][LP];                  // per block: the transposition of L in the solve
+    uint16_t vt[MAX_NC][CB * BT][16];      // per consumer wave: one chunk of v, 16-bit, row-major
 };
 
 __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, int lg) {
@@ -304,10 +312,65 @@ __device__ __forceinline__ void store_state(const f4 (&S)[KT], void* p, int dtyp
 // from level 1, rows 1, 5, .. from level 2, 3 and 11 from level 3, 7 from
 // level 4, where both of row c's operands carry the factor 1); 5 for row 15,
 // which no level supplies; -1 above the diagonal.
-__device__ __forceinline__ int pair_level(int c, int i) {
+__host__ __device__ constexpr int pair_level(int c, int i) {
     if (c < i) return -1;
-    if (c == i) return 1 + __builtin_ctz(~static_cast<unsigned>(c));
-    return 32 - __builtin_clz(static_cast<unsigned>(c ^ i));
+    if (c == i) {
+        int t = 0;
+        while ((c >> t) & 1) ++t;
+        return 1 + t;
+    }
+    int x = c ^ i, bits = 0;
+    while (x) {
+        x >>= 1;
+        ++bits;
+    }
+    return bits;
+}
+
+// Lane masks of the entries one level supplies, per accumulator slot j:
+// lane l = 16 lg + ln holds entry (row 4 lg + j, column ln) of a 16 x 16
+// tile.  Kind 0: G, strictly below the diagonal; kind 1: G^T (the mirrored
+// entry of the symmetric level product), strictly above; kind 2: A, on or
+// below the diagonal.  Constants, so a selection is one v_cndmask with the
+// mask in VCC.
+constexpr uint64_t level_mask(int lev, int j, int kind) {
+    uint64_t m = 0;
+    for (int l = 0; l < 64; ++l) {
+        const int r = 4 * (l >> 4) + j, c = l & 15;
+        const bool on = kind == 0 ? (r != c && pair_level(r, c) == lev)
+                        : kind == 1 ? (r != c && pair_level(c, r) == lev)
+                                    : pair_level(r, c) == lev;
+        if (on) m |= uint64_t{1} << l;
+    }
+    return m;
+}
+
+template <int LEV, int J, int KIND>
+constexpr uint64_t kLevelMask = level_mask(LEV, J, KIND);
+
+template <int LEV, int KIND, int J>
+__device__ __forceinline__ void take_slot(f4& dst, const f4& src) {
+    constexpr uint64_t m = kLevelMask<LEV, J, KIND>;
+    if constexpr (m != 0) dst[J] = __builtin_amdgcn_inverse_ballot_w64(m) ? src[J] : dst[J];
+}
+// dst takes src in the entries level LEV supplies (mask kind KIND).
+template <int LEV, int KIND>
+__device__ __forceinline__ void take(f4& dst, const f4& src) {
+    take_slot<LEV, KIND, 0>(dst, src);
+    take_slot<LEV, KIND, 1>(dst, src);
+    take_slot<LEV, KIND, 2>(dst, src);
+    take_slot<LEV, KIND, 3>(dst, src);
+}
+
+// c + X Y for 16 x 16 fp32 tiles on the fp32 matrix cores (four 16x16x4
+// steps): xt is the accumulator layout of X^T (lane (ln, lg) slot u holds
+// X[ln][4 lg + u], the A operand of step u) and y the accumulator layout of
+// Y (slot u holds Y[4 lg + u][ln], the B operand); the result is in
+// accumulator layout.  Used only in chains of this one form.
+__device__ __forceinline__ f4 mm_f32(const f4& xt, const f4& y, f4 c) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) c = __builtin_amdgcn_mfma_f32_16x16x4f32(xt[u], y[u], c, 0, 0, 0);
+    return c;
 }
 
 template <int K, int NC, typename TQ>
@@ -327,12 +390,19 @@ struct Kern {
         uint32_t q[HR][QW], k[HR][QW], g[HR][GW];
         uint32_t beta[4];
     };
-    // The same block, converted: decays, fp16 q and k rows (channels in the
-    // low CH slots), beta.
+    // The same block, converted: decays a = exp(g), fp16 q and k rows
+    // (channels in the low CH slots), beta of rows 4lg .. 4lg + 3 and of row
+    // ln (the solve's row and column scales).
     struct Work {
         float al[CH][HR];
         h4 q[HR], k[HR];
         float beta[4];
+        float beta_col;
+    };
+    // What a producer carries from the first half of a superstep into the
+    // second: the level sums G (strictly lower), its mirror G^T and A.
+    struct Sums {
+        f4 G, GT, A;
     };
 
     const kda_fwd_args& a;
@@ -361,20 +431,27 @@ struct Kern {
     }
 
     // ------------------------------------------------------------ producers
-    __device__ void load_raw(Raw& r, int blk) const {
+    // Rows G0 .. G1 - 1 of the lane's half of block blk (and beta): issued in
+    // small groups between the level products, so that no wave stalls on a
+    // burst of vector memory instructions.
+    template <int G0, int G1, bool BETA>
+    __device__ void load_rows(Raw& r, int blk) const {
         const auto rq = block_rsrc(a.q, a.q_stride, sizeof(TQ), rs_q, blk);
         const auto rk = block_rsrc(a.k, a.k_stride, sizeof(TQ), rs_k, blk);
         const auto rg = block_rsrc(a.g, a.g_stride, 4, rs_g, blk);
-        const auto rb = block_rsrc(a.beta, a.beta_stride, 4, rs_b, blk);
 #pragma unroll
-        for (int i = 0; i < HR; ++i) {
+        for (int i = G0; i < G1; ++i) {
             BLoad<4 * CH>::ld(r.g[i], rg, vo_g, i * rs_g);
             BLoad<QB>::ld(r.q[i], rq, vo_q, i * rs_q);
             BLoad<QB>::ld(r.k[i], rk, vo_k, i * rs_k);
         }
+        if constexpr (BETA) {
+            const auto rb = block_rsrc(a.beta, a.beta_stride, 4, rs_b, blk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) BLoad<4>::ld(&r.beta[j], rb, vo_b, j * rs_b);
+            for (int j = 0; j < 4; ++j) BLoad<4>::ld(&r.beta[j], rb, vo_b, j * rs_b);
+        }
     }
+    __device__ void load_raw(Raw& r, int blk) const { load_rows<0, HR, true>(r, blk); }
 
     __device__ void unpack(Raw& r, Work& w) const {
         use_here(r.q);
@@ -396,6 +473,12 @@ struct Kern {
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) w.beta[j] = __uint_as_float(r.beta[j]);
+        // beta of row ln: slot ln % 4 of lane group ln / 4
+        const int src = 16 * (ln >> 2) + (lane & 15);
+        float bc = w.beta[0];
+#pragma unroll
+        for (int j = 1; j < 4; ++j) bc = (ln & 3) == j ? w.beta[j] : bc;
+        w.beta_col = __shfl(bc, src);
     }
 
     // Row r of per-channel values x[c][r], rounded to fp16, as a row vector
@@ -404,6 +487,13 @@ struct Kern {
         h4 v = {0, 0, 0, 0};
 #pragma unroll
         for (int c = 0; c < CH; ++c) v[c] = static_cast<_Float16>(x[c][r]);
+        return v;
+    }
+    // Per-channel values as a row vector.
+    static __device__ __forceinline__ h4 chanvec(const float (&x)[CH]) {
+        h4 v = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = static_cast<_Float16>(x[c]);
         return v;
     }
 
@@ -418,6 +508,17 @@ struct Kern {
             *p = v[0];
         }
     }
+    __device__ h4 get_row(const _Float16* m, int row) const {
+        const _Float16* p = m + row * KR + chan_pos(CH * cq);
+        if constexpr (CH == 4) {
+            return *reinterpret_cast<const h4*>(p);
+        } else if constexpr (CH == 2) {
+            const h2 x = *reinterpret_cast<const h2*>(p);
+            return h4{x[0], x[1], 0, 0};
+        } else {
+            return h4{*p, 0, 0, 0};
+        }
+    }
     // Rows 4part .. 4part + 3 of this lane's half of block bi into the
     // k-major lines of its channels (one 8-byte piece per channel).
     __device__ void put_kmajor(_Float16 (*kh)[2 * BT], int bi, int part, const h4 (&v)[4]) const {
@@ -427,13 +528,6 @@ struct Kern {
             const h4 piece = {v[0][c], v[1][c], v[2][c], v[3][c]};
             *reinterpret_cast<h4*>(&kh[ch][8 * ((2 * hf + part) ^ kh_swz(ch)) + 4 * bi]) = piece;
         }
-    }
-    // Row r of x[c][r] * m[c], rounded to fp16, as a row vector.
-    static __device__ __forceinline__ h4 rowvec(const float (&x)[CH][HR], const float (&m)[CH], int r) {
-        h4 v = {0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < CH; ++c) v[c] = static_cast<_Float16>(x[c][r] * m[c]);
-        return v;
     }
 
     // Level factors of the half's 8 rows, level B in 0..2 (groups of 2^(B+1)
@@ -462,37 +556,39 @@ struct Kern {
         }
     }
 
-    // Operand level LEV (1..4) of a block: X_b = k * F_b and Y_b = q * F_b,
-    // written row-major into xs / ys, b = LEV - 1.  Y_b is only read in the
-    // rows that are the later row of a level-b pair (bit b set, scaled) and
-    // in the level's reference rows (the last lower row of each group, factor
-    // 1: the diagonal of A); its other rows are not written.  Level 4 pairs
-    // the two halves: its factors are the decays from the upper half's start
-    // (pl) and to the lower half's end (sl, 1 in the reference row 7); all
-    // of its Y rows are written (a lane-dependent choice costs registers).
+    // Operands of level LEV (1..4): X = k * f and Y = q * f row-major into
+    // xs / ys.  Rows with the factor 1 (each group's reference row) take k
+    // and q as they are.  Y is read only in the rows that are the later row
+    // of a level pair and in the reference rows (the diagonal of A); its
+    // other rows are left as they are.  Level 4's factors are the in-lane
+    // running products (the upper half's prefix products from its start, the
+    // lower half's suffix products to its end); it writes every Y row.
     template <int LEV>
-    __device__ void stage(const Work& w, const float (&pl)[CH][HR], const float (&sl)[CH][HR], _Float16* xs,
+    __device__ void stage(const Work& w, const float (&pre)[CH][HR], const float (&suf)[CH][HR], _Float16* xs,
                           _Float16* ys) const {
         constexpr int bb = LEV - 1;
         float f[CH][HR];
         if constexpr (LEV <= 3) {
 #pragma unroll
             for (int c = 0; c < CH; ++c) level_factors<bb>(w.al[c], f[c]);
-        } else {
-#pragma unroll
-            for (int c = 0; c < CH; ++c)
-#pragma unroll
-                for (int r = 0; r < HR; ++r) f[c][r] = hf ? pl[c][r] : sl[c][r];
         }
 #pragma unroll
         for (int r = 0; r < HR; ++r) {
-            const h4 fr = rowvec(f, r);
-            put_row(xs, HR * hf + r, w.k[r] * fr);
             if constexpr (LEV <= 3) {
                 const bool upper = (r >> bb) & 1, ref = (r & ((2 << bb) - 1)) == (1 << bb) - 1;
-                if (upper) put_row(ys, HR * hf + r, w.q[r] * fr);
-                else if (ref) put_row(ys, HR * hf + r, w.q[r]);
+                if (ref) {
+                    put_row(xs, HR * hf + r, w.k[r]);
+                    put_row(ys, HR * hf + r, w.q[r]);
+                } else {
+                    const h4 fr = rowvec(f, r);
+                    put_row(xs, HR * hf + r, w.k[r] * fr);
+                    if (upper) put_row(ys, HR * hf + r, w.q[r] * fr);
+                }
             } else {
+                h4 fr = {0, 0, 0, 0};
+#pragma unroll
+                for (int c = 0; c < CH; ++c) fr[c] = static_cast<_Float16>(hf ? pre[c][r] : suf[c][r]);
+                put_row(xs, HR * hf + r, w.k[r] * fr);
                 put_row(ys, HR * hf + r, w.q[r] * fr);
             }
         }
@@ -513,49 +609,46 @@ struct Kern {
         return f;
     }
 
-    // Level LEV's products: G_b = X_b X_b^T and A_b = Y_b X_b^T over all K
-    // channels, keeping the entries the level supplies (accumulator layout:
-    // row 4lg + j, column ln).
+    // Level LEV's products over all K channels, X X^T (symmetric) and Y X^T,
+    // keeping the entries the level supplies: G below the diagonal, its
+    // mirror G^T above it, A on and below it.
     template <int LEV>
-    __device__ void product(const Frags& fr, f4& Gacc, f4& Aacc) const {
+    __device__ void product(const Frags& fr, Sums& sum) const {
         f4 accG = {0.f, 0.f, 0.f, 0.f}, accA = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
             accG = mfma16x16x32(fr.x[u], fr.x[u], accG);
             accA = mfma16x16x32(fr.y[u], fr.x[u], accA);
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (pair_level(4 * lg + j, ln) == LEV) {
-                if (4 * lg + j != ln) Gacc[j] = accG[j];   // G (and L) is strictly lower
-                Aacc[j] = accA[j];
-            }
-        }
+        take<LEV, 0>(sum.G, accG);
+        take<LEV, 1>(sum.GT, accG);
+        take<LEV, 2>(sum.A, accA);
     }
 
-    // M = (I + L)^-1 Diag(beta) of one block (wave p, L in accumulator
-    // layout), stored as hi/lo A-operand fragments.
-    __device__ void solve(const f4& Lc, const float (&beta)[4], _Float16 (*mh)[RP], _Float16 (*ml)[RP], int p) const {
-        float* lt = &sm.LT[p][0][0];
+    // M = (I + L)^-1 Diag(beta) of one block, L = Diag(beta) G, as hi/lo
+    // A-operand fragments.  (I + L)^-T = (I - L^T)(I + (L^2)^T)(I + (L^4)^T)
+    // (I + (L^8)^T) (L is nilpotent) on the fp32 matrix cores: a product X Y
+    // takes X^T's and Y's accumulator layouts, so the chain keeps powers and
+    // their transposes side by side; no data moves between lanes.
+    __device__ void solve(const Sums& sum, const Work& w, _Float16 (*mh)[RP], _Float16 (*ml)[RP]) const {
+        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+        f4 L, LT;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lt[(4 * lg + j) * LP + ln] = Lc[j];
-        f4 Lt;                                           // acc(L^T)
-        {
-            const float4 r = *reinterpret_cast<const float4*>(lt + ln * LP + 4 * lg);
-            Lt[0] = r.x; Lt[1] = r.y; Lt[2] = r.z; Lt[3] = r.w;
+        for (int j = 0; j < 4; ++j) {
+            L[j] = sum.G[j] * w.beta[j];          // row 4lg + j scaled by its beta
+            LT[j] = sum.GT[j] * w.beta_col;       // L^T: column ln of L^T is row ln of L
         }
-        const Split4 lc(Lc), ltt(Lt);
-        const Split4 l2(mm4(ltt, lc)), l2t(mm4(lc, ltt));  // L^2, (L^2)^T
-        const Split4 l4(mm4(l2t, l2)), l4t(mm4(l2, l2t));
-        const Split4 l8(mm4(l4t, l4));
-        f4 Q;                                            // acc(I - L^T)
+        const f4 L2 = mm_f32(LT, L, zero), L2T = mm_f32(L, LT, zero);
+        const f4 L4 = mm_f32(L2T, L2, zero), L4T = mm_f32(L2, L2T, zero);
+        const f4 L8 = mm_f32(L4T, L4, zero);
+        f4 Q;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) Q[j] = (4 * lg + j == ln ? 1.f : 0.f) - Lt[j];
-        Q = mm4(l2, Split4(Q), Q);
-        Q = mm4(l4, Split4(Q), Q);
-        Q = mm4(l8, Split4(Q), Q);                       // acc(Minv^T) = A-layout of Minv
+        for (int j = 0; j < 4; ++j) Q[j] = (4 * lg + j == ln ? 1.f : 0.f) - LT[j];
+        Q = mm_f32(L2, Q, Q);
+        Q = mm_f32(L4, Q, Q);
+        Q = mm_f32(L8, Q, Q);                    // acc((I + L)^-T) = A-layout of (I + L)^-1
 #pragma unroll
-        for (int j = 0; j < 4; ++j) Q[j] *= beta[j];
+        for (int j = 0; j < 4; ++j) Q[j] *= w.beta[j];
         h4 hi, lo;
         split4(Q, hi, lo);
         *reinterpret_cast<h4*>(&mh[ln][4 * lg]) = hi;
@@ -563,74 +656,93 @@ struct Kern {
     }
 
     // First half of a superstep for block p (bi = p % 2 of chunk cj): the
-    // level products (the next block's loads go out after the first two),
-    // the decays of the block, and every operand that needs no other block's
-    // decay.  `keep` receives, for the second half, the decays to the block
-    // end (block 0) or from the block start (block 1).
-    __device__ void phase1(Raw& raw, Work& w, f4& Gacc, f4& Aacc, float (&keep)[CH][HR], int p,
-                           ChunkOps<K>& co, int next) const {
+    // decays, the level products (with the loads of block `next` between
+    // them), and every operand that needs no other block's decay: block 0's
+    // q * E, k * E and block-local k * F (staged for G_10, A_10); block 1's
+    // block-local q * E and k * E (staged) and its k * F into the k-major
+    // lines.  The block decay E[15] goes to the stage area.
+    __device__ void phase1(Raw& raw, Work& w, Sums& sum, int p, ChunkOps<K>& co, int next) const {
         const int bi = p % CB, cj = p / CB;
         Stage<K>& st = sm.st[cj];
         unpack(raw, w);
-        Gacc = f4{0.f, 0.f, 0.f, 0.f};
-        Aacc = f4{0.f, 0.f, 0.f, 0.f};
+        sum.G = f4{0.f, 0.f, 0.f, 0.f};
+        sum.GT = sum.G;
+        sum.A = sum.G;
         // level operands are staged in the block's q * E / k * E rows, which
         // get their final values after the last level
         _Float16* xs = &co.QE[bi][0][0];
         _Float16* ys = &co.KE[bi][0][0];
-        float pl[CH][HR], sl[CH][HR];                    // decays from the half's start / to its end
-        // Levels are software-pipelined through the one staging pair: LDS
-        // serves a wave's requests in order, so level b+1's operands may be
-        // written as soon as level b's fragment reads are issued, and their
-        // VALU work covers those reads and level b's MFMAs.
-        stage<1>(w, pl, sl, xs, ys);
-        Frags fr = read_frags(xs, ys);
-        stage<2>(w, pl, sl, xs, ys);
-        product<1>(fr, Gacc, Aacc);
-        load_raw(raw, next);
-        fr = read_frags(xs, ys);
-        stage<3>(w, pl, sl, xs, ys);
-        product<2>(fr, Gacc, Aacc);
-        fr = read_frags(xs, ys);
+        // in-lane running products over the half's rows: pre (inclusive, from
+        // the half's start) and suf (exclusive, to the half's end)
+        float pre[CH][HR], suf[CH][HR];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            pl[c][0] = w.al[c][0];
+            pre[c][0] = w.al[c][0];
 #pragma unroll
-            for (int r = 1; r < HR; ++r) pl[c][r] = pl[c][r - 1] * w.al[c][r];
-            sl[c][HR - 1] = 1.f;
+            for (int r = 1; r < HR; ++r) pre[c][r] = pre[c][r - 1] * w.al[c][r];
+            suf[c][HR - 1] = 1.f;
 #pragma unroll
-            for (int r = HR - 2; r >= 0; --r) sl[c][r] = sl[c][r + 1] * w.al[c][r + 1];
+            for (int r = HR - 2; r >= 0; --r) suf[c][r] = suf[c][r + 1] * w.al[c][r + 1];
         }
-        stage<4>(w, pl, sl, xs, ys);
-        product<3>(fr, Gacc, Aacc);
+        // Levels are software-pipelined through the one staging pair: LDS
+        // serves a wave's requests in order, so level b+1's operands may be
+        // written as soon as level b's fragment reads are issued.
+        stage<1>(w, pre, suf, xs, ys);
+        Frags fr = read_frags(xs, ys);
+        stage<2>(w, pre, suf, xs, ys);
+        product<1>(fr, sum);
+        load_rows<0, 2, false>(raw, next);
         fr = read_frags(xs, ys);
-        product<4>(fr, Gacc, Aacc);
+        stage<3>(w, pre, suf, xs, ys);
+        product<2>(fr, sum);
+        load_rows<2, 4, false>(raw, next);
+        fr = read_frags(xs, ys);
+        stage<4>(w, pre, suf, xs, ys);
+        product<3>(fr, sum);
+        load_rows<4, 6, false>(raw, next);
+        fr = read_frags(xs, ys);
+        product<4>(fr, sum);
+        load_rows<6, 8, true>(raw, next);
+        // A[15][15] = <q_15, k_15>: row 15 is no level's reference row
+        {
+            float dq = 0.f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+                dq += static_cast<float>(w.q[HR - 1][c]) * static_cast<float>(w.k[HR - 1][c]);
+            dq = wave_sum(hf ? dq : 0.f);
+            if (lane == 63) sum.A[3] = dq;
+        }
 
-        // block decays: the upper half's prefix continues the lower half's,
-        // the lower half's suffix continues into the upper half
-        float mp[CH], ms[CH];
+        // the other half's total decay; the block decay E[15]
+        float other[CH];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             // the swap returns this lane's value in one slot and the other
             // half's in the other
-            const unsigned u = __float_as_uint(pl[c][HR - 1]);
+            const unsigned u = __float_as_uint(pre[c][HR - 1]);
             const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-            const float other = __uint_as_float(sw[0] != u ? sw[0] : sw[1]);
-            mp[c] = hf ? other : 1.f;
-            ms[c] = hf ? 1.f : other;
-            if (hf == 0) st.e15[bi][CH * cq + c] = pl[c][HR - 1] * other;
+            other[c] = __uint_as_float(sw[0] != u ? sw[0] : sw[1]);
+            if (hf == 0) st.e15[bi][CH * cq + c] = pre[c][HR - 1] * other[c];
         }
+        // block-local decays: E (from the block start, inclusive) = pre, times
+        // the lower half's total in the upper half; F (to the block end,
+        // exclusive) = suf, times the upper half's total in the lower half
+        float mE[CH], mF[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            mE[c] = hf ? other[c] : 1.f;
+            mF[c] = hf ? 1.f : other[c];
+        }
+        const h4 hE = chanvec(mE), hF = chanvec(mF);
         // rows are produced and stored one at a time (few registers live)
         if (bi == 0) {
             // block 0: decays from its start are decays from the chunk start
 #pragma unroll
             for (int r = 0; r < HR; ++r) {
-                const h4 e = rowvec(pl, mp, r), f = rowvec(sl, ms, r);
+                const h4 e = rowvec(pre, r) * hE, f = rowvec(suf, r) * hF;
                 put_row(&co.QE[0][0][0], HR * hf + r, w.q[r] * e);
                 put_row(&co.KE[0][0][0], HR * hf + r, w.k[r] * e);
                 put_row(&st.KH0[0][0], HR * hf + r, w.k[r] * f);
-#pragma unroll
-                for (int c = 0; c < CH; ++c) keep[c][r] = sl[c][r] * ms[c];
             }
         } else {
             // block 1: decays to its end are decays to the chunk end; its
@@ -641,12 +753,10 @@ struct Kern {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * part + i;
-                    const h4 e = rowvec(pl, mp, r);
-                    fk[i] = w.k[r] * rowvec(sl, ms, r);
+                    const h4 e = rowvec(pre, r) * hE;
+                    fk[i] = w.k[r] * (rowvec(suf, r) * hF);
                     put_row(&co.QE[1][0][0], HR * hf + r, w.q[r] * e);
                     put_row(&co.KE[1][0][0], HR * hf + r, w.k[r] * e);
-#pragma unroll
-                    for (int c = 0; c < CH; ++c) keep[c][r] = pl[c][r] * mp[c];
                 }
                 put_kmajor(co.KH, 1, part, fk);
             }
@@ -654,22 +764,22 @@ struct Kern {
     }
 
     // Second half: the operands that need the other block's decay (block 0:
-    // k * F; block 1: G_10 and A_10 from the block-local operands, then
-    // q * E and k * E from the chunk start, and the chunk decay), then A and
-    // the inverse of (I + L).
-    __device__ void phase2(const Work& w, const f4& Gacc, const f4& Aacc, const float (&keep)[CH][HR], int p,
-                           ChunkOps<K>& co) const {
+    // k * F to the chunk end; block 1: G_10 and A_10 from the block-local
+    // operands, then q * E and k * E from the chunk start, and the chunk
+    // decay), A and the inverse of (I + L).
+    __device__ void phase2(const Work& w, const Sums& sum, int p, ChunkOps<K>& co) const {
         const int bi = p % CB, cj = p / CB;
         Stage<K>& st = sm.st[cj];
         float d[CH];
 #pragma unroll
         for (int c = 0; c < CH; ++c) d[c] = st.e15[1 - bi][CH * cq + c];
+        const h4 dh = chanvec(d);
         if (bi == 0) {
 #pragma unroll
             for (int part = 0; part < 2; ++part) {
                 h4 fk[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) fk[i] = w.k[4 * part + i] * rowvec(keep, d, 4 * part + i);
+                for (int i = 0; i < 4; ++i) fk[i] = get_row(&st.KH0[0][0], HR * hf + 4 * part + i) * dh;
                 put_kmajor(co.KH, 0, part, fk);
             }
         } else {
@@ -688,111 +798,128 @@ struct Kern {
             split4(-accG, gh, gl);
             *reinterpret_cast<h4*>(&co.GH[ln][4 * lg]) = gh;
             *reinterpret_cast<h4*>(&co.GL[ln][4 * lg]) = gl;
-            const f4 as = accA * scale;
-            *reinterpret_cast<h4*>(&co.A10[ln][4 * lg]) =
-                h4{static_cast<_Float16>(as[0]), static_cast<_Float16>(as[1]), static_cast<_Float16>(as[2]),
-                   static_cast<_Float16>(as[3])};
+            *reinterpret_cast<h4*>(&co.A10[ln][4 * lg]) = to_h4(accA * scale);
+            // chunk-relative q * E and k * E: the block-local rows times the
+            // decay of block 0 (LDS serves the wave's reads above first)
 #pragma unroll
             for (int r = 0; r < HR; ++r) {
-                const h4 e = rowvec(keep, d, r);
-                put_row(&co.QE[1][0][0], HR * hf + r, w.q[r] * e);
-                put_row(&co.KE[1][0][0], HR * hf + r, w.k[r] * e);
+                const int row = HR * hf + r;
+                put_row(&co.QE[1][0][0], row, get_row(&co.QE[1][0][0], row) * dh);
+                put_row(&co.KE[1][0][0], row, get_row(&co.KE[1][0][0], row) * dh);
             }
-            if (hf == 1) {
-                // row 15 of block 1 ends the chunk
+            if (hf == 0) {
 #pragma unroll
-                for (int c = 0; c < CH; ++c) co.echunk[CH * cq + c] = keep[c][HR - 1] * d[c];
+                for (int c = 0; c < CH; ++c) co.echunk[CH * cq + c] = st.e15[1][CH * cq + c] * d[c];
             }
         }
-        // A[15][15] = <q_15, k_15>: row 15 is no level's reference row
-        f4 A = Aacc;
-        {
-            float dq = 0.f;
 #pragma unroll
-            for (int c = 0; c < CH; ++c)
-                dq += static_cast<float>(w.q[HR - 1][c]) * static_cast<float>(w.k[HR - 1][c]);
-            dq = wave_sum(hf ? dq : 0.f);
-            if (lane == 63) A[3] = dq;
-        }
-        f4 G = Gacc;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(A[j] * scale);
-            G[j] *= w.beta[j];
-        }
-        solve(G, w.beta, co.MH[bi], co.ML[bi], p);
+        for (int j = 0; j < 4; ++j) co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(sum.A[j] * scale);
+        solve(sum, w, co.MH[bi], co.ML[bi]);
     }
 
     // ------------------------------------------------------------ consumers
-    __device__ void v_load(uint32_t (&vr)[4], int blk) const {
-        const auto rv = block_rsrc(a.v, a.v_stride, sizeof(TQ), rs_v, blk);
+    // The v values of one chunk for this wave's 16 columns: 32 rows x 32
+    // bytes (16-bit inputs: row lane / 2, 8 columns a lane) or 32 x 64 bytes
+    // (fp32: rows lane / 4 and 16 + lane / 4, 4 columns a lane), one 16-byte
+    // buffer load per lane and row set; rows past T read as zero.
+    static constexpr int VW = sizeof(TQ) == 2 ? 4 : 8;
+    __device__ void v_load(uint32_t (&vr)[VW], int chunk) const {
+        const int blk = CB * chunk;
+        const int64_t e = b * a.v_stride[0] + static_cast<int64_t>(blk) * BT * a.v_stride[1] + h * a.v_stride[2];
+        const int left = rows_in(blk) + rows_in(blk + 1);
+        const auto rv = make_rsrc(static_cast<const char*>(a.v) + e * static_cast<int64_t>(sizeof(TQ)),
+                                  static_cast<uint32_t>(left) * rs_v);
+        uint32_t* w = vr;
+        BLoad<16>::ld(w, rv, vo_v, 0);
+        if constexpr (VW == 8) BLoad<16>::ld(w + 4, rv, vo_v, 16 * rs_v);
+    }
+    // The chunk's v into this wave's tile as 16-bit values (fp32 inputs are
+    // rounded to fp16 here), then the two blocks' fragments in accumulator
+    // layout (rows 4lg + j, column ln) by transposing LDS reads: in each
+    // 16-lane group, lane s reads row 4lg + s/4, columns 4 (s % 4) .. + 3,
+    // and the read hands lane i, slot j element i % 4 of lane 4j + i / 4.
+    __device__ void v_tile(uint32_t (&vr)[VW], uint16_t (*vt)[16], f4& R0, f4& R1) const {
+        use_here(vr);
+        if constexpr (VW == 4) {
+            *reinterpret_cast<u4*>(&vt[lane >> 1][8 * (lane & 1)]) = u4{vr[0], vr[1], vr[2], vr[3]};
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) BLoad<sizeof(TQ)>::ld(&vr[j], rv, vo_v, j * rs_v);
+            for (int part = 0; part < 2; ++part) {
+                const h4 x = {static_cast<_Float16>(__uint_as_float(vr[4 * part])),
+                              static_cast<_Float16>(__uint_as_float(vr[4 * part + 1])),
+                              static_cast<_Float16>(__uint_as_float(vr[4 * part + 2])),
+                              static_cast<_Float16>(__uint_as_float(vr[4 * part + 3]))};
+                *reinterpret_cast<h4*>(&vt[16 * part + (lane >> 2)][4 * (lane & 3)]) = x;
+            }
+        }
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        const int s = lane & 15;
+#pragma unroll
+        for (int bk = 0; bk < CB; ++bk) {
+            typedef __attribute__((address_space(3))) s4* lds_s4;
+            const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(&vt[16 * bk + 4 * lg + (s >> 2)][4 * (s & 3)]));
+            f4 r;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t bits = static_cast<uint16_t>(x[j]);
+                r[j] = Elem<TQ>::code == KDA_DTYPE_BF16 ? __uint_as_float(bits << 16)
+                                                        : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+            }
+            if (bk == 0) R0 = r;
+            else R1 = r;
+        }
     }
 
-    // Output rows 4lg + j of block blk (rows past T are skipped).
-    __device__ void store_o(const f4& O, int blk, int64_t col0, uint32_t ocol) const {
-        TQ* o = static_cast<TQ*>(a.o) + ((b * T + static_cast<int64_t>(blk) * BT) * a.H + h) * a.V + col0;
-        const uint32_t orow = static_cast<uint32_t>(a.H * a.V);
-        const int nrow = rows_in(blk);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (4 * lg + j < nrow) Elem<TQ>::st(o + (4 * lg + j) * orow + ocol, O[j]);
+    // Output rows of block blk from the transposed tile: lane (ln, lg) holds
+    // row ln, columns colw + 4lg .. + 3 (rows past T are skipped).
+    __device__ void store_ot(const f4& O, int blk, int64_t colw) const {
+        const int64_t row = static_cast<int64_t>(blk) * BT + ln;
+        if (ln >= rows_in(blk)) return;
+        TQ* o = static_cast<TQ*>(a.o) + ((b * T + row) * a.H + h) * a.V + colw + 4 * lg;
+        if constexpr (sizeof(TQ) == 4) {
+            *reinterpret_cast<float4*>(o) = float4{O[0], O[1], O[2], O[3]};
+        } else if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+            *reinterpret_cast<h4*>(o) = to_h4(O);
+        } else {
+            u2 w;
+            w[0] = static_cast<uint32_t>(f32_to_bf16_bits(O[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(O[1])) << 16);
+            w[1] = static_cast<uint32_t>(f32_to_bf16_bits(O[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(O[3])) << 16);
+            *reinterpret_cast<u2*>(o) = w;
+        }
     }
 
     // One chunk (blocks blk, blk + 1) of the chain for this wave's 16 state
-    // columns; the v loads of the same blocks one superstep later are issued
-    // into vraw0 / vraw1.  ck (or null): the chunk's checkpoint for the
-    // backward, in fp32: rows [0, K) the state before it, [K, K + 32) its
-    // R = V - (k * E) S, [K + 32, K + 64) its P.  The stores go out after the
-    // v loads, so that waiting for those loads never waits for them.
-    __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw0)[4], uint32_t (&vraw1)[4],
-                            f4 (&S)[KT], int64_t col0, uint32_t ocol, float* ck) const {
-        use_here(vraw0);
-        use_here(vraw1);
+    // columns (colw .. colw + 15; lane column ocol); the v load of the chunk
+    // one superstep later is issued into vraw once its values are in LDS.
+    // ck (or null): the chunk's checkpoint for the backward, in fp32: rows
+    // [0, K) the state before it, [K, K + 32) its R = V - (k * E) S,
+    // [K + 32, K + 64) its P.
+    __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw)[VW], uint16_t (*vt)[16], f4 (&S)[KT],
+                            int64_t col0, uint32_t ocol, int64_t colw, float* ck) const {
         f4 R0, R1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            R0[j] = raw_f<TQ>(vraw0[j]);
-            R1[j] = raw_f<TQ>(vraw1[j]);
-        }
-        v_load(vraw0, blk + NB);
-        v_load(vraw1, blk + 1 + NB);
+        v_tile(vraw, vt, R0, R1);
+        v_load(vraw, blk / CB + NCH);
         const int64_t V = a.V, rc = col0 + ocol;
         if (ck) store_state_t<KT>(S, ck, (4 * lg) * V + rc, V);
         float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
-        h8 shi[KU], slo[KU];
+        // S as single fp16 operands: Z and O read S once per chunk
+        h8 sh[KU];
 #pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            h4 h0, l0, h1, l1;
-            split4(S[2 * u], h0, l0);
-            split4(S[2 * u + 1], h1, l1);
-            shi[u] = cat(h0, h1);
-            slo[u] = cat(l0, l1);
-        }
-        // Z_b = (k * E)_b S and O_b = (q * E)_b S over the K channels
+        for (int u = 0; u < KU; ++u) sh[u] = cat(to_h4(S[2 * u]), to_h4(S[2 * u + 1]));
+        // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
+        // the same fragments as A and B operands the other way round, so that
+        // a lane holds four adjacent output columns of one row
         f4 Z0 = {0.f, 0.f, 0.f, 0.f}, Z1 = Z0, O0 = Z0, O1 = Z0;
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
             const int o = ln * KR + 32 * u + 8 * lg;
-            const h8 k0 = *reinterpret_cast<const h8*>(&co.KE[0][0][0] + o);
-            Z0 = mfma16x16x32(k0, shi[u], Z0);
-            Z0 = mfma16x16x32(k0, slo[u], Z0);
-            const h8 k1 = *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o);
-            Z1 = mfma16x16x32(k1, shi[u], Z1);
-            Z1 = mfma16x16x32(k1, slo[u], Z1);
+            Z0 = mfma16x16x32(*reinterpret_cast<const h8*>(&co.KE[0][0][0] + o), sh[u], Z0);
+            Z1 = mfma16x16x32(*reinterpret_cast<const h8*>(&co.KE[1][0][0] + o), sh[u], Z1);
+            O0 = mfma16x16x32(sh[u], *reinterpret_cast<const h8*>(&co.QE[0][0][0] + o), O0);
+            O1 = mfma16x16x32(sh[u], *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o), O1);
         }
-#pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            const int o = ln * KR + 32 * u + 8 * lg;
-            const h8 q0 = *reinterpret_cast<const h8*>(&co.QE[0][0][0] + o);
-            O0 = mfma16x16x32(q0, shi[u], O0);
-            O0 = mfma16x16x32(q0, slo[u], O0);
-            const h8 q1 = *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o);
-            O1 = mfma16x16x32(q1, shi[u], O1);
-            O1 = mfma16x16x32(q1, slo[u], O1);
-        }
-        // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0)
+        // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0): M (hi + lo)
+        // times a single fp16 R is one K = 32 product [M_hi | M_lo] [R ; R]
         R0 -= Z0;
         R1 -= Z1;
         if (rp) {
@@ -802,14 +929,14 @@ struct Kern {
                 rp[(16 + 4 * lg + j) * V + rc] = R1[j];
             }
         }
-        const Split4 r0(R0);
-        const f4 P0 = mm4(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg), r0.hi, r0.lo,
-                          f4{0.f, 0.f, 0.f, 0.f});
+        const h4 r0 = to_h4(R0);
+        const f4 P0 = mfma16x16x32(cat(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg)),
+                                   cat(r0, r0), f4{0.f, 0.f, 0.f, 0.f});
         const Split4 p0(P0);
         R1 = mm4(frag16(&co.GH[0][0], RP, ln, lg), frag16(&co.GL[0][0], RP, ln, lg), p0.hi, p0.lo, R1);
-        const Split4 r1(R1);
-        const f4 P1 = mm4(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg), r1.hi, r1.lo,
-                          f4{0.f, 0.f, 0.f, 0.f});
+        const h4 r1 = to_h4(R1);
+        const f4 P1 = mfma16x16x32(cat(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg)),
+                                   cat(r1, r1), f4{0.f, 0.f, 0.f, 0.f});
         const Split4 p1(P1);
         if (rp) {
 #pragma unroll
@@ -818,16 +945,17 @@ struct Kern {
                 rp[(48 + 4 * lg + j) * V + rc] = P1[j];
             }
         }
-        // O = scale (q * E) S + A P
+        // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is P's
+        // accumulator layout, A^T's B-operand layout is A's A-operand layout
         O0 *= scale;
         O1 *= scale;
         const h4 a00 = frag16(&co.AM[0][0][0], RP, ln, lg);
-        O0 = mfma16x16x32(cat(a00, a00), cat(p0.hi, p0.lo), O0);
+        O0 = mfma16x16x32(cat(p0.hi, p0.lo), cat(a00, a00), O0);
         const h8 a1 = cat(frag16(&co.A10[0][0], RP, ln, lg), frag16(&co.AM[1][0][0], RP, ln, lg));
-        O1 = mfma16x16x32(a1, cat(p0.hi, p1.hi), O1);
-        O1 = mfma16x16x32(a1, cat(p0.lo, p1.lo), O1);
-        store_o(O0, blk, col0, ocol);
-        store_o(O1, blk + 1, col0, ocol);
+        O1 = mfma16x16x32(cat(p0.hi, p1.hi), a1, O1);
+        O1 = mfma16x16x32(cat(p0.lo, p1.lo), a1, O1);
+        store_ot(O0, blk, colw);
+        store_ot(O1, blk + 1, colw);
         // S <- E[31] S + F^T P over both blocks: the k-major line of channel
         // 16t + ln gives tokens 4lg..4lg+3 of block 0 then of block 1, the
         // order of cat(P_0, P_1)
@@ -903,15 +1031,21 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         kn.vo_k = r0 * kn.rs_k + c0 * eq;
         kn.vo_g = r0 * kn.rs_g + c0 * 4u;
         kn.vo_b = static_cast<uint32_t>(4 * kn.lg) * kn.rs_b;
-        kn.vo_v = static_cast<uint32_t>(4 * kn.lg) * kn.rs_v + static_cast<uint32_t>(col) * eq;
+        // v tile loads: 16-bit inputs row lane / 2, columns 8 (lane % 2); fp32
+        // row lane / 4, columns 4 (lane % 4), of this wave's 16 columns
+        const uint32_t vrow = sizeof(TQ) == 2 ? (kn.lane >> 1) : (kn.lane >> 2);
+        const uint32_t vcol = sizeof(TQ) == 2 ? 8 * (kn.lane & 1) : 4 * (kn.lane & 3);
+        kn.vo_v = vrow * kn.rs_v + static_cast<uint32_t>(col0 + 16 * (consumer ? wave : 0) + vcol) * eq;
     }
 
     if (consumer) {
         f4 S[KT];
         load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
-        uint32_t vr[NB][4];
+        uint32_t vr[NCH][KN::VW];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) kn.v_load(vr[j], j);
+        for (int j = 0; j < NCH; ++j) kn.v_load(vr[j], j);
+        uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
+        const int64_t colw = col0 + 16 * (consumer ? wave : 0);
         for (int s = -1; s < nss; ++s) {
 #pragma unroll
             for (int cj = 0; cj < NCH; ++cj) {
@@ -920,7 +1054,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
                     // the checkpoint of chunk cc, for the backward
                     float* ck = ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K + 2 * CB * BT) * V
                                      : nullptr;
-                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[CB * cj], vr[CB * cj + 1], S, col0, ocol, ck);
+                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, col0, ocol, colw, ck);
                 }
                 __syncthreads();
             }
@@ -930,15 +1064,14 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         const int p = wave - NC;
         typename KN::Raw raw;
         typename KN::Work w;
-        f4 Gacc, Aacc;
-        float keep[CH][HR];
+        typename KN::Sums sum;
         kn.load_raw(raw, p);
         for (int s = -1; s < nss; ++s) {
             const int blk = NB * (s + 1) + p;
             ChunkOps<K>& co = sm.set[(s + 1) & 1][p / CB];
-            if (blk < nblk) kn.phase1(raw, w, Gacc, Aacc, keep, p, co, blk + NB);
+            if (blk < nblk) kn.phase1(raw, w, sum, p, co, blk + NB);
             __syncthreads();
-            if (blk < nblk) kn.phase2(w, Gacc, Aacc, keep, p, co);
+            if (blk < nblk) kn.phase2(w, sum, p, co);
             __syncthreads();
         }
     }
