@@ -193,10 +193,12 @@ __device__ __forceinline__ h4 to_h4(const f4& x) {
 __device__ __forceinline__ int chan_pos(int c) {
     return (c & ~31) | ((c & 12) << 1) | ((c & 16) >> 2) | (c & 3);
 }
-// 16-byte piece rotation of the k-major k * F lines (channel bits 2-3): the
-// 16 channel lines one consumer instruction reads land on 16 distinct bank
-// groups.
-__device__ __forceinline__ int kh_swz(int c) { return (c >> 2) & 3; }
+// The k-major k * F lines are 80 bytes apart (64 bytes of data) and their
+// 16-byte pieces are rotated by channel bits 4-5: the 16 lines one consumer
+// instruction reads start on 16 distinct groups of 4 banks, and the 32 lines
+// one producer instruction writes (channels 4 apart) on at most 2 per bank.
+constexpr int KHP = 2 * BT + 8;   // halfs per k-major line
+__device__ __forceinline__ int kh_swz(int c) { return (c >> 4) & 3; }
 
 // Operands of one chunk, as the consumers read them.
 template <int K>
@@ -204,7 +206,7 @@ struct __align__(16) ChunkOps {
     static constexpr int KR = K + 8;
     _Float16 QE[CB][BT][KR];               // q * E (decay from the chunk start), row-major
     _Float16 KE[CB][BT][KR];               // k * E
-    _Float16 KH[K][2 * BT];                // k * F (decay to the chunk end), k-major lines
+    _Float16 KH[K][KHP];                   // k * F (decay to the chunk end), k-major lines
     _Float16 AM[CB][BT][RP];               // scale * A, diagonal blocks
     _Float16 MH[CB][BT][RP];               // M hi
     _Float16 ML[CB][BT][RP];               // M lo
@@ -521,7 +523,7 @@ struct Kern {
     }
     // Rows 4part .. 4part + 3 of this lane's half of block bi into the
     // k-major lines of its channels (one 8-byte piece per channel).
-    __device__ void put_kmajor(_Float16 (*kh)[2 * BT], int bi, int part, const h4 (&v)[4]) const {
+    __device__ void put_kmajor(_Float16 (*kh)[KHP], int bi, int part, const h4 (&v)[4]) const {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int ch = CH * cq + c;
@@ -960,9 +962,9 @@ struct Kern {
         // 16t + ln gives tokens 4lg..4lg+3 of block 0 then of block 1, the
         // order of cat(P_0, P_1)
         const h8 ph = cat(p0.hi, p1.hi), pl = cat(p0.lo, p1.lo);
-        const int piece = 8 * (lg ^ ((ln >> 2) & 3));
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
+            const int piece = 8 * (lg ^ kh_swz(16 * t + ln));
             const float4 e = *reinterpret_cast<const float4*>(&co.echunk[16 * t + 4 * lg]);
             S[t][0] *= e.x; S[t][1] *= e.y; S[t][2] *= e.z; S[t][3] *= e.w;
             const h8 kf = *reinterpret_cast<const h8*>(&co.KH[16 * t + ln][piece]);
