@@ -71,7 +71,21 @@ int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) 
     }
     if (!kda::chunkwise_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
     if (args->B * args->H * args->V / 16 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
-    return kda::chunkwise_launch(*args, static_cast<hipStream_t>(stream), ckpt);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (args->qkv_dtype == KDA_DTYPE_F32) {
+        // fp32 activations: the reference computes in fp32 throughout
+        // (kimi_linear/kda.py:116), and so does the token recurrence, which
+        // gives the same function (the maths is chunk-size invariant) with the
+        // state in fp32 registers; the chunk pipeline's operands are fp16.
+        // With checkpoints the pipeline runs first for them and the recurrence
+        // then writes o and the state.
+        if (ckpt) {
+            const int st = kda::chunkwise_launch(*args, s, ckpt);
+            if (st != KDA_OK) return st;
+        }
+        return kda::recurrent_launch(*args, s);
+    }
+    return kda::chunkwise_launch(*args, s, ckpt);
 }
 
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {

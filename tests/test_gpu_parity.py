@@ -93,8 +93,31 @@ def test_config0_chunkwise(kda_pkg, wl, dtype):
     eo, es = max_abs(o, o_ref), rel(s, s_ref)
     report(f"cfg0 chunkwise {dtype}", eo, es)
     assert o.dtype == dtype
-    # bf16 output rounding alone is ~4e-3 relative on |o| ~ 0.1
-    assert eo <= (O_TOL if dtype != torch.bfloat16 else 1e-2) and es <= S_TOL
+    if dtype == torch.float32:
+        # fp32 activations are computed in fp32 throughout, like the reference's fp32 path
+        assert eo <= 1e-5 and es <= 1e-5
+    else:
+        # bf16 output rounding alone is ~4e-3 relative on |o| ~ 0.1
+        assert eo <= (O_TOL if dtype != torch.bfloat16 else 1e-2) and es <= S_TOL
+
+
+@pytest.mark.parametrize("big", ["state", "v"])
+def test_chunkwise_fp32_wide_range(kda_pkg, wl, big):
+    """fp32 inputs far outside the fp16 range (an initial state of order 1e6, or
+    v of order 1e5) keep fp32 accuracy: relative errors <= 1e-5."""
+    print(f"chunkwise fp32 wide range: large {big}", flush=True)
+    inp = wl.make_inputs(2, 192, 2, 128, 64, seed=21, qkv_dtype=torch.float32, state_std=0.02)
+    if big == "state":
+        inp["state"] = inp["state"] * 5e7                      # |S| ~ 1e6
+    else:
+        inp["v"] = inp["v"] * 1e5
+    o, s = run_chunkwise(kda_pkg, to_dev(inp), 64)
+    o_ref, s_ref = ref_chunkwise(inp, 64)
+    assert torch.isfinite(o).all() and torch.isfinite(s).all()
+    eo = max_abs(o, o_ref) / o_ref.abs().max().item()
+    es = rel(s, s_ref)
+    report(f"fp32 wide range ({big}), o max-abs relative", eo, es)
+    assert eo <= 1e-5 and es <= 1e-5
 
 
 def test_config0_chunkwise_equals_recurrent_gpu(kda_pkg, wl):
