@@ -72,6 +72,8 @@ int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) 
     if (!kda::chunkwise_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
     if (args->B * args->H * args->V / 16 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    const int chk = kda::chunkwise_check(*args);
+    if (chk != KDA_OK) return chk;
     if (args->qkv_dtype == KDA_DTYPE_F32) {
         // fp32 activations: the reference computes in fp32 throughout
         // (kimi_linear/kda.py:116), and so does the token recurrence, which

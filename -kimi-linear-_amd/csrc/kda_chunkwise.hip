@@ -1114,7 +1114,7 @@ bool chunkwise_supported(int64_t K, int64_t V) {
     return (K == 32 || K == 64 || K == 128) && V % 16 == 0;
 }
 
-int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
+int chunkwise_check(const kda_fwd_args& a) {
     // the pipeline reads gates in fp32 (the wrapper converts other dtypes)
     if (a.g_dtype != KDA_DTYPE_F32 || a.beta_dtype != KDA_DTYPE_F32) return KDA_ERR_BAD_DTYPE;
     // in-block offsets are 32-bit byte offsets: 16 token strides + one row must fit
@@ -1128,6 +1128,12 @@ int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
     if (a.T > 1 && (a.q_stride[1] < a.K || a.k_stride[1] < a.K || a.g_stride[1] < a.K ||
                     a.v_stride[1] < a.V || a.beta_stride[1] < 1))
         return KDA_ERR_UNSUPPORTED;
+    return KDA_OK;
+}
+
+int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
+    const int st = chunkwise_check(a);
+    if (st != KDA_OK) return st;
     switch (a.K) {
         case 32: return launch_k<32>(a, stream, ckpt);
         case 64: return launch_k<64>(a, stream, ckpt);

@@ -13,6 +13,8 @@ int recurrent_launch(const kda_fwd_args& a, hipStream_t stream);
 
 // Chunkwise forward (kda_chunkwise.hip).
 bool chunkwise_supported(int64_t K, int64_t V);
+// Host-side argument checks of the chunkwise contract (gate dtypes, strides).
+int chunkwise_check(const kda_fwd_args& a);
 // ckpt (nullable): fp32 [B, H, ceil(T/32), K, V], the state before each chunk
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr);
 
