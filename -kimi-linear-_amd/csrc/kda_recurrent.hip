@@ -95,6 +95,12 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
     // offset is one register and the row offset a scalar
     const uint32_t row_bytes = static_cast<uint32_t>(V) * 4u;
     const uint32_t lane_off = static_cast<uint32_t>(r0) * row_bytes + static_cast<uint32_t>(col0) * 4u;
+    // The state is read once per call, and each element's last read comes
+    // right before its write: non-temporal loads (nt) keep the read lines from
+    // being retained in the caches, which measured 30.7 -> 22.5 us per B=64
+    // H=16 d=128 decode step when the state comes from HBM (in place), at a
+    // small cost when it sits in the Infinity Cache (20.9 -> 22.2 us).
+    constexpr int kLoadNonTemporal = 2;
     float S[RPL][4];
     if (a.state_in == nullptr) {
 #pragma unroll
@@ -108,7 +114,7 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
             const auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(lane_off),
-                                                                  static_cast<int>(j * row_bytes), 0);
+                                                                  static_cast<int>(j * row_bytes), kLoadNonTemporal);
             S[j][0] = __uint_as_float(x[0]); S[j][1] = __uint_as_float(x[1]);
             S[j][2] = __uint_as_float(x[2]); S[j][3] = __uint_as_float(x[3]);
         }

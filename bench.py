@@ -137,6 +137,40 @@ def decode_bench(pkg, wl, torch, n_sets, in_place=False):
     return us
 
 
+def copy_bench(torch, n_sets=5):
+    """A plain device copy of one decode state (64 MiB read + 64 MiB written)
+    per step, n_sets buffer pairs in turn, 512 steps in one hipGraph: the
+    bandwidth reference for the decode step."""
+    n = B2 * H2 * D1 * D1
+    src = [torch.randn(n, device="cuda") for _ in range(n_sets)]
+    dst = [torch.empty_like(x) for x in src]
+
+    def run_all():
+        for t in range(STEPS2):
+            dst[t % n_sets].copy_(src[t % n_sets])
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_all()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_all()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * STEPS2)
+    del graph
+    return us
+
+
 def layer_bench(pkg, torch, reps=10):
     """The whole KDA layer at hidden 2048 (16 heads of 128, fp16 weights N(0, 0.02),
     fp32 state): a B=4 T=2048 prefill forward, and one graph-replayed decode
@@ -302,6 +336,7 @@ def main():
         us_hbm = decode_bench(pkg, wl, torch, 5)
         us_ip = decode_bench(pkg, wl, torch, 1, in_place=True)
         us_ip_hbm = decode_bench(pkg, wl, torch, 5, in_place=True)
+        us_copy = copy_bench(torch, 5)
         frac = lambda us: DECODE_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBS  # noqa: E731
         result["decode"] = {
             "workload": "kda_recurrent decode step, B=64 H=16 dk=dv=128, fp32 state, fp16 "
@@ -312,6 +347,8 @@ def main():
             "hbm_frac": frac(us_hbm),
             "us_per_step_in_place": us_ip_hbm,
             "hbm_frac_in_place": frac(us_ip_hbm),
+            "device_copy_us_rotating_320MiB": us_copy,
+            "vs_device_copy": us_copy / us_hbm,
             "cache_resident": {
                 "note": "one 64 MiB state set: stays in the Infinity Cache, not an HBM figure",
                 "us_per_step": us_mall, "frac_of_hbm_peak": frac(us_mall),
