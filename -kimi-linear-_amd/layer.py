@@ -246,16 +246,28 @@ class KimiDeltaAttention(nn.Module):
                 C = T
             rem = T % C
             body = T - rem
-            o_core = x.new_zeros(B, T, self.num_heads, self.value_head_dim)
+            # every position is written by the body or the tail (the reference
+            # zero-fills first, kda.py:516): without a tail the body's output
+            # is the result as it is
+            o_core = None
             if body > 0:
                 o_body, rec = kda_chunkwise(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
                                             beta[:, :body], initial_state=rec, chunk_size=C,
                                             state_dtype=sdtype, tile_size=self.tile_size)
-                o_core[:, :body] = o_body
+                if rem == 0:
+                    o_core = o_body
+                else:
+                    o_core = x.new_empty(B, T, self.num_heads, self.value_head_dim)
+                    o_core[:, :body] = o_body
             if rem > 0:
                 o_tail, rec = kda_recurrent(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
                                             beta[:, body:], state=rec, state_dtype=sdtype)
-                o_core[:, body:] = o_tail
+                if o_core is None:
+                    o_core = o_tail
+                else:
+                    o_core[:, body:] = o_tail
+            if o_core is None:
+                o_core = x.new_zeros(B, T, self.num_heads, self.value_head_dim)
             new_rec = rec
         out = self._output(o_core, og_low)
         if use_cache:
