@@ -33,8 +33,8 @@
 // the true decay is smaller still.
 //
 // (I + L)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8) for the nilpotent 16x16
-// L = Diag(beta) G_bb: four products and three squarings on MFMA (fp16 hi/lo
-// split operands), entirely in registers.  An MFMA accumulator holds
+// L = Diag(beta) G_bb: products and squarings on the fp32 matrix cores
+// (v_mfma_f32_16x16x4f32, no precision loss), entirely in registers.  An MFMA accumulator holds
 // X[4g+j][n] in lane n+16g, slot j -- the B-operand layout of X and the
 // A-operand layout of X^T -- so a chain that keeps X and X^T side by side
 // needs no data movement.
