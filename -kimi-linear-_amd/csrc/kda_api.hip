@@ -41,38 +41,48 @@ int validate_common(const kda_fwd_args* a, bool in_place_ok) {
     return KDA_OK;
 }
 
-}  // namespace
+// A gated call needs both parameter vectors (when there is work).
+int validate_gate(const kda_fwd_args* a, const kda_gate_args* gate) {
+    if (gate == nullptr) return KDA_ERR_NULL_POINTER;
+    if (a->B > 0 && a->H > 0 && a->T > 0 && (gate->a_log == nullptr || gate->dt_bias == nullptr))
+        return KDA_ERR_NULL_POINTER;
+    return KDA_OK;
+}
 
-extern "C" {
-
-int kda_recurrent_fwd(const kda_fwd_args* args, void* stream) {
+int recurrent_entry(const kda_fwd_args* args, const kda_gate_args* gate, void* stream) {
     // In place is safe: each workgroup loads its (b, h, column tile) slice of
     // the state before any store to it, and no other workgroup touches it.
     const int st = validate_common(args, true);
     if (st != KDA_OK) return st;
+    if (gate) {
+        const int gs = validate_gate(args, gate);
+        if (gs != KDA_OK) return gs;
+    }
     if (args->B == 0 || args->H == 0) return KDA_OK;
     if (!kda::recurrent_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
     if (args->B * args->H * args->V / 32 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
-    return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream));
+    return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream), gate);
 }
 
-int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) { return kda_chunkwise_fwd_ckpt(args, nullptr, stream); }
-
-int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) {
+int chunkwise_entry(const kda_fwd_args* args, float* ckpt, const kda_gate_args* gate, void* stream) {
     const int st = validate_common(args, false);
     if (st != KDA_OK) return st;
+    if (gate) {
+        const int gs = validate_gate(args, gate);
+        if (gs != KDA_OK) return gs;
+    }
     if (args->chunk_size <= 0 || args->T % args->chunk_size != 0) return KDA_ERR_BAD_SHAPE;
     if (args->B == 0 || args->H == 0) return KDA_OK;
     if (args->T == 0) {
         // No tokens: the result is the initial state converted to the output
         // dtype (or zeros); the recurrence kernel with an empty token loop does it.
         if (!kda::recurrent_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
-        return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream));
+        return kda::recurrent_launch(*args, static_cast<hipStream_t>(stream), gate);
     }
     if (!kda::chunkwise_supported(args->K, args->V)) return KDA_ERR_UNSUPPORTED;
     if (args->B * args->H * args->V / 16 > INT32_MAX) return KDA_ERR_BAD_SHAPE;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const int chk = kda::chunkwise_check(*args);
+    const int chk = kda::chunkwise_check(*args, gate != nullptr);
     if (chk != KDA_OK) return chk;
     if (args->qkv_dtype == KDA_DTYPE_F32) {
         // fp32 activations: the reference computes in fp32 throughout
@@ -85,9 +95,31 @@ int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) 
             const int st = kda::chunkwise_launch(*args, s, ckpt);
             if (st != KDA_OK) return st;
         }
-        return kda::recurrent_launch(*args, s);
+        return kda::recurrent_launch(*args, s, gate);
     }
-    return kda::chunkwise_launch(*args, s, ckpt);
+    return kda::chunkwise_launch(*args, s, ckpt, gate);
+}
+
+}  // namespace
+
+extern "C" {
+
+int kda_recurrent_fwd(const kda_fwd_args* args, void* stream) { return recurrent_entry(args, nullptr, stream); }
+
+int kda_recurrent_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate, void* stream) {
+    if (gate == nullptr) return KDA_ERR_NULL_POINTER;
+    return recurrent_entry(args, gate, stream);
+}
+
+int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream) { return chunkwise_entry(args, nullptr, nullptr, stream); }
+
+int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream) {
+    return chunkwise_entry(args, ckpt, nullptr, stream);
+}
+
+int kda_chunkwise_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate, void* stream) {
+    if (gate == nullptr) return KDA_ERR_NULL_POINTER;
+    return chunkwise_entry(args, nullptr, gate, stream);
 }
 
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {

@@ -72,6 +72,8 @@
 // outputs take as operands, are split into fp16 hi + lo; S (in Z and O) and
 // R = V - Z enter their products as single fp16 operands (rounded once per
 // chunk), like q * E, k * E and A.
+#include <type_traits>
+
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -162,6 +164,20 @@ __device__ __forceinline__ _Float16 raw_h(const uint32_t (&w)[W], int j) {
             return __builtin_bit_cast(_Float16, bits);
         } else {
             return static_cast<_Float16>(__uint_as_float(static_cast<uint32_t>(bits) << 16));
+        }
+    }
+}
+// Element j of a raw row of TQ values, as fp32.
+template <typename TQ, int W>
+__device__ __forceinline__ float raw_ef(const uint32_t (&w)[W], int j) {
+    if constexpr (sizeof(TQ) == 4) {
+        return __uint_as_float(w[j]);
+    } else {
+        const uint32_t bits = (w[j / 2] >> (16 * (j % 2))) & 0xffffu;
+        if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+            return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+        } else {
+            return __uint_as_float(bits << 16);
         }
     }
 }
@@ -375,7 +391,7 @@ __device__ __forceinline__ f4 mm_f32(const f4& xt, const f4& y, f4 c) {
     return c;
 }
 
-template <int K, int NC, typename TQ>
+template <int K, int NC, typename TQ, bool GATED>
 struct Kern {
     static constexpr int KT = K / 16;                   // 16-row state tiles
     static constexpr int KU = K / 32;                   // 32-wide k blocks
@@ -384,15 +400,22 @@ struct Kern {
     static constexpr int VT = 16 * NC;
     static constexpr int QB = CH * static_cast<int>(sizeof(TQ));   // bytes of a lane's q / k row
     static constexpr int QW = BLoad<QB>::W;
-    static constexpr int GW = BLoad<4 * CH>::W;
+    // g and beta as loaded: fp32 log decays and rates, or (GATED) the gate's
+    // up-projection gk and the beta logits in the dtype of q, k and v
+    using TG = typename std::conditional<GATED, TQ, float>::type;
+    static constexpr int GB = CH * static_cast<int>(sizeof(TG));   // bytes of a lane's g row
+    static constexpr int GW = BLoad<GB>::W;
+    static constexpr bool kEarlyDecay = GATED;      // see load_g
 
     // One block's raw inputs for a producer lane: its CH channels of rows
     // 8hf .. 8hf + 7, and beta of rows 4lg .. 4lg + 3 (for the solve).
     struct Raw {
         uint32_t q[HR][QW], k[HR][QW], g[HR][GW];
         uint32_t beta[4];
+        int rows;                            // GATED: rows of the block before T
     };
-    // The same block, converted: decays a = exp(g), fp16 q and k rows
+    // The same block, converted: decays a = exp(g) (GATED: formed from gk,
+    // dt_bias and exp(A_log) as in gate_decay), fp16 q and k rows
     // (channels in the low CH slots), beta of rows 4lg .. 4lg + 3 and of row
     // ln (the solve's row and column scales).
     struct Work {
@@ -413,6 +436,7 @@ struct Kern {
     float scale;
     int lane, ln, lg;
     int hf, cq;                              // producer: row half, channel group (channels CH*cq ..)
+    float gcoef[GATED ? CH : 1], gbias[GATED ? CH : 1];   // GATED: exp(A_log), dt_bias log2(e) of the channels
     uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;   // token-row strides in bytes
     uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets
 
@@ -436,34 +460,63 @@ struct Kern {
     // Rows G0 .. G1 - 1 of the lane's half of block blk (and beta): issued in
     // small groups between the level products, so that no wave stalls on a
     // burst of vector memory instructions.
-    template <int G0, int G1, bool BETA>
+    // EARLY: the gate rows are not loaded here but by load_g (a gated call).
+    template <int G0, int G1, bool BETA, bool EARLY = kEarlyDecay>
     __device__ void load_rows(Raw& r, int blk) const {
+        if constexpr (GATED && !EARLY && G0 == 0) r.rows = rows_in(blk);
         const auto rq = block_rsrc(a.q, a.q_stride, sizeof(TQ), rs_q, blk);
         const auto rk = block_rsrc(a.k, a.k_stride, sizeof(TQ), rs_k, blk);
-        const auto rg = block_rsrc(a.g, a.g_stride, 4, rs_g, blk);
+        const auto rg = block_rsrc(a.g, a.g_stride, sizeof(TG), rs_g, blk);
 #pragma unroll
         for (int i = G0; i < G1; ++i) {
-            BLoad<4 * CH>::ld(r.g[i], rg, vo_g, i * rs_g);
+            if constexpr (!EARLY) BLoad<GB>::ld(r.g[i], rg, vo_g, i * rs_g);
             BLoad<QB>::ld(r.q[i], rq, vo_q, i * rs_q);
             BLoad<QB>::ld(r.k[i], rk, vo_k, i * rs_k);
         }
         if constexpr (BETA) {
-            const auto rb = block_rsrc(a.beta, a.beta_stride, 4, rs_b, blk);
+            const auto rb = block_rsrc(a.beta, a.beta_stride, sizeof(TG), rs_b, blk);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) BLoad<4>::ld(&r.beta[j], rb, vo_b, j * rs_b);
+            for (int j = 0; j < 4; ++j) BLoad<sizeof(TG)>::ld(&r.beta[j], rb, vo_b, j * rs_b);
         }
     }
-    __device__ void load_raw(Raw& r, int blk) const { load_rows<0, HR, true>(r, blk); }
-
-    __device__ void unpack(Raw& r, Work& w) const {
-        use_here(r.q);
-        use_here(r.k);
+    __device__ void load_raw(Raw& r, int blk) const { load_rows<0, HR, true, false>(r, blk); }
+    // A gated call loads the next block's gate rows at the start of the first
+    // half and forms their decays (decays()) once the current block's decays
+    // are dead, in the middle of the first half, where the gate's
+    // transcendentals fill the level products' latency instead of preceding
+    // them.
+    __device__ void load_g(Raw& r, int blk) const {
+        r.rows = rows_in(blk);
+        const auto rg = block_rsrc(a.g, a.g_stride, sizeof(TG), rs_g, blk);
+#pragma unroll
+        for (int i = 0; i < HR; ++i) BLoad<GB>::ld(r.g[i], rg, vo_g, i * rs_g);
+    }
+    __device__ void decays(Raw& r, Work& w) const {
         use_here(r.g);
-        use_here(r.beta);
 #pragma unroll
         for (int i = 0; i < HR; ++i) {
 #pragma unroll
-            for (int c = 0; c < CH; ++c) w.al[c][i] = fast_exp(__uint_as_float(r.g[i][c]));
+            for (int c = 0; c < CH; ++c) {
+                if constexpr (GATED) {
+                    // rows past T must stay neutral (a = 1): they read gk = 0,
+                    // which the gate would turn into a decay
+                    const float a = gate_decay(fmaf(raw_ef<TG>(r.g[i], c), kLog2e, gbias[c]), gcoef[c]);
+                    w.al[c][i] = HR * hf + i < r.rows ? a : 1.f;
+                } else {
+                    w.al[c][i] = fast_exp(__uint_as_float(r.g[i][c]));
+                }
+            }
+        }
+    }
+
+    // q, k and beta (and the decays unless kEarlyDecay formed them already).
+    __device__ void unpack(Raw& r, Work& w) const {
+        use_here(r.q);
+        use_here(r.k);
+        use_here(r.beta);
+        if constexpr (!kEarlyDecay) decays(r, w);
+#pragma unroll
+        for (int i = 0; i < HR; ++i) {
             h4 qv = {0, 0, 0, 0}, kv = {0, 0, 0, 0};
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
@@ -474,7 +527,13 @@ struct Kern {
             w.k[i] = kv;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w.beta[j] = __uint_as_float(r.beta[j]);
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (GATED) {
+                w.beta[j] = 4 * lg + j < r.rows ? sigmoid_f(raw_f<TG>(r.beta[j])) : 0.f;
+            } else {
+                w.beta[j] = __uint_as_float(r.beta[j]);
+            }
+        }
         // beta of row ln: slot ln % 4 of lane group ln / 4
         const int src = 16 * (ln >> 2) + (lane & 15);
         float bc = w.beta[0];
@@ -674,6 +733,7 @@ struct Kern {
         // get their final values after the last level
         _Float16* xs = &co.QE[bi][0][0];
         _Float16* ys = &co.KE[bi][0][0];
+        if constexpr (kEarlyDecay) load_g(raw, next);
         // in-lane running products over the half's rows: pre (inclusive, from
         // the half's start) and suf (exclusive, to the half's end)
         float pre[CH][HR], suf[CH][HR];
@@ -698,6 +758,8 @@ struct Kern {
         stage<3>(w, pre, suf, xs, ys);
         product<2>(fr, sum);
         load_rows<2, 4, false>(raw, next);
+        // the current block's decays are dead: the next block's take their registers
+        if constexpr (kEarlyDecay) decays(raw, w);
         fr = read_frags(xs, ys);
         stage<4>(w, pre, suf, xs, ys);
         product<3>(fr, sum);
@@ -981,9 +1043,10 @@ struct Kern {
 // barriers; every prefetch is issued unconditionally (a block past T loads
 // zeros).  The chunks cover T rounded up to whole chunks: a padded block
 // (all rows past T) is neutral and is built like any other.
-template <int K, int NC, typename TQ>
-__global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt) {
-    using KN = Kern<K, NC, TQ>;
+template <int K, int NC, typename TQ, bool GATED>
+__global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt,
+                                                                   const kda_gate_args gate) {
+    using KN = Kern<K, NC, TQ, GATED>;
     constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
     __shared__ Smem<K> sm;
@@ -1026,12 +1089,13 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         kn.rs_q = static_cast<uint32_t>(a.q_stride[1]) * eq;
         kn.rs_k = static_cast<uint32_t>(a.k_stride[1]) * eq;
         kn.rs_v = static_cast<uint32_t>(a.v_stride[1]) * eq;
-        kn.rs_g = static_cast<uint32_t>(a.g_stride[1]) * 4u;
-        kn.rs_b = static_cast<uint32_t>(a.beta_stride[1]) * 4u;
+        const uint32_t eg = static_cast<uint32_t>(sizeof(typename KN::TG));
+        kn.rs_g = static_cast<uint32_t>(a.g_stride[1]) * eg;
+        kn.rs_b = static_cast<uint32_t>(a.beta_stride[1]) * eg;
         const uint32_t c0 = static_cast<uint32_t>(CH * kn.cq), r0 = static_cast<uint32_t>(HR * kn.hf);
         kn.vo_q = r0 * kn.rs_q + c0 * eq;
         kn.vo_k = r0 * kn.rs_k + c0 * eq;
-        kn.vo_g = r0 * kn.rs_g + c0 * 4u;
+        kn.vo_g = r0 * kn.rs_g + c0 * eg;
         kn.vo_b = static_cast<uint32_t>(4 * kn.lg) * kn.rs_b;
         // v tile loads: 16-bit inputs row lane / 2, columns 8 (lane % 2); fp32
         // row lane / 4, columns 4 (lane % 4), of this wave's 16 columns
@@ -1064,10 +1128,19 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
     } else {
         const int p = wave - NC;
+        if constexpr (GATED) {
+            const int64_t ch = kn.h * K + CH * kn.cq;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                kn.gcoef[c] = expf(gate.a_log[ch + c]);
+                kn.gbias[c] = gate.dt_bias[ch + c] * kLog2e;
+            }
+        }
         typename KN::Raw raw;
         typename KN::Work w;
         typename KN::Sums sum;
         kn.load_raw(raw, p);
+        if constexpr (KN::kEarlyDecay) kn.decays(raw, w);
         for (int s = -1; s < nss; ++s) {
             const int blk = NB * (s + 1) + p;
             ChunkOps<K>& co = sm.set[(s + 1) & 1][p / CB];
@@ -1079,32 +1152,46 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     }
 }
 
-template <int K, int NC, typename TQ>
-int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
+template <int K, int NC, typename TQ, bool GATED>
+int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
     const int64_t blocks = a.B * a.H * (a.V / (16 * NC));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ>), dim3(static_cast<unsigned>(blocks)), dim3(64 * (NC + NB)), 0,
-                       stream, a, ckpt);
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(64 * (NC + NB)), 0, stream, a, ckpt, gate);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
 // Columns per workgroup: the widest tile (64, 32 or 16 columns) that still
 // gives at least one workgroup per CU; 16 when none does (few chains).
-template <int K, typename TQ>
-int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
+template <int K, typename TQ, bool GATED>
+int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
     constexpr int64_t kCus = 256;
     const int64_t heads = a.B * a.H;
-    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ>(a, stream, ckpt);
-    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ>(a, stream, ckpt);
-    return launch_knq<K, 1, TQ>(a, stream, ckpt);
+    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ, GATED>(a, stream, ckpt, gate);
+    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ, GATED>(a, stream, ckpt, gate);
+    return launch_knq<K, 1, TQ, GATED>(a, stream, ckpt, gate);
 }
 
-template <int K>
-int launch_k(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
+template <int K, bool GATED>
+int launch_k(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
     switch (a.qkv_dtype) {
-        case KDA_DTYPE_F16: return launch_kq<K, _Float16>(a, stream, ckpt);
-        case KDA_DTYPE_BF16: return launch_kq<K, bf16_t>(a, stream, ckpt);
-        case KDA_DTYPE_F32: return launch_kq<K, float>(a, stream, ckpt);
+        case KDA_DTYPE_F16: return launch_kq<K, _Float16, GATED>(a, stream, ckpt, gate);
+        case KDA_DTYPE_BF16: return launch_kq<K, bf16_t, GATED>(a, stream, ckpt, gate);
+        case KDA_DTYPE_F32:
+            // fp32 activations take the token recurrence (gated or not); the
+            // pipeline's fp32 instantiation serves the backward's checkpoints
+            if constexpr (GATED) return KDA_ERR_BAD_DTYPE;
+            else return launch_kq<K, float, false>(a, stream, ckpt, gate);
         default: return KDA_ERR_BAD_DTYPE;
+    }
+}
+
+template <bool GATED>
+int launch_gated(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
+    switch (a.K) {
+        case 32: return launch_k<32, GATED>(a, stream, ckpt, gate);
+        case 64: return launch_k<64, GATED>(a, stream, ckpt, gate);
+        case 128: return launch_k<128, GATED>(a, stream, ckpt, gate);
+        default: return KDA_ERR_UNSUPPORTED;
     }
 }
 
@@ -1114,9 +1201,12 @@ bool chunkwise_supported(int64_t K, int64_t V) {
     return (K == 32 || K == 64 || K == 128) && V % 16 == 0;
 }
 
-int chunkwise_check(const kda_fwd_args& a) {
-    // the pipeline reads gates in fp32 (the wrapper converts other dtypes)
-    if (a.g_dtype != KDA_DTYPE_F32 || a.beta_dtype != KDA_DTYPE_F32) return KDA_ERR_BAD_DTYPE;
+int chunkwise_check(const kda_fwd_args& a, bool gated) {
+    // the pipeline reads gates in fp32 (the wrapper converts other dtypes);
+    // a gated call's gk and logits come in the dtype of q, k and v
+    if (!gated && (a.g_dtype != KDA_DTYPE_F32 || a.beta_dtype != KDA_DTYPE_F32)) return KDA_ERR_BAD_DTYPE;
+    if (gated && a.qkv_dtype != KDA_DTYPE_F32 && (a.g_dtype != a.qkv_dtype || a.beta_dtype != a.qkv_dtype))
+        return KDA_ERR_BAD_DTYPE;
     // in-block offsets are 32-bit byte offsets: 16 token strides + one row must fit
     const int64_t lim = int64_t(1) << 31;
     const int64_t ts[5] = {a.q_stride[1], a.k_stride[1], a.v_stride[1], a.g_stride[1], a.beta_stride[1]};
@@ -1131,15 +1221,14 @@ int chunkwise_check(const kda_fwd_args& a) {
     return KDA_OK;
 }
 
-int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt) {
-    const int st = chunkwise_check(a);
+int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args* gate) {
+    const int st = chunkwise_check(a, gate != nullptr);
     if (st != KDA_OK) return st;
-    switch (a.K) {
-        case 32: return launch_k<32>(a, stream, ckpt);
-        case 64: return launch_k<64>(a, stream, ckpt);
-        case 128: return launch_k<128>(a, stream, ckpt);
-        default: return KDA_ERR_UNSUPPORTED;
+    if (gate != nullptr) {
+        if (ckpt != nullptr) return KDA_ERR_UNSUPPORTED;   // the backward takes g and beta
+        return launch_gated<true>(a, stream, nullptr, *gate);
     }
+    return launch_gated<false>(a, stream, ckpt, kda_gate_args{nullptr, nullptr});
 }
 
 }  // namespace kda

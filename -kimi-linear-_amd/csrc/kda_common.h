@@ -98,6 +98,29 @@ __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+// The layer's forget gate as a decay factor (kimi_linear/kda.py:460):
+// a = exp(g), g = -coef softplus(z), coef = exp(A_log), z = gk + dt_bias,
+// taken in base 2 from zl = z log2(e) (callers form it as one fma of gk with
+// the per-channel log2(e) and dt_bias log2(e)).  With t = 2^-|zl| in (0, 1]:
+//   a = 2^(-coef s),   s = softplus(z) log2(e) = max(zl, 0) + log2(1 + t).
+// u = 1 + t is rounded; its rounding error t - (u - 1) (exact, as u - 1 is)
+// goes back in as the first-order term of log2(1 + t), so s keeps its e^z
+// behaviour for z << 0 to about an ulp without a division.  For z > 20,
+// t < 2^-28 vanishes against 1 and s = zl: torch's softplus threshold.
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float gate_decay(float zl, float coef) {
+    const float t = __builtin_amdgcn_exp2f(-fabsf(zl));
+    const float u = 1.f + t;
+    const float e = t - (u - 1.f);
+    const float s = fmaxf(zl, 0.f) + fmaf(e, kLog2e, __builtin_amdgcn_logf(u));
+    return __builtin_amdgcn_exp2f(-coef * s);
+}
+
+// beta from its logit (kimi_linear/kda.py:452); the reciprocal to about an ulp.
+__device__ __forceinline__ float sigmoid_f(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
 // fp16 hi/lo split: x ~= hi + lo with |x - hi - lo| ~ 2^-22 |x|.
 __device__ __forceinline__ void split_h(float x, _Float16& hi, _Float16& lo) {
     hi = static_cast<_Float16>(x);

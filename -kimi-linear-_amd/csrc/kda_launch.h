@@ -9,14 +9,19 @@ namespace kda {
 
 // Token-by-token recurrence (kda_recurrent.hip).
 bool recurrent_supported(int64_t K, int64_t V);
-int recurrent_launch(const kda_fwd_args& a, hipStream_t stream);
+// gate (nullable): the fused gate of kda_recurrent_gated_fwd
+int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate = nullptr);
 
 // Chunkwise forward (kda_chunkwise.hip).
 bool chunkwise_supported(int64_t K, int64_t V);
-// Host-side argument checks of the chunkwise contract (gate dtypes, strides).
-int chunkwise_check(const kda_fwd_args& a);
-// ckpt (nullable): fp32 [B, H, ceil(T/32), K, V], the state before each chunk
-int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr);
+// Host-side argument checks of the chunkwise contract (gate dtypes, strides);
+// `gated`: g and beta hold gk and the beta logits.
+int chunkwise_check(const kda_fwd_args& a, bool gated = false);
+// ckpt (nullable): fp32 [B, H, ceil(T/32), K + 64, V], the checkpoints of the
+// backward; gate (nullable): the fused gate of kda_chunkwise_gated_fwd (not
+// with ckpt)
+int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr,
+                     const kda_gate_args* gate = nullptr);
 
 // Chunkwise backward (kda_chunkwise_bwd.hip).
 bool chunkwise_bwd_supported(int64_t K, int64_t V);

@@ -8,7 +8,9 @@
 // reference runs these as ~20 separate elementwise kernels with fp16
 // round trips between them; here every projection element is read once (plus
 // the conv_size - 1 rows of context a token tile needs) and every core input
-// is written once, all arithmetic in fp32 and each output rounded once.
+// is written once, all arithmetic in fp32 and each output rounded once.  A
+// call without g and beta outputs skips the gates: the layer hands gk and the
+// beta logits to the gated core entry points, whose loaders form them.
 //
 // kda_output_fwd replaces HeadwiseRMSNorm and the sigmoid output gate of
 // _output (kda.py:258-279, 464-470): one read of the core output and of the
@@ -224,11 +226,13 @@ __device__ __forceinline__ void gate_unit(const kda_prep_args& a, int64_t b, int
         static_cast<float*>(a.beta)[(b * T + t0 + lane) * a.H + h] = sigmoid(decode_elem(rlogit, a.x_dtype));
 }
 
-// One wave per (batch, tile, part, head), part 0..2 = q, k, v, 3 = gate.
-// The host keeps the number of units below 2^31, so the unit index is split
-// with 32-bit arithmetic.
+// One wave per (batch, tile, part, head), part 0..2 = q, k, v, 3 = gate
+// (nparts = 4, or 3 when the call leaves the gates to the core).  The host
+// keeps the number of units below 2^31, so the unit index is split with
+// 32-bit arithmetic.
 template <typename XT, int CPLK, int CPLV, int TILE>
-__global__ __launch_bounds__(256) void prep_kernel(const kda_prep_args a, uint32_t ntiles, uint32_t units) {
+__global__ __launch_bounds__(256) void prep_kernel(const kda_prep_args a, uint32_t ntiles, uint32_t units,
+                                                   uint32_t nparts) {
     const int lane = threadIdx.x & 63;
     const uint32_t unit = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (unit >= units) return;
@@ -236,8 +240,8 @@ __global__ __launch_bounds__(256) void prep_kernel(const kda_prep_args a, uint32
     uint32_t u = unit;
     const int64_t h = u % H;
     u /= H;
-    const int part = static_cast<int>(u & 3u);
-    u >>= 2;
+    const int part = static_cast<int>(u % nparts);
+    u /= nparts;
     const int64_t t0 = static_cast<int64_t>(u % ntiles) * TILE;
     const int64_t b = u / ntiles;
     if (part < 2)
@@ -316,16 +320,17 @@ bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
 template <typename XT, int CPLK, int CPLV>
 void launch_prep(const kda_prep_args& a, hipStream_t stream) {
     // a single token (the decode step) gets units of one token
+    const uint32_t nparts = a.g != nullptr ? 4u : 3u;
     if (a.T == 1) {
-        const int64_t units = a.B * 4 * a.H;
+        const int64_t units = a.B * nparts * a.H;
         hipLaunchKernelGGL((prep_kernel<XT, CPLK, CPLV, 1>), dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256),
-                           0, stream, a, 1u, static_cast<uint32_t>(units));
+                           0, stream, a, 1u, static_cast<uint32_t>(units), nparts);
         return;
     }
     const int64_t ntiles = (a.T + kTile - 1) / kTile;
-    const int64_t units = a.B * ntiles * 4 * a.H;
+    const int64_t units = a.B * ntiles * nparts * a.H;
     hipLaunchKernelGGL((prep_kernel<XT, CPLK, CPLV, kTile>), dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256),
-                       0, stream, a, static_cast<uint32_t>(ntiles), static_cast<uint32_t>(units));
+                       0, stream, a, static_cast<uint32_t>(ntiles), static_cast<uint32_t>(units), nparts);
 }
 
 template <typename XT>
@@ -392,12 +397,16 @@ int validate_prep(const kda_prep_args* a) {
                 return KDA_ERR_ALIAS;
         }
     }
-    if (!a->gk || !a->a_log || !a->dt_bias || !a->beta_logit || !a->q || !a->k || !a->v || !a->g || !a->beta)
+    if (!a->q || !a->k || !a->v) return KDA_ERR_NULL_POINTER;
+    // g and beta both absent: the gates are left to the core's gated entry points
+    const bool gates = a->g != nullptr || a->beta != nullptr;
+    if (gates && (!a->gk || !a->a_log || !a->dt_bias || !a->beta_logit || !a->g || !a->beta))
         return KDA_ERR_NULL_POINTER;
     const int64_t ck = a->K / 64, cv = a->V / 64;
-    if (!vec_ok(a->gk, a->gk_stride, 2, ck, a->x_dtype) || !vec_ok(a->q, nullptr, 0, ck, a->x_dtype) ||
-        !vec_ok(a->k, nullptr, 0, ck, a->x_dtype) || !vec_ok(a->v, nullptr, 0, cv, a->x_dtype) ||
-        !vec_ok(a->g, nullptr, 0, ck, KDA_DTYPE_F32))
+    if (!vec_ok(a->q, nullptr, 0, ck, a->x_dtype) || !vec_ok(a->k, nullptr, 0, ck, a->x_dtype) ||
+        !vec_ok(a->v, nullptr, 0, cv, a->x_dtype))
+        return KDA_ERR_BAD_SHAPE;
+    if (gates && (!vec_ok(a->gk, a->gk_stride, 2, ck, a->x_dtype) || !vec_ok(a->g, nullptr, 0, ck, KDA_DTYPE_F32)))
         return KDA_ERR_BAD_SHAPE;
     const int64_t ntiles = (a->T + kTile - 1) / kTile;
     if (a->B * ntiles * 4 * a->H > INT32_MAX) return KDA_ERR_BAD_SHAPE;

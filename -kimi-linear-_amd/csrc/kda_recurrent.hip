@@ -9,14 +9,19 @@
 //   S' = Diag(a) S,   u = S'^T k,   r = S'^T q~,   d = beta (v - u)
 //   S  = S' + k d^T,  o = r + (q~ . k) d            (== S^T q~ after the update)
 //
-// Work split: one workgroup of NW waves per (b, h, V-tile of 16 NW columns);
-// wave w owns columns [16w, 16w + 16) of the tile for all K rows, so both
-// K-reductions (u, r) and q~.k stay inside the wave.  Lane l holds the four
-// columns 4 (l & 3) .. +3 of the K/16 consecutive rows starting at
-// (K/16) (l >> 2): a row segment is one 16-byte access.  The reduction over
-// the 16 row groups is two DPP row rotations (lanes 4 and 8 apart) and the
-// two cross-row swaps (16 and 32 apart), all on the VALU.  q~, k and a of a
-// token are staged once per workgroup in LDS.
+// Work split: one workgroup of NW waves per (b, h, V-tile of 4 CPL NW
+// columns); wave w owns 4 CPL columns of the tile for all K rows, lane l the
+// four columns 4 (l % CPL) .. +3 of the K CPL / 64 consecutive rows of row
+// group l / CPL: a row segment is one 16-byte access.  Both K-reductions
+// (u, r) and q~.k are sums over the lanes of one column group, inside the
+// wave (DPP row rotations and the permlane swaps of lane bits 4 and 5, all
+// on the VALU): no LDS round and no barrier.  q~, k and a of a token are
+// staged once per workgroup in LDS.
+//
+// Gated calls (kda_recurrent_gated_fwd) take the gate's up-projection gk and
+// the beta logits instead of g and beta and form, while staging the token,
+// a = exp(-exp(A_log) softplus(gk + dt_bias)) and beta = sigmoid(logit) in
+// fp32 (kimi_linear/kda.py:452-460).
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -65,7 +70,7 @@ __device__ __forceinline__ float lanegroup4_sum(float x) {
 // RPL = K CPL / 64 adjacent rows (row group l / CPL); the K-reductions are
 // sums over the lanes of one column group.
 template <int K, int NW, int CPL, bool VEC>
-__global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a) {
+__global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a, const kda_gate_args gate) {
     static_assert(CPL == 4 || CPL == 8 || CPL == 16, "column groups per wave");
     constexpr int RPL = K * CPL / 64;           // rows per lane
     constexpr int VT = 4 * CPL * NW;            // columns per workgroup
@@ -127,6 +132,18 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
                                     a.state_in_dtype);
     }
 
+    // channels this thread stages per token, and for a gated call their
+    // exp(A_log) and dt_bias, fetched once (beside the state loads)
+    constexpr int KPT = (K + 64 * NW - 1) / (64 * NW);
+    float gcoef[KPT], gbias[KPT];
+    if (gate.a_log) {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const int i = tid + 64 * NW * j;
+            gcoef[j] = i < K ? expf(gate.a_log[h * K + i]) : 0.f;
+            gbias[j] = i < K ? gate.dt_bias[h * K + i] * kLog2e : 0.f;
+        }
+    }
     const float scale = a.scale;
     for (int64_t t = 0; t < T; ++t) {
         // ---- stage token t: q~, k, exp(g) for all K rows; v, beta per lane.
@@ -140,18 +157,22 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
         for (int c = 0; c < 4; ++c) rv[c] = load_raw_elem(a.v, tv + c, a.qkv_dtype);
         const RawElem rb =
             load_raw_elem(a.beta, b * a.beta_stride[0] + t * a.beta_stride[1] + h * a.beta_stride[2], a.beta_dtype);
-        for (int i = tid; i < K; i += 64 * NW) {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const int i = tid + 64 * NW * j;
+            if (i >= K) break;
             const RawElem rq = load_raw_elem(a.q, tq + i, a.qkv_dtype);
             const RawElem rk = load_raw_elem(a.k, tk + i, a.qkv_dtype);
             const RawElem rg = load_raw_elem(a.g, tg + i, a.g_dtype);
             s_q[i] = decode_elem(rq, a.qkv_dtype) * scale;
             s_k[i] = decode_elem(rk, a.qkv_dtype);
-            s_a[i] = fast_exp(decode_elem(rg, a.g_dtype));
+            const float gv = decode_elem(rg, a.g_dtype);
+            s_a[i] = gate.a_log ? gate_decay(fmaf(gv, kLog2e, gbias[j]), gcoef[j]) : fast_exp(gv);
         }
         float v[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = decode_elem(rv[c], a.qkv_dtype);
-        const float beta = decode_elem(rb, a.beta_dtype);
+        const float beta = gate.a_log ? sigmoid_f(decode_elem(rb, a.beta_dtype)) : decode_elem(rb, a.beta_dtype);
         __syncthreads();
 
         // ---- decay, then the lane's partial K-reductions over its rows
@@ -219,31 +240,32 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <int K, int NW, int CPL>
-int launch_k_nw(const kda_fwd_args& a, hipStream_t stream) {
+int launch_k_nw(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate) {
     const dim3 grid(static_cast<unsigned>(a.B * a.H * (a.V / (4 * CPL * NW)))), block(64 * NW);
     const bool vec = (a.V & 3) == 0 && a.state_out_dtype == KDA_DTYPE_F32 && aligned16(a.state_out) &&
                      (a.state_in == nullptr || (a.state_in_dtype == KDA_DTYPE_F32 && aligned16(a.state_in)));
     if (vec)
-        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, true>), grid, block, 0, stream, a, gate);
     else
-        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, false>), grid, block, 0, stream, a, gate);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
 template <int K>
-int launch_k(const kda_fwd_args& a, hipStream_t stream) {
-    // K <= 128: 32 columns per one-wave workgroup, K / 8 x 4 state elements
-    // per lane (at K 128, 128 VGPRs: a B=64 H=16 V=128 step's 4096 waves all
-    // resident at once); K 256: 16 columns a wave, K / 16 x 4 per lane.
+int launch_k(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate) {
+    // K 128 with V % 64 == 0: one wave of 64 columns (32 rows x 4 columns a
+    // lane, 196 VGPRs: the 2048 waves of a B=64 H=16 V=128 step are all
+    // resident at once); other K <= 128: one wave of 32 columns (K / 8 rows x
+    // 4 columns a lane); K 256: 16 columns a wave (K / 16 rows a lane).
     if constexpr (K == 128) {
-        if (a.V % 64 == 0) return launch_k_nw<K, 1, 16>(a, stream);
+        if (a.V % 64 == 0) return launch_k_nw<K, 1, 16>(a, stream, gate);
     }
     if constexpr (K <= 128) {
-        if (a.V % 32 == 0) return launch_k_nw<K, 1, 8>(a, stream);
+        if (a.V % 32 == 0) return launch_k_nw<K, 1, 8>(a, stream, gate);
     }
-    if (a.V % 64 == 0) return launch_k_nw<K, 4, 4>(a, stream);
-    if (a.V % 32 == 0) return launch_k_nw<K, 2, 4>(a, stream);
-    return launch_k_nw<K, 1, 4>(a, stream);
+    if (a.V % 64 == 0) return launch_k_nw<K, 4, 4>(a, stream, gate);
+    if (a.V % 32 == 0) return launch_k_nw<K, 2, 4>(a, stream, gate);
+    return launch_k_nw<K, 1, 4>(a, stream, gate);
 }
 
 }  // namespace
@@ -253,12 +275,13 @@ bool recurrent_supported(int64_t K, int64_t V) {
     return V % 16 == 0;
 }
 
-int recurrent_launch(const kda_fwd_args& a, hipStream_t stream) {
+int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate_p) {
+    const kda_gate_args gate = gate_p ? *gate_p : kda_gate_args{nullptr, nullptr};
     switch (a.K) {
-        case 32: return launch_k<32>(a, stream);
-        case 64: return launch_k<64>(a, stream);
-        case 128: return launch_k<128>(a, stream);
-        case 256: return launch_k<256>(a, stream);
+        case 32: return launch_k<32>(a, stream, gate);
+        case 64: return launch_k<64>(a, stream, gate);
+        case 128: return launch_k<128>(a, stream, gate);
+        case 256: return launch_k<256>(a, stream, gate);
         default: return KDA_ERR_UNSUPPORTED;
     }
 }

@@ -50,10 +50,11 @@ class KdaGraphedDecoder:
     serves any number of prompts of the same batch size.
 
     The captured GEMMs read each layer's concatenated input-projection weight
-    (``KimiDeltaAttention._input_weight``) and the parameters themselves.
-    ``prefill`` refills that concatenation from the parameters (in place, so
-    the graph keeps reading valid memory) and recaptures if a buffer had to be
-    reallocated (new dtype or shape).  After updating weights between two
+    (``KimiDeltaAttention._input_weight``) and the parameters themselves, the
+    gated recurrence the layer's fp32 copies of ``A_log`` and ``dt_bias``
+    (``_gate_params``).  ``prefill`` refills these caches from the parameters
+    (in place, so the graph keeps reading valid memory) and recaptures if a
+    buffer had to be reallocated (new dtype or shape).  After updating weights between two
     ``step`` calls of one generation, call :meth:`refresh_weights`.
     """
 
@@ -73,14 +74,15 @@ class KdaGraphedDecoder:
         bufs = []
         for layer in self.layers:
             w, b = layer._input_weight()
-            bufs.append((w.data_ptr(), b.data_ptr() if b is not None else 0))
+            a_log, dt_bias = layer._gate_params()
+            bufs.append((w.data_ptr(), b.data_ptr() if b is not None else 0, a_log.data_ptr(), dt_bias.data_ptr()))
         return bufs
 
     @torch.no_grad()
     def refresh_weights(self) -> None:
         """Bring the captured step up to date with the layers' parameters:
-        refill the fused input-projection weights (in place) and recapture if
-        one of them moved.  Needed only when weights change mid-generation."""
+        refill the fused input-projection weights and the fp32 gate
+        parameters (in place) and recapture if one of them moved.  Needed only when weights change mid-generation."""
         if self.graph is None:
             return
         for layer in self.layers:

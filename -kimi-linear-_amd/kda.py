@@ -88,9 +88,12 @@ def _strides3(x: torch.Tensor):
     return (ctypes.c_int64 * 3)(*x.stride()[:3])
 
 
-def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None, ckpt=False):
+def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None, ckpt=False, gate=None):
     """Shared forward.  ``ckpt=True`` (chunkwise, inside the autograd
-    function) also returns the fp32 state before every 32-token chunk."""
+    function) also returns the fp32 state before every 32-token chunk.
+    ``gate=(a_log, dt_bias)``: g and beta are the gate's up-projection gk
+    and the beta logits, and the kernels form the gates (the gated entry
+    points)."""
     for name, x in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
         _check_tensor(name, x)
     if state is not None:
@@ -119,8 +122,14 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
     if K <= 0 or V <= 0:
         raise KdaError(f"head dims must be positive, got K={K}, V={V}")
 
+    if gate is not None:
+        for name, x in zip(("a_log", "dt_bias"), gate):
+            _check_tensor(name, x)
+            if x.numel() != H * K:
+                raise KdaError(f"{name} must be [H, K] = [{H}, {K}]; got {tuple(x.shape)}")
+
     dev = q.device
-    tensors = [q, k, v, g, beta] + [x for x in (state, state_out) if x is not None]
+    tensors = [q, k, v, g, beta] + [x for x in (state, state_out) if x is not None] + list(gate or ())
     if dev.type != "cuda" or any(x.device != dev for x in tensors):
         raise KdaError("the HIP KDA kernels need all inputs on one HIP device "
                        f"(got {', '.join(str(x.device) for x in tensors)}); there is no CPU path")
@@ -159,7 +168,12 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
     q = _as_kernel_input(q if q.dtype == qk_dtype else q.to(qk_dtype))
     k = _as_kernel_input(k if k.dtype == qk_dtype else k.to(qk_dtype))
     v = _as_kernel_input(v)
-    if kind == "chunkwise":
+    if gate is not None:
+        if kind == "chunkwise" and qk_dtype != torch.float32:
+            # the chunk pipeline reads gk and the logits in the dtype of q, k and v
+            g, beta = g.to(qk_dtype), beta.to(qk_dtype)
+        gate = tuple(x.detach().reshape(H, K).to(torch.float32).contiguous() for x in gate)
+    elif kind == "chunkwise":
         # the chunkwise pipeline reads fp32 gates (the reference upcasts them too, kda.py:119-120)
         g = g.float()
         beta = beta.float()
@@ -199,14 +213,19 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
     lib = _native.load()
     with torch.cuda.device(dev):
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        if ckpt:
+        if gate is not None:
+            gargs = _native.KdaGateArgs()
+            gargs.a_log, gargs.dt_bias = gate[0].data_ptr(), gate[1].data_ptr()
+            fn = lib.kda_chunkwise_gated_fwd if kind == "chunkwise" else lib.kda_recurrent_gated_fwd
+            status = fn(ctypes.byref(args), ctypes.byref(gargs), stream)
+        elif ckpt:
             status = lib.kda_chunkwise_fwd_ckpt(ctypes.byref(args), ctypes.c_void_p(ck.data_ptr()), stream)
         elif kind == "chunkwise":
             status = lib.kda_chunkwise_fwd(ctypes.byref(args), stream)
         else:
             status = lib.kda_recurrent_fwd(ctypes.byref(args), stream)
     if status != _native.STATUS_OK:
-        raise KdaError(f"kda_{kind}_fwd failed: {_native.status_str(status)} "
+        raise KdaError(f"kda_{kind}{'_gated' if gate is not None else ''}_fwd failed: {_native.status_str(status)} "
                        f"(B={B}, T={T}, H={H}, K={K}, V={V})")
     if kernel_s_dtype != s_dtype:
         s_out = s_out.to(s_dtype)
@@ -317,3 +336,26 @@ def kda_recurrent(q, k, v, g, beta, state=None, state_dtype=None, *, state_out=N
     buffer.  It is returned as the second output.
     """
     return _forward("recurrent", q, k, v, g, beta, state, 0, state_dtype, state_out)
+
+
+def kda_chunkwise_gated(q, k, v, gk, beta_logit, a_log, dt_bias, initial_state=None, chunk_size=64,
+                        state_dtype=None):
+    """``kda_chunkwise`` with the KDA layer's gate pre-processing fused into the
+    kernel's loads (no counterpart function in the reference; it computes
+    ``g = -exp(A_log) * softplus(gk + dt_bias)`` and ``beta = sigmoid(beta_logit)``
+    in fp32 as ``kimi_linear/kda.py:452-460`` does, then ``kda_chunkwise``).
+
+    ``gk: [B, T, H, K]`` (the gate's up-projection), ``beta_logit: [B, T, H]``,
+    ``a_log, dt_bias: [H, K]``.  For fp16 / bf16 q, k, v the gate inputs are read
+    in that dtype (converted if they come in another); g and beta never exist
+    in memory.  Forward only.  Returns ``(o, state)`` as ``kda_chunkwise``.
+    """
+    return _forward("chunkwise", q, k, v, gk, beta_logit, initial_state, int(chunk_size), state_dtype,
+                    gate=(a_log, dt_bias))
+
+
+def kda_recurrent_gated(q, k, v, gk, beta_logit, a_log, dt_bias, state=None, state_dtype=None, *,
+                        state_out=None):
+    """``kda_recurrent`` with the fused gate of :func:`kda_chunkwise_gated`
+    (gate inputs in any float dtype).  ``state_out`` as in ``kda_recurrent``."""
+    return _forward("recurrent", q, k, v, gk, beta_logit, state, 0, state_dtype, state_out, gate=(a_log, dt_bias))

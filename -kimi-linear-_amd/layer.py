@@ -16,7 +16,10 @@ Semantics kept from the reference:
 
 * ``_projections`` (``kda.py:399-461``): q, k = l2norm(SiLU(ShortConv(W x)))
   per head, v = SiLU(ShortConv(W_v x)); beta = sigmoid(W_beta x) in fp32;
-  g = -exp(A_log) * softplus(W_up W_down x + dt_bias) in fp32.  The T == 1
+  g = -exp(A_log) * softplus(W_up W_down x + dt_bias) in fp32.  The gates are
+  formed inside the core's loads (``kda_chunkwise_gated`` /
+  ``kda_recurrent_gated``) from the gate's up-projection and the beta
+  logits, so g and beta are never written to memory.  The T == 1
   cached path updates the conv windows (``kda.py:295-307``); a cached
   multi-token call continues from the cached conv inputs (chunked prefill).
 * dispatch (``kda.py:473-536``): ``use_cache`` with T == 1 goes to the
@@ -36,7 +39,7 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 
-from .kda import kda_chunkwise, kda_recurrent
+from .kda import kda_chunkwise_gated, kda_recurrent_gated
 from .layer_ops import kda_output, kda_prep
 
 
@@ -113,6 +116,7 @@ class KimiDeltaAttention(nn.Module):
         self.o_proj = nn.Linear(H * V, d, bias=bias)
         self.fp32_recurrent_state = True
         self._wcat = None          # (key, weight, bias) of the fused input projection
+        self._gcat = None          # (key, A_log, dt_bias) in fp32 for the gated core
 
     def _input_mods(self):
         return (self.in_proj_q, self.in_proj_k, self.in_proj_v, self.beta_proj, self.gk_proj[0], self.og_proj[0])
@@ -155,12 +159,36 @@ class KimiDeltaAttention(nn.Module):
         return w, b
 
     def refresh_fused_weight(self) -> None:
-        """Refill the concatenated input-projection weight from the parameters
-        (in place when the layout is unchanged).  Needed only after writes that
-        bypass autograd's version counter, such as ``p.data.copy_(...)``."""
+        """Refill the concatenated input-projection weight and the fp32 gate
+        parameters from the parameters (in place when the layout is
+        unchanged).  Needed only after writes that bypass autograd's version
+        counter, such as ``p.data.copy_(...)``."""
         if self._wcat is not None:
             self._wcat = (None, self._wcat[1], self._wcat[2])
+        if self._gcat is not None:
+            self._gcat = (None, self._gcat[1], self._gcat[2])
         self._input_weight()
+        self._gate_params()
+
+    def _gate_params(self):
+        """``A_log`` and ``dt_bias`` as contiguous fp32 ``[H, K]`` tensors for the
+        gated core (the reference casts them to fp32 too, ``kda.py:458-459``);
+        cached like :meth:`_input_weight` and refilled in place."""
+        params = (self.A_log, self.dt_bias)
+        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
+        if self._gcat is not None and self._gcat[0] == key:
+            return self._gcat[1], self._gcat[2]
+        with torch.no_grad():
+            old = self._gcat
+            if old is not None and old[1].shape == self.A_log.shape and old[1].device == self.A_log.device:
+                a, d = old[1], old[2]
+                a.copy_(self.A_log)
+                d.copy_(self.dt_bias)
+            else:
+                a = self.A_log.detach().to(torch.float32).clone().contiguous()
+                d = self.dt_bias.detach().to(torch.float32).clone().contiguous()
+        self._gcat = (key, a, d)
+        return a, d
 
     def _state_dtype(self, x):
         if self.fp32_recurrent_state and x.dtype in (torch.float16, torch.bfloat16):
@@ -175,15 +203,17 @@ class KimiDeltaAttention(nn.Module):
         return {"conv": {"q": z(H * K), "k": z(H * K), "v": z(H * V)}, "recurrent": None}
 
     def _projections(self, x, conv_cache=None, use_cache=False, conv_out=None):
-        """q, k, v, g, beta, the new conv cache and the output gate's
-        down-projection of x (``kda.py:399-461``).
+        """q, k, v, the gate's up-projection gk ``[B, T, H, K]``, the beta logits
+        ``[B, T, H]``, the new conv cache and the output gate's down-projection
+        of x (``kda.py:399-461``).
 
         The projections of x are one library GEMM (:meth:`_input_weight`) and
-        the gate's up-projection a second; everything after them -- the
-        three short convolutions with their cache, SiLU, the q/k L2 norms,
-        the forget gate and beta -- is one fused kernel (:func:`kda_prep`).
-        ``conv_out``: write the new conv cache into these tensors (may be
-        ``conv_cache`` itself for T <= 16) instead of returning new ones."""
+        the gate's up-projection a second; the three short convolutions with
+        their cache, SiLU and the q/k L2 norms are one fused kernel
+        (:func:`kda_prep`), and the forget gate and beta are formed by the
+        gated core from gk and the logits.  ``conv_out``: write the new conv
+        cache into these tensors (may be ``conv_cache`` itself for T <= 16)
+        instead of returning new ones."""
         keep = max(self.conv_size - 1, 0)
         hist = conv_cache if (use_cache and conv_cache is not None and keep > 0) else None
         convs = (self.conv_q.conv, self.conv_k.conv, self.conv_v.conv)
@@ -192,14 +222,15 @@ class KimiDeltaAttention(nn.Module):
         y = torch.nn.functional.linear(x, w, b)
         q_in, k_in, v_in, beta_logit, gk_low, og_low = torch.split(
             y, (H * K, H * K, H * V, H, self.gk_proj[0].out_features, self.og_proj[0].out_features), dim=-1)
-        q, k, v, g, beta, new_conv = kda_prep(
+        q, k, v, _, _, new_conv = kda_prep(
             q_in, k_in, v_in,
             tuple(c.weight for c in convs), tuple(c.bias for c in convs),
-            self.gk_proj[1](gk_low), self.A_log, self.dt_bias, beta_logit,
+            None, None, None, None,
             num_heads=self.num_heads, head_dim=self.head_dim, value_head_dim=self.value_head_dim,
             l2_eps=self.l2norm_eps, hist=hist, hist_out=conv_out if use_cache else None,
             want_hist=use_cache and conv_out is None)
-        return q, k, v, g, beta, new_conv, og_low
+        gk = self.gk_proj[1](gk_low).view(x.shape[0], x.shape[1], H, K)
+        return q, k, v, gk, beta_logit, new_conv, og_low
 
     def _output(self, o_core, og_low):
         """Head-wise RMSNorm, sigmoid output gate (one fused kernel,
@@ -220,12 +251,14 @@ class KimiDeltaAttention(nn.Module):
         the state per layer and token."""
         if x.shape[1] != 1:
             raise ValueError(f"decode_step_ takes one token, got x of shape {tuple(x.shape)}")
-        q, k, v, g, beta, _, og_low = self._projections(x, conv_cache=state["conv"], use_cache=True,
-                                                conv_out=state["conv"])
+        q, k, v, gk, bl, _, og_low = self._projections(x, conv_cache=state["conv"], use_cache=True,
+                                                       conv_out=state["conv"])
         rec = state["recurrent"]
         if rec is None:
             raise ValueError("decode_step_ needs an allocated recurrent state (run a prefill first)")
-        o_core, _ = kda_recurrent(q, k, v, g, beta, state=rec, state_dtype=rec.dtype, state_out=rec)
+        a_log, dt_bias = self._gate_params()
+        o_core, _ = kda_recurrent_gated(q, k, v, gk, bl, a_log, dt_bias, state=rec, state_dtype=rec.dtype,
+                                        state_out=rec)
         return self._output(o_core, og_low)
 
     def forward(self, x, state=None, use_cache=False):
@@ -236,10 +269,11 @@ class KimiDeltaAttention(nn.Module):
         conv_cache = state["conv"] if state is not None else None
         rec = state["recurrent"] if state is not None else None
         q, k, v, g, beta, new_conv, og_low = self._projections(x, conv_cache=conv_cache, use_cache=use_cache)
+        gate = self._gate_params()      # g, beta above: gk and the beta logits
         B, T = x.shape[0], x.shape[1]
         sdtype = self._state_dtype(x)
         if use_cache and T == 1:
-            o_core, new_rec = kda_recurrent(q, k, v, g, beta, state=rec, state_dtype=sdtype)
+            o_core, new_rec = kda_recurrent_gated(q, k, v, g, beta, *gate, state=rec, state_dtype=sdtype)
         else:
             C = self.chunk_size
             if 0 < T < C:
@@ -251,17 +285,17 @@ class KimiDeltaAttention(nn.Module):
             # is the result as it is
             o_core = None
             if body > 0:
-                o_body, rec = kda_chunkwise(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
-                                            beta[:, :body], initial_state=rec, chunk_size=C,
-                                            state_dtype=sdtype, tile_size=self.tile_size)
+                o_body, rec = kda_chunkwise_gated(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
+                                                  beta[:, :body], *gate, initial_state=rec, chunk_size=C,
+                                                  state_dtype=sdtype)
                 if rem == 0:
                     o_core = o_body
                 else:
                     o_core = x.new_empty(B, T, self.num_heads, self.value_head_dim)
                     o_core[:, :body] = o_body
             if rem > 0:
-                o_tail, rec = kda_recurrent(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
-                                            beta[:, body:], state=rec, state_dtype=sdtype)
+                o_tail, rec = kda_recurrent_gated(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
+                                                  beta[:, body:], *gate, state=rec, state_dtype=sdtype)
                 if o_core is None:
                     o_core = o_tail
                 else:

@@ -73,7 +73,10 @@ def kda_prep(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *
 
     Returns ``q, k [B, T, H, K]`` and ``v [B, T, H, V]`` in the activation
     dtype, ``g [B, T, H, K]`` and ``beta [B, T, H]`` in fp32, and the new conv
-    cache dict (or None).
+    cache dict (or None).  ``gk=None`` leaves the gates out (``a_log``,
+    ``dt_bias`` and ``beta_logit`` are then ignored and g, beta returned as
+    None): for a caller that hands gk and the logits to the gated core entry
+    points (:func:`kimi_linear_amd.kda.kda_chunkwise_gated`).
     """
     H, K, V = int(num_heads), int(head_dim), int(value_head_dim)
     if q_in.dim() != 3:
@@ -83,11 +86,13 @@ def kda_prep(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *
     q_in = _rows("q_in", q_in, (B, T, Dk))
     k_in = _rows("k_in", k_in, (B, T, Dk))
     v_in = _rows("v_in", v_in, (B, T, Dv))
-    gk = _rows("gk", gk, (B, T, Dk))
-    beta_logit = _rows("beta_logit", beta_logit, (B, T, H))
+    gates = gk is not None
+    if gates:
+        gk = _rows("gk", gk, (B, T, Dk))
+        beta_logit = _rows("beta_logit", beta_logit, (B, T, H))
     xs = (q_in, k_in, v_in)
     dt = q_in.dtype
-    if any(t.dtype != dt for t in (k_in, v_in, gk, beta_logit)):
+    if any(t.dtype != dt for t in (k_in, v_in) + ((gk, beta_logit) if gates else ())):
         raise KdaError("q_in, k_in, v_in, gk and beta_logit must share one dtype")
     cs = conv_w[0].shape[-1]
     keep = cs - 1
@@ -106,10 +111,11 @@ def kda_prep(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *
         bs.append(b)
     if any(w.dtype != wdt for w in ws):
         raise KdaError("the three conv weights must share one dtype")
-    a_log = a_log.reshape(-1).contiguous()
-    dt_bias = dt_bias.reshape(-1).contiguous()
-    if a_log.numel() != Dk or dt_bias.numel() != Dk or a_log.dtype != dt_bias.dtype:
-        raise KdaError(f"A_log and dt_bias must be [H, K] = [{H}, {K}] of one dtype")
+    if gates:
+        a_log = a_log.reshape(-1).contiguous()
+        dt_bias = dt_bias.reshape(-1).contiguous()
+        if a_log.numel() != Dk or dt_bias.numel() != Dk or a_log.dtype != dt_bias.dtype:
+            raise KdaError(f"A_log and dt_bias must be [H, K] = [{H}, {K}] of one dtype")
     hs = [None, None, None]
     if hist is not None:
         for i, (n, D) in enumerate(zip("qkv", (Dk, Dk, Dv))):
@@ -120,13 +126,14 @@ def kda_prep(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *
             hs[i] = h if h.is_contiguous() else h.contiguous()
     if hist_out is not None and want_hist:
         raise KdaError("pass hist_out or want_hist, not both")
-    dev = _device_check([*xs, gk, beta_logit, *ws, a_log, dt_bias] + [t for t in bs + hs if t is not None])
+    dev = _device_check([*xs, *ws] + ([gk, beta_logit, a_log, dt_bias] if gates else [])
+                        + [t for t in bs + hs if t is not None])
 
     q = torch.empty(B, T, H, K, device=dev, dtype=dt)
     k = torch.empty(B, T, H, K, device=dev, dtype=dt)
     v = torch.empty(B, T, H, V, device=dev, dtype=dt)
-    g = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
-    beta = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    g = torch.empty(B, T, H, K, device=dev, dtype=torch.float32) if gates else None
+    beta = torch.empty(B, T, H, device=dev, dtype=torch.float32) if gates else None
     new_hist = None
     if want_hist:
         new_hist = {n: torch.empty(B, keep, D, device=dev, dtype=dt) for n, D in zip("qkv", (Dk, Dk, Dv))}
@@ -155,13 +162,17 @@ def kda_prep(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *
         a.hist_in[i] = hs[i].data_ptr() if hs[i] is not None else None
         a.hist_out[i] = new_hist["qkv"[i]].data_ptr() if new_hist is not None else None
     a.w_dtype = _code("conv weight", ws[0])
-    a.gk = gk.data_ptr()
-    a.gk_stride[0], a.gk_stride[1] = gk.stride(0), gk.stride(1)
-    a.a_log, a.dt_bias = a_log.data_ptr(), dt_bias.data_ptr()
-    a.p_dtype = _code("A_log", a_log)
-    a.beta_logit = beta_logit.data_ptr()
-    a.beta_stride[0], a.beta_stride[1] = beta_logit.stride(0), beta_logit.stride(1)
-    a.q, a.k, a.v, a.g, a.beta = q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr()
+    if gates:
+        a.gk = gk.data_ptr()
+        a.gk_stride[0], a.gk_stride[1] = gk.stride(0), gk.stride(1)
+        a.a_log, a.dt_bias = a_log.data_ptr(), dt_bias.data_ptr()
+        a.p_dtype = _code("A_log", a_log)
+        a.beta_logit = beta_logit.data_ptr()
+        a.beta_stride[0], a.beta_stride[1] = beta_logit.stride(0), beta_logit.stride(1)
+        a.g, a.beta = g.data_ptr(), beta.data_ptr()
+    else:
+        a.p_dtype = _native.DTYPE_F32
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
     a.l2_eps = float(l2_eps)
     a.x_dtype = _code("activations", q_in)
     _call(_native.load().kda_prep_fwd, a, dev, f"kda_prep_fwd (B={B}, T={T}, H={H}, K={K}, V={V}, conv {cs})")

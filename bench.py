@@ -13,6 +13,9 @@ Also reported on the same line:
   the state cannot stay resident in the 256 MB Infinity Cache, each both with
   a fresh state tensor per step (the reference API) and updated in place
   (``state_out=state``, as the graph decoder runs it);
+* ``gated``: ``kda_chunkwise_gated`` at the same shape -- the layer's gate
+  pre-processing formed in the kernel's loads from fp16 gk and beta logits
+  (1282 instead of 1540 algorithmic bytes per token and head);
 * ``layer``: the whole KDA layer at hidden 2048 (projections, short
   convolutions, norms and gates around the core): a B=4 T=2048 prefill and a
   graph-replayed B=64 decode token;
@@ -44,6 +47,8 @@ B1, T1, H1, D1, C1 = 8, 4096, 16, 128, 64
 # algorithmic traffic per (token, head): q,k,v fp16 (768 B) + g fp32 (512 B) + beta (4 B)
 # + o fp16 (256 B); per (sequence, head) the fp32 state is written once (S0 = 0 is not read).
 CHUNK_BYTES = B1 * T1 * H1 * 1540 + B1 * H1 * D1 * D1 * 4
+# the gated form reads gk and the beta logit in fp16: 3 x 256 + 256 + 2 + 256 B
+GATED_BYTES = B1 * T1 * H1 * 1282 + B1 * H1 * D1 * D1 * 4
 # causal flop count per (token, head): C (3K + 2V) + 6 K V
 CHUNK_FLOPS = B1 * T1 * H1 * (C1 * (3 * D1 + 2 * D1) + 6 * D1 * D1)
 
@@ -61,7 +66,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--decode-variant", choices=["all", "fresh", "in_place", "fresh_rot5", "in_place_rot5"],
                    default="all", help="with --only decode: time one variant (for kernel traces)")
-    p.add_argument("--only", choices=["chunkwise", "decode", "layer", "backward", "copy"], default=None,
+    p.add_argument("--only", choices=["chunkwise", "gated", "decode", "layer", "backward", "copy"], default=None,
                    help="run one workload only (for profiling); 'copy' runs a plain 1 GiB "
                         "device copy used to calibrate the HBM byte counters")
     return p.parse_args()
@@ -91,6 +96,36 @@ def chunkwise_bench(pkg, wl, torch, steps, warmup):
         wall = time.perf_counter() - t0
     launch_ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
     return wall, launch_ms
+
+
+def gated_bench(pkg, wl, torch, steps, warmup):
+    """kda_chunkwise_gated at the headline shape: fp16 q/k/v, fp16 gk and beta
+    logits (the gate's pre-activations), fp32 A_log / dt_bias [H, K].  Returns
+    the mean launch time in ms (HIP events around every timed launch)."""
+    inp = wl.make_inputs(B1, T1, H1, D1, D1, device="cuda", seed=1, qkv_dtype=torch.float16)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    gk = torch.randn(B1, T1, H1, D1, device="cuda", generator=gen).half()
+    logit = torch.randn(B1, T1, H1, device="cuda", generator=gen).half()
+    a_log = torch.rand(H1, D1, device="cuda", generator=gen) * wl.LN16
+    dt_bias = torch.randn(H1, D1, device="cuda", generator=gen) * 0.1
+
+    def step():
+        return pkg.kda_chunkwise_gated(inp["q"], inp["k"], inp["v"], gk, logit, a_log, dt_bias,
+                                       chunk_size=C1, state_dtype=torch.float32)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for e0, e1 in ev:
+            e0.record(stream)
+            step()
+            e1.record(stream)
+        torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
 
 
 def decode_bench(pkg, wl, torch, n_sets, in_place=False):
@@ -362,6 +397,16 @@ def main():
         if "value" not in result:
             result.update({"value": result["backward"]["train_tokens_per_s"], "unit": "tokens/s",
                            "ms_per_step": result["backward"]["forward_ckpt_ms"] + result["backward"]["backward_ms"]})
+    if args.only in (None, "gated"):
+        ms = gated_bench(pkg, wl, torch, args.steps, args.warmup)
+        result["gated"] = {
+            "workload": "kda_chunkwise_gated, B=8 T=4096 H=16 dk=dv=128 chunk_size=64; fp16 q/k/v, fp16 gk "
+                        "and beta logits, fp32 A_log/dt_bias, fp32 state from zeros",
+            "kernel_ms": ms, "tokens_per_s": B1 * T1 / (ms * 1e-3),
+            "algorithmic_bytes": GATED_BYTES, "gbs": GATED_BYTES / (ms * 1e-3) / 1e9,
+            "hbm_frac": GATED_BYTES / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        if "value" not in result:
+            result.update({"value": B1 * T1 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms})
     if args.only in (None, "layer"):
         result["layer"] = layer_bench(pkg, torch)
         if "value" not in result:

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 7
+#define KDA_ABI_VERSION 8
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -110,6 +110,37 @@ int kda_chunkwise_fwd(const kda_fwd_args* args, void* stream);
  * it back inside its captured graph, kimi_linear/graph_decode.py:257-262).
  */
 int kda_recurrent_fwd(const kda_fwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * The KDA layer's gate pre-processing fused into the core's loads
+ * (kimi_linear/kda.py:452-460):
+ *   g    = -exp(A_log[h, c]) * softplus(gk + dt_bias[h, c])   (softplus(z) = z
+ *          for z > 20, torch's default threshold), in fp32
+ *   beta = sigmoid(beta_logit), in fp32
+ * With these two entry points args->g holds gk, the gate's up-projection
+ * output [B,T,H,K], and args->beta the beta logits [B,T,H] (same strides and
+ * dtype codes as g and beta otherwise); the kernels form g and beta while
+ * they load a token, so neither is ever written to memory: at fp16 the
+ * chunkwise call reads 2 bytes of gate per token and channel instead of
+ * the 4 of an fp32 g that a separate pre-processing pass wrote before it.
+ * Everything else is as in kda_chunkwise_fwd / kda_recurrent_fwd.
+ * ------------------------------------------------------------------------- */
+typedef struct kda_gate_args {
+    const float* a_log;            /* [H, K] contiguous fp32 */
+    const float* dt_bias;          /* [H, K] contiguous fp32 */
+} kda_gate_args;
+
+/* kda_chunkwise_fwd with the fused gate (replaces the g / beta lines of
+ * _projections, kimi_linear/kda.py:452-460, plus kda_chunkwise,
+ * kda.py:58-185).  For fp16 / bf16 q, k, v, gk and the logits must be in
+ * the same dtype (KDA_ERR_BAD_DTYPE otherwise); fp32 q, k, v run the gated
+ * token recurrence, as kda_chunkwise_fwd does, and take any gate dtypes. */
+int kda_chunkwise_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate, void* stream);
+
+/* kda_recurrent_fwd with the fused gate (kimi_linear/kda.py:452-460 plus
+ * kda_recurrent, kda.py:188-219); gk and the logits in any dtype.  In place
+ * (state_out == state_in) as kda_recurrent_fwd. */
+int kda_recurrent_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Backward of the chunkwise forward.  The reference differentiates
@@ -199,7 +230,10 @@ int kda_chunkwise_bwd_noalloc(const kda_bwd_args* args, void* stream);
  * (softplus(z) = z for z > 20) and beta = sigmoid(beta_logit), in fp32.
  * hist_out[i] (optional) receives the last conv_size - 1 inputs of
  * [hist_in | x], the conv cache of the next call; it may be hist_in itself
- * only when T <= 16. */
+ * only when T <= 16.  g and beta may both be NULL: the gates are then not
+ * computed (gk, a_log, dt_bias and beta_logit are not read and may be NULL
+ * too), for a caller that hands gk and the logits to the gated core entry
+ * points instead. */
 typedef struct kda_prep_args {
     int64_t B, T, H, K, V;         /* K, V in {64, 128, 256} */
     int64_t conv_size;             /* 1..4 */

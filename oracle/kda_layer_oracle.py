@@ -12,6 +12,8 @@ with its pieces written out independently of torch's library layers:
   ``kda.py:295-307``, and chunked prefill, ``kda.py:420-444``);
 * :func:`l2norm_ref` -- ``kda.py:313-325``;
 * :func:`head_rmsnorm_ref` -- ``kda.py:258-279``;
+* :func:`gates_ref` -- the forget gate and beta of ``kda.py:452-460`` (also the
+  checker of the gated core entry points);
 * :func:`kda_layer_ref` -- projections and gates (``kda.py:399-461``), the
   chunk/tail dispatch (``kda.py:502-530``) over the oracle kernels of
   :mod:`oracle.kda_oracle`, and the output path (``kda.py:464-470``).
@@ -77,6 +79,14 @@ def _softplus(x):
     return torch.where(x > 20, x, torch.log1p(torch.exp(torch.clamp(x, max=20))))
 
 
+def gates_ref(gk, beta_logit, a_log, dt_bias):
+    """g = -exp(A_log) * softplus(gk + dt_bias) and beta = sigmoid(logit), in fp32
+    (``kda.py:452-460``); ``gk: [B, T, H, K]``, ``beta_logit: [B, T, H]``,
+    ``a_log, dt_bias: [H, K]``."""
+    g = -torch.exp(a_log.float()) * _softplus(gk.float() + dt_bias.float())
+    return g, torch.sigmoid(beta_logit.float())
+
+
 def kda_layer_ref(params, cfg, x, state=None, use_cache=False):
     """fp32 CPU forward of the KDA layer.  ``cfg`` has ``linear_attn_config``,
     ``l2norm_eps`` and ``rms_norm_eps`` like the reference config.  Returns out,
@@ -107,9 +117,8 @@ def kda_layer_ref(params, cfg, x, state=None, use_cache=False):
     q = l2norm_ref(_silu(conv_out["q"]).view(B, T, H, K), cfg.l2norm_eps)
     k = l2norm_ref(_silu(conv_out["k"]).view(B, T, H, K), cfg.l2norm_eps)
     v = _silu(conv_out["v"]).view(B, T, H, V)
-    beta = torch.sigmoid(_linear(x, p, "beta_proj"))
     gk = _linear(_linear(x, p, "gk_proj.0"), p, "gk_proj.1").view(B, T, H, K)
-    g = -torch.exp(p["A_log"].float()) * _softplus(gk + p["dt_bias"].float())
+    g, beta = gates_ref(gk, _linear(x, p, "beta_proj"), p["A_log"], p["dt_bias"])
 
     if use_cache and T == 1:
         o_core, new_rec = kda_recurrent_ref(q, k, v, g, beta, state=rec, state_dtype=torch.float32)

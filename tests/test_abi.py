@@ -50,7 +50,9 @@ def test_abi_version_and_status_strings(native):
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
-@pytest.mark.parametrize("struct,cname", [("KdaFwdArgs", "kda_fwd_args"), ("KdaBwdArgs", "kda_bwd_args")])
+@pytest.mark.parametrize("struct,cname", [("KdaFwdArgs", "kda_fwd_args"), ("KdaBwdArgs", "kda_bwd_args"),
+                                          ("KdaGateArgs", "kda_gate_args"), ("KdaPrepArgs", "kda_prep_args"),
+                                          ("KdaOutputArgs", "kda_output_args")])
 def test_struct_layout_matches_header(native, tmp_path, struct, cname):
     cls = getattr(native, struct)
     fields = [name for name, _ in cls._fields_]
@@ -134,6 +136,24 @@ def test_host_validation_codes(native, fn):
     assert call(ctypes.byref(overlap), None) == 5                        # aliasing
     assert call(ctypes.byref(_args(native, B=0)), None) == 0             # empty: no launch
     assert call(ctypes.byref(_args(native, H=0)), None) == 0
+
+
+@pytest.mark.parametrize("fn", ["kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd"])
+def test_gated_host_validation_codes(native, fn):
+    lib = native.load()
+    call = getattr(lib, fn)
+    gate = native.KdaGateArgs()
+    gate.a_log, gate.dt_bias = 0x200000, 0x300000      # never dereferenced
+    assert call(ctypes.byref(_args(native)), None, None) == 1              # no gate
+    assert call(ctypes.byref(_args(native)), ctypes.byref(native.KdaGateArgs()), None) == 1
+    assert call(ctypes.byref(_args(native, K=48)), ctypes.byref(gate), None) == 4
+    assert call(ctypes.byref(_args(native, B=0)), ctypes.byref(native.KdaGateArgs()), None) == 0
+    if fn == "kda_chunkwise_gated_fwd":
+        # 16-bit q, k, v: the pipeline reads gk and the logits in that dtype
+        bad = _args(native, qkv_dtype=native.DTYPE_F16, g_dtype=native.DTYPE_F32, beta_dtype=native.DTYPE_F16)
+        assert call(ctypes.byref(bad), ctypes.byref(gate), None) == 3
+        bad = _args(native, qkv_dtype=native.DTYPE_BF16, g_dtype=native.DTYPE_BF16, beta_dtype=native.DTYPE_F32)
+        assert call(ctypes.byref(bad), ctypes.byref(gate), None) == 3
 
 
 def test_in_place_state_contract(native):

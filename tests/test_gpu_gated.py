@@ -1,0 +1,194 @@
+"""GPU parity of the gated core entry points (kda_chunkwise_gated, kda_recurrent_gated).
+
+These fuse the KDA layer's gate pre-processing (``kimi_linear/kda.py:452-460``:
+g = -exp(A_log) softplus(gk + dt_bias), beta = sigmoid(logit), in fp32) into
+the kernels' loads.  The checker is the oracle's ``gates_ref`` (that formula,
+pinned through the layer fixture written by the reference module) followed
+by the core oracle: the same bars as the ungated parity tests (fp16 inputs:
+o max-abs <= 2e-3, state relative error <= 1e-3; fp32: 1e-5).
+
+The decay itself is checked in isolation: with beta = 0 and an all-ones
+initial state, the final state of a call is the product of the per-token
+decays, which must match exp(sum g) computed in fp64 to a few ulps per token,
+over the whole range of z = gk + dt_bias (down to e^z far below fp32's
+epsilon, up past torch's softplus threshold of 20) and A_log up to log 64.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kda_chunkwise_ref, kda_recurrent_ref
+from oracle.kda_layer_oracle import gates_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+O_TOL = 2e-3
+S_TOL = 1e-3
+
+
+def max_abs(a, b):
+    return (a.detach().double().cpu() - b.detach().double().cpu()).abs().max().item()
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def make(B, T, H, K, V, dtype, seed=0, a_log_range=(0.0, math.log(16.0)), state_std=None):
+    """Layer-like core inputs with the gate given as gk and logits (activation
+    dtype), A_log and dt_bias fp32 [H, K]; on the CPU."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen)
+
+    q = F.normalize(randn(B, T, H, K), dim=-1).to(dtype)
+    k = F.normalize(randn(B, T, H, K), dim=-1).to(dtype)
+    v = randn(B, T, H, V).to(dtype)
+    lo, hi = a_log_range
+    a_log = torch.rand(H, K, generator=gen) * (hi - lo) + lo
+    gk = randn(B, T, H, K).to(dtype)
+    dt_bias = randn(H, K) * 0.1
+    logit = randn(B, T, H).to(dtype)
+    state = randn(B, H, K, V) * state_std if state_std is not None else None
+    return dict(q=q, k=k, v=v, gk=gk, logit=logit, a_log=a_log, dt_bias=dt_bias, state=state)
+
+
+def dev(inp):
+    return {n: (t.to(DEV) if t is not None else None) for n, t in inp.items()}
+
+
+def oracle_gates(inp):
+    return gates_ref(inp["gk"], inp["logit"], inp["a_log"], inp["dt_bias"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,T,H,state", [(2, 256, 4, False), (1, 192, 2, True), (4, 128, 16, False),
+                                         (1, 100, 2, True), (2, 10, 3, True)])
+def test_chunkwise_gated_matches_oracle(kda_pkg, dtype, B, T, H, state):
+    """(4, 128, 16): 64 chains of 64 columns -> the 32-column (NC = 2) kernel;
+    the others the 16-column one.  T = 100 and 10 end in a partial block,
+    whose padded rows must leave the state alone (chunk_size = T there)."""
+    K = V = 128
+    C = 64 if T % 64 == 0 else T
+    inp = make(B, T, H, K, V, dtype, seed=1, state_std=0.05 if state else None)
+    d = dev(inp)
+    with torch.no_grad():
+        o, s = kda_pkg.kda_chunkwise_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                           initial_state=d["state"], chunk_size=C, state_dtype=torch.float32)
+    g, beta = oracle_gates(inp)
+    o_ref, s_ref = kda_chunkwise_ref(inp["q"], inp["k"], inp["v"], g, beta, initial_state=inp["state"],
+                                     chunk_size=C, state_dtype=torch.float32)
+    eo, es = max_abs(o, o_ref), rel(s, s_ref)
+    print(f"gated chunkwise {dtype} B={B} T={T} H={H}: o max-abs {eo:.2e} state rel {es:.2e}", flush=True)
+    o_tol = O_TOL if dtype == torch.float16 else 8 * O_TOL      # bf16 carries 3 fewer mantissa bits
+    s_tol = S_TOL if dtype == torch.float16 else 8 * S_TOL
+    assert eo <= o_tol and es <= s_tol, (eo, es)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_chunkwise_gated_equals_ungated_with_the_same_gates(kda_pkg, dtype):
+    """The gated kernel and the ungated one fed g, beta from the oracle's formula
+    (computed on the host) differ only by the decay's rounding."""
+    B, T, H, K, V = 2, 320, 4, 64, 64
+    inp = make(B, T, H, K, V, dtype, seed=2, state_std=0.02)
+    d = dev(inp)
+    g, beta = oracle_gates(inp)
+    with torch.no_grad():
+        o1, s1 = kda_pkg.kda_chunkwise_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"],
+                                             d["dt_bias"], initial_state=d["state"], chunk_size=32,
+                                             state_dtype=torch.float32)
+        o2, s2 = kda_pkg.kda_chunkwise(d["q"], d["k"], d["v"], g.to(DEV), beta.to(DEV), initial_state=d["state"],
+                                       chunk_size=32, state_dtype=torch.float32)
+    eo, es = rel(o1, o2), rel(s1, s2)
+    print(f"gated vs ungated {dtype}: o rel {eo:.2e} state rel {es:.2e}", flush=True)
+    assert eo <= 1e-4 and es <= 1e-4, (eo, es)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_recurrent_gated_matches_oracle(kda_pkg, dtype):
+    B, T, H, K, V = 3, 40, 4, 128, 128
+    inp = make(B, T, H, K, V, dtype, seed=3, state_std=0.02)
+    d = dev(inp)
+    with torch.no_grad():
+        o, s = kda_pkg.kda_recurrent_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                           state=d["state"], state_dtype=torch.float32)
+    g, beta = oracle_gates(inp)
+    o_ref, s_ref = kda_recurrent_ref(inp["q"], inp["k"], inp["v"], g, beta, state=inp["state"],
+                                     state_dtype=torch.float32)
+    eo, es = rel(o, o_ref), rel(s, s_ref)
+    print(f"gated recurrent {dtype}: o rel {eo:.2e} state rel {es:.2e}", flush=True)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert eo <= tol and es <= tol, (eo, es)
+
+
+def test_chunkwise_gated_fp32_runs_the_recurrence(kda_pkg):
+    """fp32 activations: the gated call is fp32 throughout (the gated recurrence)."""
+    B, T, H, K, V = 1, 128, 2, 64, 64
+    inp = make(B, T, H, K, V, torch.float32, seed=4, state_std=0.1)
+    d = dev(inp)
+    with torch.no_grad():
+        o, s = kda_pkg.kda_chunkwise_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                           initial_state=d["state"], chunk_size=64, state_dtype=torch.float32)
+    g, beta = oracle_gates(inp)
+    o_ref, s_ref = kda_chunkwise_ref(inp["q"], inp["k"], inp["v"], g, beta, initial_state=inp["state"],
+                                     chunk_size=64, state_dtype=torch.float32)
+    assert rel(o, o_ref) <= 1e-5 and rel(s, s_ref) <= 1e-5
+
+
+def _decay_case(T, H, K, dtype, seed):
+    """gk whose z = gk + dt_bias sits, per channel, near a level spread from -60
+    to 40 over the channels; A_log from log 1 to log 64; logits that make beta
+    exactly 0."""
+    gen = torch.Generator().manual_seed(seed)
+    a_log = torch.rand(H, K, generator=gen) * math.log(64.0)
+    dt_bias = torch.randn(H, K, generator=gen) * 0.1
+    level = torch.linspace(-60.0, 40.0, H * K)[torch.randperm(H * K, generator=gen)].reshape(H, K)
+    z = level + 0.5 * torch.randn(1, T, H, K, generator=gen)
+    gk = (z - dt_bias).to(dtype)
+    logit = torch.full((1, T, H), -6.0e4).to(dtype)      # sigmoid -> 0 in fp32
+    q = F.normalize(torch.randn(1, T, H, K, generator=gen), dim=-1).to(dtype)
+    k = F.normalize(torch.randn(1, T, H, K, generator=gen), dim=-1).to(dtype)
+    v = torch.randn(1, T, H, K, generator=gen).to(dtype)
+    # the decay each token applies, in fp64 from the values the kernel reads
+    zz = gk.double() + dt_bias.double()
+    sp = torch.where(zz > 20, zz, torch.log1p(torch.exp(torch.clamp(zz, max=20))))
+    g64 = -torch.exp(a_log.double()) * sp
+    return dict(q=q, k=k, v=v, gk=gk, logit=logit, a_log=a_log, dt_bias=dt_bias), g64
+
+
+@pytest.mark.parametrize("path", ["recurrent_f32", "recurrent_f16", "chunkwise_f16"])
+def test_gated_decay_over_the_whole_gate_range(kda_pkg, path):
+    """beta = 0 and S_0 = 1: the final state row of channel c is prod_t a_t(c).
+    Per token the decay must be right to a few ulps of its exponent, from
+    e^z < 1e-26 (where log(1 + e^z) in fp32 would round to 0) past z = 20."""
+    dtype = torch.float32 if path.endswith("f32") else torch.float16
+    T, H, K = (1, 4, 128) if path.startswith("recurrent") else (32, 2, 64)
+    inp, g64 = _decay_case(T, H, K, dtype, seed=5)
+    d = dev(inp)
+    s0 = torch.ones(1, H, K, K, device=DEV)
+    fn = kda_pkg.kda_recurrent_gated if path.startswith("recurrent") else kda_pkg.kda_chunkwise_gated
+    kw = dict(state=s0) if path.startswith("recurrent") else dict(initial_state=s0, chunk_size=T)
+    with torch.no_grad():
+        _, s = fn(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                  state_dtype=torch.float32, **kw)
+    got = s[0, :, :, 0].double().cpu()                    # [H, K]: every column is the same
+    assert torch.equal(s[0].cpu(), s[0, :, :, :1].cpu().expand(H, K, K))
+    logsum = g64[0].sum(0)                                # [H, K], log of the exact product
+    want = torch.exp(logsum)
+    live = logsum > -80.0                                 # products above fp32's normal range
+    # per channel, a few ulps of the exponent per token: T (1 + |log prod|) 2^-21
+    # (the form without the rounding correction of log2(1 + t) exceeds this
+    # by 2.5-7x on these inputs, the corrected one stays below 0.4x on the CPU)
+    err = (got - want).abs() / want
+    ratio = (err / ((T * 2.0 ** -21) * (1.0 + logsum.abs())))[live].max().item()
+    print(f"{path}: {int(live.sum())} live channels, max error / bound {ratio:.2f}", flush=True)
+    assert ratio <= 1.0, ratio
+    assert (got[~live] <= 1e-30).all()

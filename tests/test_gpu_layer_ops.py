@@ -181,3 +181,17 @@ def test_prep_gate_softplus_tails(ops):
     err = ((got[3].double().cpu() - ref).abs() / ref.abs()).max().item()
     print(f"[prep softplus tails] max rel err {err:.2e}", flush=True)
     assert (got[3] < 0).all() and err <= 1e-5
+
+
+@pytest.mark.parametrize("T", [1, 37])
+def test_prep_without_gates_matches_prep_with_gates(ops, T):
+    """A call that leaves the gates to the core (gk=None) writes the same q, k, v
+    and conv cache, bit for bit, and returns no g and beta."""
+    B, H, K, V, cs = 2, 2, 128, 128, 4
+    xs, ws, bs, gk, a_log, dt_bias, beta_logit = make_prep_inputs(B, T, H, K, V, cs, torch.float16, seed=11)
+    kw = dict(num_heads=H, head_dim=K, value_head_dim=V, l2_eps=1e-6, want_hist=True)
+    q1, k1, v1, g1, b1, h1 = ops.kda_prep(*xs, ws, bs, gk, a_log, dt_bias, beta_logit, **kw)
+    q2, k2, v2, g2, b2, h2 = ops.kda_prep(*xs, ws, bs, None, None, None, None, **kw)
+    assert g2 is None and b2 is None and g1 is not None
+    for a, b in ((q1, q2), (k1, k2), (v1, v2)) + tuple((h1[n], h2[n]) for n in "qkv"):
+        assert torch.equal(a, b)
