@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -51,6 +51,13 @@ class KdaGateArgs(ctypes.Structure):
     """Mirror of ``struct kda_gate_args`` (include/kda_hip.h)."""
 
     _fields_ = [("a_log", ctypes.c_void_p), ("dt_bias", ctypes.c_void_p)]
+
+
+class KdaOutEpilogue(ctypes.Structure):
+    """Mirror of ``struct kda_out_epilogue`` (include/kda_hip.h)."""
+
+    _fields_ = [("gate", ctypes.c_void_p), ("gate_stride", ctypes.c_int64 * 2),
+                ("weight", ctypes.c_void_p), ("eps", ctypes.c_float)]
 
 
 class KdaBwdArgs(ctypes.Structure):
@@ -102,7 +109,8 @@ class KdaOutputArgs(ctypes.Structure):
 
 
 EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_chunkwise_fwd_ckpt",
-                    "kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd", "kda_chunkwise_bwd",
+                    "kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd", "kda_chunkwise_fused_fwd",
+                    "kda_chunkwise_bwd",
                     "kda_chunkwise_bwd_workspace_size", "kda_chunkwise_bwd_noalloc",
                     "kda_prep_fwd", "kda_output_fwd", "kda_status_str", "kda_abi_version")
 
@@ -140,6 +148,9 @@ def load() -> ctypes.CDLL:
         for name in ("kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd"):
             getattr(lib, name).argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.POINTER(KdaGateArgs), ctypes.c_void_p]
             getattr(lib, name).restype = ctypes.c_int
+        lib.kda_chunkwise_fused_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.POINTER(KdaGateArgs),
+                                                ctypes.POINTER(KdaOutEpilogue), ctypes.c_void_p]
+        lib.kda_chunkwise_fused_fwd.restype = ctypes.c_int
         lib.kda_chunkwise_fwd_ckpt.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_void_p, ctypes.c_void_p]
         lib.kda_chunkwise_fwd_ckpt.restype = ctypes.c_int
         lib.kda_chunkwise_bwd.argtypes = [ctypes.POINTER(KdaBwdArgs), ctypes.c_void_p]

@@ -122,6 +122,27 @@ int kda_chunkwise_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate,
     return chunkwise_entry(args, nullptr, gate, stream);
 }
 
+int kda_chunkwise_fused_fwd(const kda_fwd_args* args, const kda_gate_args* gate, const kda_out_epilogue* out,
+                            void* stream) {
+    const int st = validate_common(args, false);
+    if (st != KDA_OK) return st;
+    if (gate) {
+        const int gs = validate_gate(args, gate);
+        if (gs != KDA_OK) return gs;
+    }
+    if (out == nullptr) return KDA_ERR_NULL_POINTER;
+    if (args->chunk_size <= 0 || args->T % args->chunk_size != 0) return KDA_ERR_BAD_SHAPE;
+    if (!(out->eps >= 0.f)) return KDA_ERR_BAD_SHAPE;
+    if (!kda::chunkwise_fused_supported(*args)) return KDA_ERR_UNSUPPORTED;
+    if (args->B == 0 || args->H == 0) return KDA_OK;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // no tokens: no outputs, the state passes through (the recurrence's empty loop)
+    if (args->T == 0) return kda::recurrent_launch(*args, s, gate);
+    if (out->gate == nullptr || out->weight == nullptr) return KDA_ERR_NULL_POINTER;
+    if (args->B * args->H > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    return kda::chunkwise_fused_launch(*args, s, gate, *out);
+}
+
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
     if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0) return 0;
     if (T > (int64_t{1} << 40) || B * H > (int64_t{1} << 31) || K > 4096 || V > 4096) return 0;

@@ -239,11 +239,20 @@ struct __align__(16) Stage {
     float e15[CB][K];                      // per block: decay over the block
 };
 constexpr int MAX_NC = 4;        // consumer waves per workgroup (at most)
-template <int K>
+// Row sums of squares of a chunk's outputs, per consumer wave, for the fused
+// output epilogue: [chunk parity][block][row][wave].
+template <bool EPI>
+struct RowParts {
+    float p[2][CB][BT][MAX_NC];
+};
+template <>
+struct RowParts<false> {};
+template <int K, int CG, bool EPI>
 struct __align__(16) Smem {
     ChunkOps<K> set[2][NCH];
     Stage<K> st[NCH];
-    uint16_t vt[MAX_NC][CB * BT][16];      // per consumer wave: one chunk of v, 16-bit, row-major
+    uint16_t vt[MAX_NC][CG][CB * BT][16];  // per consumer wave and column group: one chunk of v, 16-bit
+    RowParts<EPI> rows;
 };
 
 __device__ __forceinline__ h4 frag16(const _Float16* base, int stride, int row, int lg) {
@@ -391,13 +400,16 @@ __device__ __forceinline__ f4 mm_f32(const f4& xt, const f4& y, f4 c) {
     return c;
 }
 
-template <int K, int NC, typename TQ, bool GATED>
+// CG: 16-column groups per consumer wave; EPI: the output epilogue (the
+// layer's head-wise RMSNorm and sigmoid output gate) on the o tile, which
+// needs a head's whole V row in one workgroup (16 NC CG == V).
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false>
 struct Kern {
     static constexpr int KT = K / 16;                   // 16-row state tiles
     static constexpr int KU = K / 32;                   // 32-wide k blocks
     static constexpr int CH = K / 32;                   // channels per producer lane
     static constexpr int KR = K + 8;                    // padded row of a row-major operand
-    static constexpr int VT = 16 * NC;
+    static constexpr int VT = 16 * NC * CG;            // state columns per workgroup
     static constexpr int QB = CH * static_cast<int>(sizeof(TQ));   // bytes of a lane's q / k row
     static constexpr int QW = BLoad<QB>::W;
     // g and beta as loaded: fp32 log decays and rates, or (GATED) the gate's
@@ -431,7 +443,7 @@ struct Kern {
     };
 
     const kda_fwd_args& a;
-    Smem<K>& sm;
+    Smem<K, CG, EPI>& sm;
     int64_t b, h, T;
     float scale;
     int lane, ln, lg;
@@ -440,7 +452,7 @@ struct Kern {
     uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;   // token-row strides in bytes
     uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets
 
-    __device__ Kern(const kda_fwd_args& args, Smem<K>& s) : a(args), sm(s) {}
+    __device__ Kern(const kda_fwd_args& args, Smem<K, CG, EPI>& s) : a(args), sm(s) {}
 
     // Rows of block `blk` that lie before T (0..BT).
     __device__ int rows_in(int blk) const {
@@ -882,22 +894,27 @@ struct Kern {
     }
 
     // ------------------------------------------------------------ consumers
-    // The v values of one chunk for this wave's 16 columns: 32 rows x 32
-    // bytes (16-bit inputs: row lane / 2, 8 columns a lane) or 32 x 64 bytes
-    // (fp32: rows lane / 4 and 16 + lane / 4, 4 columns a lane), one 16-byte
-    // buffer load per lane and row set; rows past T read as zero.
+    // A consumer wave owns CG groups of 16 state columns, colw + 16 g ..
+    // + 15 for group g (lane column ln of each).  The chunk operands read from
+    // LDS (q * E, k * E, k * F, M, G_10, A) are shared by the groups.
+    //
+    // The v values of one chunk for one group: 32 rows x 32 bytes (16-bit
+    // inputs: row lane / 2, 8 columns a lane) or 32 x 64 bytes (fp32: rows
+    // lane / 4 and 16 + lane / 4, 4 columns a lane), one 16-byte buffer load
+    // per lane and row set; rows past T read as zero.
     static constexpr int VW = sizeof(TQ) == 2 ? 4 : 8;
-    __device__ void v_load(uint32_t (&vr)[VW], int chunk) const {
+    __device__ void v_load(uint32_t (&vr)[VW], int chunk, int grp) const {
         const int blk = CB * chunk;
         const int64_t e = b * a.v_stride[0] + static_cast<int64_t>(blk) * BT * a.v_stride[1] + h * a.v_stride[2];
         const int left = rows_in(blk) + rows_in(blk + 1);
         const auto rv = make_rsrc(static_cast<const char*>(a.v) + e * static_cast<int64_t>(sizeof(TQ)),
                                   static_cast<uint32_t>(left) * rs_v);
+        const uint32_t go = static_cast<uint32_t>(16 * grp * sizeof(TQ));
         uint32_t* w = vr;
-        BLoad<16>::ld(w, rv, vo_v, 0);
-        if constexpr (VW == 8) BLoad<16>::ld(w + 4, rv, vo_v, 16 * rs_v);
+        BLoad<16>::ld(w, rv, vo_v, go);
+        if constexpr (VW == 8) BLoad<16>::ld(w + 4, rv, vo_v, go + 16 * rs_v);
     }
-    // The chunk's v into this wave's tile as 16-bit values (fp32 inputs are
+    // The chunk's v into a group's tile as 16-bit values (fp32 inputs are
     // rounded to fp16 here), then the two blocks' fragments in accumulator
     // layout (rows 4lg + j, column ln) by transposing LDS reads: in each
     // 16-lane group, lane s reads row 4lg + s/4, columns 4 (s % 4) .. + 3,
@@ -934,12 +951,12 @@ struct Kern {
         }
     }
 
-    // Output rows of block blk from the transposed tile: lane (ln, lg) holds
-    // row ln, columns colw + 4lg .. + 3 (rows past T are skipped).
-    __device__ void store_ot(const f4& O, int blk, int64_t colw) const {
+    // Four values of one output row to o (TQ): lane (ln, lg) holds row ln of
+    // block blk, columns col + 4lg .. + 3 (rows past T are skipped).
+    __device__ void store_row4(const f4& O, int blk, int64_t col) const {
         const int64_t row = static_cast<int64_t>(blk) * BT + ln;
         if (ln >= rows_in(blk)) return;
-        TQ* o = static_cast<TQ*>(a.o) + ((b * T + row) * a.H + h) * a.V + colw + 4 * lg;
+        TQ* o = static_cast<TQ*>(a.o) + ((b * T + row) * a.H + h) * a.V + col + 4 * lg;
         if constexpr (sizeof(TQ) == 4) {
             *reinterpret_cast<float4*>(o) = float4{O[0], O[1], O[2], O[3]};
         } else if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
@@ -952,86 +969,196 @@ struct Kern {
         }
     }
 
-    // One chunk (blocks blk, blk + 1) of the chain for this wave's 16 state
-    // columns (colw .. colw + 15; lane column ocol); the v load of the chunk
-    // one superstep later is issued into vraw once its values are in LDS.
-    // ck (or null): the chunk's checkpoint for the backward, in fp32: rows
-    // [0, K) the state before it, [K, K + 32) its R = V - (k * E) S,
-    // [K + 32, K + 64) its P.
-    __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw)[VW], uint16_t (*vt)[16], f4 (&S)[KT],
-                            int64_t col0, uint32_t ocol, int64_t colw, float* ck) const {
-        f4 R0, R1;
-        v_tile(vraw, vt, R0, R1);
-        v_load(vraw, blk / CB + NCH);
-        const int64_t V = a.V, rc = col0 + ocol;
-        if (ck) store_state_t<KT>(S, ck, (4 * lg) * V + rc, V);
-        float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
-        // S as single fp16 operands: Z and O read S once per chunk
-        h8 sh[KU];
+    // EPI: a chunk's outputs, rounded to TQ as the reference's o_core is, held
+    // over one barrier while the other consumer waves' row sums of squares
+    // arrive, with the output gate's pre-activations of the same entries.
+    struct Pend {
+        f4 o[EPI ? CG : 1][CB];
+        u2 gt[EPI ? CG : 1][CB];
+        int blk;
+    };
+    const void* og = nullptr;                // EPI: the output gate's pre-activations [B, T, H*V]
+    int64_t og_s0 = 0, og_s1 = 0;            //      and their (batch, token) strides
+    float eps = 0.f;                         //      the norm's epsilon
+    float wn[EPI ? CG : 1][4];               //      the norm weight of the lane's columns
+
+    // EPI: the pre-activations of the output gate for the lane's entries of
+    // block blk (rows past T read as zero).
+    __device__ u2 gate_load(int blk, int64_t col) const {
+        const int64_t gs1 = og_s1;
+        const int64_t e = b * og_s0 + static_cast<int64_t>(blk) * BT * gs1 + h * a.V + col;
+        const auto r = make_rsrc(static_cast<const TQ*>(og) + e,
+                                 static_cast<uint32_t>(rows_in(blk) * gs1 * static_cast<int64_t>(sizeof(TQ))));
+        uint32_t w[2];
+        BLoad<8>::ld(w, r, static_cast<uint32_t>((ln * gs1 + 4 * lg) * static_cast<int64_t>(sizeof(TQ))), 0);
+        return u2{w[0], w[1]};
+    }
+
+    // EPI, after the barrier that follows a chunk: the head's row norms from
+    // every consumer wave's partial sums, then y = TQ(TQ(o rstd w) sigmoid(gate))
+    // (kimi_linear/kda.py:273-279, 468), stored in place of o.
+    __device__ void finish(const Pend& pd, int64_t colw, int wave) const {
+        const float (*parts)[BT][MAX_NC] = sm.rows.p[(pd.blk / CB) & 1];
+        const float inv_v = 1.f / static_cast<float>(a.V);
 #pragma unroll
-        for (int u = 0; u < KU; ++u) sh[u] = cat(to_h4(S[2 * u]), to_h4(S[2 * u + 1]));
+        for (int bk = 0; bk < CB; ++bk) {
+            const float4 pt = *reinterpret_cast<const float4*>(&parts[bk][ln][0]);
+            float tot = pt.x;
+            if (NC > 1) tot += pt.y;
+            if (NC > 2) tot += pt.z + pt.w;
+            const float rstd = rsqrtf(tot * inv_v + eps);
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+                f4 y;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t bits = (pd.gt[g][bk][j / 2] >> (16 * (j % 2))) & 0xffffu;
+                    const float z = Elem<TQ>::code == KDA_DTYPE_BF16
+                                        ? __uint_as_float(bits << 16)
+                                        : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+                    const float n = round_elem<TQ>((pd.o[g][bk][j] * rstd) * wn[g][j]);
+                    y[j] = n * sigmoid_f(z);
+                }
+                store_row4(y, pd.blk + bk, colw + 16 * g);
+            }
+        }
+        (void)wave;
+    }
+
+    // One chunk (blocks blk, blk + 1) of the chain for this wave's CG column
+    // groups; the v load of the chunk one superstep later is issued into
+    // vraw once its values are in LDS.  ck (or null): the chunk's checkpoint
+    // for the backward, in fp32: rows [0, K) the state before it, [K, K + 32)
+    // its R = V - (k * E) S, [K + 32, K + 64) its P.  EPI: the outputs go to
+    // pd (and their row sums of squares to LDS) instead of o.
+    __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw)[CG][VW],
+                            uint16_t (*vt)[CB * BT][16], f4 (&S)[CG][KT], int64_t colw, float* ck, Pend& pd,
+                            int wave) const {
+        f4 R[CG][CB];
+#pragma unroll
+        for (int g = 0; g < CG; ++g) {
+            v_tile(vraw[g], vt[g], R[g][0], R[g][1]);
+            v_load(vraw[g], blk / CB + NCH, g);
+        }
+        const int64_t V = a.V;
+        if (ck) {
+#pragma unroll
+            for (int g = 0; g < CG; ++g) store_state_t<KT>(S[g], ck, (4 * lg) * V + colw + 16 * g + ln, V);
+        }
+        float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
         // the same fragments as A and B operands the other way round, so that
-        // a lane holds four adjacent output columns of one row
-        f4 Z0 = {0.f, 0.f, 0.f, 0.f}, Z1 = Z0, O0 = Z0, O1 = Z0;
+        // a lane holds four adjacent output columns of one row.  S enters as
+        // single fp16 operands: Z and O read it once per chunk.
+        f4 Z[CG][CB], O[CG][CB];
+#pragma unroll
+        for (int g = 0; g < CG; ++g)
+#pragma unroll
+            for (int bk = 0; bk < CB; ++bk) Z[g][bk] = O[g][bk] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
             const int o = ln * KR + 32 * u + 8 * lg;
-            Z0 = mfma16x16x32(*reinterpret_cast<const h8*>(&co.KE[0][0][0] + o), sh[u], Z0);
-            Z1 = mfma16x16x32(*reinterpret_cast<const h8*>(&co.KE[1][0][0] + o), sh[u], Z1);
-            O0 = mfma16x16x32(sh[u], *reinterpret_cast<const h8*>(&co.QE[0][0][0] + o), O0);
-            O1 = mfma16x16x32(sh[u], *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o), O1);
+            const h8 k0 = *reinterpret_cast<const h8*>(&co.KE[0][0][0] + o);
+            const h8 k1 = *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o);
+            const h8 q0 = *reinterpret_cast<const h8*>(&co.QE[0][0][0] + o);
+            const h8 q1 = *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o);
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+                const h8 sh = cat(to_h4(S[g][2 * u]), to_h4(S[g][2 * u + 1]));
+                Z[g][0] = mfma16x16x32(k0, sh, Z[g][0]);
+                Z[g][1] = mfma16x16x32(k1, sh, Z[g][1]);
+                O[g][0] = mfma16x16x32(sh, q0, O[g][0]);
+                O[g][1] = mfma16x16x32(sh, q1, O[g][1]);
+            }
         }
         // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0): M (hi + lo)
         // times a single fp16 R is one K = 32 product [M_hi | M_lo] [R ; R]
-        R0 -= Z0;
-        R1 -= Z1;
-        if (rp) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                rp[(4 * lg + j) * V + rc] = R0[j];
-                rp[(16 + 4 * lg + j) * V + rc] = R1[j];
-            }
-        }
-        const h4 r0 = to_h4(R0);
-        const f4 P0 = mfma16x16x32(cat(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg)),
-                                   cat(r0, r0), f4{0.f, 0.f, 0.f, 0.f});
-        const Split4 p0(P0);
-        R1 = mm4(frag16(&co.GH[0][0], RP, ln, lg), frag16(&co.GL[0][0], RP, ln, lg), p0.hi, p0.lo, R1);
-        const h4 r1 = to_h4(R1);
-        const f4 P1 = mfma16x16x32(cat(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg)),
-                                   cat(r1, r1), f4{0.f, 0.f, 0.f, 0.f});
-        const Split4 p1(P1);
-        if (rp) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                rp[(32 + 4 * lg + j) * V + rc] = P0[j];
-                rp[(48 + 4 * lg + j) * V + rc] = P1[j];
-            }
-        }
-        // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is P's
-        // accumulator layout, A^T's B-operand layout is A's A-operand layout
-        O0 *= scale;
-        O1 *= scale;
+        const h8 m0 = cat(frag16(&co.MH[0][0][0], RP, ln, lg), frag16(&co.ML[0][0][0], RP, ln, lg));
+        const h8 m1 = cat(frag16(&co.MH[1][0][0], RP, ln, lg), frag16(&co.ML[1][0][0], RP, ln, lg));
+        const h4 gh = frag16(&co.GH[0][0], RP, ln, lg), gl = frag16(&co.GL[0][0], RP, ln, lg);
         const h4 a00 = frag16(&co.AM[0][0][0], RP, ln, lg);
-        O0 = mfma16x16x32(cat(p0.hi, p0.lo), cat(a00, a00), O0);
         const h8 a1 = cat(frag16(&co.A10[0][0], RP, ln, lg), frag16(&co.AM[1][0][0], RP, ln, lg));
-        O1 = mfma16x16x32(cat(p0.hi, p1.hi), a1, O1);
-        O1 = mfma16x16x32(cat(p0.lo, p1.lo), a1, O1);
-        store_ot(O0, blk, colw);
-        store_ot(O1, blk + 1, colw);
+        h8 ph[CG], pl[CG];
+#pragma unroll
+        for (int g = 0; g < CG; ++g) {
+            const int64_t rc = colw + 16 * g + ln;
+            R[g][0] -= Z[g][0];
+            R[g][1] -= Z[g][1];
+            if (rp) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    rp[(4 * lg + j) * V + rc] = R[g][0][j];
+                    rp[(16 + 4 * lg + j) * V + rc] = R[g][1][j];
+                }
+            }
+            const h4 r0 = to_h4(R[g][0]);
+            const f4 P0 = mfma16x16x32(m0, cat(r0, r0), f4{0.f, 0.f, 0.f, 0.f});
+            const Split4 p0(P0);
+            R[g][1] = mm4(gh, gl, p0.hi, p0.lo, R[g][1]);
+            const h4 r1 = to_h4(R[g][1]);
+            const f4 P1 = mfma16x16x32(m1, cat(r1, r1), f4{0.f, 0.f, 0.f, 0.f});
+            const Split4 p1(P1);
+            if (rp) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    rp[(32 + 4 * lg + j) * V + rc] = P0[j];
+                    rp[(48 + 4 * lg + j) * V + rc] = P1[j];
+                }
+            }
+            // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is
+            // P's accumulator layout, A^T's B-operand layout is A's A-operand
+            // layout
+            O[g][0] *= scale;
+            O[g][1] *= scale;
+            O[g][0] = mfma16x16x32(cat(p0.hi, p0.lo), cat(a00, a00), O[g][0]);
+            O[g][1] = mfma16x16x32(cat(p0.hi, p1.hi), a1, O[g][1]);
+            O[g][1] = mfma16x16x32(cat(p0.lo, p1.lo), a1, O[g][1]);
+            ph[g] = cat(p0.hi, p1.hi);
+            pl[g] = cat(p0.lo, p1.lo);
+        }
+        if constexpr (EPI) {
+            // outputs rounded to TQ (the reference's o_core), their row sums of
+            // squares over this wave's columns to LDS, the values held for the
+            // norm
+            const int par = (blk / CB) & 1;
+#pragma unroll
+            for (int bk = 0; bk < CB; ++bk) {
+                float ss = 0.f;
+#pragma unroll
+                for (int g = 0; g < CG; ++g) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float x = round_elem<TQ>(O[g][bk][j]);
+                        pd.o[g][bk][j] = x;
+                        ss = fmaf(x, x, ss);
+                    }
+                    pd.gt[g][bk] = gate_load(blk + bk, colw + 16 * g);
+                }
+                ss = lanegroup4_sum(ss);
+                if (lg == 0) sm.rows.p[par][bk][ln][wave] = ss;
+            }
+            pd.blk = blk;
+        } else {
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+                store_row4(O[g][0], blk, colw + 16 * g);
+                store_row4(O[g][1], blk + 1, colw + 16 * g);
+            }
+        }
         // S <- E[31] S + F^T P over both blocks: the k-major line of channel
         // 16t + ln gives tokens 4lg..4lg+3 of block 0 then of block 1, the
         // order of cat(P_0, P_1)
-        const h8 ph = cat(p0.hi, p1.hi), pl = cat(p0.lo, p1.lo);
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
             const int piece = 8 * (lg ^ kh_swz(16 * t + ln));
             const float4 e = *reinterpret_cast<const float4*>(&co.echunk[16 * t + 4 * lg]);
-            S[t][0] *= e.x; S[t][1] *= e.y; S[t][2] *= e.z; S[t][3] *= e.w;
             const h8 kf = *reinterpret_cast<const h8*>(&co.KH[16 * t + ln][piece]);
-            S[t] = mfma16x16x32(kf, ph, S[t]);
-            S[t] = mfma16x16x32(kf, pl, S[t]);
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+                S[g][t][0] *= e.x; S[g][t][1] *= e.y; S[g][t][2] *= e.z; S[g][t][3] *= e.w;
+                S[g][t] = mfma16x16x32(kf, ph[g], S[g][t]);
+                S[g][t] = mfma16x16x32(kf, pl[g], S[g][t]);
+            }
         }
     }
 };
@@ -1043,14 +1170,21 @@ struct Kern {
 // barriers; every prefetch is issued unconditionally (a block past T loads
 // zeros).  The chunks cover T rounded up to whole chunks: a padded block
 // (all rows past T) is neutral and is built like any other.
-template <int K, int NC, typename TQ, bool GATED>
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false>
 __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt,
-                                                                   const kda_gate_args gate) {
-    using KN = Kern<K, NC, TQ, GATED>;
+                                                                   const kda_gate_args gate,
+                                                                   const kda_out_epilogue epi) {
+    using KN = Kern<K, NC, TQ, GATED, CG, EPI>;
     constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
-    __shared__ Smem<K> sm;
+    __shared__ Smem<K, CG, EPI> sm;
     KN kn(a, sm);
+    if constexpr (EPI) {
+        kn.og = epi.gate;
+        kn.og_s0 = epi.gate_stride[0];
+        kn.og_s1 = epi.gate_stride[1];
+        kn.eps = epi.eps;
+    }
 
     const int64_t H = a.H, V = a.V;
     const int nvt = static_cast<int>(V / VT);
@@ -1079,10 +1213,9 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     const int nss = (ncc + NCH - 1) / NCH;               // supersteps
 
     const bool consumer = wave < NC;
-    // consumer state: S[t][j] = S[16t + 4lg + j][col], col = col0 + ocol
+    // consumer state: S[g][t][j] = S[16t + 4lg + j][colw + 16g + ln]
     const int64_t col0 = static_cast<int64_t>(vt) * VT;
-    const uint32_t ocol = static_cast<uint32_t>(16 * (consumer ? wave : 0) + kn.ln);
-    const int64_t col = col0 + ocol;
+    const int64_t colw = col0 + 16 * CG * (consumer ? wave : 0);
     const int64_t sbase = (kn.b * H + kn.h) * static_cast<int64_t>(K) * V;
     {
         const uint32_t eq = static_cast<uint32_t>(sizeof(TQ));
@@ -1101,31 +1234,54 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         // row lane / 4, columns 4 (lane % 4), of this wave's 16 columns
         const uint32_t vrow = sizeof(TQ) == 2 ? (kn.lane >> 1) : (kn.lane >> 2);
         const uint32_t vcol = sizeof(TQ) == 2 ? 8 * (kn.lane & 1) : 4 * (kn.lane & 3);
-        kn.vo_v = vrow * kn.rs_v + static_cast<uint32_t>(col0 + 16 * (consumer ? wave : 0) + vcol) * eq;
+        kn.vo_v = vrow * kn.rs_v + static_cast<uint32_t>(colw + vcol) * eq;
     }
 
     if (consumer) {
-        f4 S[KT];
-        load_state<KT>(S, a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + col, V);
-        uint32_t vr[NCH][KN::VW];
+        f4 S[CG][KT];
 #pragma unroll
-        for (int j = 0; j < NCH; ++j) kn.v_load(vr[j], j);
-        uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
-        const int64_t colw = col0 + 16 * (consumer ? wave : 0);
+        for (int g = 0; g < CG; ++g)
+            load_state<KT>(S[g], a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + colw + 16 * g + kn.ln, V);
+        uint32_t vr[NCH][CG][KN::VW];
+#pragma unroll
+        for (int j = 0; j < NCH; ++j)
+#pragma unroll
+            for (int g = 0; g < CG; ++g) kn.v_load(vr[j][g], j, g);
+        uint16_t (*vt)[CB * BT][16] = sm.vt[consumer ? wave : 0];
+        typename KN::Pend pd;
+        bool pending = false;
+        if constexpr (EPI) {
+#pragma unroll
+            for (int g = 0; g < CG; ++g)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kn.wn[g][j] = epi.weight[kn.h * V + colw + 16 * g + 4 * kn.lg + j];
+        }
         for (int s = -1; s < nss; ++s) {
 #pragma unroll
             for (int cj = 0; cj < NCH; ++cj) {
                 const int cc = NCH * s + cj;
+                if constexpr (EPI) {
+                    // the previous chunk's outputs, now that every wave's row
+                    // sums are in LDS (one barrier ago)
+                    if (pending) kn.finish(pd, colw, wave);
+                    pending = false;
+                }
                 if (s >= 0 && cc < ncc) {
                     // the checkpoint of chunk cc, for the backward
                     float* ck = ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K + 2 * CB * BT) * V
                                      : nullptr;
-                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, col0, ocol, colw, ck);
+                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, colw, ck, pd, wave);
+                    pending = EPI;
                 }
                 __syncthreads();
             }
         }
-        store_state<KT>(S, a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + col, V);
+        if constexpr (EPI) {
+            if (pending) kn.finish(pd, colw, wave);
+        }
+#pragma unroll
+        for (int g = 0; g < CG; ++g)
+            store_state<KT>(S[g], a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + colw + 16 * g + kn.ln, V);
     } else {
         const int p = wave - NC;
         if constexpr (GATED) {
@@ -1152,12 +1308,28 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     }
 }
 
-template <int K, int NC, typename TQ, bool GATED>
-int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
-    const int64_t blocks = a.B * a.H * (a.V / (16 * NC));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(64 * (NC + NB)), 0, stream, a, ckpt, gate);
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false>
+int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate,
+               const kda_out_epilogue& epi = kda_out_epilogue{}) {
+    const int64_t blocks = a.B * a.H * (a.V / (16 * NC * CG));
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(64 * (NC + NB)), 0, stream, a, ckpt, gate, epi);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
+}
+
+// The fused output epilogue: one workgroup per (b, h), 4 consumer waves of
+// V / 64 column groups.
+template <int K, typename TQ, bool GATED>
+int launch_epi(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate, const kda_out_epilogue& epi) {
+    if (a.V == 64) return launch_knq<K, 4, TQ, GATED, 1, true>(a, stream, nullptr, gate, epi);
+    if (a.V == 128) return launch_knq<K, 4, TQ, GATED, 2, true>(a, stream, nullptr, gate, epi);
+    return KDA_ERR_UNSUPPORTED;
+}
+template <typename TQ, bool GATED>
+int launch_epi_k(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate, const kda_out_epilogue& epi) {
+    if (a.K == 64) return launch_epi<64, TQ, GATED>(a, stream, gate, epi);
+    if (a.K == 128) return launch_epi<128, TQ, GATED>(a, stream, gate, epi);
+    return KDA_ERR_UNSUPPORTED;
 }
 
 // Columns per workgroup: the widest tile (64, 32 or 16 columns) that still
@@ -1219,6 +1391,26 @@ int chunkwise_check(const kda_fwd_args& a, bool gated) {
                     a.v_stride[1] < a.V || a.beta_stride[1] < 1))
         return KDA_ERR_UNSUPPORTED;
     return KDA_OK;
+}
+
+bool chunkwise_fused_supported(const kda_fwd_args& a) {
+    return (a.K == 64 || a.K == 128) && (a.V == 64 || a.V == 128) &&
+           (a.qkv_dtype == KDA_DTYPE_F16 || a.qkv_dtype == KDA_DTYPE_BF16);
+}
+
+int chunkwise_fused_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate,
+                           const kda_out_epilogue& epi) {
+    const int st = chunkwise_check(a, gate != nullptr);
+    if (st != KDA_OK) return st;
+    if (!chunkwise_fused_supported(a)) return KDA_ERR_UNSUPPORTED;
+    // the gate rows are read through one descriptor per block: rows may not overlap
+    if (epi.gate_stride[1] < a.H * a.V || epi.gate_stride[0] < 0 ||
+        (BT + 1) * epi.gate_stride[1] * 2 >= (int64_t(1) << 31))
+        return KDA_ERR_UNSUPPORTED;
+    const kda_gate_args g = gate ? *gate : kda_gate_args{nullptr, nullptr};
+    if (a.qkv_dtype == KDA_DTYPE_F16)
+        return gate ? launch_epi_k<_Float16, true>(a, stream, g, epi) : launch_epi_k<_Float16, false>(a, stream, g, epi);
+    return gate ? launch_epi_k<bf16_t, true>(a, stream, g, epi) : launch_epi_k<bf16_t, false>(a, stream, g, epi);
 }
 
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args* gate) {

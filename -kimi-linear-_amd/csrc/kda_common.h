@@ -88,6 +88,14 @@ template <> struct Elem<bf16_t> {
     static constexpr int code = KDA_DTYPE_BF16;
 };
 
+// x rounded to T and back: the value a T tensor would hold.
+template <typename T>
+__device__ __forceinline__ float round_elem(float x) {
+    if constexpr (Elem<T>::code == KDA_DTYPE_F32) return x;
+    else if constexpr (Elem<T>::code == KDA_DTYPE_F16) return static_cast<float>(static_cast<_Float16>(x));
+    else return bf16_bits_to_f32(f32_to_bf16_bits(x));
+}
+
 // Clamp to +-60000 keeping NaN (the comparisons are false for NaN).
 __device__ __forceinline__ float clamp_fp16_safe(float x) {
     return x > kFp16MaxSafe ? kFp16MaxSafe : (x < -kFp16MaxSafe ? -kFp16MaxSafe : x);
@@ -134,6 +142,22 @@ __device__ __forceinline__ float rowgroup_sum(float x) {
     x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
     // permlane16_swap(x, x) returns x of lane l & ~16 and of lane l | 16;
     // permlane32_swap likewise for bit 5: the sum of both is the pair sum
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return x;
+}
+
+// Sum of x over the 4 lanes that share l & 15 (all-reduce): the permlane
+// swaps of bits 4 and 5.
+__device__ __forceinline__ float lanegroup4_sum(float x) {
     {
         const unsigned u = __float_as_uint(x);
         const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);

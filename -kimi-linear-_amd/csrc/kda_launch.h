@@ -22,6 +22,10 @@ int chunkwise_check(const kda_fwd_args& a, bool gated = false);
 // with ckpt)
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr,
                      const kda_gate_args* gate = nullptr);
+// The chunkwise forward with the layer's output epilogue (kda_chunkwise_fused_fwd).
+bool chunkwise_fused_supported(const kda_fwd_args& a);
+int chunkwise_fused_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate,
+                           const kda_out_epilogue& epi);
 
 // Chunkwise backward (kda_chunkwise_bwd.hip).
 bool chunkwise_bwd_supported(int64_t K, int64_t V);

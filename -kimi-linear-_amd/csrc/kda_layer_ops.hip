@@ -69,7 +69,6 @@ __device__ __forceinline__ float round_to(float x) {
     return to_f(from_f<XT>(x));
 }
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
 
 // log(1 + x) for x in [0, 1] to about an ulp: with u = 1 + x rounded,
 // log(u) x / (u - 1) cancels the rounding of u (u == 1 when x is below half an
@@ -154,7 +153,7 @@ __device__ __forceinline__ void conv_unit(const kda_prep_args& a, int i, int64_t
 #pragma unroll
             for (int j = 0; j < kMaxConv; ++j)
                 if (j < cs) u = fmaf(w[j][c], win[t + j][c], u);
-            s[c] = u * sigmoid(u);
+            s[c] = u * sigmoid_f(u);
             ss = fmaf(s[c], s[c], ss);
         }
         if (i < 2) {
@@ -223,7 +222,7 @@ __device__ __forceinline__ void gate_unit(const kda_prep_args& a, int64_t b, int
         if (t < n) st<float, CPL>(g + t * D, o);
     }
     if (lane < n)
-        static_cast<float*>(a.beta)[(b * T + t0 + lane) * a.H + h] = sigmoid(decode_elem(rlogit, a.x_dtype));
+        static_cast<float*>(a.beta)[(b * T + t0 + lane) * a.H + h] = sigmoid_f(decode_elem(rlogit, a.x_dtype));
 }
 
 // One wave per (batch, tile, part, head), part 0..2 = q, k, v, 3 = gate
@@ -294,7 +293,7 @@ __global__ __launch_bounds__(256) void output_kernel(const kda_output_args a, ui
         const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(V) + a.eps);
         float y[CPL];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) y[c] = round_to<XT>((o[r][c] * rstd) * w[c]) * sigmoid(gt[r][c]);
+        for (int c = 0; c < CPL; ++c) y[c] = round_to<XT>((o[r][c] * rstd) * w[c]) * sigmoid_f(gt[r][c]);
         if (r < n) st<XT, CPL>(yp + r * a.H * V, y);
     }
 }

@@ -50,22 +50,6 @@ __device__ __forceinline__ float lanegroup8_sum(float x) {
     return x;
 }
 
-// Sum of x over the 4 lanes that share l & 15 (all-reduce): the permlane
-// swaps of bits 4 and 5.
-__device__ __forceinline__ float lanegroup4_sum(float x) {
-    {
-        const unsigned u = __float_as_uint(x);
-        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    {
-        const unsigned u = __float_as_uint(x);
-        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    return x;
-}
-
 // Lane l of a wave holds 4 adjacent state columns (column group l % CPL) of
 // RPL = K CPL / 64 adjacent rows (row group l / CPL); the K-reductions are
 // sums over the lanes of one column group.

@@ -88,12 +88,14 @@ def _strides3(x: torch.Tensor):
     return (ctypes.c_int64 * 3)(*x.stride()[:3])
 
 
-def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None, ckpt=False, gate=None):
+def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=None, ckpt=False, gate=None,
+             epilogue=None):
     """Shared forward.  ``ckpt=True`` (chunkwise, inside the autograd
     function) also returns the fp32 state before every 32-token chunk.
     ``gate=(a_log, dt_bias)``: g and beta are the gate's up-projection gk
     and the beta logits, and the kernels form the gates (the gated entry
-    points)."""
+    points).  ``epilogue=(og, weight, eps)`` (chunkwise): the output is the
+    layer's o_proj input y instead of o (kda_chunkwise_fused_fwd)."""
     for name, x in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
         _check_tensor(name, x)
     if state is not None:
@@ -154,6 +156,20 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
         if state_out.requires_grad and torch.is_grad_enabled():
             raise KdaError("state_out is written in place: it must not require grad under grad mode")
 
+    if epilogue is not None:
+        og, w_norm, eps = epilogue
+        _check_tensor("og", og)
+        _check_tensor("norm weight", w_norm)
+        if tuple(og.shape) != (B, T, H * V) or og.device != dev:
+            raise KdaError(f"og must be [B, T, H*V] = [{B}, {T}, {H * V}] on {dev}; got {tuple(og.shape)}")
+        if w_norm.numel() != H * V:
+            raise KdaError(f"the norm weight must be [H, V] = [{H}, {V}]; got {tuple(w_norm.shape)}")
+        if v.dtype not in (torch.float16, torch.bfloat16) or K not in (64, 128) or V not in (64, 128):
+            raise KdaError("the fused output epilogue takes fp16 / bf16 q, k, v and K, V in (64, 128)")
+        og = og.to(v.dtype)
+        if og.stride(-1) != 1 or (T > 1 and og.stride(1) < H * V):
+            og = og.contiguous()
+        epilogue = (og, w_norm.detach().reshape(H, V).to(torch.float32).contiguous(), float(eps))
     o = torch.empty(B, T, H, V, device=dev, dtype=out_dtype)
     s_out = state_out if state_out is not None else torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
     # per 32-token chunk: the state before it (K rows), then the chunk's R and P (32 rows each)
@@ -213,7 +229,18 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
     lib = _native.load()
     with torch.cuda.device(dev):
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        if gate is not None:
+        if epilogue is not None:
+            gargs = None
+            if gate is not None:
+                gargs = _native.KdaGateArgs()
+                gargs.a_log, gargs.dt_bias = gate[0].data_ptr(), gate[1].data_ptr()
+            eargs = _native.KdaOutEpilogue()
+            eargs.gate = epilogue[0].data_ptr()
+            eargs.gate_stride[0], eargs.gate_stride[1] = epilogue[0].stride(0), epilogue[0].stride(1)
+            eargs.weight, eargs.eps = epilogue[1].data_ptr(), epilogue[2]
+            status = lib.kda_chunkwise_fused_fwd(ctypes.byref(args), ctypes.byref(gargs) if gargs else None,
+                                                 ctypes.byref(eargs), stream)
+        elif gate is not None:
             gargs = _native.KdaGateArgs()
             gargs.a_log, gargs.dt_bias = gate[0].data_ptr(), gate[1].data_ptr()
             fn = lib.kda_chunkwise_gated_fwd if kind == "chunkwise" else lib.kda_recurrent_gated_fwd
@@ -225,7 +252,8 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
         else:
             status = lib.kda_recurrent_fwd(ctypes.byref(args), stream)
     if status != _native.STATUS_OK:
-        raise KdaError(f"kda_{kind}{'_gated' if gate is not None else ''}_fwd failed: {_native.status_str(status)} "
+        name = "fused" if epilogue is not None else ("gated" if gate is not None else "")
+        raise KdaError(f"kda_{kind}{'_' + name if name else ''}_fwd failed: {_native.status_str(status)} "
                        f"(B={B}, T={T}, H={H}, K={K}, V={V})")
     if kernel_s_dtype != s_dtype:
         s_out = s_out.to(s_dtype)
@@ -359,3 +387,22 @@ def kda_recurrent_gated(q, k, v, gk, beta_logit, a_log, dt_bias, state=None, sta
     """``kda_recurrent`` with the fused gate of :func:`kda_chunkwise_gated`
     (gate inputs in any float dtype).  ``state_out`` as in ``kda_recurrent``."""
     return _forward("recurrent", q, k, v, gk, beta_logit, state, 0, state_dtype, state_out, gate=(a_log, dt_bias))
+
+
+def kda_chunkwise_fused(q, k, v, gk, beta_logit, a_log, dt_bias, og, norm_weight, eps, initial_state=None,
+                        chunk_size=64, state_dtype=None):
+    """:func:`kda_chunkwise_gated` with the KDA layer's output epilogue on the
+    kernel's output tile (no counterpart function in the reference; it
+    computes what ``_output`` does before ``o_proj``, ``kimi_linear/kda.py:
+    258-279, 464-470``): ``y = x(x(rmsnorm(x(o)) * norm_weight) * sigmoid(og))``
+    with x() the rounding to the activation dtype, as the reference's
+    HeadwiseRMSNorm and output gate round.
+
+    ``og: [B, T, H*V]`` (the output gate's up-projection), ``norm_weight:
+    [H, V]``.  fp16 / bf16 q, k, v; K and V in (64, 128).  Forward only.
+    Returns ``(y [B, T, H*V] in v.dtype, state)``.
+    """
+    o, s = _forward("chunkwise", q, k, v, gk, beta_logit, initial_state, int(chunk_size), state_dtype,
+                    gate=(a_log, dt_bias), epilogue=(og, norm_weight, eps))
+    B, T, H, V = o.shape
+    return o.view(B, T, H * V), s

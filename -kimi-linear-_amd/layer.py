@@ -29,7 +29,15 @@ Semantics kept from the reference:
 * state dtype (``kda.py:392-396``): an fp32 recurrent state when x is fp16 or
   bf16, else the kernel default (v.dtype).
 * ``_output`` (``kda.py:464-470``): head-wise RMSNorm, sigmoid output gate in
-  fp32, output projection.
+  fp32, output projection.  When the whole call is one chunkwise body (T a
+  multiple of the chunk size, fp16/bf16 activations, K and V in {64, 128}),
+  the norm and the gate can run on the chunk kernel's output tile
+  (``kda_chunkwise_fused``: one workgroup per head, the core output never
+  written).  ``fuse_output`` chooses: True, False, or None (default) for the
+  faster of the two as measured -- fused when B H V / 64 exceeds the 256 CUs
+  (the split kernel would need a second round of workgroups: 265 against
+  450 us at B=16 T=2048 H=16 d=128), split otherwise (206 against 249 us
+  at B=4).
 """
 
 from __future__ import annotations
@@ -39,7 +47,7 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 
-from .kda import kda_chunkwise_gated, kda_recurrent_gated
+from .kda import kda_chunkwise_fused, kda_chunkwise_gated, kda_recurrent_gated
 from .layer_ops import kda_output, kda_prep
 
 
@@ -117,6 +125,7 @@ class KimiDeltaAttention(nn.Module):
         self.fp32_recurrent_state = True
         self._wcat = None          # (key, weight, bias) of the fused input projection
         self._gcat = None          # (key, A_log, dt_bias) in fp32 for the gated core
+        self.fuse_output = None    # output epilogue in the chunk kernel: True, False, None = by shape
 
     def _input_mods(self):
         return (self.in_proj_q, self.in_proj_k, self.in_proj_v, self.beta_proj, self.gk_proj[0], self.og_proj[0])
@@ -189,6 +198,18 @@ class KimiDeltaAttention(nn.Module):
                 d = self.dt_bias.detach().to(torch.float32).clone().contiguous()
         self._gcat = (key, a, d)
         return a, d
+
+    def _fused_output_ok(self, x):
+        if self.fuse_output is False:
+            return False
+        ok = (x.dtype in (torch.float16, torch.bfloat16) and self.head_dim in (64, 128)
+              and self.value_head_dim in (64, 128))
+        if self.fuse_output is None:
+            # the split kernel runs B H V / 64 workgroups of 64 columns at
+            # most; the fused one B H, each somewhat slower: it pays when the
+            # split one needs more than one round on the 256 CUs
+            ok = ok and x.shape[0] * self.num_heads * (self.value_head_dim // 64) > 256
+        return ok
 
     def _state_dtype(self, x):
         if self.fp32_recurrent_state and x.dtype in (torch.float16, torch.bfloat16):
@@ -272,12 +293,22 @@ class KimiDeltaAttention(nn.Module):
         gate = self._gate_params()      # g, beta above: gk and the beta logits
         B, T = x.shape[0], x.shape[1]
         sdtype = self._state_dtype(x)
+        C = self.chunk_size
+        if 0 < T < C:
+            C = T
+        if not (use_cache and T == 1) and T > 0 and T % C == 0 and self._fused_output_ok(x):
+            # one chunkwise body and no tail: the output epilogue runs on the
+            # chunk kernel's tiles and its result is the o_proj input
+            og = self.og_proj[1](og_low)
+            y, new_rec = kda_chunkwise_fused(q, k, v, g, beta, *gate, og, self.g_norm.weight, self.g_norm.eps,
+                                             initial_state=rec, chunk_size=C, state_dtype=sdtype)
+            out = self.o_proj(y)
+            if use_cache:
+                return out, {"conv": new_conv, "recurrent": new_rec}
+            return out
         if use_cache and T == 1:
             o_core, new_rec = kda_recurrent_gated(q, k, v, g, beta, *gate, state=rec, state_dtype=sdtype)
         else:
-            C = self.chunk_size
-            if 0 < T < C:
-                C = T
             rem = T % C
             body = T - rem
             # every position is written by the body or the tail (the reference

@@ -16,6 +16,8 @@ Also reported on the same line:
 * ``gated``: ``kda_chunkwise_gated`` at the same shape -- the layer's gate
   pre-processing formed in the kernel's loads from fp16 gk and beta logits
   (1282 instead of 1540 algorithmic bytes per token and head);
+* ``long_context``: ``kda_chunkwise`` on one long sequence, B=1 T=32768 H=16
+  (fp32 initial state, strong decay): 16 chains of 512 chunks each;
 * ``layer``: the whole KDA layer at hidden 2048 (projections, short
   convolutions, norms and gates around the core): a B=4 T=2048 prefill and a
   graph-replayed B=64 decode token;
@@ -66,7 +68,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--decode-variant", choices=["all", "fresh", "in_place", "fresh_rot5", "in_place_rot5"],
                    default="all", help="with --only decode: time one variant (for kernel traces)")
-    p.add_argument("--only", choices=["chunkwise", "gated", "decode", "layer", "backward", "copy"], default=None,
+    p.add_argument("--only", choices=["chunkwise", "gated", "long", "decode", "layer", "backward", "copy"],
+                   default=None,
                    help="run one workload only (for profiling); 'copy' runs a plain 1 GiB "
                         "device copy used to calibrate the HBM byte counters")
     return p.parse_args()
@@ -126,6 +129,32 @@ def gated_bench(pkg, wl, torch, steps, warmup):
             e1.record(stream)
         torch.cuda.synchronize()
     return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+
+
+def long_context_bench(pkg, wl, torch, reps=3):
+    """kda_chunkwise at B=1 T=32768 H=16 dk=dv=128 (fp16 q/k/v, fp32 g/beta,
+    A_log ~ U(log 4, log 64), fp32 S0 ~ N(0, 0.02)); mean launch time in ms."""
+    import math
+    B3, T3 = 1, 32768
+    inp = wl.make_inputs(B3, T3, H1, D1, D1, device="cuda", seed=3, qkv_dtype=torch.float16,
+                         a_log_range=(math.log(4.0), math.log(64.0)), state_std=0.02)
+    args = (inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"])
+    with torch.no_grad():
+        for _ in range(2):
+            pkg.kda_chunkwise(*args, initial_state=inp["state"], chunk_size=C1, state_dtype=torch.float32)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            pkg.kda_chunkwise(*args, initial_state=inp["state"], chunk_size=C1, state_dtype=torch.float32)
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = B3 * T3 * H1 * 1540 + 2 * B3 * H1 * D1 * D1 * 4
+    return {"workload": "kda_chunkwise, B=1 T=32768 H=16 dk=dv=128 chunk_size=64; fp16 q/k/v, fp32 g/beta "
+                        "(A_log ~ U(log 4, log 64)), fp32 S0 ~ N(0, 0.02)",
+            "ms": ms, "tokens_per_s": B3 * T3 / (ms * 1e-3), "algorithmic_bytes": nbytes,
+            "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
 def decode_bench(pkg, wl, torch, n_sets, in_place=False):
@@ -232,6 +261,19 @@ def layer_bench(pkg, torch, reps=10):
         e1.record()
         torch.cuda.synchronize()
         prefill_ms = e0.elapsed_time(e1) / reps
+        # a larger batch: 256 heads, where the layer runs the output epilogue
+        # inside the chunk kernel (one workgroup per head)
+        xb = torch.randn(16, 2048, 2048, device="cuda", dtype=torch.float16)
+        for _ in range(2):
+            layer(xb)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps // 2):
+            layer(xb)
+        e1.record()
+        torch.cuda.synchronize()
+        prefill16_ms = e0.elapsed_time(e1) / (reps // 2)
+        del xb
         dec = KdaGraphedDecoder([layer])
         xd = torch.randn(64, 17, 2048, device="cuda", dtype=torch.float16)
         dec.prefill(xd[:, :16])
@@ -249,6 +291,8 @@ def layer_bench(pkg, torch, reps=10):
     return {"workload": "KimiDeltaAttention hidden 2048, 16 heads x 128, fp16 weights, fp32 state",
             "prefill_B4_T2048_ms": prefill_ms,
             "prefill_tokens_per_s": 4 * 2048 / (prefill_ms * 1e-3),
+            "prefill_B16_T2048_ms": prefill16_ms,
+            "prefill_B16_tokens_per_s": 16 * 2048 / (prefill16_ms * 1e-3),
             "decode_B64_graph_us_per_token": decode_us}
 
 
@@ -407,6 +451,11 @@ def main():
             "hbm_frac": GATED_BYTES / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         if "value" not in result:
             result.update({"value": B1 * T1 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms})
+    if args.only in (None, "long"):
+        result["long_context"] = long_context_bench(pkg, wl, torch)
+        if "value" not in result:
+            result.update({"value": result["long_context"]["tokens_per_s"], "unit": "tokens/s",
+                           "ms_per_step": result["long_context"]["ms"]})
     if args.only in (None, "layer"):
         result["layer"] = layer_bench(pkg, torch)
         if "value" not in result:

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 8
+#define KDA_ABI_VERSION 9
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -141,6 +141,29 @@ int kda_chunkwise_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate,
  * kda_recurrent, kda.py:188-219); gk and the logits in any dtype.  In place
  * (state_out == state_in) as kda_recurrent_fwd. */
 int kda_recurrent_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate, void* stream);
+
+/* The layer's output epilogue -- HeadwiseRMSNorm and the sigmoid output gate
+ * of _output (kimi_linear/kda.py:258-279, 464-470) -- applied by the
+ * chunkwise kernel to its output tile before anything is written:
+ *   n = TQ(TQ(o) * rsqrt(mean over V of TQ(o)^2 + eps) * weight[h])
+ *   y = TQ(n * sigmoid(gate))
+ * (TQ: rounded to the dtype of q, k, v, as the reference's o_core and norm
+ * output are); args->o receives y, [B, T, H, V] = the o_proj input
+ * [B, T, H*V]. */
+typedef struct kda_out_epilogue {
+    const void* gate;              /* [B, T, H*V] output-gate up-projection, qkv dtype */
+    int64_t gate_stride[2];        /* (batch, token) strides in elements; channels contiguous */
+    const float* weight;           /* [H, V] contiguous fp32 (the norm weight) */
+    float eps;
+} kda_out_epilogue;
+
+/* kda_chunkwise_gated_fwd (gate != NULL) or kda_chunkwise_fwd (gate == NULL)
+ * with the output epilogue: one workgroup holds a head's whole V row.  q, k, v
+ * fp16 or bf16, K in {64, 128}, V in {64, 128} (KDA_ERR_UNSUPPORTED
+ * otherwise).  The rest of the layer's forward around the core is
+ * kda_prep_fwd before and the o_proj GEMM after. */
+int kda_chunkwise_fused_fwd(const kda_fwd_args* args, const kda_gate_args* gate, const kda_out_epilogue* out,
+                            void* stream);
 
 /* ---------------------------------------------------------------------------
  * Backward of the chunkwise forward.  The reference differentiates

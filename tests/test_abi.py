@@ -51,7 +51,8 @@ def test_abi_version_and_status_strings(native):
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 @pytest.mark.parametrize("struct,cname", [("KdaFwdArgs", "kda_fwd_args"), ("KdaBwdArgs", "kda_bwd_args"),
-                                          ("KdaGateArgs", "kda_gate_args"), ("KdaPrepArgs", "kda_prep_args"),
+                                          ("KdaGateArgs", "kda_gate_args"), ("KdaOutEpilogue", "kda_out_epilogue"),
+                                          ("KdaPrepArgs", "kda_prep_args"),
                                           ("KdaOutputArgs", "kda_output_args")])
 def test_struct_layout_matches_header(native, tmp_path, struct, cname):
     cls = getattr(native, struct)
@@ -154,6 +155,28 @@ def test_gated_host_validation_codes(native, fn):
         assert call(ctypes.byref(bad), ctypes.byref(gate), None) == 3
         bad = _args(native, qkv_dtype=native.DTYPE_BF16, g_dtype=native.DTYPE_BF16, beta_dtype=native.DTYPE_F32)
         assert call(ctypes.byref(bad), ctypes.byref(gate), None) == 3
+
+
+def test_fused_host_validation_codes(native):
+    lib = native.load()
+    call = lib.kda_chunkwise_fused_fwd
+    gate = native.KdaGateArgs()
+    gate.a_log, gate.dt_bias = 0x200000, 0x300000      # never dereferenced
+    out = native.KdaOutEpilogue()
+    out.gate, out.weight, out.eps = 0x400000, 0x500000, 1e-6
+    out.gate_stride[0], out.gate_stride[1] = 16 * 64, 64
+    f16 = dict(qkv_dtype=native.DTYPE_F16, g_dtype=native.DTYPE_F16, beta_dtype=native.DTYPE_F16)
+    assert call(ctypes.byref(_args(native, **f16)), ctypes.byref(gate), None, None) == 1      # no epilogue
+    assert call(ctypes.byref(_args(native)), ctypes.byref(gate), ctypes.byref(out), None) == 4  # fp32: no kernel
+    assert call(ctypes.byref(_args(native, V=96, **f16)), ctypes.byref(gate), ctypes.byref(out), None) == 4
+    assert call(ctypes.byref(_args(native, T=20, **f16)), ctypes.byref(gate), ctypes.byref(out), None) == 2
+    bad = native.KdaOutEpilogue()
+    bad.gate, bad.weight, bad.eps = 0x400000, 0x500000, -1.0
+    assert call(ctypes.byref(_args(native, **f16)), ctypes.byref(gate), ctypes.byref(bad), None) == 2
+    nog = native.KdaOutEpilogue()
+    nog.eps = 1e-6
+    assert call(ctypes.byref(_args(native, **f16)), ctypes.byref(gate), ctypes.byref(nog), None) == 1
+    assert call(ctypes.byref(_args(native, B=0, **f16)), ctypes.byref(gate), ctypes.byref(out), None) == 0
 
 
 def test_in_place_state_contract(native):

@@ -192,3 +192,34 @@ def test_gated_decay_over_the_whole_gate_range(kda_pkg, path):
     print(f"{path}: {int(live.sum())} live channels, max error / bound {ratio:.2f}", flush=True)
     assert ratio <= 1.0, ratio
     assert (got[~live] <= 1e-30).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K,V,T", [(128, 128, 192), (64, 64, 128), (128, 64, 100), (64, 128, 64)])
+def test_chunkwise_fused_matches_gated_plus_output_kernel(kda_pkg, dtype, K, V, T):
+    """The output epilogue on the chunk kernel's tiles (one workgroup per head,
+    4 consumer waves of V / 64 column groups) against the gated chunk kernel
+    followed by the separate output kernel: the state bit for bit (same
+    arithmetic per column), y within an output ulp or two (the row sums of
+    squares are added in another order)."""
+    import importlib
+    ops = importlib.import_module("kimi_linear_amd.layer_ops")
+    B, H = 2, 3
+    inp = make(B, T, H, K, V, dtype, seed=9, state_std=0.05)
+    d = dev(inp)
+    gen = torch.Generator().manual_seed(10)
+    og = torch.randn(B, T, H * V, generator=gen).to(dtype).to(DEV)
+    w = (1 + 0.1 * torch.randn(H, V, generator=gen)).to(DEV)
+    C = 64 if T % 64 == 0 else T
+    with torch.no_grad():
+        y, s1 = kda_pkg.kda_chunkwise_fused(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                            og, w, 1e-5, initial_state=d["state"], chunk_size=C,
+                                            state_dtype=torch.float32)
+        o, s2 = kda_pkg.kda_chunkwise_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                            initial_state=d["state"], chunk_size=C, state_dtype=torch.float32)
+        y_ref = ops.kda_output(o, og, w, 1e-5)
+    assert torch.equal(s1, s2)
+    err = ((y.double() - y_ref.double()).abs() / y_ref.double().abs().clamp(min=1.0)).max().item()
+    tol = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
+    print(f"fused epilogue {dtype} K={K} V={V} T={T}: y err {err:.2e}", flush=True)
+    assert err <= tol, err

@@ -157,3 +157,26 @@ def test_layer_config4_full_shape(kda_pkg):
     es = rel(st["recurrent"][sel], st_ref["recurrent"])
     print(f"[layer config 4] out rel {e:.3e} state rel {es:.3e}", flush=True)
     assert e <= TOL[torch.float16] and es <= TOL[torch.float16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd,T", [(128, 128), (64, 192), (128, 40)])
+def test_layer_fused_output_vs_oracle(kda_pkg, dtype, hd, T):
+    """The output epilogue on the chunk kernel's tiles (fuse_output=True: one
+    workgroup per head) against the oracle, and against the same layer run
+    with the split kernels (fuse_output=False), state included."""
+    m, cfg, p = make_layer(kda_pkg, dtype, seed=21, head_dim=hd, value_head_dim=hd, num_heads=2, hidden_size=256)
+    x = make_x(2, T, 256, dtype, seed=22)
+    with torch.no_grad():
+        m.fuse_output = True
+        out_f, st_f = m(x.to(DEV), use_cache=True)
+        m.fuse_output = False
+        out_s, st_s = m(x.to(DEV), use_cache=True)
+    ref, st_ref = kda_layer_ref(p, cfg, x, use_cache=True)
+    e, es = rel(out_f, ref), rel(st_f["recurrent"], st_ref["recurrent"])
+    ed = rel(out_f, out_s)
+    print(f"[layer fused output {dtype} d={hd} T={T}] out rel {e:.2e} state rel {es:.2e} vs split {ed:.2e}",
+          flush=True)
+    assert e <= TOL[dtype] and es <= TOL[dtype]
+    assert torch.equal(st_f["recurrent"], st_s["recurrent"])
+    assert ed <= TOL[dtype] / 4
