@@ -1332,12 +1332,20 @@ int launch_epi_k(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args&
     return KDA_ERR_UNSUPPORTED;
 }
 
-// Columns per workgroup: the widest tile (64, 32 or 16 columns) that still
-// gives at least one workgroup per CU; 16 when none does (few chains).
+// Columns per workgroup: 128 when 64-column tiles outnumber the CUs, else
+// the widest tile (64, 32 or 16 columns) that still gives at least one
+// workgroup per CU; 16 when none does (few chains).
 template <int K, typename TQ, bool GATED>
 int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
     constexpr int64_t kCus = 256;
     const int64_t heads = a.B * a.H;
+    // More 64-column tiles than CUs: 128-column workgroups (consumer waves of
+    // two 16-column groups), whose ~20 % longer superstep beats a second
+    // round of workgroups (measured 265 against 450 us at B=16 T=2048 H=16
+    // d=128).  16-bit inputs only (the fp32 instantiation serves checkpoints).
+    if constexpr (sizeof(TQ) == 2) {
+        if (a.V % 128 == 0 && heads * (a.V / 64) > kCus) return launch_knq<K, 4, TQ, GATED, 2>(a, stream, ckpt, gate);
+    }
     if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ, GATED>(a, stream, ckpt, gate);
     if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ, GATED>(a, stream, ckpt, gate);
     return launch_knq<K, 1, TQ, GATED>(a, stream, ckpt, gate);

@@ -35,9 +35,8 @@ Semantics kept from the reference:
   (``kda_chunkwise_fused``: one workgroup per head, the core output never
   written).  ``fuse_output`` chooses: True, False, or None (default) for the
   faster of the two as measured -- fused when B H V / 64 exceeds the 256 CUs
-  (the split kernel would need a second round of workgroups: 265 against
-  450 us at B=16 T=2048 H=16 d=128), split otherwise (206 against 249 us
-  at B=4).
+  (265 against 294 us at B=16 T=2048 H=16 d=128), split otherwise (201
+  against 250 us at B=4).
 """
 
 from __future__ import annotations

@@ -180,6 +180,28 @@ def test_chunkwise_mid_head_counts(kda_pkg, wl, B, H, T):
     assert eo <= O_TOL and es <= S_TOL
 
 
+@pytest.mark.parametrize("K,dtype", [(128, torch.float16), (64, torch.bfloat16), (32, torch.float16)])
+def test_chunkwise_many_heads_wide_tiles(kda_pkg, wl, K, dtype):
+    """More 64-column tiles than CUs (3 x 64 heads x V=128): 128-column
+    workgroups whose consumer waves own two 16-column groups.  Every column's
+    arithmetic is the narrower kernel's, so one sequence run alone (64 heads,
+    64-column tiles) must give the same bits; two heads are checked against
+    the oracle."""
+    B, T, H, V = 3, 96, 64, 128
+    print(f"chunkwise wide tiles B={B} H={H} T={T} K={K} V={V} {dtype}", flush=True)
+    inp = to_dev(wl.make_inputs(B, T, H, K, V, seed=K, qkv_dtype=dtype, state_std=0.02))
+    o, s = run_chunkwise(kda_pkg, inp, 32)
+    one = {n: (t[1:2] if t is not None else None) for n, t in inp.items()}
+    o1, s1 = run_chunkwise(kda_pkg, one, 32)
+    assert torch.equal(o[1:2], o1) and torch.equal(s[1:2], s1)
+    sub = to_cpu(wl.slice_heads(inp, slice(2, 3), slice(5, 64, 50)))
+    o_ref, s_ref = ref_chunkwise(sub, 32)
+    eo, es = max_abs(o[2:3, :, 5:64:50], o_ref), rel(s[2:3, 5:64:50], s_ref)
+    report(f"wide tiles K={K} {dtype}", eo, es)
+    tol = 1 if dtype == torch.float16 else 8       # bf16 carries 3 fewer mantissa bits
+    assert eo <= tol * O_TOL and es <= tol * S_TOL
+
+
 @pytest.mark.parametrize("V", [128, 256])
 def test_recurrent_k256(kda_pkg, wl, V):
     """Head dim K = 256 (16 state columns a wave): fp32 recurrence vs the oracle."""
