@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -110,6 +110,7 @@ class KdaOutputArgs(ctypes.Structure):
 
 EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_chunkwise_fwd_ckpt",
                     "kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd", "kda_chunkwise_fused_fwd",
+                    "kda_chunkwise_long_fwd", "kda_chunkwise_long_workspace_size",
                     "kda_chunkwise_bwd",
                     "kda_chunkwise_bwd_workspace_size", "kda_chunkwise_bwd_noalloc",
                     "kda_prep_fwd", "kda_output_fwd", "kda_status_str", "kda_abi_version")
@@ -148,6 +149,11 @@ def load() -> ctypes.CDLL:
         for name in ("kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd"):
             getattr(lib, name).argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.POINTER(KdaGateArgs), ctypes.c_void_p]
             getattr(lib, name).restype = ctypes.c_int
+        lib.kda_chunkwise_long_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.c_int64, ctypes.c_void_p,
+                                               ctypes.c_void_p]
+        lib.kda_chunkwise_long_fwd.restype = ctypes.c_int
+        lib.kda_chunkwise_long_workspace_size.argtypes = [ctypes.c_int64] * 6
+        lib.kda_chunkwise_long_workspace_size.restype = ctypes.c_size_t
         lib.kda_chunkwise_fused_fwd.argtypes = [ctypes.POINTER(KdaFwdArgs), ctypes.POINTER(KdaGateArgs),
                                                 ctypes.POINTER(KdaOutEpilogue), ctypes.c_void_p]
         lib.kda_chunkwise_fused_fwd.restype = ctypes.c_int

@@ -122,6 +122,30 @@ int kda_chunkwise_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate,
     return chunkwise_entry(args, nullptr, gate, stream);
 }
 
+size_t kda_chunkwise_long_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t segments) {
+    if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0 || segments < 1) return 0;
+    if (B * H > (int64_t{1} << 31) || K > 4096 || V > 4096 || segments > (int64_t{1} << 20)) return 0;
+    return static_cast<size_t>(kda::long_workspace_bytes(B, H, K, V, segments));
+}
+
+int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* workspace, void* stream) {
+    if (segments == 1) return chunkwise_entry(args, nullptr, nullptr, stream);
+    const int st = validate_common(args, false);
+    if (st != KDA_OK) return st;
+    if (segments < 1) return KDA_ERR_BAD_SHAPE;
+    if (args->chunk_size <= 0 || args->T % args->chunk_size != 0 || args->T % segments != 0) return KDA_ERR_BAD_SHAPE;
+    if (!kda::chunkwise_trans_supported(*args)) return KDA_ERR_UNSUPPORTED;
+    if (args->B == 0 || args->H == 0) return KDA_OK;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (args->T == 0) return kda::recurrent_launch(*args, s);
+    if (workspace == nullptr) return KDA_ERR_NULL_POINTER;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 15) != 0) return KDA_ERR_BAD_SHAPE;
+    if (args->B * segments * args->H * ((args->V + args->K) / 16) > INT32_MAX) return KDA_ERR_BAD_SHAPE;
+    const int chk = kda::chunkwise_check(*args);
+    if (chk != KDA_OK) return chk;
+    return kda::long_launch(*args, segments, workspace, s);
+}
+
 int kda_chunkwise_fused_fwd(const kda_fwd_args* args, const kda_gate_args* gate, const kda_out_epilogue* out,
                             void* stream) {
     const int st = validate_common(args, false);

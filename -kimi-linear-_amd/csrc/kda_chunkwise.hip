@@ -403,7 +403,11 @@ __device__ __forceinline__ f4 mm_f32(const f4& xt, const f4& y, f4 c) {
 // CG: 16-column groups per consumer wave; EPI: the output epilogue (the
 // layer's head-wise RMSNorm and sigmoid output gate) on the o tile, which
 // needs a head's whole V row in one workgroup (16 NC CG == V).
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false>
+// TRANS: the first pass of a split long sequence (kda_chunkwise_long_fwd):
+// state columns V .. V + K carry the chain's transition -- they start from
+// the identity and see v = 0 -- beside the V columns of its own state from
+// zero; no o is written.
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false>
 struct Kern {
     static constexpr int KT = K / 16;                   // 16-row state tiles
     static constexpr int KU = K / 32;                   // 32-wide k blocks
@@ -903,7 +907,13 @@ struct Kern {
     // lane / 4 and 16 + lane / 4, 4 columns a lane), one 16-byte buffer load
     // per lane and row set; rows past T read as zero.
     static constexpr int VW = sizeof(TQ) == 2 ? 4 : 8;
+    bool vzero = false;                      // TRANS: this wave's columns read v = 0
     __device__ void v_load(uint32_t (&vr)[VW], int chunk, int grp) const {
+        if (TRANS && vzero) {
+#pragma unroll
+            for (int i = 0; i < VW; ++i) vr[i] = 0u;
+            return;
+        }
         const int blk = CB * chunk;
         const int64_t e = b * a.v_stride[0] + static_cast<int64_t>(blk) * BT * a.v_stride[1] + h * a.v_stride[2];
         const int left = rows_in(blk) + rows_in(blk + 1);
@@ -1138,7 +1148,7 @@ struct Kern {
                 if (lg == 0) sm.rows.p[par][bk][ln][wave] = ss;
             }
             pd.blk = blk;
-        } else {
+        } else if constexpr (!TRANS) {
 #pragma unroll
             for (int g = 0; g < CG; ++g) {
                 store_row4(O[g][0], blk, colw + 16 * g);
@@ -1170,11 +1180,11 @@ struct Kern {
 // barriers; every prefetch is issued unconditionally (a block past T loads
 // zeros).  The chunks cover T rounded up to whole chunks: a padded block
 // (all rows past T) is neutral and is built like any other.
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false>
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false>
 __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt,
                                                                    const kda_gate_args gate,
                                                                    const kda_out_epilogue epi) {
-    using KN = Kern<K, NC, TQ, GATED, CG, EPI>;
+    using KN = Kern<K, NC, TQ, GATED, CG, EPI, TRANS>;
     constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
     __shared__ Smem<K, CG, EPI> sm;
@@ -1187,7 +1197,8 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     }
 
     const int64_t H = a.H, V = a.V;
-    const int nvt = static_cast<int>(V / VT);
+    const int64_t VS = V + (TRANS ? K : 0);             // state columns
+    const int nvt = static_cast<int>(VS / VT);
     // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs, so
     // renumber them to put consecutive logical workgroups -- the V-tiles of
     // one head, which all read the head's q, k and g -- on one XCD and its L2.
@@ -1216,7 +1227,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     // consumer state: S[g][t][j] = S[16t + 4lg + j][colw + 16g + ln]
     const int64_t col0 = static_cast<int64_t>(vt) * VT;
     const int64_t colw = col0 + 16 * CG * (consumer ? wave : 0);
-    const int64_t sbase = (kn.b * H + kn.h) * static_cast<int64_t>(K) * V;
+    const int64_t sbase = (kn.b * H + kn.h) * static_cast<int64_t>(K) * VS;
     {
         const uint32_t eq = static_cast<uint32_t>(sizeof(TQ));
         kn.rs_q = static_cast<uint32_t>(a.q_stride[1]) * eq;
@@ -1239,9 +1250,21 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
 
     if (consumer) {
         f4 S[CG][KT];
+        if constexpr (TRANS) {
+            // the chain's own state from zero; the transition columns from the identity
+            kn.vzero = colw >= V;
 #pragma unroll
-        for (int g = 0; g < CG; ++g)
-            load_state<KT>(S[g], a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + colw + 16 * g + kn.ln, V);
+            for (int g = 0; g < CG; ++g)
+#pragma unroll
+                for (int t = 0; t < KT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        S[g][t][j] = kn.vzero && 16 * t + 4 * kn.lg + j == colw - V + 16 * g + kn.ln ? 1.f : 0.f;
+        } else {
+#pragma unroll
+            for (int g = 0; g < CG; ++g)
+                load_state<KT>(S[g], a.state_in, a.state_in_dtype, sbase + (4 * kn.lg) * V + colw + 16 * g + kn.ln, V);
+        }
         uint32_t vr[NCH][CG][KN::VW];
 #pragma unroll
         for (int j = 0; j < NCH; ++j)
@@ -1281,7 +1304,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         }
 #pragma unroll
         for (int g = 0; g < CG; ++g)
-            store_state<KT>(S[g], a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * V + colw + 16 * g + kn.ln, V);
+            store_state<KT>(S[g], a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * VS + colw + 16 * g + kn.ln, VS);
     } else {
         const int p = wave - NC;
         if constexpr (GATED) {
@@ -1308,13 +1331,24 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     }
 }
 
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false>
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false>
 int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate,
                const kda_out_epilogue& epi = kda_out_epilogue{}) {
-    const int64_t blocks = a.B * a.H * (a.V / (16 * NC * CG));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI>), dim3(static_cast<unsigned>(blocks)),
+    const int64_t blocks = a.B * a.H * ((a.V + (TRANS ? K : 0)) / (16 * NC * CG));
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI, TRANS>), dim3(static_cast<unsigned>(blocks)),
                        dim3(64 * (NC + NB)), 0, stream, a, ckpt, gate, epi);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
+}
+
+// The first pass of a split long sequence: 64-column tiles over the V state
+// columns and the K transition columns (128-column tiles when they would
+// outnumber the CUs).
+template <int K, typename TQ>
+int launch_trans(const kda_fwd_args& a, hipStream_t stream) {
+    const kda_gate_args none{nullptr, nullptr};
+    if (a.B * a.H * ((a.V + K) / 64) > 256 && (a.V + K) % 128 == 0)
+        return launch_knq<K, 4, TQ, false, 2, false, true>(a, stream, nullptr, none);
+    return launch_knq<K, 4, TQ, false, 1, false, true>(a, stream, nullptr, none);
 }
 
 // The fused output epilogue: one workgroup per (b, h), 4 consumer waves of
@@ -1419,6 +1453,20 @@ int chunkwise_fused_launch(const kda_fwd_args& a, hipStream_t stream, const kda_
     if (a.qkv_dtype == KDA_DTYPE_F16)
         return gate ? launch_epi_k<_Float16, true>(a, stream, g, epi) : launch_epi_k<_Float16, false>(a, stream, g, epi);
     return gate ? launch_epi_k<bf16_t, true>(a, stream, g, epi) : launch_epi_k<bf16_t, false>(a, stream, g, epi);
+}
+
+bool chunkwise_trans_supported(const kda_fwd_args& a) {
+    return (a.K == 64 || a.K == 128) && a.V % 64 == 0 &&
+           (a.qkv_dtype == KDA_DTYPE_F16 || a.qkv_dtype == KDA_DTYPE_BF16);
+}
+
+int chunkwise_trans_launch(const kda_fwd_args& a, hipStream_t stream) {
+    const int st = chunkwise_check(a, false);
+    if (st != KDA_OK) return st;
+    if (!chunkwise_trans_supported(a)) return KDA_ERR_UNSUPPORTED;
+    if (a.qkv_dtype == KDA_DTYPE_F16)
+        return a.K == 64 ? launch_trans<64, _Float16>(a, stream) : launch_trans<128, _Float16>(a, stream);
+    return a.K == 64 ? launch_trans<64, bf16_t>(a, stream) : launch_trans<128, bf16_t>(a, stream);
 }
 
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args* gate) {

@@ -22,10 +22,19 @@ int chunkwise_check(const kda_fwd_args& a, bool gated = false);
 // with ckpt)
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr,
                      const kda_gate_args* gate = nullptr);
+// The first pass of a split long sequence (kda_chunkwise_long_fwd): per chain
+// the state from zero and the transition, state_out [B, H, K, V + K] fp32.
+bool chunkwise_trans_supported(const kda_fwd_args& a);
+int chunkwise_trans_launch(const kda_fwd_args& a, hipStream_t stream);
 // The chunkwise forward with the layer's output epilogue (kda_chunkwise_fused_fwd).
 bool chunkwise_fused_supported(const kda_fwd_args& a);
 int chunkwise_fused_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate,
                            const kda_out_epilogue& epi);
+
+// Long sequences split into segments (kda_long.hip): workspace bytes for P
+// segments, and the three passes (T % P == 0, checked by the caller).
+int64_t long_workspace_bytes(int64_t B, int64_t H, int64_t K, int64_t V, int64_t P);
+int long_launch(const kda_fwd_args& a, int64_t P, void* workspace, hipStream_t stream);
 
 // Chunkwise backward (kda_chunkwise_bwd.hip).
 bool chunkwise_bwd_supported(int64_t K, int64_t V);

@@ -229,7 +229,17 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
     lib = _native.load()
     with torch.cuda.device(dev):
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        if epilogue is not None:
+        segments = 1
+        if kind == "chunkwise" and not ckpt and gate is None and epilogue is None and state_out is None:
+            # one batch stride must serve the split views (sequences back to back)
+            if B == 1 or all(x.stride(0) == T * x.stride(1) for x in (q, k, v, g, beta)):
+                segments = long_segments(B, T, H, K, V, qk_dtype)
+        if segments > 1:
+            ws = torch.empty(int(lib.kda_chunkwise_long_workspace_size(B, T, H, K, V, segments)), device=dev,
+                             dtype=torch.uint8)
+            status = lib.kda_chunkwise_long_fwd(ctypes.byref(args), ctypes.c_int64(segments),
+                                                ctypes.c_void_p(ws.data_ptr()), stream)
+        elif epilogue is not None:
             gargs = None
             if gate is not None:
                 gargs = _native.KdaGateArgs()
@@ -261,6 +271,24 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
 
 
 CKPT_SPACING = 32   # tokens between the forward's state checkpoints (kda_chunkwise_fwd_ckpt)
+LONG_MIN_SEGMENT = 1024    # shortest segment worth a split (kda_chunkwise_long_fwd)
+CU_COUNT = 256
+
+
+def long_segments(B, T, H, K, V, dtype) -> int:
+    """Segments for kda_chunkwise_long_fwd: the largest power of two that keeps
+    the second pass within one round of 64-column workgroups on the 256 CUs
+    and segments of at least LONG_MIN_SEGMENT tokens; 1 (one pass) when the
+    chains alone fill half the CUs or the shape has no split kernel."""
+    if dtype not in (torch.float16, torch.bfloat16) or K not in (64, 128) or V % 64 != 0:
+        return 1
+    tiles = B * H * (V // 64)
+    if tiles == 0 or 2 * tiles > CU_COUNT:
+        return 1
+    P = 1
+    while (2 * P * tiles <= CU_COUNT and T % (2 * P) == 0 and T // (2 * P) >= LONG_MIN_SEGMENT):
+        P *= 2
+    return P
 BWD_TILE = 32       # the native backward takes V in multiples of this
 
 

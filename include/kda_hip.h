@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 9
+#define KDA_ABI_VERSION 10
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -164,6 +164,24 @@ typedef struct kda_out_epilogue {
  * kda_prep_fwd before and the o_proj GEMM after. */
 int kda_chunkwise_fused_fwd(const kda_fwd_args* args, const kda_gate_args* gate, const kda_out_epilogue* out,
                             void* stream);
+
+/* ---------------------------------------------------------------------------
+ * kda_chunkwise_fwd on long sequences with few (batch, head) chains, split
+ * into `segments` pieces of T / segments tokens that run in parallel.  The
+ * state map of a segment is affine in the state entering it (S_end = Phi
+ * S_start + S_loc): a first pass computes every segment's S_loc and Phi
+ * (K x K), a short sequential pass composes them (the segments' initial
+ * states and the final state, fp32), and a second pass writes the outputs
+ * from the true initial states.  Same arguments and results as
+ * kda_chunkwise_fwd (the same function, rounded differently), for q, k, v
+ * fp16 or bf16, K in {64, 128}, V a multiple of 64, T % segments == 0 and,
+ * with B > 1, each input's batch stride T times its token stride
+ * (KDA_ERR_UNSUPPORTED otherwise).  workspace: device memory of
+ * kda_chunkwise_long_workspace_size() bytes, 16-byte aligned, contents on
+ * entry irrelevant.  segments == 1 is kda_chunkwise_fwd.
+ * ------------------------------------------------------------------------- */
+size_t kda_chunkwise_long_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t segments);
+int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* workspace, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Backward of the chunkwise forward.  The reference differentiates
