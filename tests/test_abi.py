@@ -179,6 +179,22 @@ def test_fused_host_validation_codes(native):
     assert call(ctypes.byref(_args(native, B=0, **f16)), ctypes.byref(gate), ctypes.byref(out), None) == 0
 
 
+def test_long_host_validation_codes(native):
+    lib = native.load()
+    call = lib.kda_chunkwise_long_fwd
+    f16 = dict(qkv_dtype=native.DTYPE_F16, T=64, chunk_size=16)
+    assert call(ctypes.byref(_args(native, **f16)), 0, None, None) == 2            # no segments
+    assert call(ctypes.byref(_args(native, **f16)), 3, None, None) == 2            # T % segments
+    assert call(ctypes.byref(_args(native, T=64, chunk_size=16)), 2, None, None) == 4  # fp32: no split kernel
+    assert call(ctypes.byref(_args(native, K=32, **f16)), 2, None, None) == 4
+    assert call(ctypes.byref(_args(native, **f16)), 2, None, None) == 1            # no workspace
+    assert call(ctypes.byref(_args(native, **f16)), 2, ctypes.c_void_p(0x100008), None) == 2  # misaligned
+    assert call(ctypes.byref(_args(native, B=0, **f16)), 2, None, None) == 0
+    size = lib.kda_chunkwise_long_workspace_size
+    assert size(1, 32768, 16, 128, 128, 8) == 4 * 8 * 16 * 128 * (3 * 128 + 128)
+    assert size(1, 64, 1, 64, 64, 0) == 0
+
+
 def test_in_place_state_contract(native):
     lib = native.load()
     same = _args(native, K=48)           # K=48 has no kernel: validation ends before any launch
