@@ -141,24 +141,27 @@ def test_backward_unsupported_head_dims_raise(kda_pkg, wl):
                               chunk_size=16)
 
 
-def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl):
+@pytest.mark.parametrize("B,V,dtype", [(16, 64, torch.float32), (9, 128, torch.float16)])
+def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl, B, V, dtype):
     """256 (batch, head) chains of 64 columns: the checkpointing forward runs its
-    widest instantiation (four 16-column consumer waves a workgroup) and the
+    widest instantiation (four 16-column consumer waves a workgroup; at V=128
+    and 144 chains, 128-column workgroups of two column groups a wave) and the
     gradients come from its checkpoints.  They must equal the gradients of the
     same sequences run one at a time (16 chains: one-wave instantiation), and
     sequence 0 must match the fp64 oracle."""
-    B, T, H, K, V = 16, 64, 16, 64, 64
-    print(f"backward wide launch B={B} T={T} H={H} K={K} V={V}", flush=True)
-    xs, wo, ws = _case(wl, B, T, H, K, V, seed=31, dtype=torch.float32, state=True)
+    T, H, K = 64, 16, 64
+    print(f"backward wide launch B={B} T={T} H={H} K={K} V={V} {dtype}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=31, dtype=dtype, state=True)
     wide = _native_grads(kda_pkg, xs, wo, ws, 32)
-    for b in (0, 7, 15):
+    for b in (0, 7, B - 1):
         sub = [x[b:b + 1] for x in xs]
         one = _native_grads(kda_pkg, sub, wo[b:b + 1], ws[b:b + 1], 32)
         for name, a, r in zip(NAMES, wide, one):
             err = _rel(a[b:b + 1], r)
             assert err <= 1e-6, (b, name, err)
     ref = _ref_grads([x[:1] for x in xs], wo[:1], ws[:1], 32)
+    tol = 2e-3 if dtype == torch.float32 else 2e-2
     for name, a, r in zip(NAMES, wide, ref):
         err = _rel(a[:1], r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
-        assert err <= 2e-3, (name, err)
+        assert err <= tol, (name, err)
