@@ -42,18 +42,22 @@
 // Pipeline, one workgroup per (b, h, 16*NC state columns), in supersteps of
 // NB = 4 blocks (two chunks), each split in two halves by workgroup barriers:
 //   NC consumer waves: wave w owns state columns [16w, 16w+16) for all K rows
-//     as MFMA accumulators and runs the chain over chunk 0 of superstep s in
-//     the first half and chunk 1 in the second.
+//     as MFMA accumulators and runs the chain over both chunks of superstep s
+//     in the first half.  With NC = NB, consumer wave p inverts (I + L) of
+//     block p of superstep s+1 in the second half.
 //   NB producer waves, one per block: wave p builds every operand of block
 //     NB*(s+1) + p.  Lane l holds K/32 adjacent channels of the block's rows
 //     8 (l / 32) .. +7, which one 8-byte (fp16) load per row brings in for
 //     all K channels of two rows.  First half: decays, the level operands
-//     and their products, the operands that need no other block's decay, the
-//     block-local operands of the chunk's off-diagonal products, the block
-//     decay E[15].  Second half, once the other block's decay is known: the
-//     chunk-relative operands, G_10 and A_10 (block 1's wave), A and the
-//     inverse of (I + L).  The next block's loads are issued in the first
-//     half and land during the rest of the superstep.
+//     and their products (A to its operand, G to the solve), the operands
+//     with decays from the block start, the block-local operands of the
+//     chunk's off-diagonal products, the block decay E[15].  Second half,
+//     once the other block's decay is known: block 0's k * F to the chunk
+//     end, G_10 and A_10 (block 1's wave), the chunk decay (and, with fewer
+//     consumer waves than blocks, the inverse of (I + L)).  Block 1's
+//     q * E and k * E keep the decay from its own start: the consumers apply
+//     block 0's decay to the state instead.  The next block's loads are
+//     issued in the first half and land during the rest of the superstep.
 // Operand slots alternate between two sets, so the producers of superstep
 // s+1 and the consumers of superstep s never touch the same slot.
 //
@@ -220,7 +224,7 @@ __device__ __forceinline__ int kh_swz(int c) { return (c >> 4) & 3; }
 template <int K>
 struct __align__(16) ChunkOps {
     static constexpr int KR = K + 8;
-    _Float16 QE[CB][BT][KR];               // q * E (decay from the chunk start), row-major
+    _Float16 QE[CB][BT][KR];               // q * E (decay from the block start), row-major
     _Float16 KE[CB][BT][KR];               // k * E
     _Float16 KH[K][KHP];                   // k * F (decay to the chunk end), k-major lines
     _Float16 AM[CB][BT][RP];               // scale * A, diagonal blocks
@@ -230,6 +234,7 @@ struct __align__(16) ChunkOps {
     _Float16 GH[BT][RP];                   // -G_10 hi
     _Float16 GL[BT][RP];                   // -G_10 lo
     float echunk[K];                       // decay over the chunk, E[31]
+    float d0[K];                           // decay over block 0, E[15]
 };
 // Producer-only exchange of one chunk within a superstep: written in the
 // first half, read in the second.
@@ -247,11 +252,20 @@ struct RowParts {
 };
 template <>
 struct RowParts<false> {};
+// The solve's inputs per block of a superstep: the level sums G (strictly
+// lower, fp32, rows padded to 17 words) and beta, written by the block's
+// producer once its level products are done, read by the wave that inverts
+// (I + L) after the superstep's middle barrier.
+struct __align__(16) SolveIn {
+    float g[NB][BT][BT + 1];
+    float beta[NB][BT];
+};
 template <int K, int CG, bool EPI>
 struct __align__(16) Smem {
     ChunkOps<K> set[2][NCH];
     Stage<K> st[NCH];
-    uint16_t vt[MAX_NC][CG][CB * BT][16];  // per consumer wave and column group: one chunk of v, 16-bit
+    uint16_t vt[MAX_NC][CB * BT][16];      // per consumer wave: one chunk of v (one column group at a time), 16-bit
+    SolveIn sv;
     RowParts<EPI> rows;
 };
 
@@ -422,6 +436,10 @@ struct Kern {
     static constexpr int GB = CH * static_cast<int>(sizeof(TG));   // bytes of a lane's g row
     static constexpr int GW = BLoad<GB>::W;
     static constexpr bool kEarlyDecay = GATED;      // see load_g
+    // With one consumer wave per block, consumer wave p inverts (I + L) of
+    // block p in the second half of a superstep, where it has no chunk to run;
+    // otherwise the block's producer does, at the end of its second half.
+    static constexpr bool kConsumerSolve = NC == NB;
 
     // One block's raw inputs for a producer lane: its CH channels of rows
     // 8hf .. 8hf + 7, and beta of rows 4lg .. 4lg + 3 (for the solve).
@@ -432,16 +450,13 @@ struct Kern {
     };
     // The same block, converted: decays a = exp(g) (GATED: formed from gk,
     // dt_bias and exp(A_log) as in gate_decay), fp16 q and k rows
-    // (channels in the low CH slots), beta of rows 4lg .. 4lg + 3 and of row
-    // ln (the solve's row and column scales).
+    // (channels in the low CH slots), beta of rows 4lg .. 4lg + 3.
     struct Work {
         float al[CH][HR];
         h4 q[HR], k[HR];
         float beta[4];
-        float beta_col;
     };
-    // What a producer carries from the first half of a superstep into the
-    // second: the level sums G (strictly lower), its mirror G^T and A.
+    // The level sums of a block: G (strictly lower), its mirror G^T and A.
     struct Sums {
         f4 G, GT, A;
     };
@@ -550,12 +565,6 @@ struct Kern {
                 w.beta[j] = __uint_as_float(r.beta[j]);
             }
         }
-        // beta of row ln: slot ln % 4 of lane group ln / 4
-        const int src = 16 * (ln >> 2) + (lane & 15);
-        float bc = w.beta[0];
-#pragma unroll
-        for (int j = 1; j < 4; ++j) bc = (ln & 3) == j ? w.beta[j] : bc;
-        w.beta_col = __shfl(bc, src);
     }
 
     // Row r of per-channel values x[c][r], rounded to fp16, as a row vector
@@ -707,13 +716,17 @@ struct Kern {
     // (I + (L^8)^T) (L is nilpotent) on the fp32 matrix cores: a product X Y
     // takes X^T's and Y's accumulator layouts, so the chain keeps powers and
     // their transposes side by side; no data moves between lanes.
-    __device__ void solve(const Sums& sum, const Work& w, _Float16 (*mh)[RP], _Float16 (*ml)[RP]) const {
+    // The inputs are block p's in the solve exchange area (put_solve_in).
+    __device__ void solve(int p, _Float16 (*mh)[RP], _Float16 (*ml)[RP]) const {
+        const float (*g)[BT + 1] = sm.sv.g[p];
+        const f4 bt = *reinterpret_cast<const f4*>(&sm.sv.beta[p][4 * lg]);   // beta of rows 4lg + j
+        const float bc = sm.sv.beta[p][ln];                                   // beta of row ln
         const f4 zero = {0.f, 0.f, 0.f, 0.f};
         f4 L, LT;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            L[j] = sum.G[j] * w.beta[j];          // row 4lg + j scaled by its beta
-            LT[j] = sum.GT[j] * w.beta_col;       // L^T: column ln of L^T is row ln of L
+            L[j] = g[4 * lg + j][ln] * bt[j];     // row 4lg + j scaled by its beta
+            LT[j] = g[ln][4 * lg + j] * bc;       // L^T: column ln of L^T is row ln of L
         }
         const f4 L2 = mm_f32(LT, L, zero), L2T = mm_f32(L, LT, zero);
         const f4 L4 = mm_f32(L2T, L2, zero), L4T = mm_f32(L2, L2T, zero);
@@ -725,7 +738,7 @@ struct Kern {
         Q = mm_f32(L4, Q, Q);
         Q = mm_f32(L8, Q, Q);                    // acc((I + L)^-T) = A-layout of (I + L)^-1
 #pragma unroll
-        for (int j = 0; j < 4; ++j) Q[j] *= w.beta[j];
+        for (int j = 0; j < 4; ++j) Q[j] *= bt[j];
         h4 hi, lo;
         split4(Q, hi, lo);
         *reinterpret_cast<h4*>(&mh[ln][4 * lg]) = hi;
@@ -736,12 +749,14 @@ struct Kern {
     // decays, the level products (with the loads of block `next` between
     // them), and every operand that needs no other block's decay: block 0's
     // q * E, k * E and block-local k * F (staged for G_10, A_10); block 1's
-    // block-local q * E and k * E (staged) and its k * F into the k-major
-    // lines.  The block decay E[15] goes to the stage area.
-    __device__ void phase1(Raw& raw, Work& w, Sums& sum, int p, ChunkOps<K>& co, int next) const {
+    // block-local q * E and k * E (its operands and those of G_10, A_10) and
+    // its k * F into the k-major lines.  The block decay E[15] goes to the
+    // stage area (block 0's also to the consumers).
+    __device__ void phase1(Raw& raw, Work& w, int p, ChunkOps<K>& co, int next) const {
         const int bi = p % CB, cj = p / CB;
         Stage<K>& st = sm.st[cj];
         unpack(raw, w);
+        Sums sum;
         sum.G = f4{0.f, 0.f, 0.f, 0.f};
         sum.GT = sum.G;
         sum.A = sum.G;
@@ -792,6 +807,13 @@ struct Kern {
             dq = wave_sum(hf ? dq : 0.f);
             if (lane == 63) sum.A[3] = dq;
         }
+        // the block's sums are complete: A to its operand, G and beta to the solve
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(sum.A[j] * scale);
+            sm.sv.g[p][4 * lg + j][ln] = sum.G[j];
+        }
+        if (ln == 0) *reinterpret_cast<f4*>(&sm.sv.beta[p][4 * lg]) = f4{w.beta[0], w.beta[1], w.beta[2], w.beta[3]};
 
         // the other half's total decay; the block decay E[15]
         float other[CH];
@@ -802,7 +824,11 @@ struct Kern {
             const unsigned u = __float_as_uint(pre[c][HR - 1]);
             const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
             other[c] = __uint_as_float(sw[0] != u ? sw[0] : sw[1]);
-            if (hf == 0) st.e15[bi][CH * cq + c] = pre[c][HR - 1] * other[c];
+            if (hf == 0) {
+                const float e = pre[c][HR - 1] * other[c];
+                st.e15[bi][CH * cq + c] = e;
+                if (bi == 0) co.d0[CH * cq + c] = e;
+            }
         }
         // block-local decays: E (from the block start, inclusive) = pre, times
         // the lower half's total in the upper half; F (to the block end,
@@ -845,9 +871,9 @@ struct Kern {
 
     // Second half: the operands that need the other block's decay (block 0:
     // k * F to the chunk end; block 1: G_10 and A_10 from the block-local
-    // operands, then q * E and k * E from the chunk start, and the chunk
-    // decay), A and the inverse of (I + L).
-    __device__ void phase2(const Work& w, const Sums& sum, int p, ChunkOps<K>& co) const {
+    // operands and the chunk decay), and the inverse of (I + L) when no
+    // consumer wave takes it.
+    __device__ void phase2(int p, ChunkOps<K>& co) const {
         const int bi = p % CB, cj = p / CB;
         Stage<K>& st = sm.st[cj];
         float d[CH];
@@ -879,22 +905,12 @@ struct Kern {
             *reinterpret_cast<h4*>(&co.GH[ln][4 * lg]) = gh;
             *reinterpret_cast<h4*>(&co.GL[ln][4 * lg]) = gl;
             *reinterpret_cast<h4*>(&co.A10[ln][4 * lg]) = to_h4(accA * scale);
-            // chunk-relative q * E and k * E: the block-local rows times the
-            // decay of block 0 (LDS serves the wave's reads above first)
-#pragma unroll
-            for (int r = 0; r < HR; ++r) {
-                const int row = HR * hf + r;
-                put_row(&co.QE[1][0][0], row, get_row(&co.QE[1][0][0], row) * dh);
-                put_row(&co.KE[1][0][0], row, get_row(&co.KE[1][0][0], row) * dh);
-            }
             if (hf == 0) {
 #pragma unroll
                 for (int c = 0; c < CH; ++c) co.echunk[CH * cq + c] = st.e15[1][CH * cq + c] * d[c];
             }
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(sum.A[j] * scale);
-        solve(sum, w, co.MH[bi], co.ML[bi]);
+        if constexpr (!kConsumerSolve) solve(p, co.MH[bi], co.ML[bi]);
     }
 
     // ------------------------------------------------------------ consumers
@@ -1042,12 +1058,12 @@ struct Kern {
     // its R = V - (k * E) S, [K + 32, K + 64) its P.  EPI: the outputs go to
     // pd (and their row sums of squares to LDS) instead of o.
     __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw)[CG][VW],
-                            uint16_t (*vt)[CB * BT][16], f4 (&S)[CG][KT], int64_t colw, float* ck, Pend& pd,
+                            uint16_t (*vt)[16], f4 (&S)[CG][KT], int64_t colw, float* ck, Pend& pd,
                             int wave) const {
         f4 R[CG][CB];
 #pragma unroll
         for (int g = 0; g < CG; ++g) {
-            v_tile(vraw[g], vt[g], R[g][0], R[g][1]);
+            v_tile(vraw[g], vt, R[g][0], R[g][1]);
             v_load(vraw[g], blk / CB + NCH, g);
         }
         const int64_t V = a.V;
@@ -1058,8 +1074,10 @@ struct Kern {
         float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
         // the same fragments as A and B operands the other way round, so that
-        // a lane holds four adjacent output columns of one row.  S enters as
-        // single fp16 operands: Z and O read it once per chunk.
+        // a lane holds four adjacent output columns of one row.  Block 1's
+        // operands hold decays from its own start, so its products take
+        // Diag(E[15]) S, block 0's decay applied to the state rows.  The state
+        // enters as single fp16 operands, rounded once per chunk.
         f4 Z[CG][CB], O[CG][CB];
 #pragma unroll
         for (int g = 0; g < CG; ++g)
@@ -1072,13 +1090,18 @@ struct Kern {
             const h8 k1 = *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o);
             const h8 q0 = *reinterpret_cast<const h8*>(&co.QE[0][0][0] + o);
             const h8 q1 = *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o);
+            // block 0's decay on the state rows of tiles 2u and 2u + 1
+            const float4 da = *reinterpret_cast<const float4*>(&co.d0[32 * u + 4 * lg]);
+            const float4 db = *reinterpret_cast<const float4*>(&co.d0[32 * u + 16 + 4 * lg]);
+            const f4 fa = {da.x, da.y, da.z, da.w}, fb = {db.x, db.y, db.z, db.w};
 #pragma unroll
             for (int g = 0; g < CG; ++g) {
                 const h8 sh = cat(to_h4(S[g][2 * u]), to_h4(S[g][2 * u + 1]));
+                const h8 sd = cat(to_h4(S[g][2 * u] * fa), to_h4(S[g][2 * u + 1] * fb));
                 Z[g][0] = mfma16x16x32(k0, sh, Z[g][0]);
-                Z[g][1] = mfma16x16x32(k1, sh, Z[g][1]);
+                Z[g][1] = mfma16x16x32(k1, sd, Z[g][1]);
                 O[g][0] = mfma16x16x32(sh, q0, O[g][0]);
-                O[g][1] = mfma16x16x32(sh, q1, O[g][1]);
+                O[g][1] = mfma16x16x32(sd, q1, O[g][1]);
             }
         }
         // P_0 = M_00 (V_0 - Z_0);  P_1 = M_11 (V_1 - Z_1 - G_10 P_0): M (hi + lo)
@@ -1270,37 +1293,43 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         for (int j = 0; j < NCH; ++j)
 #pragma unroll
             for (int g = 0; g < CG; ++g) kn.v_load(vr[j][g], j, g);
-        uint16_t (*vt)[CB * BT][16] = sm.vt[consumer ? wave : 0];
-        typename KN::Pend pd;
-        bool pending = false;
+        uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
+        typename KN::Pend pd[NCH];
         if constexpr (EPI) {
 #pragma unroll
             for (int g = 0; g < CG; ++g)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) kn.wn[g][j] = epi.weight[kn.h * V + colw + 16 * g + 4 * kn.lg + j];
         }
+        // First half: the superstep's chunks one after the other; second
+        // half (after the producers' first): the chunks' outputs (EPI: every
+        // wave's row sums are in LDS now) and the solve of block `wave` of the
+        // next superstep.
         for (int s = -1; s < nss; ++s) {
 #pragma unroll
             for (int cj = 0; cj < NCH; ++cj) {
                 const int cc = NCH * s + cj;
-                if constexpr (EPI) {
-                    // the previous chunk's outputs, now that every wave's row
-                    // sums are in LDS (one barrier ago)
-                    if (pending) kn.finish(pd, colw, wave);
-                    pending = false;
-                }
                 if (s >= 0 && cc < ncc) {
                     // the checkpoint of chunk cc, for the backward
                     float* ck = ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K + 2 * CB * BT) * V
                                      : nullptr;
-                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, colw, ck, pd, wave);
-                    pending = EPI;
+                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, colw, ck, pd[cj], wave);
                 }
-                __syncthreads();
             }
-        }
-        if constexpr (EPI) {
-            if (pending) kn.finish(pd, colw, wave);
+            __syncthreads();
+            if constexpr (EPI) {
+#pragma unroll
+                for (int cj = 0; cj < NCH; ++cj)
+                    if (s >= 0 && NCH * s + cj < ncc) kn.finish(pd[cj], colw, wave);
+            }
+            if constexpr (KN::kConsumerSolve) {
+                const int nb = NB * (s + 1) + wave;
+                if (nb < nblk) {
+                    ChunkOps<K>& nx = sm.set[(s + 1) & 1][wave / CB];
+                    kn.solve(wave, nx.MH[wave % CB], nx.ML[wave % CB]);
+                }
+            }
+            __syncthreads();
         }
 #pragma unroll
         for (int g = 0; g < CG; ++g)
@@ -1317,15 +1346,14 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         }
         typename KN::Raw raw;
         typename KN::Work w;
-        typename KN::Sums sum;
         kn.load_raw(raw, p);
         if constexpr (KN::kEarlyDecay) kn.decays(raw, w);
         for (int s = -1; s < nss; ++s) {
             const int blk = NB * (s + 1) + p;
             ChunkOps<K>& co = sm.set[(s + 1) & 1][p / CB];
-            if (blk < nblk) kn.phase1(raw, w, sum, p, co, blk + NB);
+            if (blk < nblk) kn.phase1(raw, w, p, co, blk + NB);
             __syncthreads();
-            if (blk < nblk) kn.phase2(w, sum, p, co);
+            if (blk < nblk) kn.phase2(p, co);
             __syncthreads();
         }
     }
