@@ -995,14 +995,26 @@ struct Kern {
         }
     }
 
-    // EPI: a chunk's outputs, rounded to TQ as the reference's o_core is, held
-    // over one barrier while the other consumer waves' row sums of squares
-    // arrive, with the output gate's pre-activations of the same entries.
+    // EPI: a chunk's outputs, rounded to TQ as the reference's o_core is and
+    // held as TQ bits (two a word) over one barrier while the other consumer
+    // waves' row sums of squares arrive, with the output gate's
+    // pre-activations of the same entries.
     struct Pend {
-        f4 o[EPI ? CG : 1][CB];
+        u2 o[EPI ? CG : 1][CB];
         u2 gt[EPI ? CG : 1][CB];
         int blk;
     };
+    // The 16-bit TQ element j of a pair of packed words, as a float.
+    static __device__ __forceinline__ float unpack16(const u2& w, int j) {
+        const uint32_t bits = (w[j / 2] >> (16 * (j % 2))) & 0xffffu;
+        return Elem<TQ>::code == KDA_DTYPE_BF16 ? __uint_as_float(bits << 16)
+                                                : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+    }
+    // The bits of x (a value of TQ) as a 16-bit element.
+    static __device__ __forceinline__ uint32_t bits16(float x) {
+        if constexpr (Elem<TQ>::code == KDA_DTYPE_BF16) return f32_to_bf16_bits(x);
+        else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    }
     const void* og = nullptr;                // EPI: the output gate's pre-activations [B, T, H*V]
     int64_t og_s0 = 0, og_s1 = 0;            //      and their (batch, token) strides
     float eps = 0.f;                         //      the norm's epsilon
@@ -1038,11 +1050,8 @@ struct Kern {
                 f4 y;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t bits = (pd.gt[g][bk][j / 2] >> (16 * (j % 2))) & 0xffffu;
-                    const float z = Elem<TQ>::code == KDA_DTYPE_BF16
-                                        ? __uint_as_float(bits << 16)
-                                        : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-                    const float n = round_elem<TQ>((pd.o[g][bk][j] * rstd) * wn[g][j]);
+                    const float z = unpack16(pd.gt[g][bk], j);
+                    const float n = round_elem<TQ>((unpack16(pd.o[g][bk], j) * rstd) * wn[g][j]);
                     y[j] = n * sigmoid_f(z);
                 }
                 store_row4(y, pd.blk + bk, colw + 16 * g);
@@ -1159,12 +1168,14 @@ struct Kern {
                 float ss = 0.f;
 #pragma unroll
                 for (int g = 0; g < CG; ++g) {
+                    uint32_t ob[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const float x = round_elem<TQ>(O[g][bk][j]);
-                        pd.o[g][bk][j] = x;
+                        ob[j] = bits16(x);
                         ss = fmaf(x, x, ss);
                     }
+                    pd.o[g][bk] = u2{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16)};
                     pd.gt[g][bk] = gate_load(blk + bk, colw + 16 * g);
                 }
                 ss = lanegroup4_sum(ss);
