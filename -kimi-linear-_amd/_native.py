@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -108,12 +108,47 @@ class KdaOutputArgs(ctypes.Structure):
     ]
 
 
+class KdaPrepBwdArgs(ctypes.Structure):
+    """Mirror of ``struct kda_prep_bwd_args`` (include/kda_hip.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int64), ("T", ctypes.c_int64), ("H", ctypes.c_int64),
+        ("K", ctypes.c_int64), ("V", ctypes.c_int64), ("conv_size", ctypes.c_int64),
+        ("x", _ptr3), ("x_stride", (ctypes.c_int64 * 2) * 3),
+        ("conv_w", _ptr3), ("conv_b", _ptr3), ("w_dtype", ctypes.c_int32),
+        ("dy", _ptr3), ("dx", _ptr3), ("dw", _ptr3), ("db", _ptr3),
+        ("gk", ctypes.c_void_p), ("gk_stride", ctypes.c_int64 * 2),
+        ("a_log", ctypes.c_void_p), ("dt_bias", ctypes.c_void_p), ("p_dtype", ctypes.c_int32),
+        ("beta_logit", ctypes.c_void_p), ("beta_stride", ctypes.c_int64 * 2),
+        ("dg", ctypes.c_void_p), ("dbeta", ctypes.c_void_p),
+        ("dgk", ctypes.c_void_p), ("dbeta_logit", ctypes.c_void_p),
+        ("da_log", ctypes.c_void_p), ("ddt_bias", ctypes.c_void_p),
+        ("l2_eps", ctypes.c_float), ("x_dtype", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+    ]
+
+
+class KdaOutputBwdArgs(ctypes.Structure):
+    """Mirror of ``struct kda_output_bwd_args`` (include/kda_hip.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int64), ("T", ctypes.c_int64), ("H", ctypes.c_int64), ("V", ctypes.c_int64),
+        ("o", ctypes.c_void_p), ("o_stride", ctypes.c_int64 * 3),
+        ("gate", ctypes.c_void_p), ("gate_stride", ctypes.c_int64 * 2),
+        ("weight", ctypes.c_void_p), ("w_dtype", ctypes.c_int32),
+        ("dy", ctypes.c_void_p), ("d_o", ctypes.c_void_p), ("dgate", ctypes.c_void_p),
+        ("dweight", ctypes.c_void_p), ("eps", ctypes.c_float), ("x_dtype", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+    ]
+
+
 EXPORTED_SYMBOLS = ("kda_chunkwise_fwd", "kda_recurrent_fwd", "kda_chunkwise_fwd_ckpt",
                     "kda_chunkwise_gated_fwd", "kda_recurrent_gated_fwd", "kda_chunkwise_fused_fwd",
                     "kda_chunkwise_long_fwd", "kda_chunkwise_long_workspace_size",
                     "kda_chunkwise_bwd",
                     "kda_chunkwise_bwd_workspace_size", "kda_chunkwise_bwd_noalloc",
-                    "kda_prep_fwd", "kda_output_fwd", "kda_status_str", "kda_abi_version")
+                    "kda_prep_fwd", "kda_output_fwd", "kda_prep_bwd", "kda_prep_bwd_workspace_size",
+                    "kda_output_bwd", "kda_output_bwd_workspace_size", "kda_status_str", "kda_abi_version")
 
 _lib = None
 _lock = threading.Lock()
@@ -169,6 +204,14 @@ def load() -> ctypes.CDLL:
         lib.kda_prep_fwd.restype = ctypes.c_int
         lib.kda_output_fwd.argtypes = [ctypes.POINTER(KdaOutputArgs), ctypes.c_void_p]
         lib.kda_output_fwd.restype = ctypes.c_int
+        lib.kda_prep_bwd.argtypes = [ctypes.POINTER(KdaPrepBwdArgs), ctypes.c_void_p]
+        lib.kda_prep_bwd.restype = ctypes.c_int
+        lib.kda_prep_bwd_workspace_size.argtypes = [ctypes.c_int64] * 6
+        lib.kda_prep_bwd_workspace_size.restype = ctypes.c_size_t
+        lib.kda_output_bwd.argtypes = [ctypes.POINTER(KdaOutputBwdArgs), ctypes.c_void_p]
+        lib.kda_output_bwd.restype = ctypes.c_int
+        lib.kda_output_bwd_workspace_size.argtypes = [ctypes.c_int64] * 4
+        lib.kda_output_bwd_workspace_size.restype = ctypes.c_size_t
         lib.kda_status_str.argtypes = [ctypes.c_int]
         lib.kda_status_str.restype = ctypes.c_char_p
         lib.kda_abi_version.argtypes = []

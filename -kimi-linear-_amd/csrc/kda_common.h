@@ -129,6 +129,21 @@ __device__ __forceinline__ float sigmoid_f(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
 
+// log(1 + x) for x in [0, 1] to about an ulp: with u = 1 + x rounded,
+// log(u) x / (u - 1) cancels the rounding of u (u == 1 when x is below half an
+// ulp of 1, and then log(1 + x) = x to fp32 precision).
+__device__ __forceinline__ float log1p_unit(float x) {
+    const float u = 1.f + x;
+    return u == 1.f ? x : __logf(u) * (x / (u - 1.f));
+}
+
+// softplus with torch's default threshold: z for z > 20, else
+// log(1 + e^z) = max(z, 0) + log1p(e^-|z|), which keeps its e^z behaviour for
+// z << 0 (log(1 + e^z) in fp32 rounds to 0 below z ~ -17)
+__device__ __forceinline__ float softplus(float z) {
+    return z > 20.f ? z : fmaxf(z, 0.f) + log1p_unit(__expf(-fabsf(z)));
+}
+
 // fp16 hi/lo split: x ~= hi + lo with |x - hi - lo| ~ 2^-22 |x|.
 __device__ __forceinline__ void split_h(float x, _Float16& hi, _Float16& lo) {
     hi = static_cast<_Float16>(x);

@@ -70,20 +70,6 @@ __device__ __forceinline__ float round_to(float x) {
 }
 
 
-// log(1 + x) for x in [0, 1] to about an ulp: with u = 1 + x rounded,
-// log(u) x / (u - 1) cancels the rounding of u (u == 1 when x is below half an
-// ulp of 1, and then log(1 + x) = x to fp32 precision).
-__device__ __forceinline__ float log1p_unit(float x) {
-    const float u = 1.f + x;
-    return u == 1.f ? x : __logf(u) * (x / (u - 1.f));
-}
-
-// softplus with torch's default threshold: z for z > 20, else
-// log(1 + e^z) = max(z, 0) + log1p(e^-|z|), which keeps its e^z behaviour for
-// z << 0 (log(1 + e^z) in fp32 rounds to 0 below z ~ -17)
-__device__ __forceinline__ float softplus(float z) {
-    return z > 20.f ? z : fmaxf(z, 0.f) + log1p_unit(__expf(-fabsf(z)));
-}
 
 // A small parameter element of a runtime dtype: the load is unconditional
 // (a NULL or out-of-range element reads `fallback`'s first word instead and is

@@ -9,8 +9,12 @@ cache, SiLU, L2 norms, gates; RMSNorm and output gate) runs in the two fused
 kernels of :mod:`kimi_linear_amd.layer_ops`.  ``ShortConv`` and
 ``HeadwiseRMSNorm`` below only hold parameters under the reference's names.
 
-The core is forward-only (it raises on inputs that require grad under grad
-mode): run the layer under ``torch.no_grad()`` or ``torch.inference_mode()``.
+Under grad mode with parameters or x that require grad, ``forward`` runs the
+training path (:meth:`KimiDeltaAttention._train_forward`): the same function,
+differentiable end to end -- native backward kernels for the pre-processing
+(conv, SiLU, L2 norms, gates) and the output epilogue, the native chunkwise
+backward for the core over the whole sequence -- without a cache or state.
+Inference runs under ``torch.no_grad()`` or ``torch.inference_mode()``.
 
 Semantics kept from the reference:
 
@@ -46,8 +50,8 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 
-from .kda import kda_chunkwise_fused, kda_chunkwise_gated, kda_recurrent_gated
-from .layer_ops import kda_output, kda_prep
+from .kda import KdaError, kda_chunkwise, kda_chunkwise_fused, kda_chunkwise_gated, kda_recurrent_gated
+from .layer_ops import kda_output, kda_output_train, kda_prep, kda_prep_train
 
 
 class HeadwiseRMSNorm(nn.Module):
@@ -281,9 +285,48 @@ class KimiDeltaAttention(nn.Module):
                                         state_out=rec)
         return self._output(o_core, og_low)
 
+    def _train_forward(self, x):
+        """The layer's forward for training (``kda.py:473-536`` differentiated by
+        autograd in the reference, ``scripts/train_musicgpt_fp16.py:519-523``):
+        the six projections of x as one differentiable GEMM over the
+        concatenated weights, the pre-processing (:func:`kda_prep_train`: conv,
+        SiLU, L2 norms and the gates g, beta), the core over the whole sequence
+        (:func:`kda_chunkwise`, any T: the recurrence is chunk-size invariant,
+        so the reference's chunkwise body plus recurrent tail is the same
+        function), the output epilogue (:func:`kda_output_train`) and o_proj.
+        Every step has a native backward; no cache, no state."""
+        H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+        B, T = x.shape[0], x.shape[1]
+        mods = self._input_mods()
+        w = torch.cat([m.weight for m in mods], 0)
+        b = torch.cat([m.bias for m in mods]) if mods[0].bias is not None else None
+        y = torch.nn.functional.linear(x, w, b)
+        q_in, k_in, v_in, beta_logit, gk_low, og_low = torch.split(
+            y, (H * K, H * K, H * V, H, self.gk_proj[0].out_features, self.og_proj[0].out_features), dim=-1)
+        if T == 0:
+            return self.o_proj(x.new_zeros(B, 0, H * V))
+        convs = (self.conv_q.conv, self.conv_k.conv, self.conv_v.conv)
+        gk = self.gk_proj[1](gk_low)
+        q, k, v, g, beta = kda_prep_train(q_in, k_in, v_in, tuple(c.weight for c in convs),
+                                          tuple(c.bias for c in convs), gk, self.A_log, self.dt_bias, beta_logit,
+                                          num_heads=H, head_dim=K, value_head_dim=V, l2_eps=self.l2norm_eps)
+        C = self.chunk_size if T % self.chunk_size == 0 else T
+        o_core, _ = kda_chunkwise(q, k, v, g, beta, chunk_size=C, state_dtype=self._state_dtype(x))
+        gate = self.og_proj[1](og_low)
+        if gate.dtype != o_core.dtype:
+            gate = gate.to(o_core.dtype)
+        return self.o_proj(kda_output_train(o_core, gate, self.g_norm.weight, self.g_norm.eps))
+
     def forward(self, x, state=None, use_cache=False):
         """x: [B, T, d]; ``state`` = {"conv": {"q", "k", "v"}, "recurrent"}.
-        Returns out, or (out, new_state) with ``use_cache``."""
+        Returns out, or (out, new_state) with ``use_cache``.  Under grad mode
+        with x or a parameter requiring grad: the training path (no cache, no
+        state; see :meth:`_train_forward`)."""
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            if use_cache or state is not None:
+                raise KdaError("the training path (grad mode with parameters that require grad) takes no cache "
+                               "or state; run cached prefill and decode under torch.no_grad()")
+            return self._train_forward(x)
         if use_cache and state is None:
             state = self.init_state(x.shape[0], device=x.device, dtype=x.dtype)
         conv_cache = state["conv"] if state is not None else None

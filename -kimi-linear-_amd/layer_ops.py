@@ -211,3 +211,180 @@ def kda_output(o, gate, weight, eps):
     a.y, a.eps, a.x_dtype = y.data_ptr(), float(eps), _code("o", o)
     _call(_native.load().kda_output_fwd, a, dev, f"kda_output_fwd (B={B}, T={T}, H={H}, V={V})")
     return y
+
+
+def _c(t):
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def kda_prep_backward(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, dq, dk, dv, dg, dbeta, *,
+                      num_heads, head_dim, value_head_dim, l2_eps):
+    """Gradients of :func:`kda_prep` (a call without a conv cache) from those
+    of its outputs: ``dq, dk [B, T, H, K]``, ``dv [B, T, H, V]`` and, with the
+    gates, ``dg [B, T, H, K]``, ``dbeta [B, T, H]`` (fp32).
+
+    Returns ``(dq_in, dk_in, dv_in, dw, db, dgk, dbeta_logit, da_log, ddt_bias)``:
+    the projections' gradients in their dtype, the conv weights' ``dw`` (three
+    ``[D, 1, conv_size]``) and ``db`` (three ``[D]`` or None) in the weights'
+    dtype, and for the gates ``dgk [B, T, H*K]``, ``dbeta_logit [B, T, H]``,
+    ``da_log``, ``ddt_bias`` (shaped and typed as ``a_log``, ``dt_bias``), or
+    None without gates.  Sums over tokens are fp32 and run in a fixed order.
+    """
+    H, K, V = int(num_heads), int(head_dim), int(value_head_dim)
+    B, T = q_in.shape[0], q_in.shape[1]
+    Dk, Dv = H * K, H * V
+    xs = (_rows("q_in", q_in, (B, T, Dk)), _rows("k_in", k_in, (B, T, Dk)), _rows("v_in", v_in, (B, T, Dv)))
+    dt = xs[0].dtype
+    dys = tuple(_c(d.to(dt)).view(B, T, D) for d, D in zip((dq, dk, dv), (Dk, Dk, Dv)))
+    cs = conv_w[0].shape[-1]
+    ws = [_c(w) for w in conv_w]
+    wdt = ws[0].dtype
+    bs = [_c(b) if b is not None else None for b in conv_b]
+    gates = gk is not None
+    dev = xs[0].device
+    dxs = [torch.empty_like(x, memory_format=torch.contiguous_format) for x in xs]
+    dws = [torch.empty(D, cs, device=dev, dtype=torch.float32) for D in (Dk, Dk, Dv)]
+    dbs = [torch.empty(D, device=dev, dtype=torch.float32) if b is not None else None
+           for b, D in zip(bs, (Dk, Dk, Dv))]
+    out_g = (None, None, None, None)
+    if gates:
+        gk = _rows("gk", gk, (B, T, Dk))
+        beta_logit = _rows("beta_logit", beta_logit, (B, T, H))
+        al, db_ = _c(a_log.reshape(-1)), _c(dt_bias.reshape(-1))
+        dg = _c(dg.float()).view(B, T, Dk)
+        dbeta = _c(dbeta.float()).view(B, T, H)
+        dgk = torch.empty(B, T, Dk, device=dev, dtype=dt)
+        dlogit = torch.empty(B, T, H, device=dev, dtype=dt)
+        dal = torch.empty(Dk, device=dev, dtype=torch.float32)
+        ddt = torch.empty(Dk, device=dev, dtype=torch.float32)
+    if B * T * H > 0:
+        lib = _native.load()
+        ws_bytes = lib.kda_prep_bwd_workspace_size(B, T, H, K, V, cs)
+        work = torch.empty(max(1, (ws_bytes + 3) // 4), device=dev, dtype=torch.float32)
+        a = _native.KdaPrepBwdArgs()
+        a.B, a.T, a.H, a.K, a.V, a.conv_size = B, T, H, K, V, cs
+        for i in range(3):
+            a.x[i] = xs[i].data_ptr()
+            a.x_stride[i][0], a.x_stride[i][1] = xs[i].stride(0), xs[i].stride(1)
+            a.conv_w[i] = ws[i].data_ptr()
+            a.conv_b[i] = bs[i].data_ptr() if bs[i] is not None else None
+            a.dy[i] = dys[i].data_ptr()
+            a.dx[i] = dxs[i].data_ptr()
+            a.dw[i] = dws[i].data_ptr()
+            a.db[i] = dbs[i].data_ptr() if dbs[i] is not None else None
+        a.w_dtype = _code("conv weight", ws[0])
+        if gates:
+            a.gk = gk.data_ptr()
+            a.gk_stride[0], a.gk_stride[1] = gk.stride(0), gk.stride(1)
+            a.a_log, a.dt_bias, a.p_dtype = al.data_ptr(), db_.data_ptr(), _code("A_log", al)
+            a.beta_logit = beta_logit.data_ptr()
+            a.beta_stride[0], a.beta_stride[1] = beta_logit.stride(0), beta_logit.stride(1)
+            a.dg, a.dbeta = dg.data_ptr(), dbeta.data_ptr()
+            a.dgk, a.dbeta_logit = dgk.data_ptr(), dlogit.data_ptr()
+            a.da_log, a.ddt_bias = dal.data_ptr(), ddt.data_ptr()
+        else:
+            a.p_dtype = _native.DTYPE_F32
+        a.l2_eps = float(l2_eps)
+        a.x_dtype = _code("activations", xs[0])
+        a.workspace = work.data_ptr()
+        _call(lib.kda_prep_bwd, a, dev, f"kda_prep_bwd (B={B}, T={T}, H={H}, K={K}, V={V}, conv {cs})")
+    else:
+        for t in dxs + dws + [d for d in dbs if d is not None] + ([dgk, dlogit, dal, ddt] if gates else []):
+            t.zero_()
+    if gates:
+        out_g = (dgk, dlogit, dal.view_as(a_log).to(a_log.dtype), ddt.view_as(dt_bias).to(dt_bias.dtype))
+    dw = tuple(d.view(-1, 1, cs).to(wdt) for d in dws)
+    db = tuple(d.to(wdt) if d is not None else None for d in dbs)
+    return (dxs[0], dxs[1], dxs[2], dw, db) + out_g
+
+
+def kda_output_backward(o, gate, weight, eps, dy):
+    """Gradients of :func:`kda_output` from ``dy [B, T, H*V]``: ``(do [B, T, H, V],
+    dgate [B, T, H*V], dweight [H, V])``, the first two in o's dtype, the
+    last in weight's (an fp32 sum over tokens in a fixed order).  The
+    rounding of the normalised value counts as the identity."""
+    B, T, H, V = o.shape
+    if o.stride(-1) != 1:
+        o = o.contiguous()
+    gate = _rows("gate", gate, (B, T, H * V))
+    weight = _c(weight)
+    dy = _c(dy.to(o.dtype)).view(B, T, H * V)
+    dev = o.device
+    do = torch.empty(B, T, H, V, device=dev, dtype=o.dtype)
+    dgate = torch.empty(B, T, H * V, device=dev, dtype=o.dtype)
+    dw = torch.empty(H * V, device=dev, dtype=torch.float32)
+    if do.numel() == 0:
+        dw.zero_()
+        return do, dgate, dw.view(H, V).to(weight.dtype)
+    lib = _native.load()
+    work = torch.empty(max(1, (lib.kda_output_bwd_workspace_size(B, T, H, V) + 3) // 4), device=dev,
+                       dtype=torch.float32)
+    a = _native.KdaOutputBwdArgs()
+    a.B, a.T, a.H, a.V = B, T, H, V
+    a.o = o.data_ptr()
+    a.o_stride[0], a.o_stride[1], a.o_stride[2] = o.stride(0), o.stride(1), o.stride(2)
+    a.gate = gate.data_ptr()
+    a.gate_stride[0], a.gate_stride[1] = gate.stride(0), gate.stride(1)
+    a.weight, a.w_dtype = weight.data_ptr(), _code("weight", weight)
+    a.dy, a.d_o, a.dgate, a.dweight = dy.data_ptr(), do.data_ptr(), dgate.data_ptr(), dw.data_ptr()
+    a.eps, a.x_dtype, a.workspace = float(eps), _code("o", o), work.data_ptr()
+    _call(lib.kda_output_bwd, a, dev, f"kda_output_bwd (B={B}, T={T}, H={H}, V={V})")
+    return do, dgate, dw.view(H, V).to(weight.dtype)
+
+
+class _PrepFn(torch.autograd.Function):
+    """kda_prep (with the gates, no conv cache) with the native backward."""
+
+    @staticmethod
+    def forward(ctx, q_in, k_in, v_in, wq, wk, wv, bq, bk, bv, gk, beta_logit, a_log, dt_bias, meta):
+        H, K, V, eps = meta
+        q, k, v, g, beta, _ = kda_prep(q_in, k_in, v_in, (wq, wk, wv), (bq, bk, bv), gk, a_log, dt_bias, beta_logit,
+                                       num_heads=H, head_dim=K, value_head_dim=V, l2_eps=eps)
+        ctx.save_for_backward(q_in, k_in, v_in, wq, wk, wv, bq, bk, bv, gk, beta_logit, a_log, dt_bias)
+        ctx.meta = meta
+        return q, k, v, g, beta
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv, dg, dbeta):
+        q_in, k_in, v_in, wq, wk, wv, bq, bk, bv, gk, beta_logit, a_log, dt_bias = ctx.saved_tensors
+        H, K, V, eps = ctx.meta
+        B, T = q_in.shape[0], q_in.shape[1]
+        z = lambda *s: torch.zeros(*s, device=q_in.device, dtype=torch.float32)  # noqa: E731
+        dq = dq if dq is not None else z(B, T, H, K)
+        dk = dk if dk is not None else z(B, T, H, K)
+        dv = dv if dv is not None else z(B, T, H, V)
+        dg = dg if dg is not None else z(B, T, H, K)
+        dbeta = dbeta if dbeta is not None else z(B, T, H)
+        dqi, dki, dvi, dw, db, dgk, dlogit, dal, ddt = kda_prep_backward(
+            q_in, k_in, v_in, (wq, wk, wv), (bq, bk, bv), gk, a_log, dt_bias, beta_logit, dq, dk, dv, dg, dbeta,
+            num_heads=H, head_dim=K, value_head_dim=V, l2_eps=eps)
+        return (dqi, dki, dvi, dw[0], dw[1], dw[2], db[0], db[1], db[2], dgk, dlogit, dal, ddt, None)
+
+
+class _OutputFn(torch.autograd.Function):
+    """kda_output with the native backward."""
+
+    @staticmethod
+    def forward(ctx, o, gate, weight, eps):
+        ctx.save_for_backward(o, gate, weight)
+        ctx.eps = eps
+        return kda_output(o, gate, weight, eps)
+
+    @staticmethod
+    def backward(ctx, dy):
+        o, gate, weight = ctx.saved_tensors
+        do, dgate, dw = kda_output_backward(o, gate, weight, ctx.eps, dy)
+        return do, dgate, dw, None
+
+
+def kda_prep_train(q_in, k_in, v_in, conv_w, conv_b, gk, a_log, dt_bias, beta_logit, *, num_heads, head_dim,
+                   value_head_dim, l2_eps):
+    """:func:`kda_prep` with the gates and without a conv cache, differentiable
+    (native forward and backward kernels): ``(q, k, v, g, beta)``."""
+    return _PrepFn.apply(q_in, k_in, v_in, *conv_w, *conv_b, gk, beta_logit, a_log, dt_bias,
+                         (int(num_heads), int(head_dim), int(value_head_dim), float(l2_eps)))
+
+
+def kda_output_train(o, gate, weight, eps):
+    """:func:`kda_output`, differentiable (native forward and backward kernels)."""
+    return _OutputFn.apply(o, gate, weight, float(eps))

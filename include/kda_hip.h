@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 10
+#define KDA_ABI_VERSION 11
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -321,6 +321,82 @@ typedef struct kda_output_args {
 } kda_output_args;
 
 int kda_output_fwd(const kda_output_args* args, void* stream);
+
+/* Gradients of kda_prep_fwd, for training through the layer (the reference
+ * differentiates _projections, kimi_linear/kda.py:399-461, by autograd;
+ * scripts/train_musicgpt_fp16.py:519-523 trains the whole layer).  Given dy,
+ * the gradients of the forward's q, k, v outputs, and the forward's inputs
+ * (no conv cache: a training call starts from zeros), per tensor i:
+ *   dx[i]   [B, T, D]        gradient of the projection x[i]
+ *   dw[i]   [D, conv_size]   gradient of the conv weight, fp32
+ *   db[i]   [D]              gradient of the conv bias, fp32 (NULL: skipped)
+ * through the L2 norm (its 1/l2_eps clamp included), SiLU and the causal
+ * convolution; and, when gk is not NULL, through the gates from dg and dbeta
+ * (fp32, the gradients of g and beta):
+ *   dgk [B, T, H*K] and dbeta_logit [B, T, H] (x dtype), da_log and ddt_bias
+ *   [H*K] (fp32).
+ * Every sum over tokens runs in fp32 per workgroup tile, then over the tiles
+ * in a fixed order (run-to-run identical).  K, V in {64, 128}.  workspace:
+ * kda_prep_bwd_workspace_size() bytes of device memory (16-byte aligned); the
+ * call allocates nothing. */
+typedef struct kda_prep_bwd_args {
+    int64_t B, T, H, K, V;         /* K, V in {64, 128} */
+    int64_t conv_size;             /* 1..4 */
+    const void* x[3];              /* the forward's q, k, v projections [B, T, D], x dtype */
+    int64_t x_stride[3][2];        /* (batch, token) strides in elements; channels contiguous */
+    const void* conv_w[3];         /* [D, conv_size] contiguous */
+    const void* conv_b[3];         /* [D] or NULL */
+    int32_t w_dtype;               /* kda_dtype of conv_w and conv_b */
+    const void* dy[3];             /* gradients of q, k [B, T, H, K] and v [B, T, H, V], contiguous, x dtype */
+    void* dx[3];                   /* [B, T, D] contiguous, x dtype */
+    float* dw[3];                  /* [D, conv_size] */
+    float* db[3];                  /* [D] or NULL */
+    const void* gk;                /* [B, T, H*K] gate up-projection, x dtype, or NULL (no gates) */
+    int64_t gk_stride[2];
+    const void* a_log;             /* [H*K] */
+    const void* dt_bias;           /* [H*K] */
+    int32_t p_dtype;               /* kda_dtype of a_log and dt_bias */
+    const void* beta_logit;        /* [B, T, H], x dtype */
+    int64_t beta_stride[2];
+    const float* dg;               /* [B, T, H, K] contiguous */
+    const float* dbeta;            /* [B, T, H] contiguous */
+    void* dgk;                     /* [B, T, H*K] contiguous, x dtype */
+    void* dbeta_logit;             /* [B, T, H] contiguous, x dtype */
+    float* da_log;                 /* [H*K] */
+    float* ddt_bias;               /* [H*K] */
+    float l2_eps;
+    int32_t x_dtype;
+    void* workspace;
+} kda_prep_bwd_args;
+
+size_t kda_prep_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t conv_size);
+int kda_prep_bwd(const kda_prep_bwd_args* args, void* stream);
+
+/* Gradients of kda_output_fwd (the reference differentiates HeadwiseRMSNorm
+ * and the output gate, kimi_linear/kda.py:258-279, 464-470, by autograd):
+ * from dy [B, T, H*V], the gradients of o (d_o [B, T, H, V]) and of the gate
+ * (dgate [B, T, H*V]) in x dtype, and of the norm weight (dweight [H*V],
+ * fp32; token sums as in kda_prep_bwd).  The rounding of the normalised value
+ * to x dtype counts as the identity.  V in {64, 128}. */
+typedef struct kda_output_bwd_args {
+    int64_t B, T, H, V;            /* V in {64, 128} */
+    const void* o;                 /* the forward's o [B, T, H, V], x dtype */
+    int64_t o_stride[3];           /* (batch, token, head) strides; V contiguous */
+    const void* gate;              /* the forward's gate [B, T, H*V], x dtype */
+    int64_t gate_stride[2];
+    const void* weight;            /* [H, V] contiguous */
+    int32_t w_dtype;
+    const void* dy;                /* [B, T, H*V] contiguous, x dtype */
+    void* d_o;                     /* [B, T, H, V] contiguous, x dtype */
+    void* dgate;                   /* [B, T, H*V] contiguous, x dtype */
+    float* dweight;                /* [H*V] */
+    float eps;
+    int32_t x_dtype;
+    void* workspace;               /* kda_output_bwd_workspace_size() bytes */
+} kda_output_bwd_args;
+
+size_t kda_output_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t V);
+int kda_output_bwd(const kda_output_bwd_args* args, void* stream);
 
 /* Human-readable name of a kda_status code (static storage). */
 const char* kda_status_str(int status);

@@ -19,6 +19,9 @@ with its pieces written out independently of torch's library layers:
   :mod:`oracle.kda_oracle`, and the output path (``kda.py:464-470``).
 
 Parameters are taken from a ``state_dict`` with the reference's key names.
+fp64 inputs stay fp64 (everything else is computed in fp32), and
+``keep_graph=True`` keeps the autograd graph to the parameters and x: the
+tests differentiate the fp64 oracle to check the layer's training path.
 
 Pinning: ``tests/test_layer_oracle.py`` checks the convolution against
 ``torch.nn.functional.conv1d``, the norms against ``F.normalize`` and
@@ -36,39 +39,45 @@ import torch
 from .kda_oracle import kda_chunkwise_ref, kda_recurrent_ref
 
 
+def _f(x):
+    """fp64 stays fp64; anything else is computed in fp32."""
+    return x if x.dtype == torch.float64 else x.float()
+
+
 def short_conv_ref(x, weight, bias=None, history=None):
     """Causal depthwise conv.  x: [B, T, D]; weight: [D, 1, C]; history:
-    [B, C-1, D] of earlier inputs (zeros when None).  Returns [B, T, D] fp32."""
-    x = x.float()
+    [B, C-1, D] of earlier inputs (zeros when None).  Returns [B, T, D] fp32
+    (fp64 for fp64 x)."""
+    x = _f(x)
     B, T, D = x.shape
     C = weight.shape[-1]
-    w = weight.float().reshape(D, C)
+    w = _f(weight).reshape(D, C)
     if history is None:
-        history = torch.zeros(B, C - 1, D)
-    full = torch.cat([history.float(), x], dim=1)          # [B, C-1+T, D]
-    out = torch.zeros(B, T, D)
+        history = torch.zeros(B, C - 1, D, dtype=x.dtype)
+    full = torch.cat([_f(history).to(x.dtype), x], dim=1)          # [B, C-1+T, D]
+    out = torch.zeros(B, T, D, dtype=x.dtype)
     for c in range(C):
-        out += full[:, c:c + T] * w[:, c]
+        out = out + full[:, c:c + T] * w[:, c]
     if bias is not None:
-        out += bias.float()
+        out = out + _f(bias)
     return out
 
 
 def l2norm_ref(x, eps):
-    x = x.float()
+    x = _f(x)
     n = torch.sqrt((x * x).sum(-1, keepdim=True))
     return x / torch.clamp(n, min=eps)
 
 
 def head_rmsnorm_ref(x, weight, eps):
-    x = x.float()
-    return x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * weight.float()
+    x = _f(x)
+    return x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * _f(weight)
 
 
 def _linear(x, p, name):
-    y = x @ p[name + ".weight"].float().t()
+    y = x @ _f(p[name + ".weight"]).t()
     b = p.get(name + ".bias")
-    return y + b.float() if b is not None else y
+    return y + _f(b) if b is not None else y
 
 
 def _silu(x):
@@ -83,23 +92,29 @@ def gates_ref(gk, beta_logit, a_log, dt_bias):
     """g = -exp(A_log) * softplus(gk + dt_bias) and beta = sigmoid(logit), in fp32
     (``kda.py:452-460``); ``gk: [B, T, H, K]``, ``beta_logit: [B, T, H]``,
     ``a_log, dt_bias: [H, K]``."""
-    g = -torch.exp(a_log.float()) * _softplus(gk.float() + dt_bias.float())
-    return g, torch.sigmoid(beta_logit.float())
+    g = -torch.exp(_f(a_log)) * _softplus(_f(gk) + _f(dt_bias))
+    return g, torch.sigmoid(_f(beta_logit))
 
 
-def kda_layer_ref(params, cfg, x, state=None, use_cache=False):
-    """fp32 CPU forward of the KDA layer.  ``cfg`` has ``linear_attn_config``,
-    ``l2norm_eps`` and ``rms_norm_eps`` like the reference config.  Returns out,
-    or (out, new_state) with ``use_cache``."""
+def kda_layer_ref(params, cfg, x, state=None, use_cache=False, keep_graph=False):
+    """fp32 CPU forward of the KDA layer (fp64 for fp64 x and parameters).
+    ``cfg`` has ``linear_attn_config``, ``l2norm_eps`` and ``rms_norm_eps`` like
+    the reference config.  Returns out, or (out, new_state) with ``use_cache``.
+    ``keep_graph``: do not detach params and x (for autograd)."""
     la = cfg.linear_attn_config
     H, K, V, Cs = la["num_heads"], la["head_dim"], la["value_head_dim"], la["conv_size"]
-    p = {k: v.detach().cpu() for k, v in params.items()}
-    x = x.detach().cpu().float()
+    if keep_graph:
+        p = dict(params)
+        x = _f(x)
+    else:
+        p = {k: v.detach().cpu() for k, v in params.items()}
+        x = _f(x.detach().cpu())
+    cd = x.dtype
     B, T, _ = x.shape
     keep = max(Cs - 1, 0)
     if use_cache and state is None:
-        state = {"conv": {"q": torch.zeros(B, keep, H * K), "k": torch.zeros(B, keep, H * K),
-                          "v": torch.zeros(B, keep, H * V)}, "recurrent": None}
+        state = {"conv": {"q": torch.zeros(B, keep, H * K, dtype=cd), "k": torch.zeros(B, keep, H * K, dtype=cd),
+                          "v": torch.zeros(B, keep, H * V, dtype=cd)}, "recurrent": None}
     conv = state["conv"] if state is not None else None
     rec = state["recurrent"] if state is not None else None
 
@@ -107,12 +122,12 @@ def kda_layer_ref(params, cfg, x, state=None, use_cache=False):
     conv_out, new_conv = {}, None
     hist = use_cache and conv is not None and keep > 0
     for n in ("q", "k", "v"):
-        h = conv[n].float() if hist else None
+        h = _f(conv[n]) if hist else None
         conv_out[n] = short_conv_ref(ins[n], p[f"conv_{n}.conv.weight"], p.get(f"conv_{n}.conv.bias"), h)
     if use_cache:
         new_conv = {}
         for n in ("q", "k", "v"):
-            full = torch.cat([conv[n].float(), ins[n]], dim=1) if hist else ins[n]
+            full = torch.cat([_f(conv[n]).to(cd), ins[n]], dim=1) if hist else ins[n]
             new_conv[n] = full[:, full.shape[1] - keep:] if keep else full[:, :0]
     q = l2norm_ref(_silu(conv_out["q"]).view(B, T, H, K), cfg.l2norm_eps)
     k = l2norm_ref(_silu(conv_out["k"]).view(B, T, H, K), cfg.l2norm_eps)
@@ -128,14 +143,17 @@ def kda_layer_ref(params, cfg, x, state=None, use_cache=False):
             C = T
         rem = T % C
         body = T - rem
-        o_core = torch.zeros(B, T, H, V)
+        sd = torch.float64 if cd == torch.float64 else torch.float32
+        parts = []
         if body > 0:
-            o_core[:, :body], rec = kda_chunkwise_ref(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
-                                                      beta[:, :body], initial_state=rec, chunk_size=C,
-                                                      state_dtype=torch.float32)
+            o_b, rec = kda_chunkwise_ref(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
+                                         beta[:, :body], initial_state=rec, chunk_size=C, state_dtype=sd)
+            parts.append(o_b)
         if rem > 0:
-            o_core[:, body:], rec = kda_recurrent_ref(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
-                                                      beta[:, body:], state=rec, state_dtype=torch.float32)
+            o_t, rec = kda_recurrent_ref(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
+                                         beta[:, body:], state=rec, state_dtype=sd)
+            parts.append(o_t)
+        o_core = torch.cat(parts, dim=1) if parts else torch.zeros(B, T, H, V, dtype=cd)
         new_rec = rec
     o = head_rmsnorm_ref(o_core, p["g_norm.weight"], cfg.rms_norm_eps)
     gate = torch.sigmoid(_linear(_linear(x, p, "og_proj.0"), p, "og_proj.1").view(B, T, H, V))

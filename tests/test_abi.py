@@ -53,7 +53,9 @@ def test_abi_version_and_status_strings(native):
 @pytest.mark.parametrize("struct,cname", [("KdaFwdArgs", "kda_fwd_args"), ("KdaBwdArgs", "kda_bwd_args"),
                                           ("KdaGateArgs", "kda_gate_args"), ("KdaOutEpilogue", "kda_out_epilogue"),
                                           ("KdaPrepArgs", "kda_prep_args"),
-                                          ("KdaOutputArgs", "kda_output_args")])
+                                          ("KdaOutputArgs", "kda_output_args"),
+                                          ("KdaPrepBwdArgs", "kda_prep_bwd_args"),
+                                          ("KdaOutputBwdArgs", "kda_output_bwd_args")])
 def test_struct_layout_matches_header(native, tmp_path, struct, cname):
     cls = getattr(native, struct)
     fields = [name for name, _ in cls._fields_]
@@ -273,3 +275,59 @@ def test_noalloc_backward_rejects_shapes_beyond_its_buffer(native):
     assert lib.kda_chunkwise_bwd_noalloc(ctypes.byref(a), None) == 1     # NULL input first
     a.B = 0
     assert lib.kda_chunkwise_bwd_noalloc(ctypes.byref(a), None) == 0     # empty: nothing to do
+
+
+def test_layer_backward_workspace_sizes(native):
+    """prep: per 64-token tile, every conv channel's taps and bias plus two gate
+    parameters per q/k channel (fp32); output: per 32-token tile, H * V."""
+    lib = native.load()
+    assert lib.kda_prep_bwd_workspace_size(2, 130, 4, 64, 128, 4) == 2 * 3 * ((2 * 256 + 512) * 5 + 2 * 256) * 4
+    assert lib.kda_prep_bwd_workspace_size(1, 0, 4, 64, 64, 4) == 0
+    assert lib.kda_prep_bwd_workspace_size(1, 16, 4, 64, 64, 0) == 0
+    assert lib.kda_output_bwd_workspace_size(2, 33, 4, 64) == 2 * 2 * 4 * 64 * 4
+    assert lib.kda_output_bwd_workspace_size(2, 0, 4, 64) == 0
+
+
+def test_layer_backward_host_validation_codes(native):
+    lib = native.load()
+    fake = 0x100000   # never dereferenced: every case here fails validation first
+
+    def pargs(**kw):
+        a = native.KdaPrepBwdArgs()
+        a.B, a.T, a.H, a.K, a.V, a.conv_size = 1, 64, 2, 64, 64, 4
+        for i in range(3):
+            a.x[i] = a.conv_w[i] = a.dy[i] = a.dx[i] = a.dw[i] = fake
+        a.workspace = fake
+        a.l2_eps, a.x_dtype, a.w_dtype = 1e-6, native.DTYPE_F16, native.DTYPE_F32
+        for name, val in kw.items():
+            setattr(a, name, val)
+        return ctypes.byref(a)
+
+    call = lib.kda_prep_bwd
+    assert call(None, None) == 1
+    assert call(pargs(T=-1), None) == 2
+    assert call(pargs(K=32), None) == 4 and call(pargs(V=256), None) == 4
+    assert call(pargs(conv_size=5), None) == 4
+    assert call(pargs(x_dtype=9), None) == 3
+    assert call(pargs(l2_eps=0.0), None) == 2
+    assert call(pargs(workspace=None), None) == 1
+    assert call(pargs(gk=fake), None) == 1            # gates without their other pointers
+    assert call(pargs(T=0), None) == 0                # nothing to do
+
+    def oargs(**kw):
+        a = native.KdaOutputBwdArgs()
+        a.B, a.T, a.H, a.V = 1, 8, 2, 64
+        for f in ("o", "gate", "weight", "dy", "d_o", "dgate", "dweight", "workspace"):
+            setattr(a, f, fake)
+        a.eps, a.x_dtype, a.w_dtype = 1e-6, native.DTYPE_F16, native.DTYPE_F32
+        for name, val in kw.items():
+            setattr(a, name, val)
+        return ctypes.byref(a)
+
+    call = lib.kda_output_bwd
+    assert call(None, None) == 1
+    assert call(oargs(V=96), None) == 4
+    assert call(oargs(w_dtype=7), None) == 3
+    assert call(oargs(eps=-1.0), None) == 2
+    assert call(oargs(dweight=None), None) == 1
+    assert call(oargs(T=0), None) == 0
