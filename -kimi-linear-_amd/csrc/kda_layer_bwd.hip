@@ -13,8 +13,8 @@
 //       du = ds sigmoid(u) (1 + u (1 - sigmoid(u)))          (SiLU)
 //       dx[t] = sum_j w[j] du[t + cm - j]                     (causal conv)
 //     and the tile's shares of dw[j] = sum_t du[t] x[t - cm + j], db = sum du.
-//     A 16-token step needs du for cm rows past itself: those are evaluated
-//     again by the next step.  Gates: dgk = dg (-exp(A_log)) sigmoid(z),
+//     An 8-token step needs du for cm rows past itself: those are evaluated
+//     again by the next step (short steps keep the wave's registers few).  Gates: dgk = dg (-exp(A_log)) sigmoid(z),
 //     dbeta_logit = dbeta beta (1 - beta), and the tile's shares of
 //     dA_log = sum dg g and ddt_bias = sum dgk.
 //   output_bwd_kernel, one wave per (batch, 32-token tile, head):
@@ -33,7 +33,7 @@ namespace kda {
 namespace {
 
 constexpr int kMaxConvB = 4;      // largest conv_size (as the forward)
-constexpr int kStep = 16;         // tokens per step of a prep unit
+constexpr int kStep = 8;          // tokens per step of a prep unit
 constexpr int kPrepTile = 64;     // tokens per prep unit
 constexpr int kOutStep = 8;       // tokens per step of an output unit
 constexpr int kOutTile = 32;      // tokens per output unit
@@ -411,9 +411,18 @@ __global__ __launch_bounds__(256) void colsum_kernel(const ColSums c) {
     const ColSum d = c.s[blockIdx.y];
     const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (d.src == nullptr || k >= d.n) return;
-    float acc = 0.f;
-    for (int64_t r = 0; r < c.rows; ++r) acc += d.src[r * d.n + k];
-    d.dst[k] = acc;
+    // eight independent partial sums keep eight loads in flight; the order of
+    // the additions is fixed
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t r = 0;
+    for (; r + 8 <= c.rows; r += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += d.src[(r + u) * d.n + k];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        if (r + u < c.rows) acc[u] += d.src[(r + u) * d.n + k];
+    d.dst[k] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
 }
 
 int launch_colsum(const ColSums& c, int count, hipStream_t stream) {

@@ -241,8 +241,10 @@ def copy_bench(torch, n_sets=5):
 
 def layer_bench(pkg, torch, reps=10):
     """The whole KDA layer at hidden 2048 (16 heads of 128, fp16 weights N(0, 0.02),
-    fp32 state): a B=4 T=2048 prefill forward, and one graph-replayed decode
-    token at B=64 (the layer's static state updated in place)."""
+    fp32 state): a B=4 T=2048 prefill forward, one training step (forward and
+    backward to every parameter and x) at the same shape, and one
+    graph-replayed decode token at B=64 (the layer's static state updated in
+    place)."""
     from kimi_linear_amd.graph_decode import KdaGraphedDecoder
 
     cfg = pkg.linear_attn_config(hidden_size=2048, num_heads=16)
@@ -278,6 +280,23 @@ def layer_bench(pkg, torch, reps=10):
         torch.cuda.synchronize()
         prefill16_ms = e0.elapsed_time(e1) / (reps // 2)
         del xb
+    # training step: the differentiable path, gradients of every parameter and x
+    xt = x.clone().requires_grad_()
+    gout = torch.randn(4, 2048, 2048, device="cuda", dtype=torch.float16)
+    for _ in range(2):
+        layer(xt).backward(gout)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps // 2):
+        layer.zero_grad(set_to_none=True)
+        xt.grad = None
+        layer(xt).backward(gout)
+    e1.record()
+    torch.cuda.synchronize()
+    train_ms = e0.elapsed_time(e1) / (reps // 2)
+    del xt, gout
+    layer.zero_grad(set_to_none=True)
+    with torch.no_grad():
         dec = KdaGraphedDecoder([layer])
         xd = torch.randn(64, 17, 2048, device="cuda", dtype=torch.float16)
         dec.prefill(xd[:, :16])
@@ -297,6 +316,8 @@ def layer_bench(pkg, torch, reps=10):
             "prefill_tokens_per_s": 4 * 2048 / (prefill_ms * 1e-3),
             "prefill_B16_T2048_ms": prefill16_ms,
             "prefill_B16_tokens_per_s": 16 * 2048 / (prefill16_ms * 1e-3),
+            "train_step_B4_T2048_ms": train_ms,
+            "train_tokens_per_s": 4 * 2048 / (train_ms * 1e-3),
             "decode_B64_graph_us_per_token": decode_us}
 
 
