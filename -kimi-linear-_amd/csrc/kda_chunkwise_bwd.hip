@@ -94,6 +94,32 @@ __device__ __forceinline__ f4 tile_mm(FA fa, FB fb, int ln, int lg, f4 acc) {
     return acc;
 }
 
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+// x as a bf16 pair: hi = bf16(x), lo = bf16(x - hi).
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    const __bf16 h = static_cast<__bf16>(x);
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x - static_cast<float>(h)));
+}
+
+// acc += X Y^T for one 16 x 16 tile over the VT = 32 columns of a step, X and
+// Y bf16 pairs (rows of VB elements; xh/xl, yh/yl: row ln of the tile's X and
+// Y rows): hi hi + hi lo + lo hi on the bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16; the dropped lo lo term is ~2^-16 relative).
+// Lane (ln, lg) supplies columns 8 lg .. 8 lg + 7 of both and holds
+// D[4 lg + j][ln] in slot j, the layout of tile_mm.  Only this form runs in
+// these accumulator chains.
+__device__ __forceinline__ f4 mm_pair(const uint16_t* xh, const uint16_t* xl, const uint16_t* yh,
+                                      const uint16_t* yl, int lg, f4 acc) {
+    const bf8 ah = *reinterpret_cast<const bf8*>(xh + 8 * lg), al = *reinterpret_cast<const bf8*>(xl + 8 * lg);
+    const bf8 bh = *reinterpret_cast<const bf8*>(yh + 8 * lg), bl = *reinterpret_cast<const bf8*>(yl + 8 * lg);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    return acc;
+}
+
 // ------------------------------------------------------------------ kernel 1
 
 template <int K>
@@ -504,20 +530,45 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
 
 // Rows padded to a multiple of 4 floats plus 4: 16-byte vector reads along a
 // row, and consecutive rows 4 banks apart.
+// The column step's tiles: S and dS (K rows), dO, R, P, dP, dR (CT rows), VT
+// columns each.  PAIR (16-bit activations): bf16 pairs, x = hi + lo (hi = x
+// rounded to bf16, lo = the rest rounded to bf16: |x - hi - lo| <= 2^-18 |x|),
+// rows of VB elements (80 bytes: every MFMA fragment, 8 consecutive columns,
+// is one 16-byte read), for the bf16 matrix cores.  Otherwise (fp32
+// activations) fp32 rows of VP floats for the fp32 matrix cores, exact
+// products.
+constexpr int VB = VT + 8;
+constexpr int VP = VT + 4;
+template <int K, bool PAIR>
+struct StepTiles;
 template <int K>
-struct __align__(16) ChunkSmem {
-    static constexpr int KP = K + 4, VP = VT + 4;
-    float q[CT][KP];            // scale * q
-    float k[CT][KP];
-    float gc[CT][KP];           // in-chunk cumulative log decay G
-    float e[CT][KP];            // exp(G); then, per element, dG
-    float S[K][VP];             // state at the chunk start (checkpoint), VT columns
-    float dS[K][VP];            // gradient of the state at the chunk end, VT columns
+struct StepTiles<K, true> {
+    uint16_t S[2][K][VB];       // state at the chunk start (checkpoint): hi, lo
+    uint16_t dS[2][K][VB];      // gradient of the state at the chunk end
+    uint16_t dO[2][CT][VB];
+    uint16_t R[2][CT][VB];
+    uint16_t P[2][CT][VB];
+    uint16_t dP[2][CT][VB];
+    uint16_t dR[2][CT][VB];
+};
+template <int K>
+struct StepTiles<K, false> {
+    float S[K][VP];
+    float dS[K][VP];
     float dO[CT][VP];
     float R[CT][VP];
     float P[CT][VP];
     float dP[CT][VP];
     float dR[CT][VP];
+};
+template <int K, bool PAIR>
+struct __align__(16) ChunkSmem {
+    static constexpr int KP = K + 4;
+    float q[CT][KP];            // scale * q
+    float k[CT][KP];
+    float gc[CT][KP];           // in-chunk cumulative log decay G
+    float e[CT][KP];            // exp(G); then, per element, dG
+    StepTiles<K, PAIR> st;
     float A[CT][CT + 1];        // A (i <= c)
     float L[CT][CT + 1];        // L (i < c)
     float N[CT][CT + 1];        // (I + Diag(beta) L)^-1
@@ -532,7 +583,7 @@ struct __align__(16) ChunkSmem {
     // the element step's copies of dA and dX live in the dS area when it is
     // large enough (K = 128), here otherwise
     static constexpr int CPY = 4 * CT * (CT + 4);
-    static constexpr bool CPY_IN_DS = K * VP >= CPY;
+    static constexpr bool CPY_IN_DS = sizeof(StepTiles<K, PAIR>::dS) / 4 >= CPY;   // floats in the dS area
     float cpy[CPY_IN_DS ? 4 : CPY];
 };
 static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
@@ -544,7 +595,8 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     constexpr int SPT = K * VT / NT;        // state tile elements per thread
     constexpr int TPR = VT / SPT;           // threads per state row
     static_assert(NT / K * K <= CT * (CT + 1), "the row-group sums fit Y");
-    __shared__ ChunkSmem<K> sm;
+    constexpr bool PAIR = sizeof(TI) == 2;
+    __shared__ ChunkSmem<K, PAIR> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
     const TI* dop = static_cast<const TI*>(a.d_o);
@@ -657,18 +709,34 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     const int r0t = 16 * ((w >> 1) & 1), c0t = 16 * (w & 1);
     f4 accm = {0.f, 0.f, 0.f, 0.f};         // dA (waves 0-3), dM (waves 4-7)
     f4 dqe = accm, dke = accm, dkf = accm;
-    float deps = 0.f;
+    float deps = 0.f;            // this thread's share of rowsum(dS * S) for row st_row
     for (int vt = 0; vt < nvt; ++vt) {
+        auto& tl = sm.st;
 #pragma unroll
-        for (int j = 0; j < SPT; ++j) {
-            sm.S[st_row][st_col + j] = ps[j];
-            sm.dS[st_row][st_col + j] = pds[j];
+        for (int j = 0; j < SPT; ++j) deps = fmaf(pds[j], ps[j], deps);
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int j = 0; j < SPT; ++j) {
+                split_bf16(ps[j], tl.S[0][st_row][st_col + j], tl.S[1][st_row][st_col + j]);
+                split_bf16(pds[j], tl.dS[0][st_row][st_col + j], tl.dS[1][st_row][st_col + j]);
+            }
+            split_bf16(pr, tl.R[0][tc][tv], tl.R[1][tc][tv]);
+            split_bf16(pp, tl.P[0][tc][tv], tl.P[1][tc][tv]);
+            split_bf16(Elem<TI>::ld(&pdo), tl.dO[0][tc][tv], tl.dO[1][tc][tv]);
+            split_bf16(pdp, tl.dP[0][tc][tv], tl.dP[1][tc][tv]);
+            split_bf16(pdr, tl.dR[0][tc][tv], tl.dR[1][tc][tv]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < SPT; ++j) {
+                tl.S[st_row][st_col + j] = ps[j];
+                tl.dS[st_row][st_col + j] = pds[j];
+            }
+            tl.R[tc][tv] = pr;
+            tl.P[tc][tv] = pp;
+            tl.dO[tc][tv] = Elem<TI>::ld(&pdo);
+            tl.dP[tc][tv] = pdp;
+            tl.dR[tc][tv] = pdr;
         }
-        sm.R[tc][tv] = pr;
-        sm.P[tc][tv] = pp;
-        sm.dO[tc][tv] = Elem<TI>::ld(&pdo);
-        sm.dP[tc][tv] = pdp;
-        sm.dR[tc][tv] = pdr;
         {
             const int64_t row = static_cast<int64_t>(n) * CT + tc;
             if (row < T) Elem<TI>::st(dvp + ((b * T + row) * H + h) * V + static_cast<int64_t>(vt) * VT + tv, pdr);
@@ -677,32 +745,46 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         __syncthreads();
 
         // waves 0-3: dA += dO P^T; waves 4-7: dM += dP R^T; every element wave:
-        // d(q~E) += dO S^T, d(kE) -= dR S^T, d(kF) += P dS^T; deps
-        if (w < 4)
-            accm = tile_mm<VT>([&](int r, int v) { return sm.dO[r0t + r][v]; },
-                               [&](int v, int i) { return sm.P[c0t + i][v]; }, ln, lg, accm);
-        else if (w < 8)
-            accm = tile_mm<VT>([&](int r, int v) { return sm.dP[r0t + r][v]; },
-                               [&](int v, int i) { return sm.R[c0t + i][v]; }, ln, lg, accm);
-        if (tw) {
-            dqe = tile_mm<VT>([&](int r, int v) { return sm.dO[ert + r][v]; },
-                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dqe);
-            dke = tile_mm<VT>([&](int r, int v) { return -sm.dR[ert + r][v]; },
-                              [&](int v, int kc) { return sm.S[ekk - ln + kc][v]; }, ln, lg, dke);
-            dkf = tile_mm<VT>([&](int r, int v) { return sm.P[ert + r][v]; },
-                              [&](int v, int kc) { return sm.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
-        }
-        if (t >= 512 && t - 512 < K) {
-            const int x = t - 512;
-#pragma unroll 8
-            for (int vv = 0; vv < VT; ++vv) deps += sm.dS[x][vv] * sm.S[x][vv];
+        // d(q~E) += dO S^T, d(kE) -= dR S^T (accumulated as + and negated
+        // below), d(kF) += P dS^T
+        if constexpr (PAIR) {
+            if (w < 8) {
+                const uint16_t (*xa)[CT][VB] = w < 4 ? tl.dO : tl.dP;
+                const uint16_t (*ya)[CT][VB] = w < 4 ? tl.P : tl.R;
+                accm = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], ya[0][c0t + ln], ya[1][c0t + ln], lg, accm);
+            }
+            if (tw) {
+                const int er = ert + ln, sr = ekk;      // rows of the element tile and of its channels
+                dqe = mm_pair(tl.dO[0][er], tl.dO[1][er], tl.S[0][sr], tl.S[1][sr], lg, dqe);
+                dke = mm_pair(tl.dR[0][er], tl.dR[1][er], tl.S[0][sr], tl.S[1][sr], lg, dke);
+                dkf = mm_pair(tl.P[0][er], tl.P[1][er], tl.dS[0][sr], tl.dS[1][sr], lg, dkf);
+            }
+        } else {
+            if (w < 4)
+                accm = tile_mm<VT>([&](int r, int v) { return tl.dO[r0t + r][v]; },
+                                   [&](int v, int i) { return tl.P[c0t + i][v]; }, ln, lg, accm);
+            else if (w < 8)
+                accm = tile_mm<VT>([&](int r, int v) { return tl.dP[r0t + r][v]; },
+                                   [&](int v, int i) { return tl.R[c0t + i][v]; }, ln, lg, accm);
+            if (tw) {
+                dqe = tile_mm<VT>([&](int r, int v) { return tl.dO[ert + r][v]; },
+                                  [&](int v, int kc) { return tl.S[ekk - ln + kc][v]; }, ln, lg, dqe);
+                dke = tile_mm<VT>([&](int r, int v) { return tl.dR[ert + r][v]; },
+                                  [&](int v, int kc) { return tl.S[ekk - ln + kc][v]; }, ln, lg, dke);
+                dkf = tile_mm<VT>([&](int r, int v) { return tl.P[ert + r][v]; },
+                                  [&](int v, int kc) { return tl.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
+            }
         }
         __syncthreads();
     }
+    dke = f4{0.f, 0.f, 0.f, 0.f} - dke;
+    // deps: the shares of the TPR threads of each state row
+#pragma unroll
+    for (int m = 1; m < TPR; m <<= 1) deps += __shfl_xor(deps, m);
     // 16-byte-aligned copies for the element step (in the dS area, no longer
     // read, when it is large enough): dA by rows and by columns, dX (the
     // final dM) by rows and by columns
-    float* cpy = ChunkSmem<K>::CPY_IN_DS ? &sm.dS[0][0] : &sm.cpy[0];
+    float* cpy = ChunkSmem<K, PAIR>::CPY_IN_DS ? reinterpret_cast<float*>(&sm.st.dS) : &sm.cpy[0];
     float (*dAr)[CT + 4] = reinterpret_cast<float (*)[CT + 4]>(cpy);
     float (*dAc)[CT + 4] = dAr + CT;
     float (*dXr)[CT + 4] = dAr + 2 * CT;
@@ -721,12 +803,12 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
             }
         }
     }
-    if (t >= 512 && t - 512 < K) sm.deps[t - 512] = deps;
+    if (t % TPR == 0) sm.deps[st_row] = deps;
     __syncthreads();
 
     // ------------------------------- dbeta (M = N Diag(beta)), dN in place
     // column sums of dM * N: over the two rows of each wave, then over the waves
-    float* red = &sm.S[0][0];               // [NT / 64][CT]; S is no longer read
+    float* red = reinterpret_cast<float*>(&sm.st.S);   // [NT / 64][CT]; S is no longer read
     {
         const int c = t / CT, i = t % CT;
         const float dm = sm.dM[c][i];
@@ -887,7 +969,7 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     // ------------------------------- dg (reverse in-chunk cumsum), dbeta
     // thread (rg, kk): suffix sums over its rows, then over the later row groups
     {
-        float* gtot = &sm.dS[0][0];         // [NT / K][K]; dS is no longer read
+        float* gtot = reinterpret_cast<float*>(&sm.st.dS);   // [NT / K][K]; dS is no longer read
         float sfx[RPT];
         float acc = 0.f;
 #pragma unroll
