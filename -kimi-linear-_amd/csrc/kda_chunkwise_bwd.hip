@@ -327,33 +327,55 @@ __global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, con
 
 // ------------------------------------------------------------------ kernel 2
 
+// The chain's operands as bf16 hi/lo pairs ([0] hi, [1] lo, as in the chunk
+// kernel's column steps), each laid out along its contraction so that every
+// MFMA fragment (8 consecutive elements) is one 16-byte read: the transposed
+// (q~*E), (k*E), A, N, dO, dP, dR and dS, and k*F as it is.
+constexpr int NS = 512;         // threads per workgroup of bwd_state_kernel
+constexpr int NWS = NS / 64;    // its waves
+
 template <int K, int VA>
 struct __align__(16) StateSmem {
-    static constexpr int KP = K + 4, AP = VA + 4;
-    float qe[CT][KP];           // scale q exp(G)
-    float ke[CT][KP];           // k exp(G)
-    float kf[CT][KP];           // k exp(G_last - G)
-    float dS[K][AP];            // gradient of the state at the chunk end, then at its start
-    float dO[CT][AP];
-    float dP[CT][AP];
-    float dR[CT][AP];
-    float A[CT][CT + 1];
-    float N[CT][CT + 1];
-    float tot[NT / K][K];       // per row group, the sum of its g
+    static constexpr int KB = K + 8, TB = CT + 8;
+    uint16_t qeT[2][K][TB];     // (scale q exp(G))^T: [channel][token]
+    uint16_t keT[2][K][TB];     // (k exp(G))^T
+    uint16_t kf[2][CT][KB];     // k exp(G_last - G): [token][channel]
+    uint16_t dST[2][VA][KB];    // dS^T at the chunk end: [column][channel]
+    uint16_t dOT[2][VA][TB];    // dO^T: [column][token]
+    uint16_t dPT[2][VA][TB];
+    uint16_t dRT[2][VA][TB];
+    uint16_t AT[2][CT][TB];     // A^T: [c][c2] = A[c2][c]
+    uint16_t NT_[2][CT][TB];    // N^T
+    float tot[NS / K][K];       // per row group, the sum of its g
     float beta[CT];
     float eps[K];
 };
 
+// Four values of consecutive rows (a lane's accumulator slots) into a
+// transposed bf16 pair row: hi and lo, 8 bytes each.
+__device__ __forceinline__ void put4_pair(uint16_t* hi, uint16_t* lo, const f4& x) {
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split_bf16(x[j], h[j], l[j]);
+    *reinterpret_cast<uint2*>(hi) = uint2{h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16)};
+    *reinterpret_cast<uint2*>(lo) = uint2{l[0] | (uint32_t(l[1]) << 16), l[2] | (uint32_t(l[3]) << 16)};
+}
+
+// One workgroup per (b, h, VA state columns), the chunks in reverse.  dS, the
+// gradient of the state, stays in fp32 accumulators (tile ti = w + 16 m of
+// each wave: channels 16 (ti / VTL), columns 16 (ti % VTL)) and is copied as a
+// transposed bf16 pair for the next chunk's dP product.  All products on the
+// bf16 matrix cores as pairs (mm_pair, ~2^-17 relative per product).
 template <int K, int VA, typename TI>
-__global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, const BwdWs ws) {
-    constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
-    constexpr int DPT = CT * VA / NT;       // dO elements per thread
-    constexpr int SPT = K * VA / NT;        // dS elements per thread
+__global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, const BwdWs ws) {
+    constexpr int RPT = CT * K / NS;        // consecutive rows per thread, one channel
+    constexpr int DPT = CT * VA / NS;       // dO elements per thread
     constexpr int VTL = VA / 16;            // 16-column tiles
     constexpr int NDP = 2 * VTL;            // tiles of dP and dR (CT x VA)
     constexpr int NTS = (K / 16) * VTL;     // tiles of dS (K x VA)
-    constexpr int TPW = (NTS + 15) / 16;    // dS tiles per wave
-    static_assert(RPT >= 1 && DPT >= 1 && SPT >= 1 && NDP <= 16, "thread mapping");
+    constexpr int TPW = (NTS + NWS - 1) / NWS;  // dS tiles per wave
+    constexpr int APT = CT * CT / NS;       // elements of A (and of N) per thread
+    static_assert(RPT >= 1 && DPT >= 1 && NDP <= NWS, "thread mapping");
     __shared__ StateSmem<K, VA> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
@@ -367,48 +389,63 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
     const int x = t % K, rg = t / K;
 
-    for (int j = 0; j < SPT; ++j) {
-        const int e = t + NT * j, r = e / VA, c = e % VA;
-        sm.dS[r][c] = a.d_state_out ? a.d_state_out[(bh * K + r) * V + v0 + c] : 0.f;
+    // dS at the end of the sequence into the accumulators and its pair copy
+    f4 accs[TPW];
+#pragma unroll
+    for (int m = 0; m < TPW; ++m) {
+        const int ti = w + NWS * m;
+        if (ti < NTS) {
+            const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                accs[m][j] = a.d_state_out ? a.d_state_out[(bh * K + r0 + 4 * lg + j) * V + v0 + c0 + ln] : 0.f;
+            put4_pair(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
+        }
     }
 
     // fetched elements stay in the input dtype until they are staged: a
     // conversion next to its load would wait for it
     TI pq[RPT], pk[RPT], pdo[DPT];
-    float pg[RPT], pa = 0.f, pn = 0.f, pb = 0.f;
+    float pg[RPT], pa[APT], pn[APT], pb = 0.f;
+    // global addresses as a per-chunk uniform base plus a loop-invariant
+    // 32-bit offset per thread (registers for the pipeline, not for addresses)
+    const uint32_t HK = static_cast<uint32_t>(H * K), HV = static_cast<uint32_t>(H * V);
+    const uint32_t oqk = static_cast<uint32_t>(RPT * rg) * HK + x;
     auto fetch = [&](int n) {
+        const int64_t r0 = static_cast<int64_t>(n) * CT;
+        const TI* qn = qp + ((b * T + r0) * H + h) * K;
+        const TI* kn = kp + ((b * T + r0) * H + h) * K;
+        const float* gn = a.g + ((b * T + r0) * H + h) * K;
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
-            const int64_t row = static_cast<int64_t>(n) * CT + RPT * rg + j;
             pq[j] = pk[j] = TI{};
             pg[j] = 0.f;
-            if (row < T) {
-                const int64_t o = ((b * T + row) * H + h) * K + x;
-                pq[j] = qp[o];
-                pk[j] = kp[o];
-                pg[j] = a.g[o];
+            if (r0 + RPT * rg + j < T) {
+                const uint32_t o = oqk + j * HK;
+                pq[j] = qn[o];
+                pk[j] = kn[o];
+                pg[j] = gn[o];
             }
         }
+        const TI* don = dop + ((b * T + r0) * H + h) * V + v0;
 #pragma unroll
         for (int j = 0; j < DPT; ++j) {
-            const int e = t + NT * j;
-            const int64_t row = static_cast<int64_t>(n) * CT + e / VA;
-            pdo[j] = row < T ? dop[((b * T + row) * H + h) * V + v0 + e % VA] : TI{};
+            const int e = t + NS * j;
+            pdo[j] = r0 + e / VA < T ? don[static_cast<uint32_t>(e / VA) * HV + e % VA] : TI{};
         }
         const int64_t cb = bh * nck + n;
-        pa = ws.A[cb * CT * CT + t];
-        pn = ws.N[cb * CT * CT + t];
-        if (t < CT) {
-            const int64_t row = static_cast<int64_t>(n) * CT + t;
-            pb = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
+#pragma unroll
+        for (int j = 0; j < APT; ++j) {
+            pa[j] = ws.A[cb * CT * CT + t + NS * j];
+            pn[j] = ws.N[cb * CT * CT + t + NS * j];
         }
+        if (t < CT) pb = r0 + t < T ? a.beta[(b * T + r0) * H + h + static_cast<uint32_t>(t) * H] : 0.f;
     };
     if (nck > 0) fetch(nck - 1);
 
-    f4 accs[TPW];
     for (int n = nck - 1; n >= 0; --n) {
         const int64_t cb = bh * nck + n;
-        // stage chunk n; fetch chunk n - 1
+        // stage chunk n (A^T, N^T, dO^T as pairs, the row groups' g sums); fetch chunk n - 1
         float cq[RPT], ck[RPT], cg[RPT];
         float run = 0.f;
 #pragma unroll
@@ -420,12 +457,16 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         }
         sm.tot[rg][x] = run;
 #pragma unroll
-        for (int j = 0; j < DPT; ++j) {
-            const int e = t + NT * j;
-            sm.dO[e / VA][e % VA] = Elem<TI>::ld(&pdo[j]);
+        for (int j = 0; j < APT; ++j) {
+            const int e = t + NS * j;
+            split_bf16(pa[j], sm.AT[0][e % CT][e / CT], sm.AT[1][e % CT][e / CT]);
+            split_bf16(pn[j], sm.NT_[0][e % CT][e / CT], sm.NT_[1][e % CT][e / CT]);
         }
-        sm.A[t / CT][t % CT] = pa;
-        sm.N[t / CT][t % CT] = pn;
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) {
+            const int e = t + NS * j, c = e / VA, v = e % VA;
+            split_bf16(Elem<TI>::ld(&pdo[j]), sm.dOT[0][v][c], sm.dOT[1][v][c]);
+        }
         if (t < CT) sm.beta[t] = pb;
         if (n > 0) fetch(n - 1);
         __syncthreads();
@@ -434,7 +475,7 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         {
             float pre = 0.f, last = 0.f;
 #pragma unroll
-            for (int r = 0; r < NT / K; ++r) {
+            for (int r = 0; r < NS / K; ++r) {
                 const float s = sm.tot[r][x];
                 pre += r < rg ? s : 0.f;
                 last += s;
@@ -444,45 +485,47 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
                 const int c = RPT * rg + j;
                 const float G = pre + cg[j];
                 const float E = __expf(G), F = __expf(last - G);
-                sm.qe[c][x] = a.scale * cq[j] * E;
-                sm.ke[c][x] = ck[j] * E;
-                sm.kf[c][x] = ck[j] * F;
+                split_bf16(a.scale * cq[j] * E, sm.qeT[0][x][c], sm.qeT[1][x][c]);
+                split_bf16(ck[j] * E, sm.keT[0][x][c], sm.keT[1][x][c]);
+                split_bf16(ck[j] * F, sm.kf[0][c][x], sm.kf[1][c][x]);
             }
             if (rg == 0) sm.eps[x] = __expf(last);
         }
         __syncthreads();
 
-        // dS_end to the workspace; dP = (k*F) dS + A^T dO; Diag(eps) dS + (q~*E)^T dO
-        for (int j = 0; j < SPT; ++j) {
-            const int e = t + NT * j, r = e / VA, c = e % VA;
-            ws.dS[(cb * K + r) * V + v0 + c] = sm.dS[r][c];
+        // dS_end to the workspace; dP = (k*F) dS + A^T dO; dS <- Diag(eps) dS + (q~*E)^T dO
+#pragma unroll
+        for (int m = 0; m < TPW; ++m) {
+            const int ti = w + NWS * m;
+            if (ti < NTS) {
+                const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
+                float* dsn = ws.dS + cb * K * V + v0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dsn[static_cast<uint32_t>(r0 + 4 * lg + j) * V + c0 + ln] = accs[m][j];
+            }
         }
         if (w < NDP) {
             const int r0t = 16 * (w / VTL), c0t = 16 * (w % VTL);
             f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = tile_mm<K>([&](int r, int xx) { return sm.kf[r0t + r][xx]; },
-                             [&](int xx, int v) { return sm.dS[xx][c0t + v]; }, ln, lg, acc);
-            acc = tile_mm<CT>([&](int r, int c2) { return sm.A[c2][r0t + r]; },
-                              [&](int c2, int v) { return sm.dO[c2][c0t + v]; }, ln, lg, acc);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = r0t + 4 * lg + j;
-                sm.dP[c][c0t + ln] = acc[j];
-                ws.dP[(cb * CT + c) * V + v0 + c0t + ln] = acc[j];
-            }
+            for (int u = 0; u < K / 32; ++u)
+                acc = mm_pair(&sm.kf[0][r0t + ln][32 * u], &sm.kf[1][r0t + ln][32 * u], &sm.dST[0][c0t + ln][32 * u],
+                              &sm.dST[1][c0t + ln][32 * u], lg, acc);
+            acc = mm_pair(sm.AT[0][r0t + ln], sm.AT[1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[1][c0t + ln], lg, acc);
+            float* dpn = ws.dP + cb * CT * V + v0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln] = acc[j];
+            put4_pair(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[1][c0t + ln][r0t + 4 * lg], acc);
         }
 #pragma unroll
         for (int m = 0; m < TPW; ++m) {
-            const int ti = w + 16 * m;
+            const int ti = w + NWS * m;
             if (ti < NTS) {
-                const int r0t = 16 * (ti / VTL), c0t = 16 * (ti % VTL);
+                const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int xx = r0t + 4 * lg + j;
-                    accs[m][j] = sm.eps[xx] * sm.dS[xx][c0t + ln];
-                }
-                accs[m] = tile_mm<CT>([&](int r, int c) { return sm.qe[c][r0t + r]; },
-                                      [&](int c, int v) { return sm.dO[c][c0t + v]; }, ln, lg, accs[m]);
+                for (int j = 0; j < 4; ++j) accs[m][j] *= sm.eps[r0 + 4 * lg + j];
+                accs[m] = mm_pair(sm.qeT[0][r0 + ln], sm.qeT[1][r0 + ln], sm.dOT[0][c0 + ln], sm.dOT[1][c0 + ln], lg,
+                                  accs[m]);
             }
         }
         __syncthreads();
@@ -490,38 +533,43 @@ __global__ __launch_bounds__(NT) void bwd_state_kernel(const kda_bwd_args a, con
         // dR = M^T dP = Diag(beta) N^T dP (= dV, which bwd_chunk_kernel writes out)
         if (w < NDP) {
             const int r0t = 16 * (w / VTL), c0t = 16 * (w % VTL);
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = tile_mm<CT>([&](int r, int c2) { return sm.N[c2][r0t + r]; },
-                              [&](int c2, int v) { return sm.dP[c2][c0t + v]; }, ln, lg, acc);
+            f4 acc = mm_pair(sm.NT_[0][r0t + ln], sm.NT_[1][r0t + ln], sm.dPT[0][c0t + ln], sm.dPT[1][c0t + ln], lg,
+                             f4{0.f, 0.f, 0.f, 0.f});
+            float* drn = ws.dR + cb * CT * V + v0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int c = r0t + 4 * lg + j;
-                const float dr = acc[j] * sm.beta[c];
-                sm.dR[c][c0t + ln] = dr;
-                ws.dR[(cb * CT + c) * V + v0 + c0t + ln] = dr;
+                acc[j] *= sm.beta[r0t + 4 * lg + j];
+                drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln] = acc[j];
             }
+            put4_pair(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[1][c0t + ln][r0t + 4 * lg], acc);
         }
         __syncthreads();
 
-        // dS_start = Diag(eps) dS + (q~*E)^T dO - (k*E)^T dR
+        // dS_start = Diag(eps) dS + (q~*E)^T dO - (k*E)^T dR, and its pair copy
+        // for the next chunk's dP (read after the next chunk's first barrier)
 #pragma unroll
         for (int m = 0; m < TPW; ++m) {
-            const int ti = w + 16 * m;
+            const int ti = w + NWS * m;
             if (ti < NTS) {
-                const int r0t = 16 * (ti / VTL), c0t = 16 * (ti % VTL);
-                accs[m] = tile_mm<CT>([&](int r, int c) { return -sm.ke[c][r0t + r]; },
-                                      [&](int c, int v) { return sm.dR[c][c0t + v]; }, ln, lg, accs[m]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) sm.dS[r0t + 4 * lg + j][c0t + ln] = accs[m][j];
+                const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
+                const f4 kr = mm_pair(sm.keT[0][r0 + ln], sm.keT[1][r0 + ln], sm.dRT[0][c0 + ln], sm.dRT[1][c0 + ln],
+                                      lg, f4{0.f, 0.f, 0.f, 0.f});
+                accs[m] -= kr;
+                put4_pair(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
             }
         }
-        // the next chunk's staging writes none of ke, dR, dS: no barrier here
+        // the next chunk's staging writes none of keT, dRT, dST before its
+        // first barrier: no barrier here
     }
-    __syncthreads();
     if (a.d_state_in) {
-        for (int j = 0; j < SPT; ++j) {
-            const int e = t + NT * j, r = e / VA, c = e % VA;
-            a.d_state_in[(bh * K + r) * V + v0 + c] = sm.dS[r][c];
+#pragma unroll
+        for (int m = 0; m < TPW; ++m) {
+            const int ti = w + NWS * m;
+            if (ti < NTS) {
+                const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a.d_state_in[(bh * K + r0 + 4 * lg + j) * V + v0 + c0 + ln] = accs[m][j];
+            }
         }
     }
 }
@@ -1007,10 +1055,10 @@ int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
     if (a.V % 64 == 0)
-        hipLaunchKernelGGL((bwd_state_kernel<K, 64, TI>), dim3(static_cast<unsigned>(BH * (a.V / 64))), dim3(NT), 0,
+        hipLaunchKernelGGL((bwd_state_kernel<K, 64, TI>), dim3(static_cast<unsigned>(BH * (a.V / 64))), dim3(NS), 0,
                            stream, a, ws);
     else
-        hipLaunchKernelGGL((bwd_state_kernel<K, 32, TI>), dim3(static_cast<unsigned>(BH * (a.V / 32))), dim3(NT), 0,
+        hipLaunchKernelGGL((bwd_state_kernel<K, 32, TI>), dim3(static_cast<unsigned>(BH * (a.V / 32))), dim3(NS), 0,
                            stream, a, ws);
     if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     if (nck > 0) {
