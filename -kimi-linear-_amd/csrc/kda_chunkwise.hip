@@ -103,10 +103,6 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 // (k = q = v = g = beta = 0) -- with no clamping or masking.  The row offset
 // is wave-uniform and goes in the scalar offset; the lane offset is one
 // register per tensor.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                             static_cast<int>(nbytes), 0x00020000);
-}
 template <int BYTES> struct BLoad;
 template <> struct BLoad<2> {
     static constexpr int W = 1;
@@ -140,22 +136,6 @@ template <> struct BLoad<16> {
         w[3] = x[3];
     }
 };
-
-// Values are held raw, one load per register set, and converted only where
-// they are used.  Left alone, the compiler hoists a conversion up to the
-// load, which puts a wait for the whole prefetch right after it is issued.
-// An empty volatile asm that "modifies" the registers at the point of use
-// keeps every such instruction, and the wait, there.
-template <int N>
-__device__ __forceinline__ void use_here(uint32_t (&r)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
-}
-template <int N, int M>
-__device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) use_here(r[i]);
-}
 
 // Element j of a raw row of TQ values, as fp16 (exact for fp16 inputs).
 template <typename TQ, int W>

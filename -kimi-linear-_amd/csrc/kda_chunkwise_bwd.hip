@@ -44,6 +44,7 @@
 // caller's activation dtype (fp32, fp16 or bf16; every product in fp32); g,
 // beta, the checkpoints, dg, dbeta and the state gradients are fp32.  The chunk-sized products run on the fp32
 // matrix cores (v_mfma_f32_16x16x4f32, no precision loss).
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -122,6 +123,8 @@ __device__ __forceinline__ f4 mm_pair(const uint16_t* xh, const uint16_t* xl, co
 
 // ------------------------------------------------------------------ kernel 1
 
+constexpr int NP = 512;         // threads per workgroup of bwd_pairs_kernel
+
 template <int K>
 struct __align__(16) PairSmem {
     static constexpr int KP = K + 4;
@@ -131,198 +134,351 @@ struct __align__(16) PairSmem {
     float A[CT][CT + 1];
     float L[CT][CT + 1];
     float N[CT][CT + 1];
-    float Y[CT][CT + 1];
+    float part[4][2][16][17];   // the waves' shares of A_10 and L_10; first the row groups' g sums
+    float Y[16][17];
     float beta[CT];
 };
 
-// Sum over the 16 lanes of a DPP row (every lane gets it): quad_perm xor 1,
-// xor 2, then row_ror 4 and 8.
-__device__ __forceinline__ float row16_sum(float x) {
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
-    return x;
+// The bf16 pair products of mm_pair on fragments held in registers.
+__device__ __forceinline__ f4 mfma_pair(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, f4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    return acc;
 }
 
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+
+// Eight values as bf16 pairs (hi = bf16(x), lo = bf16(x - hi)), two values
+// per conversion.
+__device__ __forceinline__ void split8(const float (&v)[8], bf8& hi, bf8& lo) {
+    w4 hw, lw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e], v[2 * e + 1]}, bf2));
+        const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xffff0000u);
+        hw[e] = hb;
+        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e] - h0, v[2 * e + 1] - h1}, bf2));
+    }
+    hi = __builtin_bit_cast(bf8, hw);
+    lo = __builtin_bit_cast(bf8, lw);
+}
+
+// Eight values as fp16, two per conversion.
+__device__ __forceinline__ h8 to_h8(const float (&v)[8]) {
+    w4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        r[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e], v[2 * e + 1]}, hf2));
+    return __builtin_bit_cast(h8, r);
+}
+
+__device__ __forceinline__ void lds8(const float* p, float (&v)[8]) {
+    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = b[e];
+    }
+}
+
+// c + X Y for 16 x 16 fp32 tiles on the fp32 matrix cores (four 16x16x4
+// steps): xt holds X^T in accumulator layout (lane (ln, lg) slot u:
+// X[ln][4 lg + u]), y holds Y in accumulator layout (slot u: Y[4 lg + u][ln]);
+// the result is in accumulator layout.
+__device__ __forceinline__ f4 mm_acc(const f4& xt, const f4& y, f4 c) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) c = __builtin_amdgcn_mfma_f32_16x16x4f32(xt[u], y[u], c, 0, 0, 0);
+    return c;
+}
+
+// A value fetched raw (16-bit values in the low half) as fp32.
+template <typename TI>
+__device__ __forceinline__ float raw_f32(uint32_t w) {
+    if constexpr (sizeof(TI) == 4) {
+        return __uint_as_float(w);
+    } else if constexpr (Elem<TI>::code == KDA_DTYPE_F16) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+    } else {
+        return __uint_as_float(w << 16);
+    }
+}
+
+// A, L and N of every chunk.  Every decay factor is a product of per-token
+// decays between two rows, kept <= 1 by factoring through a reference row
+// between them:
+//  * diagonal 16-row blocks, by decay level: a pair i < c of a block has a
+//    unique highest differing bit lev; both rows sit in the aligned group of
+//    2^(lev+1) rows whose lower half ends at ref(c) = ref(i), i <= ref < c,
+//    and exp(G_c - G_i) = exp(G_c - G_ref) exp(G_ref - G_i).  Per level, with
+//    f_r = exp(-|G_r - G_ref(r)|) for every row r of the block (ref(r): r's
+//    reference row at that level, r in either half), the products
+//    (q~ f)(k f)^T and (k f)(k f)^T over the channels hold A and L on that
+//    level's pairs (c upper, i lower); a row r whose low lev bits are all
+//    ones and bit lev clear is its own reference row (f_r = 1), so the
+//    diagonal A[r][r] comes from that level's product too, except for the
+//    block's row 15, one dot product of its own;
+//  * the block below the diagonal, through row 15 (the reference row of
+//    every such pair).
+// Products on the bf16 matrix cores as hi/lo pairs (~2^-17 relative each).
+// N = (I + X)^-1 per diagonal block, X = Diag(beta) L nilpotent:
+// (I - X)(I + X^2)(I + X^4)(I + X^8) on the fp32 matrix cores in registers,
+// then N10 = -N11 X10 N00.
+// Wave w: block w / 4, level w % 4; waves 0 .. K/32 - 1 also one 32-channel
+// step of the block below the diagonal.  Persistent: workgroup g takes
+// chunks g, g + G, ... (G workgroups) and fetches the next one's inputs into
+// registers while the current one is computed.
 template <int K, typename TI>
-__global__ __launch_bounds__(NT) void bwd_pairs_kernel(const kda_bwd_args a, const BwdWs ws) {
-    static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
-    constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
-    static_assert(NT / K * K <= CT * (CT + 1), "the row-group sums fit Y");
+__global__ __launch_bounds__(NP) void bwd_pairs_kernel(const kda_bwd_args a, const BwdWs ws, int64_t nchunks) {
+    static_assert(NP % K == 0 && (CT * K) % NP == 0 && NP / K <= 4 * 2 * 16 * 17, "thread mapping");
+    static_assert(NP / 64 == 8 && K / 32 <= 4, "wave roles");
+    constexpr int RPT = CT * K / NP;        // consecutive rows per thread, one channel
+    constexpr bool PAIR = sizeof(TI) == 4;  // fp32 activations: bf16 pairs; 16-bit: fp16 operands
+    constexpr float kLog2e = 1.4426950408889634f;
     __shared__ PairSmem<K> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
     const int64_t H = a.H, T = a.T;
     const int nck = static_cast<int>((T + CT - 1) / CT);
-    const int64_t bh = blockIdx.x / nck, b = bh / H, h = bh % H;
-    const int n = static_cast<int>(blockIdx.x % nck);
-    const int64_t cb = bh * nck + n;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
     const int kk = t % K, rg = t / K;
+    const uint32_t HK = static_cast<uint32_t>(H * K);
 
-    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk; G from
-    // per-thread partial sums and the row-group totals (in Y, free here)
-    float gl[RPT];
-    float run = 0.f;
+    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk, fetched
+    // raw through descriptors that span the chunk's rows before T (rows past
+    // T read as zero) with one lane offset per tensor and the row in the
+    // scalar offset
+    uint32_t pq[RPT], pk[RPT], pg[RPT], pb[1] = {0u};
+    const uint32_t lo_x = static_cast<uint32_t>(RPT * rg) * HK + kk;
+    auto fetch = [&](int64_t cb) {
+        const int64_t bh = cb / nck, b = bh / H, h = bh % H;
+        const int64_t r0 = (cb % nck) * CT;
+        const int64_t base = ((b * T + r0) * H + h) * K;
+        const uint32_t span = static_cast<uint32_t>((std::min<int64_t>(CT, T - r0) - 1) * H * K + K);
+        const auto rq = make_rsrc(qp + base, span * sizeof(TI)), rk = make_rsrc(kp + base, span * sizeof(TI));
+        const auto rgc = make_rsrc(a.g + base, span * 4);
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-        const int c = RPT * rg + j;
-        const int64_t row = static_cast<int64_t>(n) * CT + c;
-        float qv = 0.f, kv = 0.f, gv = 0.f;
-        if (row < T) {
-            const int64_t o = ((b * T + row) * H + h) * K + kk;
-            qv = Elem<TI>::ld(qp + o) * a.scale;
-            kv = Elem<TI>::ld(kp + o);
-            gv = a.g[o];
+        for (int j = 0; j < RPT; ++j) {
+            const uint32_t so = static_cast<uint32_t>(j) * HK;
+            if constexpr (sizeof(TI) == 2) {
+                pq[j] = __builtin_amdgcn_raw_buffer_load_b16(rq, static_cast<int>(2 * lo_x), static_cast<int>(2 * so), 0);
+                pk[j] = __builtin_amdgcn_raw_buffer_load_b16(rk, static_cast<int>(2 * lo_x), static_cast<int>(2 * so), 0);
+            } else {
+                pq[j] = __builtin_amdgcn_raw_buffer_load_b32(rq, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
+                pk[j] = __builtin_amdgcn_raw_buffer_load_b32(rk, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
+            }
+            pg[j] = __builtin_amdgcn_raw_buffer_load_b32(rgc, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
         }
-        sm.q[c][kk] = qv;
-        sm.k[c][kk] = kv;
-        run += gv;
-        gl[j] = run;
-    }
-    float* tot = &sm.Y[0][0];
-    tot[rg * K + kk] = run;
-    if (t < CT) {
-        const int64_t row = static_cast<int64_t>(n) * CT + t;
-        sm.beta[t] = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
-    }
-    __syncthreads();
-    {
-        float pre = 0.f;
+        if (t < CT) pb[0] = r0 + t < T ? __float_as_uint(a.beta[(b * T + r0 + t) * H + h]) : 0u;
+    };
+    int64_t cb = blockIdx.x;
+    if (cb < nchunks) fetch(cb);
+    for (; cb < nchunks; cb += gridDim.x) {
+        // stage this chunk (G from per-thread partial sums and the row-group
+        // totals); fetch the next one
+        use_here(pq);
+        use_here(pk);
+        use_here(pg);
+        use_here(pb);
+        float gl[RPT];
+        float run = 0.f;
 #pragma unroll
-        for (int r = 0; r < NT / K; ++r) pre += r < rg ? tot[r * K + kk] : 0.f;
+        for (int j = 0; j < RPT; ++j) {
+            const int c = RPT * rg + j;
+            sm.q[c][kk] = raw_f32<TI>(pq[j]) * a.scale;
+            sm.k[c][kk] = raw_f32<TI>(pk[j]);
+            run += __uint_as_float(pg[j]);
+            gl[j] = run;
+        }
+        float* tot = &sm.part[0][0][0][0];
+        tot[rg * K + kk] = run;
+        if (t < CT) sm.beta[t] = __uint_as_float(pb[0]);
+        if (cb + gridDim.x < nchunks) fetch(cb + gridDim.x);
+        __syncthreads();
+        {
+            float pre = 0.f;
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) sm.gc[RPT * rg + j][kk] = pre + gl[j];
-    }
-    __syncthreads();
+            for (int r = 0; r < NP / K; ++r) pre += r < rg ? tot[r * K + kk] : 0.f;
+#pragma unroll
+            for (int j = 0; j < RPT; ++j) sm.gc[RPT * rg + j][kk] = pre + gl[j];
+        }
+        __syncthreads();
 
-    // A and L on 4 x 4 blocks of entries (c, i), i <= c: the 16 lanes of a
-    // DPP row take one block, lane cg the channels cg + 16 m, and the row adds
-    // its partial sums at the end.  Waves 0-1: the 8 diagonal blocks (direct
-    // decays); waves 2-8: the 28 blocks below them, whose decays factor
-    // through the block's first row b: exp(G_c - G_i) = exp(G_c - G_b)
-    // exp(G_b - G_i) for i < b <= c, both factors <= 1.
-    if (w < 9) {
-        const int blk = t >> 4, cg = t & 15;
-        int bc, bi;
-        if (blk < 8) {
-            bc = bi = blk;
-        } else {
-            const int o = blk - 8;
-            bc = 1;
-            while ((bc + 1) * bc / 2 <= o) ++bc;
-            bi = o - bc * (bc - 1) / 2;
-        }
-        const int c0 = 4 * bc, i0 = 4 * bi;
-        float av[16], lv[16];
+        // diagonal blocks by level; lane (ln, lg) supplies row ln of both
+        // operands, channels 32 u + 8 lg .. + 7 of step u, and holds entry
+        // (c, i) = (4 lg + j, ln) of the block in slot j
+        {
+            const int p = w >> 2, lev = w & 3;
+            const int r = 16 * p + ln;
+            const bool up = (ln >> lev) & 1;
+            const int ref = 16 * p + (up ? ((ln >> lev) << lev) - 1 : (ln | ((1 << lev) - 1)));
+            // f = exp(G_r - G_ref) (upper rows) or exp(G_ref - G_r) (lower rows)
+            const float sg = up ? kLog2e : -kLog2e;
+            f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = accA;
+            float d15 = 0.f;                    // row 15's diagonal (lanes ln = 15 of level 0)
+#pragma unroll 1
+            for (int u = 0; u < K / 32; ++u) {
+                const int x0 = 32 * u + 8 * lg;
+                float qv[8], kv[8], gr[8], gf[8];
+                lds8(&sm.q[r][x0], qv);
+                lds8(&sm.k[r][x0], kv);
+                lds8(&sm.gc[r][x0], gr);
+                lds8(&sm.gc[ref][x0], gf);
+                if (lev == 0) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) av[e] = lv[e] = 0.f;
+                    for (int e = 0; e < 8; ++e) d15 = fmaf(qv[e], kv[e], d15);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float f = __builtin_amdgcn_exp2f((gr[e] - gf[e]) * sg);
+                    qv[e] *= f;
+                    kv[e] *= f;
+                }
+                if constexpr (PAIR) {
+                    bf8 qh, ql, kh, kl;
+                    split8(qv, qh, ql);
+                    split8(kv, kh, kl);
+                    accA = mfma_pair(qh, ql, kh, kl, accA);
+                    accL = mfma_pair(kh, kl, kh, kl, accL);
+                } else {
+                    const h8 qh = to_h8(qv), kh = to_h8(kv);
+                    accA = mfma16x16x32(qh, kh, accA);
+                    accL = mfma16x16x32(kh, kh, accL);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = 4 * lg + j, i = ln;
+                const int x = c ^ i;
+                // the diagonal entry of level lev: c's low lev bits ones, bit lev clear
+                const bool diag = x == 0 && ((c + 1) & ((2 << lev) - 1)) == (1 << lev);
+                if ((x >> lev) == 1 || diag) {
+                    sm.A[16 * p + c][16 * p + i] = c >= i ? accA[j] : 0.f;
+                    sm.L[16 * p + c][16 * p + i] = c > i ? accL[j] : 0.f;
+                }
+            }
+            if (lev == 0) {
+                d15 += __shfl_xor(d15, 16);
+                d15 += __shfl_xor(d15, 32);
+                if (lane == 15) {
+                    sm.A[16 * p + 15][16 * p + 15] = d15;
+                    sm.L[16 * p + 15][16 * p + 15] = 0.f;
+                }
+            }
+        }
+        __syncthreads();
+
         if (w < 2) {
-            for (int x = cg; x < K; x += 16) {
-                float gv[4], qv[4], kv[4];
+            // N_pp = (I + X)^-1, X = Diag(beta) L_pp, in accumulator layout
+            const int o = 16 * w;
+            f4 X, XT;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    gv[j] = sm.gc[c0 + j][x];
-                    qv[j] = sm.q[c0 + j][x];
-                    kv[j] = sm.k[c0 + j][x];
-                }
-#pragma unroll
-                for (int jc = 0; jc < 4; ++jc) {
-                    av[jc * 4 + jc] += qv[jc] * kv[jc];
-#pragma unroll
-                    for (int ji = 0; ji < jc; ++ji) {
-                        const float d = __expf(gv[jc] - gv[ji]) * kv[ji];
-                        av[jc * 4 + ji] += qv[jc] * d;
-                        lv[jc * 4 + ji] += kv[jc] * d;
-                    }
-                }
+            for (int j = 0; j < 4; ++j) {
+                X[j] = sm.beta[o + 4 * lg + j] * sm.L[o + 4 * lg + j][o + ln];
+                XT[j] = sm.beta[o + ln] * sm.L[o + ln][o + 4 * lg + j];
             }
-        } else {
-            for (int x = cg; x < K; x += 16) {
-                const float gb = sm.gc[c0][x];
-                float qu[4], ku[4], kw[4];
+            const f4 z = {0.f, 0.f, 0.f, 0.f};
+            const f4 X2 = mm_acc(XT, X, z), X2T = mm_acc(X, XT, z);
+            const f4 X4 = mm_acc(X2T, X2, z), X4T = mm_acc(X2, X2T, z);
+            const f4 X8T = mm_acc(X4, X4T, z);
+            f4 Q;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float uc = __expf(sm.gc[c0 + j][x] - gb);
-                    qu[j] = sm.q[c0 + j][x] * uc;
-                    ku[j] = sm.k[c0 + j][x] * uc;
-                    kw[j] = sm.k[i0 + j][x] * __expf(gb - sm.gc[i0 + j][x]);
-                }
+            for (int j = 0; j < 4; ++j) Q[j] = (4 * lg + j == ln ? 1.f : 0.f) - X[j];
+            Q = mm_acc(X2T, Q, Q);
+            Q = mm_acc(X4T, Q, Q);
+            Q = mm_acc(X8T, Q, Q);
 #pragma unroll
-                for (int jc = 0; jc < 4; ++jc)
+            for (int j = 0; j < 4; ++j) sm.N[o + 4 * lg + j][o + ln] = Q[j];
+        } else if (w >= 4 && w - 4 < K / 32) {
+            // the block below the diagonal, one 32-channel step per wave: rows
+            // 16 + ln (X) and ln (Y), reference row 15
+            const int s4 = w - 4, x0 = 32 * s4 + 8 * lg;
+            float q1[8], k1[8], g1[8], k0[8], g0[8], g15[8];
+            lds8(&sm.q[16 + ln][x0], q1);
+            lds8(&sm.k[16 + ln][x0], k1);
+            lds8(&sm.gc[16 + ln][x0], g1);
+            lds8(&sm.k[ln][x0], k0);
+            lds8(&sm.gc[ln][x0], g0);
+            lds8(&sm.gc[15][x0], g15);
 #pragma unroll
-                    for (int ji = 0; ji < 4; ++ji) {
-                        av[jc * 4 + ji] += qu[jc] * kw[ji];
-                        lv[jc * 4 + ji] += ku[jc] * kw[ji];
-                    }
+            for (int e = 0; e < 8; ++e) {
+                const float f1 = __builtin_amdgcn_exp2f((g1[e] - g15[e]) * kLog2e);
+                q1[e] *= f1;
+                k1[e] *= f1;
+                k0[e] *= __builtin_amdgcn_exp2f((g15[e] - g0[e]) * kLog2e);
+            }
+            f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = accA;
+            if constexpr (PAIR) {
+                bf8 qh, ql, kh, kl, yh, yl;
+                split8(q1, qh, ql);
+                split8(k1, kh, kl);
+                split8(k0, yh, yl);
+                accA = mfma_pair(qh, ql, yh, yl, accA);
+                accL = mfma_pair(kh, kl, yh, yl, accL);
+            } else {
+                const h8 qh = to_h8(q1), kh = to_h8(k1), yh = to_h8(k0);
+                accA = mfma16x16x32(qh, yh, accA);
+                accL = mfma16x16x32(kh, yh, accL);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sm.part[s4][0][4 * lg + j][ln] = accA[j];
+                sm.part[s4][1][4 * lg + j][ln] = accL[j];
             }
         }
-        float ao = 0.f, lo = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float as = row16_sum(av[e]), ls = row16_sum(lv[e]);
-            ao = cg == e ? as : ao;
-            lo = cg == e ? ls : lo;
-        }
-        const int jc = cg >> 2, ji = cg & 3;
-        const bool keep = w >= 2 || ji <= jc;
-        sm.A[c0 + jc][i0 + ji] = keep ? ao : 0.f;
-        sm.L[c0 + jc][i0 + ji] = keep ? lo : 0.f;
-    } else {
-        // the 28 blocks above the diagonal are zero
-        const int o = t - 9 * 64;
-        if (o < 28 * 16) {
-            const int blk = o >> 4, e = o & 15;
-            int bi = 1;
-            while ((bi + 1) * bi / 2 <= blk) ++bi;
-            const int bc = blk - bi * (bi - 1) / 2;
-            sm.A[4 * bc + (e >> 2)][4 * bi + (e & 3)] = 0.f;
-            sm.L[4 * bc + (e >> 2)][4 * bi + (e & 3)] = 0.f;
-        }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // N = (I + Diag(beta) L)^-1, blocked: the two 16 x 16 diagonal blocks by
-    // forward substitution (lane t of wave 0: column t % 16 of block t / 16,
-    // in registers), then N10 = -N11 X10 N00 on the matrix cores, in wave 0.
-    if (t < CT) {
-        const int bo = 16 * (t >> 4), jc = t & 15;
-        float col[16];
+        if (t < 64) {
+            // Y <- X10 N00, X10 = Diag(beta_1) L10 (L10 from the shares); N10 = -N11 Y
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = tile_mm<16>(
+                [&](int r, int m) {
+                    float l = 0.f;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            float s = 0.f;
+                    for (int x = 0; x < K / 32; ++x) l += sm.part[x][1][r][m];
+                    return sm.beta[16 + r] * l;
+                },
+                [&](int m, int i) { return sm.N[m][i]; }, ln, lg, acc);
 #pragma unroll
-            for (int m = 0; m < c; ++m) s += sm.L[bo + c][bo + m] * col[m];
-            col[c] = c < jc ? 0.f : (c == jc ? 1.f : -sm.beta[bo + c] * s);
+            for (int j = 0; j < 4; ++j) sm.Y[4 * lg + j][ln] = acc[j];
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+            acc = tile_mm<16>([&](int r, int m) { return sm.N[16 + r][16 + m]; },
+                              [&](int m, int i) { return sm.Y[m][i]; }, ln, lg, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.N[16 + 4 * lg + j][ln] = -acc[j];
+        } else if (w >= 4) {
+            // A_10, L_10 from the shares; zeros above the diagonal blocks
+            const int e = t - 256, c = e >> 4, i = e & 15;
+            float sa = 0.f, sl = 0.f;
+#pragma unroll
+            for (int x = 0; x < K / 32; ++x) {
+                sa += sm.part[x][0][c][i];
+                sl += sm.part[x][1][c][i];
+            }
+            sm.A[16 + c][i] = sa;
+            sm.L[16 + c][i] = sl;
+            sm.A[c][16 + i] = 0.f;
+            sm.L[c][16 + i] = 0.f;
+            sm.N[c][16 + i] = 0.f;
         }
+        __syncthreads();
+        // the next chunk's staging writes none of A, L, N
+        float* ga = ws.A + cb * CT * CT;
+        float* gL = ws.L + cb * CT * CT;
+        float* gn = ws.N + cb * CT * CT;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            sm.N[bo + c][bo + jc] = col[c];
-            if (bo == 0) sm.N[c][16 + jc] = 0.f;
+        for (int j = 0; j < CT * CT / NP; ++j) {
+            const int e = t + NP * j;
+            ga[e] = sm.A[e / CT][e % CT];
+            gL[e] = sm.L[e / CT][e % CT];
+            gn[e] = sm.N[e / CT][e % CT];
         }
     }
-    if (t < 64) {
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        // Y <- X10 N00, X10 = Diag(beta_1) L10
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = tile_mm<16>([&](int r, int m) { return sm.beta[16 + r] * sm.L[16 + r][m]; },
-                          [&](int m, int i) { return sm.N[m][i]; }, ln, lg, acc);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sm.Y[4 * lg + j][ln] = acc[j];
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        acc = f4{0.f, 0.f, 0.f, 0.f};
-        acc = tile_mm<16>([&](int r, int m) { return sm.N[16 + r][16 + m]; },
-                          [&](int m, int i) { return sm.Y[m][i]; }, ln, lg, acc);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sm.N[16 + 4 * lg + j][ln] = -acc[j];
-    }
-    __syncthreads();
-    ws.A[cb * CT * CT + t] = sm.A[t / CT][t % CT];
-    ws.L[cb * CT * CT + t] = sm.L[t / CT][t % CT];
-    ws.N[cb * CT * CT + t] = sm.N[t / CT][t % CT];
 }
 
 // ------------------------------------------------------------------ kernel 2
@@ -1044,14 +1200,26 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     }
 }
 
+// Workgroups of a persistent kernel: as many as are resident at once on the
+// current device.
+template <typename Kern>
+int persistent_grid(Kern kernel, int threads) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
+    return cus * per;
+}
+
 template <int K, typename TI>
 int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
     const int64_t BH = a.B * a.H;
     const int64_t nck = (a.T + CT - 1) / CT;
     const BwdWs ws = ws_layout(a.workspace, BH, nck, a.K, a.V);
     if (nck > 0) {
-        hipLaunchKernelGGL((bwd_pairs_kernel<K, TI>), dim3(static_cast<unsigned>(BH * nck)), dim3(NT), 0, stream,
-                           a, ws);
+        hipLaunchKernelGGL((bwd_pairs_kernel<K, TI>), dim3(static_cast<unsigned>(std::min<int64_t>(BH * nck, persistent_grid(bwd_pairs_kernel<K, TI>, NP)))),
+                           dim3(NP), 0, stream, a, ws, BH * nck);
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
     if (a.V % 64 == 0)

@@ -205,4 +205,27 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// A raw buffer descriptor over nbytes from base: loads whose offset (lane
+// offset + scalar offset) falls past nbytes return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(nbytes), 0x00020000);
+}
+
+// Values are held raw, one load per register set, and converted only where
+// they are used.  Left alone, the compiler hoists a conversion up to the
+// load, which puts a wait for the whole prefetch right after it is issued.
+// An empty volatile asm that "modifies" the registers at the point of use
+// keeps every such instruction, and the wait, there.
+template <int N>
+__device__ __forceinline__ void use_here(uint32_t (&r)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(r[i]));
+}
+template <int N, int M>
+__device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) use_here(r[i]);
+}
+
 }  // namespace kda
