@@ -732,75 +732,93 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
 
 // ------------------------------------------------------------------ kernel 3
 
-// Rows padded to a multiple of 4 floats plus 4: 16-byte vector reads along a
-// row, and consecutive rows 4 banks apart.
-// The column step's tiles: S and dS (K rows), dO, R, P, dP, dR (CT rows), VT
-// columns each.  PAIR (16-bit activations): bf16 pairs, x = hi + lo (hi = x
-// rounded to bf16, lo = the rest rounded to bf16: |x - hi - lo| <= 2^-18 |x|),
-// rows of VB elements (80 bytes: every MFMA fragment, 8 consecutive columns,
-// is one 16-byte read), for the bf16 matrix cores.  Otherwise (fp32
-// activations) fp32 rows of VP floats for the fp32 matrix cores, exact
-// products.
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t w2 __attribute__((ext_vector_type(2)));
+
+// Four values as bf16 pairs, two values per conversion.
+__device__ __forceinline__ void split4(const float (&v)[4], bf4& hi, bf4& lo) {
+    w2 hw, lw;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e], v[2 * e + 1]}, bf2));
+        const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xffff0000u);
+        hw[e] = hb;
+        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e] - h0, v[2 * e + 1] - h1}, bf2));
+    }
+    hi = __builtin_bit_cast(bf4, hw);
+    lo = __builtin_bit_cast(bf4, lw);
+}
+__device__ __forceinline__ void split4(const f4& v, bf4& hi, bf4& lo) {
+    const float a[4] = {v[0], v[1], v[2], v[3]};
+    split4(a, hi, lo);
+}
+
+// A B for one 16 x 16 tile over a contraction of 16, bf16 pairs on
+// v_mfma_f32_16x16x16_bf16: lane (ln, lg) supplies A[ln][4 lg .. 4 lg + 3]
+// and B[4 lg .. 4 lg + 3][ln] and holds D[4 lg + j][ln] in slot j.  Only this
+// form runs in these chains.
+__device__ __forceinline__ f4 mfma_pair16(const f4& a, const float (&b)[4]) {
+    bf4 ah, al, bh, bl;
+    split4(a, ah, al);
+    split4(b, bh, bl);
+    f4 acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+}
+
+// acc += X Y^T over the VT = 32 columns of a step: X a bf16 pair tile in LDS
+// (row ln of the tile: xh, xl), Y's fragment in registers (lane (ln, lg):
+// row ln, columns 8 lg .. 8 lg + 7, as a pair).
+__device__ __forceinline__ f4 mm_pair_r(const uint16_t* xh, const uint16_t* xl, const bf8& yh, const bf8& yl,
+                                        int lg, f4 acc) {
+    const bf8 ah = *reinterpret_cast<const bf8*>(xh + 8 * lg), al = *reinterpret_cast<const bf8*>(xl + 8 * lg);
+    return mfma_pair(ah, al, yh, yl, acc);
+}
+
+// The column step's shared tiles, bf16 pairs ([0] hi, [1] lo; x = hi + lo
+// with |x - hi - lo| <= 2^-18 |x|), rows of VB elements (80 bytes: every
+// MFMA fragment, 8 consecutive columns, is one 16-byte read).
 constexpr int VB = VT + 8;
-constexpr int VP = VT + 4;
-template <int K, bool PAIR>
-struct StepTiles;
 template <int K>
-struct StepTiles<K, true> {
-    uint16_t S[2][K][VB];       // state at the chunk start (checkpoint): hi, lo
-    uint16_t dS[2][K][VB];      // gradient of the state at the chunk end
+struct __align__(16) ChunkSmem {
+    static constexpr int NW = K / 16;
     uint16_t dO[2][CT][VB];
-    uint16_t R[2][CT][VB];
+    uint16_t R[2][CT][VB];      // R and P from the forward's checkpoint
     uint16_t P[2][CT][VB];
     uint16_t dP[2][CT][VB];
     uint16_t dR[2][CT][VB];
-};
-template <int K>
-struct StepTiles<K, false> {
-    float S[K][VP];
-    float dS[K][VP];
-    float dO[CT][VP];
-    float R[CT][VP];
-    float P[CT][VP];
-    float dP[CT][VP];
-    float dR[CT][VP];
-};
-template <int K, bool PAIR>
-struct __align__(16) ChunkSmem {
-    static constexpr int KP = K + 4;
-    float q[CT][KP];            // scale * q
-    float k[CT][KP];
-    float gc[CT][KP];           // in-chunk cumulative log decay G
-    float e[CT][KP];            // exp(G); then, per element, dG
-    StepTiles<K, PAIR> st;
-    float A[CT][CT + 1];        // A (i <= c)
-    float L[CT][CT + 1];        // L (i < c)
-    float N[CT][CT + 1];        // (I + Diag(beta) L)^-1
-    float dA[CT][CT + 1];       // dA (i <= c)
+    float L[CT][CT + 1];
+    float N[CT][CT + 1];
     float dM[CT][CT + 1];       // dM, then dN, then dX
-    float Y[CT][CT + 1];        // dN N^T; then, per thread, its rows' share of
-                                // sum_c d(k*F)[c] k[c] F[c] (NT floats)
+    float Y[CT][CT + 1];        // dN N^T
+    // dA (i <= c) and dX (i < c) by rows ([c][i]) and by columns ([i][c]),
+    // 16-byte rows for the element step's fragments
+    float dAr[CT][CT + 4];
+    float dAc[CT][CT + 4];
+    float dXr[CT][CT + 4];
+    float dXc[CT][CT + 4];
+    float red[NW][CT];          // the waves' column sums of dM * N
     float beta[CT];
-    float dbeta[CT];
-    float eps[K];               // exp(G_last)
-    float deps[K];              // rowsum(dS * S)
-    // the element step's copies of dA and dX live in the dS area when it is
-    // large enough (K = 128), here otherwise
-    static constexpr int CPY = 4 * CT * (CT + 4);
-    static constexpr bool CPY_IN_DS = sizeof(StepTiles<K, PAIR>::dS) / 4 >= CPY;   // floats in the dS area
-    float cpy[CPY_IN_DS ? 4 : CPY];
 };
-static_assert(CT * (CT + 1) >= NT, "the per-thread shares fit Y");
 
+// One workgroup per (b, h, chunk), K / 16 waves; wave w owns channels
+// 16 w .. 16 w + 15 for all CT rows (two 16-row element tiles), so the
+// state's and its gradient's fragments come straight from HBM into the
+// lanes that use them and the per-element step runs in registers.
+// Column steps of VT state columns: the CT-row tiles (dO, R, P, dP, dR) go
+// through LDS as bf16 pairs; every product on the bf16 matrix cores as
+// pairs.  The next step is fetched (raw, through buffer descriptors whose
+// range stops at the chunk's last row before T) while the current one is
+// computed.  About 60 KiB of LDS at K = 128: two workgroups share a CU, one
+// workgroup's HBM-bound column steps overlapping the other's element step.
 template <int K, typename TI>
-__global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, const BwdWs ws) {
-    static_assert(NT % K == 0 && (CT * K) % NT == 0, "thread mapping");
-    constexpr int RPT = CT * K / NT;        // consecutive rows per thread, one channel
-    constexpr int SPT = K * VT / NT;        // state tile elements per thread
-    constexpr int TPR = VT / SPT;           // threads per state row
-    static_assert(NT / K * K <= CT * (CT + 1), "the row-group sums fit Y");
-    constexpr bool PAIR = sizeof(TI) == 2;
-    __shared__ ChunkSmem<K, PAIR> sm;
+__global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, const BwdWs ws) {
+    constexpr int NW = K / 16, NTC = 64 * NW;
+    constexpr int EPT = CT * VT / NTC;      // tile elements per thread and tensor
+    constexpr int MPW = 8 / NW;             // dA / dM tiles per wave
+    constexpr int SZ = sizeof(TI);
+    static_assert(NTC % VT == 0 && NTC % CT == 0 && EPT >= 1 && MPW >= 1, "thread mapping");
+    __shared__ ChunkSmem<K> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
     const TI* dop = static_cast<const TI*>(a.d_o);
@@ -813,217 +831,192 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
     const int64_t bh = blockIdx.x / nck, b = bh / H, h = bh % H;
     const int n = static_cast<int>(blockIdx.x % nck);
     const int64_t cb = bh * nck + n;
+    const int64_t r0 = static_cast<int64_t>(n) * CT;
+    const int nrow = static_cast<int>(std::min<int64_t>(CT, T - r0));     // rows before T
     const int nvt = static_cast<int>(V / VT);
     const float scale = a.scale;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
-    const int kk = t % K, rg = t / K;
+    const int x = 16 * w + ln;              // the lane's channel
 
-    // ---------------------------------------------------------------- loads
-    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk.  The
-    // first column step's tiles are fetched right behind these loads.
-    float ql[RPT], kl[RPT], gl[RPT];
+    // ------------------------------------------------------------ loads
+    // q, k, g of the lane's rows 16 p + 4 lg + j, channel x (used after the
+    // column steps)
+    uint32_t rq[2][4], rk[2][4], rg[2][4];
+    {
+        const int64_t base = ((b * T + r0) * H + h) * K;
+        const uint32_t HK = static_cast<uint32_t>(H * K);
+        const uint32_t span = static_cast<uint32_t>(nrow - 1) * HK + K;
+        const auto dq = make_rsrc(qp + base, span * SZ), dk = make_rsrc(kp + base, span * SZ);
+        const auto dg = make_rsrc(a.g + base, span * 4);
+        const uint32_t vo = static_cast<uint32_t>(4 * lg) * HK + x;
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-        const int64_t row = static_cast<int64_t>(n) * CT + RPT * rg + j;
-        ql[j] = kl[j] = gl[j] = 0.f;
-        if (row < T) {
-            const int64_t o = ((b * T + row) * H + h) * K + kk;
-            ql[j] = Elem<TI>::ld(qp + o) * scale;
-            kl[j] = Elem<TI>::ld(kp + o);
-            gl[j] = a.g[o];
-        }
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t so = static_cast<uint32_t>(16 * p + j) * HK;
+                if constexpr (SZ == 2) {
+                    rq[p][j] = __builtin_amdgcn_raw_buffer_load_b16(dq, static_cast<int>(2 * vo), static_cast<int>(2 * so), 0);
+                    rk[p][j] = __builtin_amdgcn_raw_buffer_load_b16(dk, static_cast<int>(2 * vo), static_cast<int>(2 * so), 0);
+                } else {
+                    rq[p][j] = __builtin_amdgcn_raw_buffer_load_b32(dq, static_cast<int>(4 * vo), static_cast<int>(4 * so), 0);
+                    rk[p][j] = __builtin_amdgcn_raw_buffer_load_b32(dk, static_cast<int>(4 * vo), static_cast<int>(4 * so), 0);
+                }
+                rg[p][j] = __builtin_amdgcn_raw_buffer_load_b32(dg, static_cast<int>(4 * vo), static_cast<int>(4 * so), 0);
+            }
     }
-    const float al = ws.A[cb * CT * CT + t], ll = ws.L[cb * CT * CT + t], nl = ws.N[cb * CT * CT + t];
-    float bl = 0.f;
-    if (t < CT) {
-        const int64_t row = static_cast<int64_t>(n) * CT + t;
-        bl = row < T ? a.beta[(b * T + row) * H + h] : 0.f;
+#pragma unroll
+    for (int m = 0; m < CT * CT / NTC; ++m) {
+        const int e = t + NTC * m;
+        sm.L[e / CT][e % CT] = ws.L[cb * CT * CT + e];
+        sm.N[e / CT][e % CT] = ws.N[cb * CT * CT + e];
     }
+    if (t < CT) sm.beta[t] = t < nrow ? a.beta[(b * T + r0 + t) * H + h] : 0.f;
 
-    // the checkpoint of chunk cb: the state before it (K rows), then its R
-    // and P (CT rows each), V columns
-    const float* ck = a.ckpt + cb * static_cast<int64_t>(K + 2 * CT) * V;
-    float ps[SPT], pds[SPT], pr = 0.f, pp = 0.f, pdp = 0.f, pdr = 0.f;
-    TI pdo{};                               // converted when staged
-    const int st_row = t / TPR, st_col = SPT * (t % TPR);
+    // column-step fetch: the lane's fragments of S (the checkpointed state
+    // before the chunk) and dS (the gradient of the state after it), row x,
+    // columns v0 + 8 lg .. + 7; the thread's EPT elements of R, P (checkpoint),
+    // dP, dR (workspace) and dO, rows t / VT + (NTC / VT) m, column t % VT
+    const auto rck = make_rsrc(a.ckpt + cb * static_cast<int64_t>(K + 2 * CT) * V,
+                               static_cast<uint32_t>((K + 2 * CT) * V * 4));
+    const auto rds = make_rsrc(ws.dS + cb * K * V, static_cast<uint32_t>(K * V * 4));
+    const auto rdp = make_rsrc(ws.dP + cb * CT * V, static_cast<uint32_t>(CT * V * 4));
+    const auto rdr = make_rsrc(ws.dR + cb * CT * V, static_cast<uint32_t>(CT * V * 4));
+    const auto rdo = make_rsrc(dop + ((b * T + r0) * H + h) * V,
+                               static_cast<uint32_t>(((nrow - 1) * H + 1) * V * SZ));
+    const uint32_t vo_f = static_cast<uint32_t>(x * V + 8 * lg) * 4;
     const int tc = t / VT, tv = t % VT;
+    const uint32_t vo_t = static_cast<uint32_t>(tc * V + tv) * 4;
+    const uint32_t vo_o = static_cast<uint32_t>(tc * H * V + tv) * SZ;
+    uint32_t fS[8], fdS[8], fR[EPT], fP[EPT], fdP[EPT], fdR[EPT], fdO[EPT];
     auto fetch = [&](int vt) {
-        const int64_t v0 = static_cast<int64_t>(vt) * VT;
+        const uint32_t v0 = static_cast<uint32_t>(vt) * VT;
 #pragma unroll
-        for (int j = 0; j < SPT; ++j) {
-            ps[j] = ck[st_row * V + v0 + st_col + j];
-            pds[j] = ws.dS[(cb * K + st_row) * V + v0 + st_col + j];
+        for (int u = 0; u < 2; ++u) {
+            const w4 s4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rck, static_cast<int>(vo_f + 16 * u), static_cast<int>(4 * v0), 0));
+            const w4 d4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rds, static_cast<int>(vo_f + 16 * u), static_cast<int>(4 * v0), 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                fS[4 * u + e] = s4[e];
+                fdS[4 * u + e] = d4[e];
+            }
         }
-        pr = ck[(K + tc) * V + v0 + tv];
-        pp = ck[(K + CT + tc) * V + v0 + tv];
-        pdp = ws.dP[(cb * CT + tc) * V + v0 + tv];
-        pdr = ws.dR[(cb * CT + tc) * V + v0 + tv];
-        const int64_t row = static_cast<int64_t>(n) * CT + tc;
-        pdo = TI{};
-        if (row < T) pdo = dop[((b * T + row) * H + h) * V + v0 + tv];
+#pragma unroll
+        for (int m = 0; m < EPT; ++m) {
+            const uint32_t rowo = static_cast<uint32_t>((NTC / VT) * m) * static_cast<uint32_t>(V);
+            fR[m] = __builtin_amdgcn_raw_buffer_load_b32(rck, static_cast<int>(vo_t), static_cast<int>(4 * (K * V + rowo + v0)), 0);
+            fP[m] = __builtin_amdgcn_raw_buffer_load_b32(rck, static_cast<int>(vo_t), static_cast<int>(4 * ((K + CT) * V + rowo + v0)), 0);
+            fdP[m] = __builtin_amdgcn_raw_buffer_load_b32(rdp, static_cast<int>(vo_t), static_cast<int>(4 * (rowo + v0)), 0);
+            fdR[m] = __builtin_amdgcn_raw_buffer_load_b32(rdr, static_cast<int>(vo_t), static_cast<int>(4 * (rowo + v0)), 0);
+            const uint32_t so = (static_cast<uint32_t>((NTC / VT) * m) * static_cast<uint32_t>(H * V) + v0) * SZ;
+            if constexpr (SZ == 2)
+                fdO[m] = __builtin_amdgcn_raw_buffer_load_b16(rdo, static_cast<int>(vo_o), static_cast<int>(so), 0);
+            else
+                fdO[m] = __builtin_amdgcn_raw_buffer_load_b32(rdo, static_cast<int>(vo_o), static_cast<int>(so), 0);
+        }
     };
     fetch(0);
 
-    float run = 0.f;
-#pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-        const int c = RPT * rg + j;
-        sm.q[c][kk] = ql[j];
-        sm.k[c][kk] = kl[j];
-        run += gl[j];
-        gl[j] = run;
-    }
-    float* tot = &sm.Y[0][0];               // [NT / K][K]: per row group, the sum of its g
-    tot[rg * K + kk] = run;
-    if (t < CT) sm.beta[t] = bl;
-    sm.A[t / CT][t % CT] = al;
-    sm.L[t / CT][t % CT] = ll;
-    sm.N[t / CT][t % CT] = nl;
-    __syncthreads();
-
-    // ------------------------------------------- cumulative decays, eps
-    {
-        float pre = 0.f, last = 0.f;
-#pragma unroll
-        for (int r = 0; r < NT / K; ++r) {
-            const float x = tot[r * K + kk];
-            pre += r < rg ? x : 0.f;
-            last += x;
-        }
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int c = RPT * rg + j;
-            sm.gc[c][kk] = pre + gl[j];
-            sm.e[c][kk] = __expf(pre + gl[j]);
-        }
-        if (rg == 0) sm.eps[kk] = __expf(last);
-    }
-
     // ------------------------------------- sums over the state columns
-    // per VT-column step (R and P from the forward's checkpoint):
-    // dA += dO P^T, dM += dP R^T, d(q~*E) += dO S^T, d(k*E) -= dR S^T,
-    // d(k*F) += P dS^T, deps += rowsum(dS * S).  The next step's tiles are
-    // fetched into registers while the current one is computed.
-
-    constexpr int KTL = K / 16;
-    const bool tw = w < 2 * KTL;
-    // element tile of this wave: rows 16 (w / KTL) + 4 lg + j, channel 16 (w % KTL) + ln
-    const int ert = 16 * (w / KTL), ekk = 16 * (w % KTL) + ln;
-    // CT x CT tile of waves 0-7: rows r0t + 4 lg + j, columns c0t + ln
-    const int r0t = 16 * ((w >> 1) & 1), c0t = 16 * (w & 1);
-    f4 accm = {0.f, 0.f, 0.f, 0.f};         // dA (waves 0-3), dM (waves 4-7)
-    f4 dqe = accm, dke = accm, dkf = accm;
-    float deps = 0.f;            // this thread's share of rowsum(dS * S) for row st_row
+    // dA += dO P^T, dM += dP R^T (MPW tiles a wave), and per element tile p:
+    // d(q~E) += dO S^T, d(kE) -= dR S^T (accumulated as + and negated
+    // below), d(kF) += P dS^T; deps += rowsum(dS * S)
+    f4 accm[MPW];
+#pragma unroll
+    for (int m = 0; m < MPW; ++m) accm[m] = f4{0.f, 0.f, 0.f, 0.f};
+    f4 dqe[2], dke[2], dkf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) dqe[p] = dke[p] = dkf[p] = f4{0.f, 0.f, 0.f, 0.f};
+    float deps = 0.f;
     for (int vt = 0; vt < nvt; ++vt) {
-        auto& tl = sm.st;
+        use_here(fS);
+        use_here(fdS);
+        use_here(fR);
+        use_here(fP);
+        use_here(fdP);
+        use_here(fdR);
+        use_here(fdO);
 #pragma unroll
-        for (int j = 0; j < SPT; ++j) deps = fmaf(pds[j], ps[j], deps);
-        if constexpr (PAIR) {
-#pragma unroll
-            for (int j = 0; j < SPT; ++j) {
-                split_bf16(ps[j], tl.S[0][st_row][st_col + j], tl.S[1][st_row][st_col + j]);
-                split_bf16(pds[j], tl.dS[0][st_row][st_col + j], tl.dS[1][st_row][st_col + j]);
-            }
-            split_bf16(pr, tl.R[0][tc][tv], tl.R[1][tc][tv]);
-            split_bf16(pp, tl.P[0][tc][tv], tl.P[1][tc][tv]);
-            split_bf16(Elem<TI>::ld(&pdo), tl.dO[0][tc][tv], tl.dO[1][tc][tv]);
-            split_bf16(pdp, tl.dP[0][tc][tv], tl.dP[1][tc][tv]);
-            split_bf16(pdr, tl.dR[0][tc][tv], tl.dR[1][tc][tv]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < SPT; ++j) {
-                tl.S[st_row][st_col + j] = ps[j];
-                tl.dS[st_row][st_col + j] = pds[j];
-            }
-            tl.R[tc][tv] = pr;
-            tl.P[tc][tv] = pp;
-            tl.dO[tc][tv] = Elem<TI>::ld(&pdo);
-            tl.dP[tc][tv] = pdp;
-            tl.dR[tc][tv] = pdr;
+        for (int m = 0; m < EPT; ++m) {
+            const int c = tc + (NTC / VT) * m;
+            split_bf16(__uint_as_float(fR[m]), sm.R[0][c][tv], sm.R[1][c][tv]);
+            split_bf16(__uint_as_float(fP[m]), sm.P[0][c][tv], sm.P[1][c][tv]);
+            split_bf16(__uint_as_float(fdP[m]), sm.dP[0][c][tv], sm.dP[1][c][tv]);
+            split_bf16(__uint_as_float(fdR[m]), sm.dR[0][c][tv], sm.dR[1][c][tv]);
+            split_bf16(raw_f32<TI>(fdO[m]), sm.dO[0][c][tv], sm.dO[1][c][tv]);
+            if (c < nrow)
+                Elem<TI>::st(dvp + ((b * T + r0 + c) * H + h) * V + static_cast<int64_t>(vt) * VT + tv,
+                             __uint_as_float(fdR[m]));
         }
-        {
-            const int64_t row = static_cast<int64_t>(n) * CT + tc;
-            if (row < T) Elem<TI>::st(dvp + ((b * T + row) * H + h) * V + static_cast<int64_t>(vt) * VT + tv, pdr);
+        float sv[8], dsv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            sv[e] = __uint_as_float(fS[e]);
+            dsv[e] = __uint_as_float(fdS[e]);
+            deps = fmaf(sv[e], dsv[e], deps);
         }
+        bf8 sh, sl, dsh, dsl;
+        split8(sv, sh, sl);
+        split8(dsv, dsh, dsl);
         if (vt + 1 < nvt) fetch(vt + 1);
         __syncthreads();
 
-        // waves 0-3: dA += dO P^T; waves 4-7: dM += dP R^T; every element wave:
-        // d(q~E) += dO S^T, d(kE) -= dR S^T (accumulated as + and negated
-        // below), d(kF) += P dS^T
-        if constexpr (PAIR) {
-            if (w < 8) {
-                const uint16_t (*xa)[CT][VB] = w < 4 ? tl.dO : tl.dP;
-                const uint16_t (*ya)[CT][VB] = w < 4 ? tl.P : tl.R;
-                accm = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], ya[0][c0t + ln], ya[1][c0t + ln], lg, accm);
-            }
-            if (tw) {
-                const int er = ert + ln, sr = ekk;      // rows of the element tile and of its channels
-                dqe = mm_pair(tl.dO[0][er], tl.dO[1][er], tl.S[0][sr], tl.S[1][sr], lg, dqe);
-                dke = mm_pair(tl.dR[0][er], tl.dR[1][er], tl.S[0][sr], tl.S[1][sr], lg, dke);
-                dkf = mm_pair(tl.P[0][er], tl.P[1][er], tl.dS[0][sr], tl.dS[1][sr], lg, dkf);
-            }
-        } else {
-            if (w < 4)
-                accm = tile_mm<VT>([&](int r, int v) { return tl.dO[r0t + r][v]; },
-                                   [&](int v, int i) { return tl.P[c0t + i][v]; }, ln, lg, accm);
-            else if (w < 8)
-                accm = tile_mm<VT>([&](int r, int v) { return tl.dP[r0t + r][v]; },
-                                   [&](int v, int i) { return tl.R[c0t + i][v]; }, ln, lg, accm);
-            if (tw) {
-                dqe = tile_mm<VT>([&](int r, int v) { return tl.dO[ert + r][v]; },
-                                  [&](int v, int kc) { return tl.S[ekk - ln + kc][v]; }, ln, lg, dqe);
-                dke = tile_mm<VT>([&](int r, int v) { return tl.dR[ert + r][v]; },
-                                  [&](int v, int kc) { return tl.S[ekk - ln + kc][v]; }, ln, lg, dke);
-                dkf = tile_mm<VT>([&](int r, int v) { return tl.P[ert + r][v]; },
-                                  [&](int v, int kc) { return tl.dS[ekk - ln + kc][v]; }, ln, lg, dkf);
-            }
+#pragma unroll
+        for (int m = 0; m < MPW; ++m) {
+            const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
+            const uint16_t (*xa)[CT][VB] = tt < 4 ? sm.dO : sm.dP;
+            const uint16_t (*ya)[CT][VB] = tt < 4 ? sm.P : sm.R;
+            accm[m] = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], ya[0][c0t + ln], ya[1][c0t + ln], lg, accm[m]);
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int er = 16 * p + ln;
+            dqe[p] = mm_pair_r(sm.dO[0][er], sm.dO[1][er], sh, sl, lg, dqe[p]);
+            dke[p] = mm_pair_r(sm.dR[0][er], sm.dR[1][er], sh, sl, lg, dke[p]);
+            dkf[p] = mm_pair_r(sm.P[0][er], sm.P[1][er], dsh, dsl, lg, dkf[p]);
         }
         __syncthreads();
     }
-    dke = f4{0.f, 0.f, 0.f, 0.f} - dke;
-    // deps: the shares of the TPR threads of each state row
 #pragma unroll
-    for (int m = 1; m < TPR; m <<= 1) deps += __shfl_xor(deps, m);
-    // 16-byte-aligned copies for the element step (in the dS area, no longer
-    // read, when it is large enough): dA by rows and by columns, dX (the
-    // final dM) by rows and by columns
-    float* cpy = ChunkSmem<K, PAIR>::CPY_IN_DS ? reinterpret_cast<float*>(&sm.st.dS) : &sm.cpy[0];
-    float (*dAr)[CT + 4] = reinterpret_cast<float (*)[CT + 4]>(cpy);
-    float (*dAc)[CT + 4] = dAr + CT;
-    float (*dXr)[CT + 4] = dAr + 2 * CT;
-    float (*dXc)[CT + 4] = dAr + 3 * CT;
-    if (w < 8) {
+    for (int p = 0; p < 2; ++p) dke[p] = f4{0.f, 0.f, 0.f, 0.f} - dke[p];
+    // deps of channel x: the shares of the four lanes of the channel
+    deps += __shfl_xor(deps, 16);
+    deps += __shfl_xor(deps, 32);
+#pragma unroll
+    for (int m = 0; m < MPW; ++m) {
+        const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
-            const float x = i <= c ? accm[j] : 0.f;
-            if (w < 4) {
-                sm.dA[c][i] = x;
-                dAr[c][i] = x;
-                dAc[i][c] = x;
+            const float v = i <= c ? accm[m][j] : 0.f;
+            if (tt < 4) {
+                sm.dAr[c][i] = v;
+                sm.dAc[i][c] = v;
             } else {
-                sm.dM[c][i] = x;
+                sm.dM[c][i] = v;
             }
         }
     }
-    if (t % TPR == 0) sm.deps[st_row] = deps;
     __syncthreads();
 
     // ------------------------------- dbeta (M = N Diag(beta)), dN in place
-    // column sums of dM * N: over the two rows of each wave, then over the waves
-    float* red = reinterpret_cast<float*>(&sm.st.S);   // [NT / 64][CT]; S is no longer read
+    // column sums of dM * N: over the thread's entries (one column), the two
+    // halves of the wave, then the waves
     {
-        const int c = t / CT, i = t % CT;
-        const float dm = sm.dM[c][i];
-        float p = dm * sm.N[c][i];
-        p += __shfl_xor(p, 32);
-        if (lane < 32) red[w * CT + i] = p;
-        sm.dM[c][i] = dm * sm.beta[i];
+        float cs = 0.f;
+#pragma unroll
+        for (int m = 0; m < CT * CT / NTC; ++m) {
+            const int e = t + NTC * m, c = e / CT, i = e % CT;
+            const float dm = sm.dM[c][i];
+            cs = fmaf(dm, sm.N[c][i], cs);
+            sm.dM[c][i] = dm * sm.beta[i];
+        }
+        cs += __shfl_xor(cs, 32);
+        if (lane < 32) sm.red[w][lane] = cs;
     }
     __syncthreads();
     // Y = dN N^T
-    if (w < 4) {
+    for (int tt = w; tt < 4; tt += NW) {
+        const int r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
         f4 acc = {0.f, 0.f, 0.f, 0.f};
         acc = tile_mm<CT>([&](int r, int m) { return sm.dM[r0t + r][m]; },
                           [&](int m, int i) { return sm.N[c0t + i][m]; }, ln, lg, acc);
@@ -1031,172 +1024,246 @@ __global__ __launch_bounds__(NT) void bwd_chunk_kernel(const kda_bwd_args a, con
         for (int j = 0; j < 4; ++j) sm.Y[r0t + 4 * lg + j][c0t + ln] = acc[j];
     }
     __syncthreads();
-    // dX = -N^T Y, strictly lower (kept in dM)
-    if (w < 4) {
+    // dX = -N^T Y, strictly lower (kept in dM and the copies)
+    for (int tt = w; tt < 4; tt += NW) {
+        const int r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
         f4 acc = {0.f, 0.f, 0.f, 0.f};
         acc = tile_mm<CT>([&](int r, int m) { return sm.N[m][r0t + r]; },
                           [&](int m, int i) { return sm.Y[m][c0t + i]; }, ln, lg, acc);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
-            const float x = i < c ? -acc[j] : 0.f;
-            sm.dM[c][i] = x;
-            dXr[c][i] = x;
-            dXc[i][c] = x;
+            const float v = i < c ? -acc[j] : 0.f;
+            sm.dM[c][i] = v;
+            sm.dXr[c][i] = v;
+            sm.dXc[i][c] = v;
         }
     }
     __syncthreads();
-    // row sums of dX * L (over the 32 lanes of a row), plus the column sums above
-    {
-        const int c = t / CT, i = t % CT;
+    // dbeta: row sums of dX * L (over the 32 lanes of a row) plus the column sums
+#pragma unroll
+    for (int m = 0; m < CT * CT / NTC; ++m) {
+        const int e = t + NTC * m, c = e / CT, i = e % CT;
         float p = sm.dM[c][i] * sm.L[c][i];
 #pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) p += __shfl_xor(p, m);
-        if (i == 0) {
+        for (int s = 16; s >= 1; s >>= 1) p += __shfl_xor(p, s);
+        if (i == 0 && c < nrow) {
             float s = p;
 #pragma unroll
-            for (int x = 0; x < NT / 64; ++x) s += red[x * CT + c];
-            sm.dbeta[c] = s;
+            for (int u = 0; u < NW; ++u) s += sm.red[u][c];
+            a.dbeta[(b * T + r0 + c) * H + h] = s;
         }
     }
 
-    // ---------------------------- per (row, channel): dq, dk and dG
-    // Pairs of rows in different 16-row blocks (i < 16 <= c) factor their
-    // decay through row 16, exp(G_c - G_i) = exp(G_c - G_16) exp(G_16 - G_i),
-    // both <= 1: plain products on the matrix cores whose 16 x 16 output tile
-    // is the wave's own element tile (block 1's waves: the row-side sums over
-    // block 0; block 0's waves: the column-side sums over block 1).  Within a
-    // block, the lane's rows c0 .. c0 + 3 share the decay products through a
-    // reference row: for i <= c0, exp(G_c - G_i) = exp(G_c - G_c0) exp(G_c0 - G_i),
-    // and for c2 >= c3 = c0 + 3, exp(G_c2 - G_c) = exp(G_c2 - G_c3) exp(G_c3 - G_c),
-    // every factor <= 1; the few pairs between the lane's own rows are direct.
-    if (tw) {
-        auto gcol = [&](int c) { return sm.gc[c][ekk]; };
-        auto kcol = [&](int c) { return sm.k[c][ekk]; };
-        auto qcol = [&](int c) { return sm.q[c][ekk]; };
-        const int c0 = ert + 4 * lg, c3 = c0 + 3;
-        const float g0 = gcol(c0), g3 = gcol(c3);
-        float t1[4] = {0.f, 0.f, 0.f, 0.f}, t2[4] = {0.f, 0.f, 0.f, 0.f};
-        float t3[4] = {0.f, 0.f, 0.f, 0.f}, t4[4] = {0.f, 0.f, 0.f, 0.f};
-        // across the blocks, through row 16 (x0: the tile's first channel)
-        const int x0 = ekk - ln;
-        const float g16 = gcol(16);
-        f4 oa = {0.f, 0.f, 0.f, 0.f}, om = oa;
-        if (ert == 16) {
-            oa = tile_mm<16>([&](int r, int i) { return sm.dA[16 + r][i]; },
-                             [&](int i, int x) { return sm.k[i][x0 + x] * __expf(sm.gc[16][x0 + x] - sm.gc[i][x0 + x]); },
-                             ln, lg, oa);
-            om = tile_mm<16>([&](int r, int i) { return sm.dM[16 + r][i]; },
-                             [&](int i, int x) { return sm.k[i][x0 + x] * __expf(sm.gc[16][x0 + x] - sm.gc[i][x0 + x]); },
-                             ln, lg, om);
-        } else {
-            oa = tile_mm<16>([&](int r, int c2) { return sm.dA[16 + c2][r]; },
-                             [&](int c2, int x) {
-                                 return sm.q[16 + c2][x0 + x] * __expf(sm.gc[16 + c2][x0 + x] - sm.gc[16][x0 + x]);
-                             },
-                             ln, lg, oa);
-            om = tile_mm<16>([&](int r, int c2) { return sm.dM[16 + c2][r]; },
-                             [&](int c2, int x) {
-                                 return sm.beta[16 + c2] * sm.k[16 + c2][x0 + x] *
-                                        __expf(sm.gc[16 + c2][x0 + x] - sm.gc[16][x0 + x]);
-                             },
-                             ln, lg, om);
+    // ---------------------------- per (row, channel): dq, dk and dg
+    // Lane (ln, lg): rows 16 p + 4 lg + j of channel x.  T1 = sum_i dA[c,i]
+    // k_i d(c,i); T3 = sum_i dX[c,i] k_i d(c,i) (times beta_c below); T2 =
+    // sum_c2 dA[c2,c] q~_c2 d(c2,c); T4 = sum_c2 beta_c2 dX[c2,c] k_c2
+    // d(c2,c); d(c,i) = exp(G_c - G_i) for i <= c.  Every decay factor is
+    // kept <= 1 by a reference row between the two rows: row 16 across the
+    // blocks, the decay levels 3 and 2 within a block (pairs in different
+    // 4-row groups: both orientations of a level's pairs in one product),
+    // and direct exponentials within the lane's own four rows.
+    use_here(rq);
+    use_here(rk);
+    use_here(rg);
+    float qv[2][4], kv[2][4], G[2][4], bt[2][4];
+    float tot[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        float run = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            qv[p][j] = raw_f32<TI>(rq[p][j]) * scale;
+            kv[p][j] = raw_f32<TI>(rk[p][j]);
+            run += __uint_as_float(rg[p][j]);
+            G[p][j] = run;
+            bt[p][j] = sm.beta[16 * p + 4 * lg + j];
         }
-        // row side within the block, ert <= i <= c0 (dA and dM vanish above the diagonal)
-        for (int i = ert; i <= c0; ++i) {
-            const float kh = kcol(i) * __expf(g0 - gcol(i));
-            const float4 a4 = *reinterpret_cast<const float4*>(&dAc[i][c0]);
-            const float4 m4 = *reinterpret_cast<const float4*>(&dXc[i][c0]);
-            t1[0] += a4.x * kh; t1[1] += a4.y * kh; t1[2] += a4.z * kh; t1[3] += a4.w * kh;
-            t3[0] += m4.x * kh; t3[1] += m4.y * kh; t3[2] += m4.z * kh; t3[3] += m4.w * kh;
+        tot[p] = run;
+    }
+    {
+        // the earlier row groups of the channel (lanes ln + 16 l), block 0 before block 1
+        float pre0 = 0.f, pre1 = 0.f, all0 = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const float t0 = __shfl(tot[0], ln + 16 * l), t1 = __shfl(tot[1], ln + 16 * l);
+            pre0 += l < lg ? t0 : 0.f;
+            pre1 += l < lg ? t1 : 0.f;
+            all0 += t0;
         }
-        // column side within the block, c3 <= c2 < ert + 16
-        for (int c2 = c3; c2 < ert + 16; ++c2) {
-            const float hh = __expf(gcol(c2) - g3);
-            const float qh = qcol(c2) * hh, kh = sm.beta[c2] * kcol(c2) * hh;
-            const float4 a4 = *reinterpret_cast<const float4*>(&dAr[c2][c0]);
-            const float4 m4 = *reinterpret_cast<const float4*>(&dXr[c2][c0]);
-            t2[0] += a4.x * qh; t2[1] += a4.y * qh; t2[2] += a4.z * qh; t2[3] += a4.w * qh;
-            t4[0] += m4.x * kh; t4[1] += m4.y * kh; t4[2] += m4.z * kh; t4[3] += m4.w * kh;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            G[0][j] += pre0;
+            G[1][j] += all0 + pre1;
         }
-        float last = 0.f;
+    }
+    const float g16 = __shfl(G[1][0], ln), g31 = __shfl(G[1][3], ln + 48);
+    float T1[2][4], T2[2][4], T3[2][4], T4[2][4];
+    float e0[4], e1[4];         // exp(G_16 - G) of block 0's rows, exp(G - G_16) of block 1's
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        e0[j] = __expf(g16 - G[0][j]);
+        e1[j] = __expf(G[1][j] - g16);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) T1[p][j] = T2[p][j] = T3[p][j] = T4[p][j] = 0.f;
+    }
+    {
+        // across the blocks through row 16: block 1's row side over block 0's
+        // rows, block 0's column side over block 1's rows
+        float zk[4], zq[4], zb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            zk[e] = kv[0][e] * e0[e];
+            zq[e] = qv[1][e] * e1[e];
+            zb[e] = bt[1][e] * kv[1][e] * e1[e];
+        }
+        const f4 oa1 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dAr[16 + ln][4 * lg]), zk);
+        const f4 om1 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dXr[16 + ln][4 * lg]), zk);
+        const f4 oa0 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dAc[ln][16 + 4 * lg]), zq);
+        const f4 om0 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dXc[ln][16 + 4 * lg]), zb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            T1[1][j] += e1[j] * oa1[j];
+            T3[1][j] += e1[j] * om1[j];
+            T2[0][j] += e0[j] * oa0[j];
+            T4[0][j] += e0[j] * om0[j];
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int o = 16 * p;
+        // levels 3 (8-row halves, reference row 7) and 2 (4-row halves of
+        // each 8-row half, reference row 3 or 11): M Z with M[r][s] =
+        // dA[max][min] on the level's pairs, Z[s] = q~_s e_s (upper s) or
+        // k_s e_s (lower s), e = exp(-|G - G_ref|); likewise dX with Z'[s] =
+        // beta_s k_s e_s or k_s e_s.  The reference rows are row 3 of lanes
+        // ln + 16 l.
+        const float gref3 = __shfl(G[p][3], ln + 16);
+        const float gref2 = __shfl(G[p][3], ln + 16 * (lg & ~1));
+#pragma unroll
+        for (int lev = 2; lev <= 3; ++lev) {
+            const bool up = lev == 3 ? lg >= 2 : (lg & 1) != 0;
+            const float gref = lev == 3 ? gref3 : gref2;
+            float eb[4], z[4], z2[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                eb[j] = __expf(up ? G[p][j] - gref : gref - G[p][j]);
+                z[j] = eb[j] * (up ? qv[p][j] : kv[p][j]);
+                z2[j] = eb[j] * kv[p][j] * (up ? bt[p][j] : 1.f);
+            }
+            const bool pair = lev == 3 ? (ln >> 3) != (lg >> 1)
+                                       : (ln >> 3) == (lg >> 1) && ((ln >> 2) & 1) != (lg & 1);
+            const bool below = ln > 4 * lg;     // row ln after all of columns 4 lg .. 4 lg + 3
+            const f4 ar = *reinterpret_cast<const f4*>(&sm.dAr[o + ln][o + 4 * lg]);
+            const f4 ac = *reinterpret_cast<const f4*>(&sm.dAc[o + ln][o + 4 * lg]);
+            const f4 xr = *reinterpret_cast<const f4*>(&sm.dXr[o + ln][o + 4 * lg]);
+            const f4 xc = *reinterpret_cast<const f4*>(&sm.dXc[o + ln][o + 4 * lg]);
+            f4 m, m2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                m[e] = pair ? (below ? ar[e] : ac[e]) : 0.f;
+                m2[e] = pair ? (below ? xr[e] : xc[e]) : 0.f;
+            }
+            const f4 P = mfma_pair16(m, z), P2 = mfma_pair16(m2, z2);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (up) {
+                    T1[p][j] += eb[j] * P[j];
+                    T3[p][j] += eb[j] * P2[j];
+                } else {
+                    T2[p][j] += eb[j] * P[j];
+                    T4[p][j] += eb[j] * P2[j];
+                }
+            }
+        }
+        // the lane's own four rows (levels 0 and 1, and the diagonal):
+        // pe[x][y] = exp(G_y - G_x), x < y
+        float pe[4][4];
+#pragma unroll
+        for (int y = 1; y < 4; ++y)
+#pragma unroll
+            for (int z = 0; z < y; ++z) pe[z][y] = __expf(G[p][y] - G[p][z]);
+        const int c0 = o + 4 * lg;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = c0 + j;
-            const float gcc = gcol(c);
-            const float f0 = __expf(gcc - g0), f3 = __expf(g3 - gcc);
-            float T1 = f0 * t1[j], T3 = f0 * t3[j], T2 = f3 * t2[j], T4 = f3 * t4[j];
-            if (ert == 16) {
-                const float e = __expf(gcc - g16);
-                T1 += e * oa[j];
-                T3 += e * om[j];
-            } else {
-                const float e = __expf(g16 - gcc);
-                T2 += e * oa[j];
-                T4 += e * om[j];
-            }
-            // the lane's own rows: c0 < i <= c (row side), c <= c2 < c3 (column side)
+            const f4 arow = *reinterpret_cast<const f4*>(&sm.dAr[c][c0]);    // dA[c][c0 + z]
+            const f4 xrow = *reinterpret_cast<const f4*>(&sm.dXr[c][c0]);
+            const f4 acol = *reinterpret_cast<const f4*>(&sm.dAc[c][c0]);    // dA[c0 + z][c]
+            const f4 xcol = *reinterpret_cast<const f4*>(&sm.dXc[c][c0]);
+            T1[p][j] += arow[j] * kv[p][j];
+            T2[p][j] += arow[j] * qv[p][j];
 #pragma unroll
-            for (int x = 1; x < 4; ++x) {
-                if (x <= j) {
-                    const float d = __expf(gcc - gcol(c0 + x)) * kcol(c0 + x);
-                    T1 += sm.dA[c][c0 + x] * d;
-                    T3 += sm.dM[c][c0 + x] * d;
+            for (int z = 0; z < 4; ++z) {
+                if (z < j) {
+                    const float d = pe[z][j] * kv[p][z];
+                    T1[p][j] += arow[z] * d;
+                    T3[p][j] += xrow[z] * d;
                 }
-                if (x - 1 >= j) {
-                    const int c2 = c0 + x - 1;
-                    const float d = __expf(gcol(c2) - gcc);
-                    T2 += sm.dA[c2][c] * qcol(c2) * d;
-                    T4 += sm.beta[c2] * sm.dM[c2][c] * kcol(c2) * d;
+                if (z > j) {
+                    const float d = pe[j][z];
+                    T2[p][j] += acol[z] * qv[p][z] * d;
+                    T4[p][j] += bt[p][z] * xcol[z] * kv[p][z] * d;
                 }
             }
-            T3 *= sm.beta[c];
-            const float E = sm.e[c][ekk];
-            const float F = __expf(gcol(CT - 1) - gcc);
-            const float dqt = T1 + dqe[j] * E;
-            const float dk = T2 + T3 + T4 + dke[j] * E + dkf[j] * F;
-            const float qc = qcol(c), kc = kcol(c);
-            const float dgv = qc * T1 + kc * (T3 - T2 - T4) + dqe[j] * qc * E + dke[j] * kc * E - dkf[j] * kc * F;
-            last += dkf[j] * kc * F;
-            sm.e[c][ekk] = dgv;   // exp(G) is no longer read: it holds dG from here on
-            const int64_t row = static_cast<int64_t>(n) * CT + c;
-            if (row < T) {
-                const int64_t o = ((b * T + row) * H + h) * K + ekk;
+        }
+    }
+    // outputs: dq, dk per element; dG per element, then dg = the reverse
+    // in-chunk cumulative sum of dG plus deps * eps plus sum_c d(kF)_c k_c F_c
+    float dG[2][4], lsum = 0.f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 16 * p + 4 * lg + j;
+            const float E = __expf(G[p][j]), F = __expf(g31 - G[p][j]);
+            const float t3 = T3[p][j] * bt[p][j];
+            const float qc = qv[p][j], kc = kv[p][j];
+            const float dqt = T1[p][j] + dqe[p][j] * E;
+            const float dk = T2[p][j] + t3 + T4[p][j] + dke[p][j] * E + dkf[p][j] * F;
+            dG[p][j] = qc * T1[p][j] + kc * (t3 - T2[p][j] - T4[p][j]) + dqe[p][j] * qc * E + dke[p][j] * kc * E -
+                       dkf[p][j] * kc * F;
+            lsum += dkf[p][j] * kc * F;
+            if (c < nrow) {
+                const int64_t o = ((b * T + r0 + c) * H + h) * K + x;
                 Elem<TI>::st(dqp + o, dqt * scale);
                 Elem<TI>::st(dkp + o, dk);
             }
         }
-        (&sm.Y[0][0])[((w / KTL) * 4 + lg) * K + ekk] = last;
-    }
-    __syncthreads();
-
-    // ------------------------------- dg (reverse in-chunk cumsum), dbeta
-    // thread (rg, kk): suffix sums over its rows, then over the later row groups
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
     {
-        float* gtot = reinterpret_cast<float*>(&sm.st.dS);   // [NT / K][K]; dS is no longer read
-        float sfx[RPT];
-        float acc = 0.f;
+        float sfx[2][4], st[2];
 #pragma unroll
-        for (int j = RPT - 1; j >= 0; --j) {
-            acc += sm.e[RPT * rg + j][kk];
-            sfx[j] = acc;
+        for (int p = 0; p < 2; ++p) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 3; j >= 0; --j) {
+                acc += dG[p][j];
+                sfx[p][j] = acc;
+            }
+            st[p] = acc;
         }
-        gtot[rg * K + kk] = acc;
-        __syncthreads();
-        float post = sm.deps[kk] * sm.eps[kk];
+        // the later row groups of the channel; block 1 after block 0
+        float post0 = 0.f, post1 = 0.f, all1 = 0.f;
 #pragma unroll
-        for (int x = 0; x < 8; ++x) post += (&sm.Y[0][0])[x * K + kk];
-#pragma unroll
-        for (int r = 0; r < NT / K; ++r) post += r > rg ? gtot[r * K + kk] : 0.f;
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int64_t row = static_cast<int64_t>(n) * CT + RPT * rg + j;
-            if (row < T) a.dg[((b * T + row) * H + h) * K + kk] = post + sfx[j];
+        for (int l = 0; l < 4; ++l) {
+            const float s0 = __shfl(st[0], ln + 16 * l), s1 = __shfl(st[1], ln + 16 * l);
+            post0 += l > lg ? s0 : 0.f;
+            post1 += l > lg ? s1 : 0.f;
+            all1 += s1;
         }
-    }
-    if (t < CT) {
-        const int64_t row = static_cast<int64_t>(n) * CT + t;
-        if (row < T) a.dbeta[(b * T + row) * H + h] = sm.dbeta[t];
+        const float base = deps * __expf(g31) + lsum;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = 16 * p + 4 * lg + j;
+                if (c < nrow)
+                    a.dg[((b * T + r0 + c) * H + h) * K + x] =
+                        base + (p == 0 ? all1 + post0 : post1) + sfx[p][j];
+            }
     }
 }
 
@@ -1230,7 +1297,7 @@ int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
                            stream, a, ws);
     if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     if (nck > 0) {
-        hipLaunchKernelGGL((bwd_chunk_kernel<K, TI>), dim3(static_cast<unsigned>(BH * nck)), dim3(NT), 0, stream,
+        hipLaunchKernelGGL((bwd_chunk_kernel<K, TI>), dim3(static_cast<unsigned>(BH * nck)), dim3(4 * K), 0, stream,
                            a, ws);
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
