@@ -812,7 +812,7 @@ struct __align__(16) ChunkSmem {
 // computed.  About 60 KiB of LDS at K = 128: two workgroups share a CU, one
 // workgroup's HBM-bound column steps overlapping the other's element step.
 template <int K, typename TI>
-__global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, const BwdWs ws) {
+__global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void bwd_chunk_kernel(const kda_bwd_args a, const BwdWs ws) {
     constexpr int NW = K / 16, NTC = 64 * NW;
     constexpr int EPT = CT * VT / NTC;      // tile elements per thread and tensor
     constexpr int MPW = 8 / NW;             // dA / dM tiles per wave
@@ -839,10 +839,10 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
     const int x = 16 * w + ln;              // the lane's channel
 
     // ------------------------------------------------------------ loads
-    // q, k, g of the lane's rows 16 p + 4 lg + j, channel x (used after the
-    // column steps)
+    // q, k, g of the lane's rows 16 p + 4 lg + j, channel x: fetched during
+    // the last column step, used after the column steps
     uint32_t rq[2][4], rk[2][4], rg[2][4];
-    {
+    auto fetch_rows = [&]() {
         const int64_t base = ((b * T + r0) * H + h) * K;
         const uint32_t HK = static_cast<uint32_t>(H * K);
         const uint32_t span = static_cast<uint32_t>(nrow - 1) * HK + K;
@@ -863,7 +863,7 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
                 }
                 rg[p][j] = __builtin_amdgcn_raw_buffer_load_b32(dg, static_cast<int>(4 * vo), static_cast<int>(4 * so), 0);
             }
-    }
+    };
 #pragma unroll
     for (int m = 0; m < CT * CT / NTC; ++m) {
         const int e = t + NTC * m;
@@ -927,7 +927,10 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
 #pragma unroll
     for (int p = 0; p < 2; ++p) dqe[p] = dke[p] = dkf[p] = f4{0.f, 0.f, 0.f, 0.f};
     float deps = 0.f;
-    for (int vt = 0; vt < nvt; ++vt) {
+    // one column step: stage the fetched tiles, then (after the caller's
+    // fetch of what comes next and a barrier) the products
+    bf8 sh, sl, dsh, dsl;
+    auto stage = [&](int vt) {
         use_here(fS);
         use_here(fdS);
         use_here(fR);
@@ -954,12 +957,10 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
             dsv[e] = __uint_as_float(fdS[e]);
             deps = fmaf(sv[e], dsv[e], deps);
         }
-        bf8 sh, sl, dsh, dsl;
         split8(sv, sh, sl);
         split8(dsv, dsh, dsl);
-        if (vt + 1 < nvt) fetch(vt + 1);
-        __syncthreads();
-
+    };
+    auto products = [&]() {
 #pragma unroll
         for (int m = 0; m < MPW; ++m) {
             const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
@@ -974,10 +975,31 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
             dke[p] = mm_pair_r(sm.dR[0][er], sm.dR[1][er], sh, sl, lg, dke[p]);
             dkf[p] = mm_pair_r(sm.P[0][er], sm.P[1][er], dsh, dsl, lg, dkf[p]);
         }
+    };
+    for (int vt = 0; vt + 1 < nvt; ++vt) {
+        stage(vt);
+        fetch(vt + 1);
+        __syncthreads();
+        products();
         __syncthreads();
     }
+    // the last step fetches the element step's rows instead
+    stage(nvt - 1);
+    fetch_rows();
+    __syncthreads();
+    products();
+    __syncthreads();
+    // block 0's accumulators wait in the (now free) tile area while block 1's
+    // element step runs: slot i of thread t at stash[i * NTC + t]
+    float* stash = reinterpret_cast<float*>(&sm.dO[0][0][0]);
+    static_assert(12 * NTC * 4 <= 5 * sizeof(sm.dO), "the stash fits the tiles");
 #pragma unroll
-    for (int p = 0; p < 2; ++p) dke[p] = f4{0.f, 0.f, 0.f, 0.f} - dke[p];
+    for (int j = 0; j < 4; ++j) {
+        stash[(0 + j) * NTC + t] = dqe[0][j];
+        stash[(4 + j) * NTC + t] = -dke[0][j];
+        stash[(8 + j) * NTC + t] = dkf[0][j];
+    }
+    dke[1] = f4{0.f, 0.f, 0.f, 0.f} - dke[1];
     // deps of channel x: the shares of the four lanes of the channel
     deps += __shfl_xor(deps, 16);
     deps += __shfl_xor(deps, 32);
@@ -1067,7 +1089,7 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
     use_here(rq);
     use_here(rk);
     use_here(rg);
-    float qv[2][4], kv[2][4], G[2][4], bt[2][4];
+    float qv[2][4], kv[2][4], G[2][4];
     float tot[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -1078,7 +1100,6 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
             kv[p][j] = raw_f32<TI>(rk[p][j]);
             run += __uint_as_float(rg[p][j]);
             G[p][j] = run;
-            bt[p][j] = sm.beta[16 * p + 4 * lg + j];
         }
         tot[p] = run;
     }
@@ -1099,40 +1120,69 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
         }
     }
     const float g16 = __shfl(G[1][0], ln), g31 = __shfl(G[1][3], ln + 48);
-    float T1[2][4], T2[2][4], T3[2][4], T4[2][4];
-    float e0[4], e1[4];         // exp(G_16 - G) of block 0's rows, exp(G - G_16) of block 1's
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        e0[j] = __expf(g16 - G[0][j]);
-        e1[j] = __expf(G[1][j] - g16);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) T1[p][j] = T2[p][j] = T3[p][j] = T4[p][j] = 0.f;
-    }
+    asm volatile("" ::: "memory");
+    // dg = the reverse in-chunk cumulative sum of dG plus deps * eps plus
+    // sum_c d(kF)_c k_c F_c (over the channel's lanes)
+    float base;
     {
-        // across the blocks through row 16: block 1's row side over block 0's
-        // rows, block 0's column side over block 1's rows
-        float zk[4], zq[4], zb[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            zk[e] = kv[0][e] * e0[e];
-            zq[e] = qv[1][e] * e1[e];
-            zb[e] = bt[1][e] * kv[1][e] * e1[e];
-        }
-        const f4 oa1 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dAr[16 + ln][4 * lg]), zk);
-        const f4 om1 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dXr[16 + ln][4 * lg]), zk);
-        const f4 oa0 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dAc[ln][16 + 4 * lg]), zq);
-        const f4 om0 = mfma_pair16(*reinterpret_cast<const f4*>(&sm.dXc[ln][16 + 4 * lg]), zb);
+        float ls = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            T1[1][j] += e1[j] * oa1[j];
-            T3[1][j] += e1[j] * om1[j];
-            T2[0][j] += e0[j] * oa0[j];
-            T4[0][j] += e0[j] * om0[j];
+            ls += stash[(8 + j) * NTC + t] * kv[0][j] * __expf(g31 - G[0][j]);
+            ls += dkf[1][j] * kv[1][j] * __expf(g31 - G[1][j]);
         }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        base = deps * __expf(g31) + ls;
     }
+    // block 1 first (its rows' dG sums enter block 0's dg)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 1; p >= 0; --p) {
         const int o = 16 * p;
+        f4 aq, ak, af;          // this block's d(q~E), d(kE), d(kF)
+        if (p == 1) {
+            aq = dqe[1];
+            ak = dke[1];
+            af = dkf[1];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                aq[j] = stash[(0 + j) * NTC + t];
+                ak[j] = stash[(4 + j) * NTC + t];
+                af[j] = stash[(8 + j) * NTC + t];
+            }
+        }
+        float T1[4], T2[4], T3[4], T4[4], bt[4];
+        // across the blocks through row 16: block 1's row side over block 0's
+        // rows (T1, T3), block 0's column side over block 1's rows (T2, T4)
+        {
+            float z[4], z2[4], ex[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (p == 0) {
+                    const float e1 = __expf(G[1][e] - g16);
+                    z[e] = qv[1][e] * e1;
+                    z2[e] = sm.beta[16 + 4 * lg + e] * kv[1][e] * e1;
+                    ex[e] = __expf(g16 - G[0][e]);
+                } else {
+                    ex[e] = __expf(G[1][e] - g16);
+                    z[e] = kv[0][e] * __expf(g16 - G[0][e]);
+                    z2[e] = z[e];
+                }
+            }
+            const f4 oa = p == 0 ? mfma_pair16(*reinterpret_cast<const f4*>(&sm.dAc[ln][16 + 4 * lg]), z)
+                                 : mfma_pair16(*reinterpret_cast<const f4*>(&sm.dAr[16 + ln][4 * lg]), z);
+            const f4 om = p == 0 ? mfma_pair16(*reinterpret_cast<const f4*>(&sm.dXc[ln][16 + 4 * lg]), z2)
+                                 : mfma_pair16(*reinterpret_cast<const f4*>(&sm.dXr[16 + ln][4 * lg]), z2);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                T1[j] = p == 1 ? ex[j] * oa[j] : 0.f;
+                T3[j] = p == 1 ? ex[j] * om[j] : 0.f;
+                T2[j] = p == 0 ? ex[j] * oa[j] : 0.f;
+                T4[j] = p == 0 ? ex[j] * om[j] : 0.f;
+                bt[j] = sm.beta[o + 4 * lg + j];
+            }
+        }
         // levels 3 (8-row halves, reference row 7) and 2 (4-row halves of
         // each 8-row half, reference row 3 or 11): M Z with M[r][s] =
         // dA[max][min] on the level's pairs, Z[s] = q~_s e_s (upper s) or
@@ -1150,35 +1200,29 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
             for (int j = 0; j < 4; ++j) {
                 eb[j] = __expf(up ? G[p][j] - gref : gref - G[p][j]);
                 z[j] = eb[j] * (up ? qv[p][j] : kv[p][j]);
-                z2[j] = eb[j] * kv[p][j] * (up ? bt[p][j] : 1.f);
+                z2[j] = eb[j] * kv[p][j] * (up ? bt[j] : 1.f);
             }
             const bool pair = lev == 3 ? (ln >> 3) != (lg >> 1)
                                        : (ln >> 3) == (lg >> 1) && ((ln >> 2) & 1) != (lg & 1);
-            const bool below = ln > 4 * lg;     // row ln after all of columns 4 lg .. 4 lg + 3
-            const f4 ar = *reinterpret_cast<const f4*>(&sm.dAr[o + ln][o + 4 * lg]);
-            const f4 ac = *reinterpret_cast<const f4*>(&sm.dAc[o + ln][o + 4 * lg]);
-            const f4 xr = *reinterpret_cast<const f4*>(&sm.dXr[o + ln][o + 4 * lg]);
-            const f4 xc = *reinterpret_cast<const f4*>(&sm.dXc[o + ln][o + 4 * lg]);
-            f4 m, m2;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                m[e] = pair ? (below ? ar[e] : ac[e]) : 0.f;
-                m2[e] = pair ? (below ? xr[e] : xc[e]) : 0.f;
-            }
-            const f4 P = mfma_pair16(m, z), P2 = mfma_pair16(m2, z2);
+            // row ln after all of columns 4 lg .. 4 lg + 3: dA[ln][s] by rows, else dA[s][ln] by columns
+            const bool below = ln > 4 * lg;
+            const f4 ma = *reinterpret_cast<const f4*>(below ? &sm.dAr[o + ln][o + 4 * lg] : &sm.dAc[o + ln][o + 4 * lg]);
+            const f4 mx = *reinterpret_cast<const f4*>(below ? &sm.dXr[o + ln][o + 4 * lg] : &sm.dXc[o + ln][o + 4 * lg]);
+            const f4 zero = {0.f, 0.f, 0.f, 0.f};
+            const f4 P = mfma_pair16(pair ? ma : zero, z), P2 = mfma_pair16(pair ? mx : zero, z2);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 if (up) {
-                    T1[p][j] += eb[j] * P[j];
-                    T3[p][j] += eb[j] * P2[j];
+                    T1[j] += eb[j] * P[j];
+                    T3[j] += eb[j] * P2[j];
                 } else {
-                    T2[p][j] += eb[j] * P[j];
-                    T4[p][j] += eb[j] * P2[j];
+                    T2[j] += eb[j] * P[j];
+                    T4[j] += eb[j] * P2[j];
                 }
             }
         }
         // the lane's own four rows (levels 0 and 1, and the diagonal):
-        // pe[x][y] = exp(G_y - G_x), x < y
+        // pe[z][y] = exp(G_y - G_z), z < y
         float pe[4][4];
 #pragma unroll
         for (int y = 1; y < 4; ++y)
@@ -1192,78 +1236,60 @@ __global__ __launch_bounds__(4 * K) void bwd_chunk_kernel(const kda_bwd_args a, 
             const f4 xrow = *reinterpret_cast<const f4*>(&sm.dXr[c][c0]);
             const f4 acol = *reinterpret_cast<const f4*>(&sm.dAc[c][c0]);    // dA[c0 + z][c]
             const f4 xcol = *reinterpret_cast<const f4*>(&sm.dXc[c][c0]);
-            T1[p][j] += arow[j] * kv[p][j];
-            T2[p][j] += arow[j] * qv[p][j];
+            T1[j] += arow[j] * kv[p][j];
+            T2[j] += arow[j] * qv[p][j];
 #pragma unroll
             for (int z = 0; z < 4; ++z) {
                 if (z < j) {
                     const float d = pe[z][j] * kv[p][z];
-                    T1[p][j] += arow[z] * d;
-                    T3[p][j] += xrow[z] * d;
+                    T1[j] += arow[z] * d;
+                    T3[j] += xrow[z] * d;
                 }
                 if (z > j) {
                     const float d = pe[j][z];
-                    T2[p][j] += acol[z] * qv[p][z] * d;
-                    T4[p][j] += bt[p][z] * xcol[z] * kv[p][z] * d;
+                    T2[j] += acol[z] * qv[p][z] * d;
+                    T4[j] += bt[z] * xcol[z] * kv[p][z] * d;
                 }
             }
         }
-    }
-    // outputs: dq, dk per element; dG per element, then dg = the reverse
-    // in-chunk cumulative sum of dG plus deps * eps plus sum_c d(kF)_c k_c F_c
-    float dG[2][4], lsum = 0.f;
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
+        // outputs: dq, dk per element; dG per element and its reverse sums
+        float dG[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int c = 16 * p + 4 * lg + j;
+            const int c = c0 + j;
             const float E = __expf(G[p][j]), F = __expf(g31 - G[p][j]);
-            const float t3 = T3[p][j] * bt[p][j];
+            const float t3 = T3[j] * bt[j];
             const float qc = qv[p][j], kc = kv[p][j];
-            const float dqt = T1[p][j] + dqe[p][j] * E;
-            const float dk = T2[p][j] + t3 + T4[p][j] + dke[p][j] * E + dkf[p][j] * F;
-            dG[p][j] = qc * T1[p][j] + kc * (t3 - T2[p][j] - T4[p][j]) + dqe[p][j] * qc * E + dke[p][j] * kc * E -
-                       dkf[p][j] * kc * F;
-            lsum += dkf[p][j] * kc * F;
+            const float dqt = T1[j] + aq[j] * E;
+            const float dk = T2[j] + t3 + T4[j] + ak[j] * E + af[j] * F;
+            dG[j] = qc * T1[j] + kc * (t3 - T2[j] - T4[j]) + aq[j] * qc * E + ak[j] * kc * E - af[j] * kc * F;
             if (c < nrow) {
-                const int64_t o = ((b * T + r0 + c) * H + h) * K + x;
-                Elem<TI>::st(dqp + o, dqt * scale);
-                Elem<TI>::st(dkp + o, dk);
+                const int64_t off = ((b * T + r0 + c) * H + h) * K + x;
+                Elem<TI>::st(dqp + off, dqt * scale);
+                Elem<TI>::st(dkp + off, dk);
             }
         }
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    {
-        float sfx[2][4], st[2];
+        float acc = 0.f, sfx[4];
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 3; j >= 0; --j) {
-                acc += dG[p][j];
-                sfx[p][j] = acc;
-            }
-            st[p] = acc;
+        for (int j = 3; j >= 0; --j) {
+            acc += dG[j];
+            sfx[j] = acc;
         }
-        // the later row groups of the channel; block 1 after block 0
-        float post0 = 0.f, post1 = 0.f, all1 = 0.f;
+        // the later row groups of the channel in this block, then block 1's
+        // rows (for block 0)
+        float post = 0.f, all = 0.f;
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const float s0 = __shfl(st[0], ln + 16 * l), s1 = __shfl(st[1], ln + 16 * l);
-            post0 += l > lg ? s0 : 0.f;
-            post1 += l > lg ? s1 : 0.f;
-            all1 += s1;
+            const float sl = __shfl(acc, ln + 16 * l);
+            post += l > lg ? sl : 0.f;
+            all += sl;
         }
-        const float base = deps * __expf(g31) + lsum;
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = 16 * p + 4 * lg + j;
-                if (c < nrow)
-                    a.dg[((b * T + r0 + c) * H + h) * K + x] =
-                        base + (p == 0 ? all1 + post0 : post1) + sfx[p][j];
-            }
+        for (int j = 0; j < 4; ++j) {
+            const int c = c0 + j;
+            if (c < nrow) a.dg[((b * T + r0 + c) * H + h) * K + x] = base + post + sfx[j];
+        }
+        base += all;
     }
 }
 
