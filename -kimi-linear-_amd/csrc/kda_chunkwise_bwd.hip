@@ -151,6 +151,7 @@ typedef float f2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
 typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+typedef uint32_t w2 __attribute__((ext_vector_type(2)));
 
 // Eight values as bf16 pairs (hi = bf16(x), lo = bf16(x - hi)), two values
 // per conversion.
@@ -517,6 +518,31 @@ __device__ __forceinline__ void put4_pair(uint16_t* hi, uint16_t* lo, const f4& 
     *reinterpret_cast<uint2*>(lo) = uint2{l[0] | (uint32_t(l[1]) << 16), l[2] | (uint32_t(l[3]) << 16)};
 }
 
+// N (2, 4 or 8) values as bf16 pairs into N consecutive hi and lo slots
+// (one 4-, 8- or 16-byte write each; two values per conversion).
+template <int N>
+__device__ __forceinline__ void put_pairs(uint16_t* hi, uint16_t* lo, const float (&v)[N]) {
+    static_assert(N == 2 || N == 4 || N == 8, "pair run length");
+    uint32_t hw[N / 2], lw[N / 2];
+#pragma unroll
+    for (int e = 0; e < N / 2; ++e) {
+        const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e], v[2 * e + 1]}, bf2));
+        const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xffff0000u);
+        hw[e] = hb;
+        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e] - h0, v[2 * e + 1] - h1}, bf2));
+    }
+    if constexpr (N == 2) {
+        *reinterpret_cast<uint32_t*>(hi) = hw[0];
+        *reinterpret_cast<uint32_t*>(lo) = lw[0];
+    } else if constexpr (N == 4) {
+        *reinterpret_cast<w2*>(hi) = w2{hw[0], hw[1]};
+        *reinterpret_cast<w2*>(lo) = w2{lw[0], lw[1]};
+    } else {
+        *reinterpret_cast<w4*>(hi) = w4{hw[0], hw[1], hw[2], hw[3]};
+        *reinterpret_cast<w4*>(lo) = w4{lw[0], lw[1], lw[2], lw[3]};
+    }
+}
+
 // One workgroup per (b, h, VA state columns), the chunks in reverse.  dS, the
 // gradient of the state, stays in fp32 accumulators (tile ti = w + 16 m of
 // each wave: channels 16 (ti / VTL), columns 16 (ti % VTL)) and is copied as a
@@ -539,8 +565,13 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
 
     const int64_t H = a.H, T = a.T, V = a.V;
     const int nva = static_cast<int>(V / VA);
-    const int64_t bh = blockIdx.x / nva, b = bh / H, h = bh % H;
-    const int64_t v0 = static_cast<int64_t>(blockIdx.x % nva) * VA;
+    // Workgroups are dealt to the eight XCDs round robin (g % 8): with B H a
+    // multiple of 8, the nva workgroups of one (b, h) share g % 8, hence an
+    // XCD and its L2, and read that head's q, k, g from HBM once.
+    const int64_t g = blockIdx.x, BH = a.B * H;
+    const bool xcd = BH % 8 == 0;
+    const int64_t bh = xcd ? (g / 8 / nva) * 8 + g % 8 : g / nva, b = bh / H, h = bh % H;
+    const int64_t v0 = (xcd ? (g / 8) % nva : g % nva) * VA;
     const int nck = static_cast<int>((T + CT - 1) / CT);
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
     const int x = t % K, rg = t / K;
@@ -559,71 +590,94 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
         }
     }
 
-    // fetched elements stay in the input dtype until they are staged: a
-    // conversion next to its load would wait for it
-    TI pq[RPT], pk[RPT], pdo[DPT];
-    float pg[RPT], pa[APT], pn[APT], pb = 0.f;
-    // global addresses as a per-chunk uniform base plus a loop-invariant
-    // 32-bit offset per thread (registers for the pipeline, not for addresses)
+    // Fetched raw through descriptors whose range stops at the chunk's last
+    // row before T (rows past T read as zero), one lane offset per tensor and
+    // the row in the scalar offset; converted only where staged.  Thread
+    // (rg, x): rows RPT rg .. + RPT - 1 of channel x (q, k, g); thread
+    // (t % VA, t / VA): rows DPT (t / VA) .. + DPT - 1 of dO column t % VA;
+    // thread (t % CT, t / CT): rows APT (t / CT) .. + APT - 1 of A and N
+    // column t % CT -- each one contiguous run of the transposed pair arrays.
+    constexpr int SZ = sizeof(TI);
+    uint32_t pq[RPT], pk[RPT], pg[RPT], pdo[DPT], pa[APT], pn[APT], pb[1] = {0u};
     const uint32_t HK = static_cast<uint32_t>(H * K), HV = static_cast<uint32_t>(H * V);
-    const uint32_t oqk = static_cast<uint32_t>(RPT * rg) * HK + x;
+    const uint32_t lo_x = static_cast<uint32_t>(RPT * rg) * HK + x;
+    const int dv_ = t % VA, dc0 = DPT * (t / VA);
+    const uint32_t lo_o = static_cast<uint32_t>(dc0) * HV + dv_;
+    const int ai = t % CT, ac0 = APT * (t / CT);
     auto fetch = [&](int n) {
         const int64_t r0 = static_cast<int64_t>(n) * CT;
-        const TI* qn = qp + ((b * T + r0) * H + h) * K;
-        const TI* kn = kp + ((b * T + r0) * H + h) * K;
-        const float* gn = a.g + ((b * T + r0) * H + h) * K;
+        const int64_t nrow = std::min<int64_t>(CT, T - r0);
+        const int64_t base = ((b * T + r0) * H + h) * K;
+        const uint32_t span = static_cast<uint32_t>((nrow - 1) * H * K + K);
+        const auto rq = make_rsrc(qp + base, span * SZ), rk = make_rsrc(kp + base, span * SZ);
+        const auto rgc = make_rsrc(a.g + base, span * 4);
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
-            pq[j] = pk[j] = TI{};
-            pg[j] = 0.f;
-            if (r0 + RPT * rg + j < T) {
-                const uint32_t o = oqk + j * HK;
-                pq[j] = qn[o];
-                pk[j] = kn[o];
-                pg[j] = gn[o];
+            const uint32_t so = static_cast<uint32_t>(j) * HK;
+            if constexpr (SZ == 2) {
+                pq[j] = __builtin_amdgcn_raw_buffer_load_b16(rq, static_cast<int>(2 * lo_x), static_cast<int>(2 * so), 0);
+                pk[j] = __builtin_amdgcn_raw_buffer_load_b16(rk, static_cast<int>(2 * lo_x), static_cast<int>(2 * so), 0);
+            } else {
+                pq[j] = __builtin_amdgcn_raw_buffer_load_b32(rq, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
+                pk[j] = __builtin_amdgcn_raw_buffer_load_b32(rk, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
             }
+            pg[j] = __builtin_amdgcn_raw_buffer_load_b32(rgc, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
         }
-        const TI* don = dop + ((b * T + r0) * H + h) * V + v0;
+        const auto ro = make_rsrc(dop + ((b * T + r0) * H + h) * V + v0,
+                                  static_cast<uint32_t>(((nrow - 1) * H * V + VA) * SZ));
 #pragma unroll
         for (int j = 0; j < DPT; ++j) {
-            const int e = t + NS * j;
-            pdo[j] = r0 + e / VA < T ? don[static_cast<uint32_t>(e / VA) * HV + e % VA] : TI{};
+            const uint32_t so = static_cast<uint32_t>(j) * HV * SZ;
+            if constexpr (SZ == 2)
+                pdo[j] = __builtin_amdgcn_raw_buffer_load_b16(ro, static_cast<int>(2 * lo_o), static_cast<int>(so), 0);
+            else
+                pdo[j] = __builtin_amdgcn_raw_buffer_load_b32(ro, static_cast<int>(4 * lo_o), static_cast<int>(so), 0);
         }
-        const int64_t cb = bh * nck + n;
+        const float* an = ws.A + (bh * nck + n) * CT * CT;
+        const float* nn = ws.N + (bh * nck + n) * CT * CT;
 #pragma unroll
         for (int j = 0; j < APT; ++j) {
-            pa[j] = ws.A[cb * CT * CT + t + NS * j];
-            pn[j] = ws.N[cb * CT * CT + t + NS * j];
+            pa[j] = __float_as_uint(an[(ac0 + j) * CT + ai]);
+            pn[j] = __float_as_uint(nn[(ac0 + j) * CT + ai]);
         }
-        if (t < CT) pb = r0 + t < T ? a.beta[(b * T + r0) * H + h + static_cast<uint32_t>(t) * H] : 0.f;
+        if (t < CT) pb[0] = r0 + t < T ? __float_as_uint(a.beta[(b * T + r0 + t) * H + h]) : 0u;
     };
     if (nck > 0) fetch(nck - 1);
 
     for (int n = nck - 1; n >= 0; --n) {
         const int64_t cb = bh * nck + n;
         // stage chunk n (A^T, N^T, dO^T as pairs, the row groups' g sums); fetch chunk n - 1
+        use_here(pq);
+        use_here(pk);
+        use_here(pg);
+        use_here(pdo);
+        use_here(pa);
+        use_here(pn);
+        use_here(pb);
         float cq[RPT], ck[RPT], cg[RPT];
         float run = 0.f;
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
-            run += pg[j];
+            run += __uint_as_float(pg[j]);
             cg[j] = run;
-            cq[j] = Elem<TI>::ld(&pq[j]);
-            ck[j] = Elem<TI>::ld(&pk[j]);
+            cq[j] = raw_f32<TI>(pq[j]);
+            ck[j] = raw_f32<TI>(pk[j]);
         }
         sm.tot[rg][x] = run;
+        {
+            float va[APT], vn[APT], vo[DPT];
 #pragma unroll
-        for (int j = 0; j < APT; ++j) {
-            const int e = t + NS * j;
-            split_bf16(pa[j], sm.AT[0][e % CT][e / CT], sm.AT[1][e % CT][e / CT]);
-            split_bf16(pn[j], sm.NT_[0][e % CT][e / CT], sm.NT_[1][e % CT][e / CT]);
-        }
+            for (int j = 0; j < APT; ++j) {
+                va[j] = __uint_as_float(pa[j]);
+                vn[j] = __uint_as_float(pn[j]);
+            }
 #pragma unroll
-        for (int j = 0; j < DPT; ++j) {
-            const int e = t + NS * j, c = e / VA, v = e % VA;
-            split_bf16(Elem<TI>::ld(&pdo[j]), sm.dOT[0][v][c], sm.dOT[1][v][c]);
+            for (int j = 0; j < DPT; ++j) vo[j] = raw_f32<TI>(pdo[j]);
+            put_pairs(&sm.AT[0][ai][ac0], &sm.AT[1][ai][ac0], va);
+            put_pairs(&sm.NT_[0][ai][ac0], &sm.NT_[1][ai][ac0], vn);
+            put_pairs(&sm.dOT[0][dv_][dc0], &sm.dOT[1][dv_][dc0], vo);
         }
-        if (t < CT) sm.beta[t] = pb;
+        if (t < CT) sm.beta[t] = __uint_as_float(pb[0]);
         if (n > 0) fetch(n - 1);
         __syncthreads();
 
@@ -636,15 +690,18 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 pre += r < rg ? s : 0.f;
                 last += s;
             }
+            float qe[RPT], ke[RPT];
 #pragma unroll
             for (int j = 0; j < RPT; ++j) {
                 const int c = RPT * rg + j;
                 const float G = pre + cg[j];
                 const float E = __expf(G), F = __expf(last - G);
-                split_bf16(a.scale * cq[j] * E, sm.qeT[0][x][c], sm.qeT[1][x][c]);
-                split_bf16(ck[j] * E, sm.keT[0][x][c], sm.keT[1][x][c]);
+                qe[j] = a.scale * cq[j] * E;
+                ke[j] = ck[j] * E;
                 split_bf16(ck[j] * F, sm.kf[0][c][x], sm.kf[1][c][x]);
             }
+            put_pairs(&sm.qeT[0][x][RPT * rg], &sm.qeT[1][x][RPT * rg], qe);
+            put_pairs(&sm.keT[0][x][RPT * rg], &sm.keT[1][x][RPT * rg], ke);
             if (rg == 0) sm.eps[x] = __expf(last);
         }
         __syncthreads();
@@ -733,7 +790,6 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
 // ------------------------------------------------------------------ kernel 3
 
 typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
-typedef uint32_t w2 __attribute__((ext_vector_type(2)));
 
 // Four values as bf16 pairs, two values per conversion.
 __device__ __forceinline__ void split4(const float (&v)[4], bf4& hi, bf4& lo) {
