@@ -1,4 +1,4 @@
-// Chunkwise KDA backward for gfx950: fp32 throughout.
+// Chunkwise KDA backward for gfx950.
 //
 // Gradient of kda_chunkwise (kimi_linear/kda.py:58-185), whose reference is
 // differentiated by autograd (training: scripts/train_musicgpt_fp16.py:519-523).
@@ -27,23 +27,24 @@
 // Only the chain dS_end -> dP -> dR -> dS_start runs from chunk to chunk;
 // everything else is independent per chunk.  Three kernels, one fp32
 // workspace between them:
-//   1. bwd_pairs_kernel, one workgroup per (b, h, chunk): A, L and N of every
-//      chunk (functions of q, k, g and beta only).
+//   1. bwd_pairs_kernel, persistent: A, L and N of every chunk (functions of
+//      q, k, g and beta only), by decay level on the matrix cores.
 //   2. bwd_state_kernel, one workgroup per (b, h, VA state columns), the chunks
 //      in reverse: the chain above; it stores each chunk's dS_end, dP and dR
-//      (fp32) and dS_0.  The next chunk's inputs are fetched into registers while
-//      the current one is computed.
+//      (fp32) and dS_0.  The next chunk's inputs are fetched while the
+//      current one is computed.
 //   3. bwd_chunk_kernel, one workgroup per (b, h, chunk): writes dv = dR; from
 //      S, R, P (checkpoint), dS_end, dP and dR the sums over all state columns
-//      (VT at a time) of
-//      dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain through the
-//      inverse, the pairwise-decay products and the reverse cumulative sum:
-//      complete dq, dk, dg and dbeta.
+//      (VT at a time) of dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain
+//      through the inverse, the pairwise-decay products and the reverse
+//      cumulative sum: complete dq, dk, dg and dbeta.
 // Rows past T read as zero inputs, which leave the state and every gradient
 // of the rows before T unchanged.  q, k, v, dO and dq, dk, dv are in the
-// caller's activation dtype (fp32, fp16 or bf16; every product in fp32); g,
-// beta, the checkpoints, dg, dbeta and the state gradients are fp32.  The chunk-sized products run on the fp32
-// matrix cores (v_mfma_f32_16x16x4f32, no precision loss).
+// caller's activation dtype (fp32, fp16 or bf16); g, beta, the checkpoints,
+// dg, dbeta and the state gradients are fp32.  Products run on the matrix
+// cores as bf16 hi/lo pairs (~2^-17 relative each; fp32 accumulation),
+// except A and L for 16-bit activations (fp16 operands, the forward's
+// precision) and N (fp32 matrix cores).
 #include <algorithm>
 #include <atomic>
 #include <mutex>
@@ -57,8 +58,6 @@ namespace {
 
 constexpr int CT = 32;          // tokens per chunk = the forward's checkpoint spacing
 constexpr int VT = 32;          // state columns per step of bwd_chunk_kernel
-constexpr int NT = 1024;        // threads per workgroup
-static_assert(CT * VT == NT && CT * CT == NT, "one output per thread for the chunk-sized products");
 
 // Workspace, per (b, h) and chunk (index cb = (b H + h) nck + n):
 // A, L, N [CT][CT], dS_end [K][V], dP and dR [CT][V], fp32.
