@@ -1350,14 +1350,18 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 
 // Workgroups of a persistent kernel: as many as are resident at once on the
 // current device.
-template <typename Kern>
-int persistent_grid(Kern kernel, int threads) {
-    int dev = 0, cus = 0, per = 0;
+int cu_count() {
+    int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
+    return cus;
+}
+template <typename Kern>
+int persistent_grid(Kern kernel, int threads) {
+    int per = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
-    return cus * per;
+    return cu_count() * per;
 }
 
 template <int K, typename TI>
@@ -1370,7 +1374,9 @@ int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
                            dim3(NP), 0, stream, a, ws, BH * nck);
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
-    if (a.V % 64 == 0)
+    // 64 state columns a workgroup, or 32 when that leaves compute units idle
+    // (the chain is sequential: more, narrower workgroups shorten it)
+    if (a.V % 64 == 0 && BH * (a.V / 64) >= cu_count())
         hipLaunchKernelGGL((bwd_state_kernel<K, 64, TI>), dim3(static_cast<unsigned>(BH * (a.V / 64))), dim3(NS), 0,
                            stream, a, ws);
     else
