@@ -342,10 +342,29 @@ def backward_bench(pkg, wl, torch, reps=3):
         if i >= 2:
             fwd += e0.elapsed_time(e1) / reps
             bwd += e1.elapsed_time(e2) / reps
+    nbytes = backward_bytes(B1, T1, H1, D1, D1, 2)
     return {"workload": "kda_chunkwise forward (with 32-token checkpoints: state, R, P) + native backward under "
                         "autograd, B=8 T=4096 H=16 dk=dv=128; fp16 q/k/v, fp32 g/beta",
             "forward_ckpt_ms": fwd, "backward_ms": bwd,
-            "train_tokens_per_s": B1 * T1 / ((fwd + bwd) * 1e-3)}
+            "train_tokens_per_s": B1 * T1 / ((fwd + bwd) * 1e-3),
+            # the three backward kernels' algorithmic HBM bytes over the backward's
+            # wall time (autograd's own work included)
+            "backward_bytes": nbytes, "backward_hbm_frac": nbytes / (bwd * 1e-3) / (HBM_PEAK_GBS * 1e9)}
+
+
+def backward_bytes(B, T, H, K, V, sz):
+    """Algorithmic HBM bytes of kda_chunkwise_bwd's three kernels (activations of
+    sz bytes; workspace and checkpoints fp32; 32-token chunks): the pairs kernel
+    reads q, k, g, beta and writes A, L, N; the state kernel reads q, k, g, dO, A,
+    N, beta and writes dS_end, dP, dR; the chunk kernel reads the checkpoint (S, R,
+    P), dS_end, dP, dR, dO, q, k, g, L, N, beta and writes dq, dk, dv, dg, dbeta."""
+    nck = -(-T // 32)
+    qk, g, v, beta = B * T * H * K * sz, B * T * H * K * 4, B * T * H * V * sz, B * T * H * 4
+    mat, S, RP = B * H * nck * 32 * 32 * 4, B * H * nck * K * V * 4, B * H * nck * 32 * V * 4
+    pairs = 2 * qk + g + beta + 3 * mat
+    state = 2 * qk + g + v + 2 * mat + beta + S + 2 * RP
+    chunk = 2 * S + 4 * RP + v + 2 * qk + g + 2 * mat + beta + 2 * qk + v + g + beta
+    return pairs + state + chunk
 
 
 def cpu_model() -> str:
