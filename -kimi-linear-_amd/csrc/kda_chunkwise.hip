@@ -450,6 +450,15 @@ struct Kern {
     float gcoef[GATED ? CH : 1], gbias[GATED ? CH : 1];   // GATED: exp(A_log), dt_bias log2(e) of the channels
     uint32_t rs_q, rs_k, rs_g, rs_v, rs_b;   // token-row strides in bytes
     uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets
+    // kda_chunkwise_fwd_ckpt: the (b, h)'s chunk records, written by the
+    // head's first V-tile workgroup only (null otherwise): per 32-token chunk
+    // the state, R and P ((K + 64) x V) and then A, L and N (32 x 32 each)
+    float* ckm = nullptr;
+
+    // A, L, N of the chunk holding block blk (row-major 32 x 32, consecutive)
+    __device__ float* ck_mats(int blk) const {
+        return ckm + static_cast<int64_t>(blk / CB) * ckpt_record(K, a.V) + static_cast<int64_t>(K + 2 * CB * BT) * a.V;
+    }
 
     __device__ Kern(const kda_fwd_args& args, Smem<K, CG, EPI>& s) : a(args), sm(s) {}
 
@@ -697,7 +706,7 @@ struct Kern {
     // takes X^T's and Y's accumulator layouts, so the chain keeps powers and
     // their transposes side by side; no data moves between lanes.
     // The inputs are block p's in the solve exchange area (put_solve_in).
-    __device__ void solve(int p, _Float16 (*mh)[RP], _Float16 (*ml)[RP]) const {
+    __device__ void solve(int p, int blk, _Float16 (*mh)[RP], _Float16 (*ml)[RP]) const {
         const float (*g)[BT + 1] = sm.sv.g[p];
         const f4 bt = *reinterpret_cast<const f4*>(&sm.sv.beta[p][4 * lg]);   // beta of rows 4lg + j
         const float bc = sm.sv.beta[p][ln];                                   // beta of row ln
@@ -717,6 +726,13 @@ struct Kern {
         Q = mm_f32(L2, Q, Q);
         Q = mm_f32(L4, Q, Q);
         Q = mm_f32(L8, Q, Q);                    // acc((I + L)^-T) = A-layout of (I + L)^-1
+        if (ckm) {
+            // the backward's N block: N[ln][4 lg + j] = (I + L)^-1
+            float* n = ck_mats(blk) + 2 * CB * BT * CB * BT;
+            const int o = BT * (blk % CB);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) n[(o + ln) * (CB * BT) + o + 4 * lg + j] = Q[j];
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) Q[j] *= bt[j];
         h4 hi, lo;
@@ -787,7 +803,24 @@ struct Kern {
             dq = wave_sum(hf ? dq : 0.f);
             if (lane == 63) sum.A[3] = dq;
         }
-        // the block's sums are complete: A to its operand, G and beta to the solve
+        // the block's sums are complete: A to its operand, G and beta to the
+        // solve (and both to the backward's record; block 0 also zeroes the
+        // record's blocks above the diagonal)
+        if (ckm) {
+            constexpr int C = CB * BT;
+            float* ma = ck_mats(next - NB);
+            const int o = BT * bi;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ma[(o + 4 * lg + j) * C + o + ln] = sum.A[j] * scale;
+                ma[C * C + (o + 4 * lg + j) * C + o + ln] = sum.G[j];
+                if (bi == 0) {
+                    ma[(4 * lg + j) * C + BT + ln] = 0.f;
+                    ma[C * C + (4 * lg + j) * C + BT + ln] = 0.f;
+                    ma[2 * C * C + (4 * lg + j) * C + BT + ln] = 0.f;
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             co.AM[bi][4 * lg + j][ln] = static_cast<_Float16>(sum.A[j] * scale);
@@ -853,7 +886,7 @@ struct Kern {
     // k * F to the chunk end; block 1: G_10 and A_10 from the block-local
     // operands and the chunk decay), and the inverse of (I + L) when no
     // consumer wave takes it.
-    __device__ void phase2(int p, ChunkOps<K>& co) const {
+    __device__ void phase2(int p, int blk, ChunkOps<K>& co) const {
         const int bi = p % CB, cj = p / CB;
         Stage<K>& st = sm.st[cj];
         float d[CH];
@@ -880,6 +913,16 @@ struct Kern {
                 accG = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o), accG);
                 accA = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o), accA);
             }
+            if (ckm) {
+                // the backward's A_10 and L_10: slot j holds row 16 + ln, column 4 lg + j
+                constexpr int C = CB * BT;
+                float* ma = ck_mats(blk);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ma[(BT + ln) * C + 4 * lg + j] = accA[j] * scale;
+                    ma[C * C + (BT + ln) * C + 4 * lg + j] = accG[j];
+                }
+            }
             h4 gh, gl;
             split4(-accG, gh, gl);
             *reinterpret_cast<h4*>(&co.GH[ln][4 * lg]) = gh;
@@ -890,7 +933,7 @@ struct Kern {
                 for (int c = 0; c < CH; ++c) co.echunk[CH * cq + c] = st.e15[1][CH * cq + c] * d[c];
             }
         }
-        if constexpr (!kConsumerSolve) solve(p, co.MH[bi], co.ML[bi]);
+        if constexpr (!kConsumerSolve) solve(p, blk, co.MH[bi], co.ML[bi]);
     }
 
     // ------------------------------------------------------------ consumers
@@ -1194,7 +1237,7 @@ struct Kern {
 // barriers; every prefetch is issued unconditionally (a block past T loads
 // zeros).  The chunks cover T rounded up to whole chunks: a padded block
 // (all rows past T) is neutral and is built like any other.
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false>
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false, bool CKPT = false>
 __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt,
                                                                    const kda_gate_args gate,
                                                                    const kda_out_epilogue epi) {
@@ -1235,6 +1278,9 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     const int nch = static_cast<int>((a.T + BT - 1) / BT);
     const int ncc = (nch + CB - 1) / CB;                 // chunks
     const int nblk = CB * ncc;                           // blocks, padded to whole chunks
+    if constexpr (CKPT) {
+        if (ckpt != nullptr && vt == 0) kn.ckm = ckpt + (kn.b * H + kn.h) * ncc * ckpt_record(K, V);
+    }
     const int nss = (ncc + NCH - 1) / NCH;               // supersteps
 
     const bool consumer = wave < NC;
@@ -1302,8 +1348,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
                 const int cc = NCH * s + cj;
                 if (s >= 0 && cc < ncc) {
                     // the checkpoint of chunk cc, for the backward
-                    float* ck = ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * static_cast<int64_t>(K + 2 * CB * BT) * V
-                                     : nullptr;
+                    float* ck = CKPT && ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * ckpt_record(K, V) : nullptr;
                     kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, colw, ck, pd[cj], wave);
                 }
             }
@@ -1317,7 +1362,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
                 const int nb = NB * (s + 1) + wave;
                 if (nb < nblk) {
                     ChunkOps<K>& nx = sm.set[(s + 1) & 1][wave / CB];
-                    kn.solve(wave, nx.MH[wave % CB], nx.ML[wave % CB]);
+                    kn.solve(wave, nb, nx.MH[wave % CB], nx.ML[wave % CB]);
                 }
             }
             __syncthreads();
@@ -1344,17 +1389,17 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             ChunkOps<K>& co = sm.set[(s + 1) & 1][p / CB];
             if (blk < nblk) kn.phase1(raw, w, p, co, blk + NB);
             __syncthreads();
-            if (blk < nblk) kn.phase2(p, co);
+            if (blk < nblk) kn.phase2(p, blk, co);
             __syncthreads();
         }
     }
 }
 
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false>
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false, bool CKPT = false>
 int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate,
                const kda_out_epilogue& epi = kda_out_epilogue{}) {
     const int64_t blocks = a.B * a.H * ((a.V + (TRANS ? K : 0)) / (16 * NC * CG));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI, TRANS>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI, TRANS, CKPT>), dim3(static_cast<unsigned>(blocks)),
                        dim3(64 * (NC + NB)), 0, stream, a, ckpt, gate, epi);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
@@ -1392,16 +1437,28 @@ template <int K, typename TQ, bool GATED>
 int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
     constexpr int64_t kCus = 256;
     const int64_t heads = a.B * a.H;
+    // the checkpointing forward is its own instantiation: the record stores
+    // cost registers the plain forward does not pay for
+    auto go = [&](auto nc, auto cg) {
+        constexpr int NC = decltype(nc)::value, CG = decltype(cg)::value;
+        if constexpr (!GATED) {
+            if (ckpt != nullptr) return launch_knq<K, NC, TQ, GATED, CG, false, false, true>(a, stream, ckpt, gate);
+        }
+        return launch_knq<K, NC, TQ, GATED, CG>(a, stream, nullptr, gate);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
     // More 64-column tiles than CUs: 128-column workgroups (consumer waves of
     // two 16-column groups), whose ~20 % longer superstep beats a second
     // round of workgroups (measured 265 against 450 us at B=16 T=2048 H=16
     // d=128).  16-bit inputs only (the fp32 instantiation serves checkpoints).
     if constexpr (sizeof(TQ) == 2) {
-        if (a.V % 128 == 0 && heads * (a.V / 64) > kCus) return launch_knq<K, 4, TQ, GATED, 2>(a, stream, ckpt, gate);
+        if (a.V % 128 == 0 && heads * (a.V / 64) > kCus) return go(I4{}, I2{});
     }
-    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return launch_knq<K, 4, TQ, GATED>(a, stream, ckpt, gate);
-    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return launch_knq<K, 2, TQ, GATED>(a, stream, ckpt, gate);
-    return launch_knq<K, 1, TQ, GATED>(a, stream, ckpt, gate);
+    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return go(I4{}, I1{});
+    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return go(I2{}, I1{});
+    return go(I1{}, I1{});
 }
 
 template <int K, bool GATED>

@@ -2,9 +2,10 @@
 //
 // Gradient of kda_chunkwise (kimi_linear/kda.py:58-185), whose reference is
 // differentiated by autograd (training: scripts/train_musicgpt_fp16.py:519-523).
-// The forward is re-evaluated chunk by chunk from the checkpoints that
-// kda_chunkwise_fwd_ckpt writes: per CT = 32-token chunk, the state before it
-// and the chunk's R and P (below), which the forward computes anyway.
+// The forward is re-evaluated chunk by chunk from the records that
+// kda_chunkwise_fwd_ckpt writes: per CT = 32-token chunk, the state before it,
+// the chunk's R and P, A, L and the diagonal blocks of N (below), all of which
+// the forward computes anyway.
 //
 // Per (b, h) and chunk, rows c, i in [0, CT), channels k, state columns v:
 //   G = in-chunk cumulative sum of g,  E = exp(G),  F = exp(G_last - G),
@@ -27,8 +28,8 @@
 // Only the chain dS_end -> dP -> dR -> dS_start runs from chunk to chunk;
 // everything else is independent per chunk.  Three kernels, one fp32
 // workspace between them:
-//   1. bwd_pairs_kernel, persistent: A, L and N of every chunk (functions of
-//      q, k, g and beta only), by decay level on the matrix cores.
+//   1. bwd_n_kernel: N of every chunk, its block below the diagonal from the
+//      record's diagonal blocks and L.
 //   2. bwd_state_kernel, one workgroup per (b, h, VA state columns), the chunks
 //      in reverse: the chain above; it stores each chunk's dS_end, dP and dR
 //      (fp32) and dS_0.  The next chunk's inputs are fetched while the
@@ -59,25 +60,27 @@ namespace {
 constexpr int CT = 32;          // tokens per chunk = the forward's checkpoint spacing
 constexpr int VT = 32;          // state columns per step of bwd_chunk_kernel
 
-// Workspace, per (b, h) and chunk (index cb = (b H + h) nck + n):
-// A, L, N [CT][CT], dS_end [K][V], dP and dR [CT][V], fp32.
+// Per (b, h) and chunk (index cb = (b H + h) nck + n): A and L (32 x 32)
+// from the forward's chunk record (records of ms floats), and in the fp32
+// workspace N (32 x 32), dS_end [K][V], dP and dR [CT][V].
 struct BwdWs {
-    float* A;
-    float* L;
+    const float* A;
+    const float* L;
     float* N;
     float* dS;
     float* dP;
     float* dR;
+    int64_t ms;
 };
 
-BwdWs ws_layout(void* base, int64_t BH, int64_t nck, int64_t K, int64_t V) {
+BwdWs ws_layout(void* base, const float* ckpt, int64_t BH, int64_t nck, int64_t K, int64_t V) {
     float* p = static_cast<float*>(base);
-    const int64_t mat = BH * nck * CT * CT;
     BwdWs w;
-    w.A = p;
-    w.L = p + mat;
-    w.N = p + 2 * mat;
-    w.dS = p + 3 * mat;
+    w.A = ckpt + (K + 2 * CT) * V;
+    w.L = w.A + CT * CT;
+    w.ms = ckpt_record(K, V);
+    w.N = p;
+    w.dS = p + BH * nck * CT * CT;
     w.dP = w.dS + BH * nck * K * V;
     w.dR = w.dP + BH * nck * CT * V;
     return w;
@@ -122,22 +125,6 @@ __device__ __forceinline__ f4 mm_pair(const uint16_t* xh, const uint16_t* xl, co
 
 // ------------------------------------------------------------------ kernel 1
 
-constexpr int NP = 512;         // threads per workgroup of bwd_pairs_kernel
-
-template <int K>
-struct __align__(16) PairSmem {
-    static constexpr int KP = K + 4;
-    float q[CT][KP];            // scale * q
-    float k[CT][KP];
-    float gc[CT][KP];           // in-chunk cumulative log decay G
-    float A[CT][CT + 1];
-    float L[CT][CT + 1];
-    float N[CT][CT + 1];
-    float part[4][2][16][17];   // the waves' shares of A_10 and L_10; first the row groups' g sums
-    float Y[16][17];
-    float beta[CT];
-};
-
 // The bf16 pair products of mm_pair on fragments held in registers.
 __device__ __forceinline__ f4 mfma_pair(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, f4 acc) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
@@ -167,24 +154,6 @@ __device__ __forceinline__ void split8(const float (&v)[8], bf8& hi, bf8& lo) {
     lo = __builtin_bit_cast(bf8, lw);
 }
 
-// Eight values as fp16, two per conversion.
-__device__ __forceinline__ h8 to_h8(const float (&v)[8]) {
-    w4 r;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-        r[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2v{v[2 * e], v[2 * e + 1]}, hf2));
-    return __builtin_bit_cast(h8, r);
-}
-
-__device__ __forceinline__ void lds8(const float* p, float (&v)[8]) {
-    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        v[e] = a[e];
-        v[4 + e] = b[e];
-    }
-}
-
 // c + X Y for 16 x 16 fp32 tiles on the fp32 matrix cores (four 16x16x4
 // steps): xt holds X^T in accumulator layout (lane (ln, lg) slot u:
 // X[ln][4 lg + u]), y holds Y in accumulator layout (slot u: Y[4 lg + u][ln]);
@@ -207,278 +176,38 @@ __device__ __forceinline__ float raw_f32(uint32_t w) {
     }
 }
 
-// A, L and N of every chunk.  Every decay factor is a product of per-token
-// decays between two rows, kept <= 1 by factoring through a reference row
-// between them:
-//  * diagonal 16-row blocks, by decay level: a pair i < c of a block has a
-//    unique highest differing bit lev; both rows sit in the aligned group of
-//    2^(lev+1) rows whose lower half ends at ref(c) = ref(i), i <= ref < c,
-//    and exp(G_c - G_i) = exp(G_c - G_ref) exp(G_ref - G_i).  Per level, with
-//    f_r = exp(-|G_r - G_ref(r)|) for every row r of the block (ref(r): r's
-//    reference row at that level, r in either half), the products
-//    (q~ f)(k f)^T and (k f)(k f)^T over the channels hold A and L on that
-//    level's pairs (c upper, i lower); a row r whose low lev bits are all
-//    ones and bit lev clear is its own reference row (f_r = 1), so the
-//    diagonal A[r][r] comes from that level's product too, except for the
-//    block's row 15, one dot product of its own;
-//  * the block below the diagonal, through row 15 (the reference row of
-//    every such pair).
-// Products on the bf16 matrix cores as hi/lo pairs (~2^-17 relative each).
-// N = (I + X)^-1 per diagonal block, X = Diag(beta) L nilpotent:
-// (I - X)(I + X^2)(I + X^4)(I + X^8) on the fp32 matrix cores in registers,
-// then N10 = -N11 X10 N00.
-// Wave w: block w / 4, level w % 4; waves 0 .. K/32 - 1 also one 32-channel
-// step of the block below the diagonal.  Persistent: workgroup g takes
-// chunks g, g + G, ... (G workgroups) and fetches the next one's inputs into
-// registers while the current one is computed.
-template <int K, typename TI>
-__global__ __launch_bounds__(NP) void bwd_pairs_kernel(const kda_bwd_args a, const BwdWs ws, int64_t nchunks) {
-    static_assert(NP % K == 0 && (CT * K) % NP == 0 && NP / K <= 4 * 2 * 16 * 17, "thread mapping");
-    static_assert(NP / 64 == 8 && K / 32 <= 4, "wave roles");
-    constexpr int RPT = CT * K / NP;        // consecutive rows per thread, one channel
-    constexpr bool PAIR = sizeof(TI) == 4;  // fp32 activations: bf16 pairs; 16-bit: fp16 operands
-    constexpr float kLog2e = 1.4426950408889634f;
-    __shared__ PairSmem<K> sm;
-    const TI* qp = static_cast<const TI*>(a.q);
-    const TI* kp = static_cast<const TI*>(a.k);
-    const int64_t H = a.H, T = a.T;
-    const int nck = static_cast<int>((T + CT - 1) / CT);
+// N = (I + Diag(beta) L)^-1 of every chunk into the workspace.  The
+// forward's solve left the diagonal blocks N00, N11 in the chunk record;
+// N10 = -N11 X10 N00 with X10 = Diag(beta_1) L10 on the fp32 matrix cores.
+// One wave per chunk, four chunks a workgroup; no barriers.
+__global__ __launch_bounds__(256) void bwd_n_kernel(const kda_bwd_args a, const BwdWs ws, int64_t nchunks) {
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
-    const int kk = t % K, rg = t / K;
-    const uint32_t HK = static_cast<uint32_t>(H * K);
-
-    // thread (rg, kk): rows RPT rg .. RPT rg + RPT - 1 of channel kk, fetched
-    // raw through descriptors that span the chunk's rows before T (rows past
-    // T read as zero) with one lane offset per tensor and the row in the
-    // scalar offset
-    uint32_t pq[RPT], pk[RPT], pg[RPT], pb[1] = {0u};
-    const uint32_t lo_x = static_cast<uint32_t>(RPT * rg) * HK + kk;
-    auto fetch = [&](int64_t cb) {
-        const int64_t bh = cb / nck, b = bh / H, h = bh % H;
-        const int64_t r0 = (cb % nck) * CT;
-        const int64_t base = ((b * T + r0) * H + h) * K;
-        const uint32_t span = static_cast<uint32_t>((std::min<int64_t>(CT, T - r0) - 1) * H * K + K);
-        const auto rq = make_rsrc(qp + base, span * sizeof(TI)), rk = make_rsrc(kp + base, span * sizeof(TI));
-        const auto rgc = make_rsrc(a.g + base, span * 4);
+    const int64_t cb = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (cb >= nchunks) return;
+    const int64_t H = a.H, T = a.T;
+    const int64_t nck = (T + CT - 1) / CT;
+    const int64_t bh = cb / nck, b = bh / H, h = bh % H, r0 = (cb % nck) * CT;
+    const float* L = ws.L + cb * ws.ms;
+    const float* Nr = ws.A + cb * ws.ms + 2 * CT * CT;      // the record's N
+    float* N = ws.N + cb * CT * CT;
+    const int64_t row1 = r0 + 16 + ln;
+    const float b1 = row1 < T ? a.beta[(b * T + row1) * H + h] : 0.f;
+    f4 xt, n00, n11t;
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const uint32_t so = static_cast<uint32_t>(j) * HK;
-            if constexpr (sizeof(TI) == 2) {
-                pq[j] = __builtin_amdgcn_raw_buffer_load_b16(rq, static_cast<int>(2 * lo_x), static_cast<int>(2 * so), 0);
-                pk[j] = __builtin_amdgcn_raw_buffer_load_b16(rk, static_cast<int>(2 * lo_x), static_cast<int>(2 * so), 0);
-            } else {
-                pq[j] = __builtin_amdgcn_raw_buffer_load_b32(rq, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
-                pk[j] = __builtin_amdgcn_raw_buffer_load_b32(rk, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
-            }
-            pg[j] = __builtin_amdgcn_raw_buffer_load_b32(rgc, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
-        }
-        if (t < CT) pb[0] = r0 + t < T ? __float_as_uint(a.beta[(b * T + r0 + t) * H + h]) : 0u;
-    };
-    int64_t cb = blockIdx.x;
-    if (cb < nchunks) fetch(cb);
-    for (; cb < nchunks; cb += gridDim.x) {
-        // stage this chunk (G from per-thread partial sums and the row-group
-        // totals); fetch the next one
-        use_here(pq);
-        use_here(pk);
-        use_here(pg);
-        use_here(pb);
-        float gl[RPT];
-        float run = 0.f;
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int c = RPT * rg + j;
-            sm.q[c][kk] = raw_f32<TI>(pq[j]) * a.scale;
-            sm.k[c][kk] = raw_f32<TI>(pk[j]);
-            run += __uint_as_float(pg[j]);
-            gl[j] = run;
-        }
-        float* tot = &sm.part[0][0][0][0];
-        tot[rg * K + kk] = run;
-        if (t < CT) sm.beta[t] = __uint_as_float(pb[0]);
-        if (cb + gridDim.x < nchunks) fetch(cb + gridDim.x);
-        __syncthreads();
-        {
-            float pre = 0.f;
-#pragma unroll
-            for (int r = 0; r < NP / K; ++r) pre += r < rg ? tot[r * K + kk] : 0.f;
-#pragma unroll
-            for (int j = 0; j < RPT; ++j) sm.gc[RPT * rg + j][kk] = pre + gl[j];
-        }
-        __syncthreads();
-
-        // diagonal blocks by level; lane (ln, lg) supplies row ln of both
-        // operands, channels 32 u + 8 lg .. + 7 of step u, and holds entry
-        // (c, i) = (4 lg + j, ln) of the block in slot j
-        {
-            const int p = w >> 2, lev = w & 3;
-            const int r = 16 * p + ln;
-            const bool up = (ln >> lev) & 1;
-            const int ref = 16 * p + (up ? ((ln >> lev) << lev) - 1 : (ln | ((1 << lev) - 1)));
-            // f = exp(G_r - G_ref) (upper rows) or exp(G_ref - G_r) (lower rows)
-            const float sg = up ? kLog2e : -kLog2e;
-            f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = accA;
-            float d15 = 0.f;                    // row 15's diagonal (lanes ln = 15 of level 0)
-#pragma unroll 1
-            for (int u = 0; u < K / 32; ++u) {
-                const int x0 = 32 * u + 8 * lg;
-                float qv[8], kv[8], gr[8], gf[8];
-                lds8(&sm.q[r][x0], qv);
-                lds8(&sm.k[r][x0], kv);
-                lds8(&sm.gc[r][x0], gr);
-                lds8(&sm.gc[ref][x0], gf);
-                if (lev == 0) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) d15 = fmaf(qv[e], kv[e], d15);
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float f = __builtin_amdgcn_exp2f((gr[e] - gf[e]) * sg);
-                    qv[e] *= f;
-                    kv[e] *= f;
-                }
-                if constexpr (PAIR) {
-                    bf8 qh, ql, kh, kl;
-                    split8(qv, qh, ql);
-                    split8(kv, kh, kl);
-                    accA = mfma_pair(qh, ql, kh, kl, accA);
-                    accL = mfma_pair(kh, kl, kh, kl, accL);
-                } else {
-                    const h8 qh = to_h8(qv), kh = to_h8(kv);
-                    accA = mfma16x16x32(qh, kh, accA);
-                    accL = mfma16x16x32(kh, kh, accL);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = 4 * lg + j, i = ln;
-                const int x = c ^ i;
-                // the diagonal entry of level lev: c's low lev bits ones, bit lev clear
-                const bool diag = x == 0 && ((c + 1) & ((2 << lev) - 1)) == (1 << lev);
-                if ((x >> lev) == 1 || diag) {
-                    sm.A[16 * p + c][16 * p + i] = c >= i ? accA[j] : 0.f;
-                    sm.L[16 * p + c][16 * p + i] = c > i ? accL[j] : 0.f;
-                }
-            }
-            if (lev == 0) {
-                d15 += __shfl_xor(d15, 16);
-                d15 += __shfl_xor(d15, 32);
-                if (lane == 15) {
-                    sm.A[16 * p + 15][16 * p + 15] = d15;
-                    sm.L[16 * p + 15][16 * p + 15] = 0.f;
-                }
-            }
-        }
-        __syncthreads();
-
-        if (w < 2) {
-            // N_pp = (I + X)^-1, X = Diag(beta) L_pp, in accumulator layout
-            const int o = 16 * w;
-            f4 X, XT;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                X[j] = sm.beta[o + 4 * lg + j] * sm.L[o + 4 * lg + j][o + ln];
-                XT[j] = sm.beta[o + ln] * sm.L[o + ln][o + 4 * lg + j];
-            }
-            const f4 z = {0.f, 0.f, 0.f, 0.f};
-            const f4 X2 = mm_acc(XT, X, z), X2T = mm_acc(X, XT, z);
-            const f4 X4 = mm_acc(X2T, X2, z), X4T = mm_acc(X2, X2T, z);
-            const f4 X8T = mm_acc(X4, X4T, z);
-            f4 Q;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) Q[j] = (4 * lg + j == ln ? 1.f : 0.f) - X[j];
-            Q = mm_acc(X2T, Q, Q);
-            Q = mm_acc(X4T, Q, Q);
-            Q = mm_acc(X8T, Q, Q);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sm.N[o + 4 * lg + j][o + ln] = Q[j];
-        } else if (w >= 4 && w - 4 < K / 32) {
-            // the block below the diagonal, one 32-channel step per wave: rows
-            // 16 + ln (X) and ln (Y), reference row 15
-            const int s4 = w - 4, x0 = 32 * s4 + 8 * lg;
-            float q1[8], k1[8], g1[8], k0[8], g0[8], g15[8];
-            lds8(&sm.q[16 + ln][x0], q1);
-            lds8(&sm.k[16 + ln][x0], k1);
-            lds8(&sm.gc[16 + ln][x0], g1);
-            lds8(&sm.k[ln][x0], k0);
-            lds8(&sm.gc[ln][x0], g0);
-            lds8(&sm.gc[15][x0], g15);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float f1 = __builtin_amdgcn_exp2f((g1[e] - g15[e]) * kLog2e);
-                q1[e] *= f1;
-                k1[e] *= f1;
-                k0[e] *= __builtin_amdgcn_exp2f((g15[e] - g0[e]) * kLog2e);
-            }
-            f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = accA;
-            if constexpr (PAIR) {
-                bf8 qh, ql, kh, kl, yh, yl;
-                split8(q1, qh, ql);
-                split8(k1, kh, kl);
-                split8(k0, yh, yl);
-                accA = mfma_pair(qh, ql, yh, yl, accA);
-                accL = mfma_pair(kh, kl, yh, yl, accL);
-            } else {
-                const h8 qh = to_h8(q1), kh = to_h8(k1), yh = to_h8(k0);
-                accA = mfma16x16x32(qh, yh, accA);
-                accL = mfma16x16x32(kh, yh, accL);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sm.part[s4][0][4 * lg + j][ln] = accA[j];
-                sm.part[s4][1][4 * lg + j][ln] = accL[j];
-            }
-        }
-        __syncthreads();
-
-        if (t < 64) {
-            // Y <- X10 N00, X10 = Diag(beta_1) L10 (L10 from the shares); N10 = -N11 Y
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = tile_mm<16>(
-                [&](int r, int m) {
-                    float l = 0.f;
-#pragma unroll
-                    for (int x = 0; x < K / 32; ++x) l += sm.part[x][1][r][m];
-                    return sm.beta[16 + r] * l;
-                },
-                [&](int m, int i) { return sm.N[m][i]; }, ln, lg, acc);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sm.Y[4 * lg + j][ln] = acc[j];
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            acc = f4{0.f, 0.f, 0.f, 0.f};
-            acc = tile_mm<16>([&](int r, int m) { return sm.N[16 + r][16 + m]; },
-                              [&](int m, int i) { return sm.Y[m][i]; }, ln, lg, acc);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sm.N[16 + 4 * lg + j][ln] = -acc[j];
-        } else if (w >= 4) {
-            // A_10, L_10 from the shares; zeros above the diagonal blocks
-            const int e = t - 256, c = e >> 4, i = e & 15;
-            float sa = 0.f, sl = 0.f;
-#pragma unroll
-            for (int x = 0; x < K / 32; ++x) {
-                sa += sm.part[x][0][c][i];
-                sl += sm.part[x][1][c][i];
-            }
-            sm.A[16 + c][i] = sa;
-            sm.L[16 + c][i] = sl;
-            sm.A[c][16 + i] = 0.f;
-            sm.L[c][16 + i] = 0.f;
-            sm.N[c][16 + i] = 0.f;
-        }
-        __syncthreads();
-        // the next chunk's staging writes none of A, L, N
-        float* ga = ws.A + cb * CT * CT;
-        float* gL = ws.L + cb * CT * CT;
-        float* gn = ws.N + cb * CT * CT;
-#pragma unroll
-        for (int j = 0; j < CT * CT / NP; ++j) {
-            const int e = t + NP * j;
-            ga[e] = sm.A[e / CT][e % CT];
-            gL[e] = sm.L[e / CT][e % CT];
-            gn[e] = sm.N[e / CT][e % CT];
-        }
+    for (int u = 0; u < 4; ++u) {
+        xt[u] = b1 * L[(16 + ln) * CT + 4 * lg + u];          // X10[ln][4 lg + u]
+        n00[u] = Nr[(4 * lg + u) * CT + ln];                  // N00[4 lg + u][ln]
+        n11t[u] = Nr[(16 + ln) * CT + 16 + 4 * lg + u];       // N11[ln][4 lg + u]
     }
+    const f4 y = mm_acc(xt, n00, f4{0.f, 0.f, 0.f, 0.f});    // X10 N00
+    const f4 n10 = mm_acc(n11t, y, f4{0.f, 0.f, 0.f, 0.f});  // N11 X10 N00
+#pragma unroll
+    for (int m = 0; m < CT * CT / 64; ++m) {
+        const int e = lane + 64 * m, r = e / CT, c = e % CT;
+        if (r < 16 || c >= 16) N[e] = r < 16 && c >= 16 ? 0.f : Nr[e];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) N[(16 + 4 * lg + j) * CT + ln] = -n10[j];
 }
 
 // ------------------------------------------------------------------ kernel 2
@@ -632,7 +361,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             else
                 pdo[j] = __builtin_amdgcn_raw_buffer_load_b32(ro, static_cast<int>(4 * lo_o), static_cast<int>(so), 0);
         }
-        const float* an = ws.A + (bh * nck + n) * CT * CT;
+        const float* an = ws.A + (bh * nck + n) * ws.ms;
         const float* nn = ws.N + (bh * nck + n) * CT * CT;
 #pragma unroll
         for (int j = 0; j < APT; ++j) {
@@ -922,7 +651,7 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 #pragma unroll
     for (int m = 0; m < CT * CT / NTC; ++m) {
         const int e = t + NTC * m;
-        sm.L[e / CT][e % CT] = ws.L[cb * CT * CT + e];
+        sm.L[e / CT][e % CT] = ws.L[cb * ws.ms + e];
         sm.N[e / CT][e % CT] = ws.N[cb * CT * CT + e];
     }
     if (t < CT) sm.beta[t] = t < nrow ? a.beta[(b * T + r0 + t) * H + h] : 0.f;
@@ -931,7 +660,7 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     // before the chunk) and dS (the gradient of the state after it), row x,
     // columns v0 + 8 lg .. + 7; the thread's EPT elements of R, P (checkpoint),
     // dP, dR (workspace) and dO, rows t / VT + (NTC / VT) m, column t % VT
-    const auto rck = make_rsrc(a.ckpt + cb * static_cast<int64_t>(K + 2 * CT) * V,
+    const auto rck = make_rsrc(a.ckpt + cb * ckpt_record(K, V),
                                static_cast<uint32_t>((K + 2 * CT) * V * 4));
     const auto rds = make_rsrc(ws.dS + cb * K * V, static_cast<uint32_t>(K * V * 4));
     const auto rdp = make_rsrc(ws.dP + cb * CT * V, static_cast<uint32_t>(CT * V * 4));
@@ -1348,8 +1077,7 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     }
 }
 
-// Workgroups of a persistent kernel: as many as are resident at once on the
-// current device.
+// Compute units of the current device.
 int cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1357,21 +1085,15 @@ int cu_count() {
         cus = 256;
     return cus;
 }
-template <typename Kern>
-int persistent_grid(Kern kernel, int threads) {
-    int per = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
-    return cu_count() * per;
-}
 
 template <int K, typename TI>
 int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
     const int64_t BH = a.B * a.H;
     const int64_t nck = (a.T + CT - 1) / CT;
-    const BwdWs ws = ws_layout(a.workspace, BH, nck, a.K, a.V);
+    const BwdWs ws = ws_layout(a.workspace, a.ckpt, BH, nck, a.K, a.V);
     if (nck > 0) {
-        hipLaunchKernelGGL((bwd_pairs_kernel<K, TI>), dim3(static_cast<unsigned>(std::min<int64_t>(BH * nck, persistent_grid(bwd_pairs_kernel<K, TI>, NP)))),
-                           dim3(NP), 0, stream, a, ws, BH * nck);
+        hipLaunchKernelGGL(bwd_n_kernel, dim3(static_cast<unsigned>((BH * nck + 3) / 4)), dim3(256), 0, stream, a, ws,
+                           BH * nck);
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
     // 64 state columns a workgroup, or 32 when that leaves compute units idle
@@ -1409,11 +1131,11 @@ bool chunkwise_bwd_supported(int64_t K, int64_t V) {
 
 int64_t chunkwise_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
     const int64_t nck = (T + CT - 1) / CT;
-    return B * H * nck * (3 * CT * CT + K * V + 2 * CT * V) * static_cast<int64_t>(sizeof(float));
+    return B * H * nck * (CT * CT + K * V + 2 * CT * V) * static_cast<int64_t>(sizeof(float));
 }
 
-// Static scratch of kda_chunkwise_bwd_noalloc: the workspace of the three
-// kernels (A, L, N, dS_end, dP, dR) for shapes that fit.  The array's name is
+// Static scratch of kda_chunkwise_bwd_noalloc: the workspace of the
+// kernels (N, dS_end, dP, dR) for shapes that fit.  The array's name is
 // a host-side stand-in; kernels get the device address hipGetSymbolAddress
 // returns for the current device, kept per device.
 static __device__ __align__(256) unsigned char scratch[KDA_BWD_SCRATCH_BYTES];

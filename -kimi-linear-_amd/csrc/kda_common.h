@@ -228,4 +228,9 @@ __device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
     for (int i = 0; i < N; ++i) use_here(r[i]);
 }
 
+// Floats of one 32-token chunk's record in kda_chunkwise_fwd_ckpt's output:
+// the state before the chunk (K rows), the chunk's R and P (32 rows each),
+// all V wide, then its A, L and N (32 x 32 each, row-major).
+__host__ __device__ constexpr int64_t ckpt_record(int64_t K, int64_t V) { return (K + 64) * V + 3 * 32 * 32; }
+
 }  // namespace kda

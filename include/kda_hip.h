@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 11
+#define KDA_ABI_VERSION 12
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -190,11 +190,16 @@ int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* wor
  * torch.autograd.Function around the HIP forward binds instead.
  * ------------------------------------------------------------------------- */
 
-/* kda_chunkwise_fwd, plus per 32-token chunk, in fp32: the state before the
- * chunk and the chunk's R = V - (k * E) S and P = (I + Diag(beta) L)^-1
- * Diag(beta) R (the solve's result): ckpt is [B, H, ceil(T/32), K + 64, V]
- * contiguous, rows [0, K) the state, [K, K + 32) R, [K + 32, K + 64) P (the
- * input of kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
+/* kda_chunkwise_fwd, plus per 32-token chunk a record, in fp32: the state
+ * before the chunk, the chunk's R = V - (k * E) S and P = (I + Diag(beta)
+ * L)^-1 Diag(beta) R (the solve's result), then its A (scale times the decayed
+ * q k^T, i <= c), L (the decayed k k^T, i < c) and N = (I + Diag(beta) L)^-1
+ * with its block below the diagonal zero (the solve uses only the 16-row
+ * diagonal blocks): ckpt is [B, H, ceil(T/32), KDA_CKPT_RECORD(K, V)]
+ * contiguous, each record (K + 64) x V (rows [0, K) the state, [K, K + 32) R,
+ * [K + 32, K + 64) P) followed by three row-major 32 x 32 matrices (the input
+ * of kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
+#define KDA_CKPT_RECORD(K, V) (((K) + 64) * (V) + 3 * 32 * 32)
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 
 /* Every tensor is contiguous in the forward layout: q, k, g, dq, dk, dg
@@ -226,7 +231,7 @@ typedef struct kda_bwd_args {
 } kda_bwd_args;
 
 /* Bytes of workspace kda_chunkwise_bwd needs: per (b, h) and 32-token chunk,
- * (3 * 32 * 32 + K * V + 2 * 32 * V) floats.  0 for a bad or empty shape. */
+ * (32 * 32 + K * V + 2 * 32 * V) floats.  0 for a bad or empty shape. */
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 
 int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
