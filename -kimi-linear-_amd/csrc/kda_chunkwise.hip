@@ -731,7 +731,7 @@ struct Kern {
             float* n = ck_mats(blk) + 2 * CB * BT * CB * BT;
             const int o = BT * (blk % CB);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) n[(o + ln) * (CB * BT) + o + 4 * lg + j] = Q[j];
+            for (int j = 0; j < 4; ++j) __builtin_nontemporal_store(Q[j], &n[(o + ln) * (CB * BT) + o + 4 * lg + j]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) Q[j] *= bt[j];
@@ -812,12 +812,12 @@ struct Kern {
             const int o = BT * bi;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                ma[(o + 4 * lg + j) * C + o + ln] = sum.A[j] * scale;
-                ma[C * C + (o + 4 * lg + j) * C + o + ln] = sum.G[j];
+                __builtin_nontemporal_store(sum.A[j] * scale, &ma[(o + 4 * lg + j) * C + o + ln]);
+                __builtin_nontemporal_store(sum.G[j], &ma[C * C + (o + 4 * lg + j) * C + o + ln]);
                 if (bi == 0) {
-                    ma[(4 * lg + j) * C + BT + ln] = 0.f;
-                    ma[C * C + (4 * lg + j) * C + BT + ln] = 0.f;
-                    ma[2 * C * C + (4 * lg + j) * C + BT + ln] = 0.f;
+                    __builtin_nontemporal_store(0.f, &ma[(4 * lg + j) * C + BT + ln]);
+                    __builtin_nontemporal_store(0.f, &ma[C * C + (4 * lg + j) * C + BT + ln]);
+                    __builtin_nontemporal_store(0.f, &ma[2 * C * C + (4 * lg + j) * C + BT + ln]);
                 }
             }
         }
@@ -919,8 +919,8 @@ struct Kern {
                 float* ma = ck_mats(blk);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    ma[(BT + ln) * C + 4 * lg + j] = accA[j] * scale;
-                    ma[C * C + (BT + ln) * C + 4 * lg + j] = accG[j];
+                    __builtin_nontemporal_store(accA[j] * scale, &ma[(BT + ln) * C + 4 * lg + j]);
+                    __builtin_nontemporal_store(accG[j], &ma[C * C + (BT + ln) * C + 4 * lg + j]);
                 }
             }
             h4 gh, gl;
@@ -1101,7 +1101,12 @@ struct Kern {
         const int64_t V = a.V;
         if (ck) {
 #pragma unroll
-            for (int g = 0; g < CG; ++g) store_state_t<KT>(S[g], ck, (4 * lg) * V + colw + 16 * g + ln, V);
+            for (int g = 0; g < CG; ++g)
+#pragma unroll
+                for (int t = 0; t < KT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        __builtin_nontemporal_store(S[g][t][j], &ck[(4 * lg + 16 * t + j) * V + colw + 16 * g + ln]);
         }
         float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
@@ -1152,8 +1157,8 @@ struct Kern {
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    rp[(4 * lg + j) * V + rc] = R[g][0][j];
-                    rp[(16 + 4 * lg + j) * V + rc] = R[g][1][j];
+                    __builtin_nontemporal_store(R[g][0][j], &rp[(4 * lg + j) * V + rc]);
+                    __builtin_nontemporal_store(R[g][1][j], &rp[(16 + 4 * lg + j) * V + rc]);
                 }
             }
             const h4 r0 = to_h4(R[g][0]);
@@ -1166,8 +1171,8 @@ struct Kern {
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    rp[(32 + 4 * lg + j) * V + rc] = P0[j];
-                    rp[(48 + 4 * lg + j) * V + rc] = P1[j];
+                    __builtin_nontemporal_store(P0[j], &rp[(32 + 4 * lg + j) * V + rc]);
+                    __builtin_nontemporal_store(P1[j], &rp[(48 + 4 * lg + j) * V + rc]);
                 }
             }
             // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is

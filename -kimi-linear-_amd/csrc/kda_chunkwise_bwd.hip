@@ -442,7 +442,8 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
                 float* dsn = ws.dS + cb * K * V + v0;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) dsn[static_cast<uint32_t>(r0 + 4 * lg + j) * V + c0 + ln] = accs[m][j];
+                for (int j = 0; j < 4; ++j)
+                    __builtin_nontemporal_store(accs[m][j], &dsn[static_cast<uint32_t>(r0 + 4 * lg + j) * V + c0 + ln]);
             }
         }
         if (w < NDP) {
@@ -455,7 +456,8 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             acc = mm_pair(sm.AT[0][r0t + ln], sm.AT[1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[1][c0t + ln], lg, acc);
             float* dpn = ws.dP + cb * CT * V + v0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln] = acc[j];
+            for (int j = 0; j < 4; ++j)
+                __builtin_nontemporal_store(acc[j], &dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             put4_pair(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[1][c0t + ln][r0t + 4 * lg], acc);
         }
 #pragma unroll
@@ -480,7 +482,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc[j] *= sm.beta[r0t + 4 * lg + j];
-                drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln] = acc[j];
+                __builtin_nontemporal_store(acc[j], &drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             }
             put4_pair(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[1][c0t + ln][r0t + 4 * lg], acc);
         }
