@@ -141,15 +141,18 @@ def test_backward_unsupported_head_dims_raise(kda_pkg, wl):
                               chunk_size=16)
 
 
-@pytest.mark.parametrize("B,V,dtype", [(16, 64, torch.float32), (9, 128, torch.float16)])
-def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl, B, V, dtype):
+@pytest.mark.parametrize("B,K,V,dtype", [(16, 64, 64, torch.float32), (9, 64, 128, torch.float16),
+                                         (9, 128, 128, torch.float16)])
+def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl, B, K, V, dtype):
     """256 (batch, head) chains of 64 columns: the checkpointing forward runs its
     widest instantiation (four 16-column consumer waves a workgroup; at V=128
     and 144 chains, 128-column workgroups of two column groups a wave) and the
-    gradients come from its checkpoints.  They must equal the gradients of the
-    same sequences run one at a time (16 chains: one-wave instantiation), and
-    sequence 0 must match the fp64 oracle."""
-    T, H, K = 64, 16, 64
+    gradients come from its checkpoints; the state kernel runs 64-column
+    workgroups (at K = V = 128 fp16: the instantiations of the B=8 T=4096 H=16
+    training workload).  They must equal the gradients of the same sequences
+    run one at a time (16 chains: one-wave forward, 32-column state kernel),
+    and sequence 0 must match the fp64 oracle."""
+    T, H = 64, 16
     print(f"backward wide launch B={B} T={T} H={H} K={K} V={V} {dtype}", flush=True)
     xs, wo, ws = _case(wl, B, T, H, K, V, seed=31, dtype=dtype, state=True)
     wide = _native_grads(kda_pkg, xs, wo, ws, 32)
