@@ -24,12 +24,15 @@ Differences that are deliberate:
 
 * HIP tensors only.  There is no CPU path and no fallback: CPU tensors, a
   missing ``libkda_hip.so`` or an unsupported head size raise.
-* ``kda_chunkwise`` is differentiable: under grad mode, with any input that
-  requires grad, it runs as a ``torch.autograd.Function`` whose backward is
-  the native kernel ``kda_chunkwise_bwd`` (the reference is differentiated by
-  autograd through its torch ops).  Head dims K in {32, 64, 128} and V a
-  multiple of 32.  ``kda_recurrent`` is forward-only: inputs that require
-  grad under grad mode raise.
+* ``kda_chunkwise`` and ``kda_recurrent`` are differentiable: under grad
+  mode, with any input that requires grad, each runs as a
+  ``torch.autograd.Function`` whose backward is the native kernel
+  ``kda_chunkwise_bwd`` (the reference is differentiated by autograd through
+  its torch ops).  The recurrence and the chunkwise form are one function of
+  the inputs, so the recurrence's backward recomputes the chunkwise forward's
+  checkpoints and runs the same kernels, with the fp16 output clamp's mask
+  applied to the incoming gradient.  Head dims K in {32, 64, 128} and V a
+  multiple of 32.
 
 Every call is asynchronous on the current stream, allocates only through the
 torch caching allocator and never synchronises, so it can be captured in a
@@ -385,18 +388,73 @@ def kda_chunkwise(q, k, v, g, beta, initial_state=None, chunk_size=64, tile_size
     return _forward("chunkwise", q, k, v, g, beta, initial_state, int(chunk_size), state_dtype)
 
 
+class _RecurrentFn(torch.autograd.Function):
+    """kda_recurrent with a native backward.  The outputs come from the token
+    kernel.  The gradient of the recurrence (``kda.py:196-219``) equals that of
+    its chunkwise form (``kda.py:111-185``): the backward recomputes the
+    chunkwise forward with checkpoints on the saved inputs and runs
+    ``kda_chunkwise_bwd``.  An fp16 ``o`` was clamped to +-FP16_MAX_SAFE
+    (``kda.py:217-218``): the gradient of a clamped (or NaN) entry is zero."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, state, state_dtype):
+        o, s = _forward("recurrent", q, k, v, g, beta, state, 0, state_dtype)
+        # differentiate what the backward kernels read: q, k in v's dtype, the gates in fp32
+        ctx.save_for_backward(q.to(v.dtype), k.to(v.dtype), v, g.float(), beta.float(), state,
+                              o if o.dtype is torch.float16 else None)
+        ctx.state_dtype = state_dtype
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, g.dtype, beta.dtype,
+                      state.dtype if state is not None else None)
+        return o, s
+
+    @staticmethod
+    def backward(ctx, d_o, d_state):
+        q, k, v, g, beta, state, o16 = ctx.saved_tensors
+        tq, tk, tv, tg, tb, ts = ctx.dtypes
+        need_ds0 = ctx.needs_input_grad[5]
+        B, T, H, K = q.shape
+        V = v.shape[-1]
+        if T == 0:
+            zero = lambda shape, dt: torch.zeros(shape, device=q.device, dtype=dt)  # noqa: E731
+            ds0 = None
+            if need_ds0:
+                ds0 = d_state.to(ts) if d_state is not None else zero((B, H, K, V), ts)
+            return (zero(q.shape, tq), zero(k.shape, tk), zero(v.shape, tv), zero(g.shape, tg),
+                    zero(beta.shape, tb), ds0, None)
+        if d_o is None:
+            d_o = torch.zeros(v.shape, device=v.device, dtype=torch.float32)
+        elif o16 is not None:
+            d_o = d_o * (o16.abs() < FP16_MAX_SAFE)
+        _, _, ckpt = _forward("chunkwise", q, k, v, g, beta, state, 1, ctx.state_dtype, ckpt=True)
+        dq, dk, dv, dg, dbeta, ds0 = _chunkwise_backward(q, k, v, g, beta, ckpt, d_o, d_state, need_ds0)
+        return (dq.to(tq), dk.to(tk), dv.to(tv), dg.to(tg), dbeta.to(tb),
+                ds0.to(ts) if need_ds0 else None, None)
+
+
 def kda_recurrent(q, k, v, g, beta, state=None, state_dtype=None, *, state_out=None):
     """Token-by-token KDA recurrence on gfx950 (signature of kimi_linear/kda.py:188).
 
-    Any ``T >= 0``; ``T == 1`` is the decode step.
+    Any ``T >= 0``; ``T == 1`` is the decode step.  Differentiable under grad
+    mode (K in {32, 64, 128}, V a multiple of 32; see ``_RecurrentFn``).
 
     ``state_out`` (keyword-only, no counterpart in the reference) receives the
     new state instead of a fresh tensor: a contiguous ``[B, H, K, V]`` HIP
     tensor of dtype ``state_dtype or v.dtype``.  It may be ``state`` itself --
     an in-place update, which saves a decode loop with static state buffers
     (a captured graph) the copy of the whole state back into its input
-    buffer.  It is returned as the second output.
+    buffer.  It is returned as the second output.  Under autograd the state is
+    always a new tensor: ``state_out`` is for loops that run without grad.
     """
+    inputs = [x for x in (q, k, v, g, beta, state) if isinstance(x, torch.Tensor)]
+    if torch.is_grad_enabled() and any(x.requires_grad for x in inputs):
+        K, V = q.shape[-1], v.shape[-1]
+        if state_out is not None:
+            raise KdaError("state_out is an in-place update: kda_recurrent under autograd returns a new "
+                           "state (call under torch.no_grad() or detach the inputs to use state_out)")
+        if K not in (32, 64, 128) or V % BWD_TILE != 0:
+            raise KdaError(f"the native backward supports K in (32, 64, 128) and V a multiple of "
+                           f"{BWD_TILE}; got K={K}, V={V} (call under torch.no_grad() for the forward)")
+        return _RecurrentFn.apply(q, k, v, g, beta, state, state_dtype)
     return _forward("recurrent", q, k, v, g, beta, state, 0, state_dtype, state_out)
 
 

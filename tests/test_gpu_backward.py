@@ -1,4 +1,5 @@
-"""GPU parity of the native chunkwise backward (kda_chunkwise under autograd).
+"""GPU parity of the native chunkwise backward (kda_chunkwise and
+kda_recurrent under autograd).
 
 Reference: autograd of the oracle ``kda_chunkwise_ref`` in fp64 on the CPU
 (pinned by finite differences and by the recurrence in
@@ -16,7 +17,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from oracle import kda_chunkwise_ref
+from oracle import kda_chunkwise_ref, kda_recurrent_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -168,3 +169,76 @@ def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl, B, K, V, dtype):
         err = _rel(a[:1], r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
         assert err <= tol, (name, err)
+
+
+def _native_rec_grads(pkg, xs, wo, ws):
+    leaves = [x.to(DEV).clone().requires_grad_(True) if x is not None else None for x in xs]
+    o, s = pkg.kda_recurrent(*leaves[:5], state=leaves[5], state_dtype=torch.float32)
+    ((o.double() * wo.to(DEV)).sum() + (s.double() * ws.to(DEV)).sum()).backward()
+    torch.cuda.synchronize()
+    return [x.grad if x is not None else None for x in leaves]
+
+
+def _ref_rec_grads(xs, wo, ws, dtype=torch.float64):
+    leaves = [(x.to(dtype) if dtype is not None else x).clone().requires_grad_(True) if x is not None else None
+              for x in xs]
+    o, s = kda_recurrent_ref(*leaves[:5], state=leaves[5], state_dtype=torch.float64)
+    ((o.double() * wo).sum() + (s.double() * ws).sum()).backward()
+    return [x.grad if x is not None else None for x in leaves]
+
+
+@pytest.mark.parametrize("B,T,H,K,V,dtype,state", [
+    (1, 37, 2, 64, 64, torch.float32, True),      # T a multiple of no chunk size
+    (2, 5, 3, 128, 32, torch.float32, False),
+    (3, 1, 4, 32, 64, torch.float32, True),       # one decode step
+    (1, 50, 2, 64, 64, torch.bfloat16, True),
+])
+def test_recurrent_backward(kda_pkg, wl, B, T, H, K, V, dtype, state):
+    """kda_recurrent under autograd (kda.py:188-219 is differentiated by torch's
+    autograd in the reference) against autograd of the fp64 recurrence oracle;
+    gradients keep the inputs' dtypes."""
+    print(f"recurrent backward B={B} T={T} H={H} K={K} V={V} {dtype} state={state}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=200 + T, dtype=dtype, state=state)
+    ref = _ref_rec_grads(xs, wo, ws)
+    got = _native_rec_grads(kda_pkg, xs, wo, ws)
+    tol = 2e-3 if dtype == torch.float32 else 2e-2
+    for name, x, a, r in zip(NAMES, xs, got, ref):
+        if r is None:
+            assert a is None
+            continue
+        assert a.dtype == x.dtype and a.shape == r.shape
+        err = _rel(a, r)
+        print(f"  d{name}: rel {err:.2e}", flush=True)
+        assert err <= tol, (name, err)
+
+
+def test_recurrent_backward_fp16_clamp(kda_pkg, wl):
+    """An fp16 o is clamped to +-60000 (kda.py:217-218) and a clamped entry
+    passes no gradient.  With beta = 1 and unit keys, k_t^T S_t = v_t, so
+    q = 32 k (q~ = 4 k) gives o_t = 4 v_t exactly: v[..., 0] = 25000 puts
+    column 0 of o at 1e5, far past the clamp, the other columns at 4 v.  The
+    final-state weight of column 0 is zero, so every gradient of column 0
+    comes through the clamped outputs: an unmasked d_o would show in dv[..., 0]
+    (4 w_o instead of 0) and in dq, dk, dg."""
+    B, T, H, K, V = 1, 12, 2, 64, 32
+    inp = wl.make_inputs(B, T, H, K, V, seed=41, qkv_dtype=torch.float16)
+    k = inp["k"]
+    q = (k.float() * 32).half()
+    v = inp["v"].clone()
+    v[..., 0] = 25000.0
+    beta = torch.ones(B, T, H)
+    xs = [q, k, v, inp["g"], beta, None]
+    gen = torch.Generator().manual_seed(43)
+    wo = torch.randn(B, T, H, V, generator=gen, dtype=torch.float64)
+    ws = torch.randn(B, H, K, V, generator=gen, dtype=torch.float64)
+    ws[..., 0] = 0.0
+    with torch.no_grad():
+        o, _ = kda_pkg.kda_recurrent(*[x.to(DEV) for x in xs[:5]], state_dtype=torch.float32)
+    assert bool((o[..., 0].float() == 60000.0).all()) and float(o[..., 1:].float().abs().max()) < 100
+    ref = _ref_rec_grads(xs, wo, ws, dtype=None)
+    got = _native_rec_grads(kda_pkg, xs, wo, ws)
+    assert float(got[2][..., 0].abs().max()) == 0.0
+    for name, a, r in zip(NAMES[:5], got, ref):
+        err = _rel(a, r)
+        print(f"  d{name}: rel {err:.2e}", flush=True)
+        assert err <= 2e-2, (name, err)

@@ -398,8 +398,14 @@ def test_chunkwise_graph_replays(kda_pkg, wl):
 
 
 def test_grad_inputs_rejected(kda_pkg, wl):
-    """The recurrence is forward-only (the chunkwise kernel has a native backward)."""
+    """Under autograd the recurrence returns a new state (no state_out) and
+    needs a head size the native backward takes; its gradients are checked in
+    test_gpu_backward.py."""
     inp = to_dev(wl.make_inputs(1, 16, 1, 64, 64, seed=11, qkv_dtype=torch.float32))
     q = inp["q"].clone().requires_grad_(True)
-    with pytest.raises(kda_pkg.KdaError, match="forward-only"):
-        kda_pkg.kda_recurrent(q, inp["k"], inp["v"], inp["g"], inp["beta"])
+    s_out = torch.empty(1, 1, 64, 64, device=q.device)
+    with pytest.raises(kda_pkg.KdaError, match="in-place"):
+        kda_pkg.kda_recurrent(q, inp["k"], inp["v"], inp["g"], inp["beta"], state_out=s_out)
+    big = to_dev(wl.make_inputs(1, 4, 1, 256, 64, seed=12, qkv_dtype=torch.float32))
+    with pytest.raises(kda_pkg.KdaError, match="backward supports"):
+        kda_pkg.kda_recurrent(big["q"].clone().requires_grad_(True), big["k"], big["v"], big["g"], big["beta"])
