@@ -286,16 +286,22 @@ CU_COUNT = 256
 
 def long_segments(B, T, H, K, V, dtype) -> int:
     """Segments for kda_chunkwise_long_fwd: the largest power of two that keeps
-    the second pass within one round of 64-column workgroups on the 256 CUs
-    and segments of at least LONG_MIN_SEGMENT tokens; 1 (one pass) when the
-    chains alone fill half the CUs or the shape has no split kernel."""
+    the third pass (every segment's chain from its true initial state) within
+    one round of workgroups on the 256 CUs -- 128-column workgroups when V is a
+    multiple of 128 (the chunk kernel takes them once 64-column ones would
+    outnumber the CUs), else 64-column ones -- and segments of at least
+    LONG_MIN_SEGMENT tokens; 1 (one pass) when the chains alone fill half the
+    CUs or the shape has no split kernel.  At B=1 T=32768 H=16 d=128: 16
+    segments (0.60 ms against 0.68 ms with 8, whose third pass fills one
+    round of 64-column workgroups)."""
     if dtype not in (torch.float16, torch.bfloat16) or K not in (64, 128) or V % 64 != 0:
         return 1
     tiles = B * H * (V // 64)
     if tiles == 0 or 2 * tiles > CU_COUNT:
         return 1
+    units = B * H * (V // 128) if V % 128 == 0 else tiles
     P = 1
-    while (2 * P * tiles <= CU_COUNT and T % (2 * P) == 0 and T // (2 * P) >= LONG_MIN_SEGMENT):
+    while (2 * P * units <= CU_COUNT and T % (2 * P) == 0 and T // (2 * P) >= LONG_MIN_SEGMENT):
         P *= 2
     return P
 BWD_TILE = 32       # the native backward takes V in multiples of this

@@ -128,6 +128,8 @@ def test_long_split_zero_inputs_carry_the_state(kda_pkg, wl, native):
 def test_wrapper_splits_the_config3_shape(kda_pkg):
     """The wrapper picks the split for one long sequence of 16 heads."""
     kda = __import__("kimi_linear_amd.kda", fromlist=["long_segments"])
-    assert kda.long_segments(1, 32768, 16, 128, 128, torch.float16) == 8
+    assert kda.long_segments(1, 32768, 16, 128, 128, torch.float16) == 16
+    assert kda.long_segments(1, 32768, 16, 128, 64, torch.float16) == 16
+    assert kda.long_segments(1, 8192, 16, 128, 128, torch.float16) == 8
     assert kda.long_segments(8, 4096, 16, 128, 128, torch.float16) == 1
     assert kda.long_segments(1, 32768, 16, 128, 128, torch.float32) == 1
