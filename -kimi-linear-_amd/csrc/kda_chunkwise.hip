@@ -1435,9 +1435,8 @@ int launch_epi_k(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args&
     return KDA_ERR_UNSUPPORTED;
 }
 
-// Columns per workgroup: 128 when 64-column tiles outnumber the CUs, else
-// the widest tile (64, 32 or 16 columns) that still gives at least one
-// workgroup per CU; 16 when none does (few chains).
+// Columns per workgroup (16, 32, 64 or 128): the fewest rounds of
+// workgroups on the 256 CUs, see the cost below.
 template <int K, typename TQ, bool GATED>
 int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate) {
     constexpr int64_t kCus = 256;
@@ -1454,15 +1453,30 @@ int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I4 = std::integral_constant<int, 4>;
-    // More 64-column tiles than CUs: 128-column workgroups (consumer waves of
-    // two 16-column groups), whose ~20 % longer superstep beats a second
-    // round of workgroups (measured 265 against 450 us at B=16 T=2048 H=16
-    // d=128).  16-bit inputs only (the fp32 instantiation serves checkpoints).
+    // A superstep takes about as long in a 16-, 32- or 64-column workgroup
+    // (the producers' chain sets it) and ~10 % longer in a 128-column one
+    // (consumer waves of two 16-column groups; 16-bit inputs only, the fp32
+    // instantiation serves checkpoints), so the time is about rounds of
+    // workgroups x that factor: pick the cheapest, the narrower tile on a tie
+    // (measured at T=2048 H=16 d=128, gated, one round against 1.5-2: B=3
+    // 178 against 348 us, B=6 182 against 350 us; B=16 220 us in 128-column
+    // workgroups against 368 us in two rounds of 64-column ones).
+    const int64_t w1 = a.V % 16 == 0 ? heads * (a.V / 16) : 0;
+    const int64_t w2 = a.V % 32 == 0 ? heads * (a.V / 32) : 0;
+    const int64_t w4 = a.V % 64 == 0 ? heads * (a.V / 64) : 0;
+    const int64_t w8 = sizeof(TQ) == 2 && a.V % 128 == 0 ? heads * (a.V / 128) : 0;
+    // cost in tenths of a one-round superstep
+    auto cost = [&](int64_t wgs, int64_t tenths) { return ((wgs + kCus - 1) / kCus) * tenths; };
+    int best = 1;
+    int64_t best_cost = cost(w1, 10);
+    if (w2 > 0 && cost(w2, 10) < best_cost) best = 2, best_cost = cost(w2, 10);
+    if (w4 > 0 && cost(w4, 10) < best_cost) best = 4, best_cost = cost(w4, 10);
+    if (w8 > 0 && cost(w8, 11) < best_cost) best = 8, best_cost = cost(w8, 11);
     if constexpr (sizeof(TQ) == 2) {
-        if (a.V % 128 == 0 && heads * (a.V / 64) > kCus) return go(I4{}, I2{});
+        if (best == 8) return go(I4{}, I2{});
     }
-    if (a.V % 64 == 0 && heads * (a.V / 64) >= kCus) return go(I4{}, I1{});
-    if (a.V % 32 == 0 && heads * (a.V / 32) >= kCus) return go(I2{}, I1{});
+    if (best == 4) return go(I4{}, I1{});
+    if (best == 2) return go(I2{}, I1{});
     return go(I1{}, I1{});
 }
 

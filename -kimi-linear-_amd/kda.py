@@ -291,9 +291,14 @@ def long_segments(B, T, H, K, V, dtype) -> int:
     multiple of 128 (the chunk kernel takes them once 64-column ones would
     outnumber the CUs), else 64-column ones -- and segments of at least
     LONG_MIN_SEGMENT tokens; 1 (one pass) when the chains alone fill half the
-    CUs or the shape has no split kernel.  At B=1 T=32768 H=16 d=128: 16
-    segments (0.60 ms against 0.68 ms with 8, whose third pass fills one
-    round of 64-column workgroups)."""
+    CUs, when fewer than 4 segments would result, or when the shape has no
+    split kernel.  At B=1 T=32768 H=16 d=128: 16 segments (0.60 ms against
+    0.68 ms with 8, whose third pass fills one round of 64-column
+    workgroups).  The split pays roughly one superstep of the first pass (the
+    transition columns) and one of the third for every superstep of a
+    segment, against one superstep per 64 tokens in one pass: with 2
+    segments it is slower (B=3 T=2048 H=16: 253 against ~180 us), from 4 on
+    faster (B=1 T=4096: 174 against ~300 us)."""
     if dtype not in (torch.float16, torch.bfloat16) or K not in (64, 128) or V % 64 != 0:
         return 1
     tiles = B * H * (V // 64)
@@ -303,7 +308,7 @@ def long_segments(B, T, H, K, V, dtype) -> int:
     P = 1
     while (2 * P * units <= CU_COUNT and T % (2 * P) == 0 and T // (2 * P) >= LONG_MIN_SEGMENT):
         P *= 2
-    return P
+    return P if P >= 4 else 1
 BWD_TILE = 32       # the native backward takes V in multiples of this
 
 

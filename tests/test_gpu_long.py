@@ -132,4 +132,6 @@ def test_wrapper_splits_the_config3_shape(kda_pkg):
     assert kda.long_segments(1, 32768, 16, 128, 64, torch.float16) == 16
     assert kda.long_segments(1, 8192, 16, 128, 128, torch.float16) == 8
     assert kda.long_segments(8, 4096, 16, 128, 128, torch.float16) == 1
+    assert kda.long_segments(1, 4096, 16, 128, 128, torch.float16) == 4
+    assert kda.long_segments(2, 2048, 16, 128, 128, torch.float16) == 1    # 2 segments: one pass is faster
     assert kda.long_segments(1, 32768, 16, 128, 128, torch.float32) == 1
