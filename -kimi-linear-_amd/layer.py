@@ -50,7 +50,8 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 
-from .kda import KdaError, kda_chunkwise, kda_chunkwise_fused, kda_chunkwise_gated, kda_recurrent_gated
+from .kda import (KdaError, kda_chunkwise, kda_chunkwise_fused, kda_chunkwise_gated, kda_recurrent,
+                  kda_recurrent_gated, long_segments)
 from .layer_ops import kda_output, kda_output_train, kda_prep, kda_prep_train
 
 
@@ -226,7 +227,7 @@ class KimiDeltaAttention(nn.Module):
         z = lambda dim: torch.zeros(batch, keep, dim, device=device, dtype=dtype)  # noqa: E731
         return {"conv": {"q": z(H * K), "k": z(H * K), "v": z(H * V)}, "recurrent": None}
 
-    def _projections(self, x, conv_cache=None, use_cache=False, conv_out=None):
+    def _projections(self, x, conv_cache=None, use_cache=False, conv_out=None, gates=False):
         """q, k, v, the gate's up-projection gk ``[B, T, H, K]``, the beta logits
         ``[B, T, H]``, the new conv cache and the output gate's down-projection
         of x (``kda.py:399-461``).
@@ -235,9 +236,11 @@ class KimiDeltaAttention(nn.Module):
         the gate's up-projection a second; the three short convolutions with
         their cache, SiLU and the q/k L2 norms are one fused kernel
         (:func:`kda_prep`), and the forget gate and beta are formed by the
-        gated core from gk and the logits.  ``conv_out``: write the new conv
-        cache into these tensors (may be ``conv_cache`` itself for T <= 16)
-        instead of returning new ones."""
+        gated core from gk and the logits.  ``gates``: the fused kernel forms
+        them instead and g ``[B, T, H, K]``, beta ``[B, T, H]`` (fp32) take the
+        places of gk and the logits, for the ungated core.  ``conv_out``: write
+        the new conv cache into these tensors (may be ``conv_cache`` itself for
+        T <= 16) instead of returning new ones."""
         keep = max(self.conv_size - 1, 0)
         hist = conv_cache if (use_cache and conv_cache is not None and keep > 0) else None
         convs = (self.conv_q.conv, self.conv_k.conv, self.conv_v.conv)
@@ -246,15 +249,18 @@ class KimiDeltaAttention(nn.Module):
         y = torch.nn.functional.linear(x, w, b)
         q_in, k_in, v_in, beta_logit, gk_low, og_low = torch.split(
             y, (H * K, H * K, H * V, H, self.gk_proj[0].out_features, self.og_proj[0].out_features), dim=-1)
-        q, k, v, _, _, new_conv = kda_prep(
+        gk = self.gk_proj[1](gk_low)
+        gate_in = (gk, *self._gate_params(), beta_logit) if gates else (None, None, None, None)
+        q, k, v, g, beta, new_conv = kda_prep(
             q_in, k_in, v_in,
             tuple(c.weight for c in convs), tuple(c.bias for c in convs),
-            None, None, None, None,
+            *gate_in,
             num_heads=self.num_heads, head_dim=self.head_dim, value_head_dim=self.value_head_dim,
             l2_eps=self.l2norm_eps, hist=hist, hist_out=conv_out if use_cache else None,
             want_hist=use_cache and conv_out is None)
-        gk = self.gk_proj[1](gk_low).view(x.shape[0], x.shape[1], H, K)
-        return q, k, v, gk, beta_logit, new_conv, og_low
+        if gates:
+            return q, k, v, g, beta, new_conv, og_low
+        return q, k, v, gk.view(x.shape[0], x.shape[1], H, K), beta_logit, new_conv, og_low
 
     def _output(self, o_core, og_low):
         """Head-wise RMSNorm, sigmoid output gate (one fused kernel,
@@ -331,14 +337,23 @@ class KimiDeltaAttention(nn.Module):
             state = self.init_state(x.shape[0], device=x.device, dtype=x.dtype)
         conv_cache = state["conv"] if state is not None else None
         rec = state["recurrent"] if state is not None else None
-        q, k, v, g, beta, new_conv, og_low = self._projections(x, conv_cache=conv_cache, use_cache=use_cache)
-        gate = self._gate_params()      # g, beta above: gk and the beta logits
         B, T = x.shape[0], x.shape[1]
         sdtype = self._state_dtype(x)
         C = self.chunk_size
         if 0 < T < C:
             C = T
-        if not (use_cache and T == 1) and T > 0 and T % C == 0 and self._fused_output_ok(x):
+        body = T - T % C if T > 0 else 0
+        fused = not (use_cache and T == 1) and T > 0 and T % C == 0 and self._fused_output_ok(x)
+        # Few chains over a long body: the ungated core splits the sequence
+        # into parallel segments (kda_chunkwise_long_fwd), which the gated one
+        # does not, so the pre-processing kernel forms g and beta (B=1 T=4096
+        # H=16 d=128: 179 against 347 us for the core).
+        split = (not fused and not (use_cache and T == 1) and body > 0 and (B == 1 or body == T)
+                 and long_segments(B, body, self.num_heads, self.head_dim, self.value_head_dim, x.dtype) > 1)
+        q, k, v, g, beta, new_conv, og_low = self._projections(x, conv_cache=conv_cache, use_cache=use_cache,
+                                                               gates=split)
+        gate = self._gate_params()      # unless split, g and beta above are gk and the beta logits
+        if fused:
             # one chunkwise body and no tail: the output epilogue runs on the
             # chunk kernel's tiles and its result is the o_proj input
             og = self.og_proj[1](og_low)
@@ -352,23 +367,30 @@ class KimiDeltaAttention(nn.Module):
             o_core, new_rec = kda_recurrent_gated(q, k, v, g, beta, *gate, state=rec, state_dtype=sdtype)
         else:
             rem = T % C
-            body = T - rem
             # every position is written by the body or the tail (the reference
             # zero-fills first, kda.py:516): without a tail the body's output
             # is the result as it is
             o_core = None
-            if body > 0:
+            if body > 0 and split:
+                o_body, rec = kda_chunkwise(q[:, :body], k[:, :body], v[:, :body], g[:, :body], beta[:, :body],
+                                            initial_state=rec, chunk_size=C, state_dtype=sdtype)
+            elif body > 0:
                 o_body, rec = kda_chunkwise_gated(q[:, :body], k[:, :body], v[:, :body], g[:, :body],
                                                   beta[:, :body], *gate, initial_state=rec, chunk_size=C,
                                                   state_dtype=sdtype)
+            if body > 0:
                 if rem == 0:
                     o_core = o_body
                 else:
                     o_core = x.new_empty(B, T, self.num_heads, self.value_head_dim)
                     o_core[:, :body] = o_body
-            if rem > 0:
+            if rem > 0 and split:
+                o_tail, rec = kda_recurrent(q[:, body:], k[:, body:], v[:, body:], g[:, body:], beta[:, body:],
+                                            state=rec, state_dtype=sdtype)
+            elif rem > 0:
                 o_tail, rec = kda_recurrent_gated(q[:, body:], k[:, body:], v[:, body:], g[:, body:],
                                                   beta[:, body:], *gate, state=rec, state_dtype=sdtype)
+            if rem > 0:
                 if o_core is None:
                     o_core = o_tail
                 else:

@@ -280,6 +280,19 @@ def layer_bench(pkg, torch, reps=10):
         torch.cuda.synchronize()
         prefill16_ms = e0.elapsed_time(e1) / (reps // 2)
         del xb
+        # one long prompt: 16 chains, where the core splits the sequence into
+        # parallel segments
+        xl = torch.randn(1, 16384, 2048, device="cuda", dtype=torch.float16)
+        for _ in range(2):
+            layer(xl)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps // 2):
+            layer(xl)
+        e1.record()
+        torch.cuda.synchronize()
+        prefill_long_ms = e0.elapsed_time(e1) / (reps // 2)
+        del xl
     # training step: the differentiable path, gradients of every parameter and x
     xt = x.clone().requires_grad_()
     gout = torch.randn(4, 2048, 2048, device="cuda", dtype=torch.float16)
@@ -316,6 +329,8 @@ def layer_bench(pkg, torch, reps=10):
             "prefill_tokens_per_s": 4 * 2048 / (prefill_ms * 1e-3),
             "prefill_B16_T2048_ms": prefill16_ms,
             "prefill_B16_tokens_per_s": 16 * 2048 / (prefill16_ms * 1e-3),
+            "prefill_B1_T16384_ms": prefill_long_ms,
+            "prefill_B1_T16384_tokens_per_s": 16384 / (prefill_long_ms * 1e-3),
             "train_step_B4_T2048_ms": train_ms,
             "train_tokens_per_s": 4 * 2048 / (train_ms * 1e-3),
             "decode_B64_graph_us_per_token": decode_us}

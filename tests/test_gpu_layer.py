@@ -180,3 +180,28 @@ def test_layer_fused_output_vs_oracle(kda_pkg, dtype, hd, T):
     assert e <= TOL[dtype] and es <= TOL[dtype]
     assert torch.equal(st_f["recurrent"], st_s["recurrent"])
     assert ed <= TOL[dtype] / 4
+
+
+def test_layer_long_prefill_takes_the_split_core(kda_pkg, monkeypatch):
+    """One long sequence over few heads: the pre-processing kernel forms g and
+    beta and the ungated core splits the body into 4 parallel segments (the
+    gated core has no split).  Output and recurrent state against the oracle
+    and against the same layer run with the split turned off."""
+    layer_mod = __import__("kimi_linear_amd.layer", fromlist=["long_segments"])
+    dtype = torch.float16
+    m, cfg, p = make_layer(kda_pkg, dtype, seed=5)
+    la = cfg.linear_attn_config
+    T = 4096 + 22                                   # body of 4096 + recurrent tail
+    assert layer_mod.long_segments(1, 4096, la["num_heads"], la["head_dim"], la["value_head_dim"], dtype) == 4
+    x = make_x(1, T, 256, dtype, seed=6)
+    print(f"[layer long prefill fp16 B=1 T={T} H={la['num_heads']}]", flush=True)
+    with torch.no_grad():
+        out, st = m(x.to(DEV), use_cache=True)
+        monkeypatch.setattr(layer_mod, "long_segments", lambda *a: 1)
+        out1, st1 = m(x.to(DEV), use_cache=True)
+    ref, st_ref = kda_layer_ref(p, cfg, x, use_cache=True)
+    e, es = rel(out, ref), rel(st["recurrent"], st_ref["recurrent"])
+    e1, es1 = rel(out, out1), rel(st["recurrent"], st1["recurrent"])
+    print(f"  vs oracle: out {e:.3e} state {es:.3e}; vs one pass: out {e1:.3e} state {es1:.3e}", flush=True)
+    assert e <= TOL[dtype] and es <= TOL[dtype]
+    assert e1 <= TOL[dtype] and es1 <= TOL[dtype]
