@@ -1099,8 +1099,12 @@ int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
         if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
     }
     // 64 state columns a workgroup, or 32 when that leaves compute units idle
-    // (the chain is sequential: more, narrower workgroups shorten it)
-    if (a.V % 64 == 0 && BH * (a.V / 64) >= cu_count())
+    // and the 32-column workgroups still fit one round (the chain is
+    // sequential: more, narrower workgroups shorten it, a second round
+    // lengthens it; forward + backward at T=2048 H=16 d=128: B=4 0.80 ms
+    // with 32 columns against 0.84 ms, B=6 1.05 ms with 64 against 1.19 ms)
+    const int64_t cus = cu_count();
+    if (a.V % 64 == 0 && (BH * (a.V / 64) >= cus || BH * (a.V / 32) > cus))
         hipLaunchKernelGGL((bwd_state_kernel<K, 64, TI>), dim3(static_cast<unsigned>(BH * (a.V / 64))), dim3(NS), 0,
                            stream, a, ws);
     else
