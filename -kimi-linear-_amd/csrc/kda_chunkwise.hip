@@ -1372,9 +1372,13 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             }
             __syncthreads();
         }
+        // a null state_out (the output pass of a split long sequence) keeps no final state
+        if (a.state_out != nullptr) {
 #pragma unroll
-        for (int g = 0; g < CG; ++g)
-            store_state<KT>(S[g], a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * VS + colw + 16 * g + kn.ln, VS);
+            for (int g = 0; g < CG; ++g)
+                store_state<KT>(S[g], a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * VS + colw + 16 * g + kn.ln,
+                                VS);
+        }
     } else {
         const int p = wave - NC;
         if constexpr (GATED) {

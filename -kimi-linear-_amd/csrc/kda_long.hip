@@ -120,7 +120,7 @@ bool split_strides(int64_t (&st)[3], int64_t B, int64_t T, int64_t P) {
 }  // namespace
 
 int64_t long_workspace_bytes(int64_t B, int64_t H, int64_t K, int64_t V, int64_t P) {
-    return 4 * B * P * H * K * (3 * V + K);
+    return 4 * B * P * H * K * (2 * V + K);
 }
 
 int long_launch(const kda_fwd_args& a, int64_t P, void* workspace, hipStream_t stream) {
@@ -134,7 +134,6 @@ int long_launch(const kda_fwd_args& a, int64_t P, void* workspace, hipStream_t s
         return KDA_ERR_UNSUPPORTED;
     float* seg = static_cast<float*>(workspace);
     float* sstart = seg + B * P * H * K * (V + K);
-    float* dummy = sstart + B * P * H * K * V;
 
     // 1. per chain: the state from zero and the transition
     kda_fwd_args a1 = s;
@@ -155,12 +154,12 @@ int long_launch(const kda_fwd_args& a, int64_t P, void* workspace, hipStream_t s
                            stream, seg, sstart, a.state_in, a.state_in_dtype, a.state_out, a.state_out_dtype, B, H, V, P);
     if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
 
-    // 3. per chain from its true initial state: the outputs (its final state,
-    // the next segment's initial one, is not needed again)
+    // 3. per chain from its true initial state: the outputs only (its final
+    // state, the next segment's initial one, is known already: no state_out)
     kda_fwd_args a3 = s;
     a3.state_in = sstart;
     a3.state_in_dtype = KDA_DTYPE_F32;
-    a3.state_out = dummy;
+    a3.state_out = nullptr;
     a3.state_out_dtype = KDA_DTYPE_F32;
     return chunkwise_launch(a3, stream);
 }

@@ -302,6 +302,11 @@ class KimiDeltaAttention(nn.Module):
         function), the output epilogue (:func:`kda_output_train`) and o_proj.
         Every step has a native backward; no cache, no state."""
         H, K, V = self.num_heads, self.head_dim, self.value_head_dim
+        if K not in (64, 128) or V not in (64, 128):
+            # the pre-processing backward (kda_prep_bwd) takes head dims 64 and 128:
+            # refuse before any forward work rather than inside backward
+            raise KdaError(f"the layer's training path supports head_dim and value_head_dim in (64, 128); got "
+                           f"{K} and {V} (run the forward under torch.no_grad())")
         B, T = x.shape[0], x.shape[1]
         mods = self._input_mods()
         w = torch.cat([m.weight for m in mods], 0)

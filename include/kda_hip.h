@@ -247,7 +247,10 @@ int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
  * three kernels use instead a static device buffer of KDA_BWD_SCRATCH_BYTES
  * that the library holds on every GPU it runs on until the process ends
  * (resolved once per device, on the first call with that device current;
- * `stream` must belong to the current device).  Shapes whose
+ * `stream` must belong to the current device).  That first call resolves a
+ * symbol address, which may load the code object: make it outside graph
+ * capture (an eager warm-up call); later calls on the device only launch
+ * kernels and may be captured.  Shapes whose
  * kda_chunkwise_bwd_workspace_size() exceeds KDA_BWD_SCRATCH_BYTES return
  * KDA_ERR_TOO_LARGE before any launch.  Every call on one GPU shares that
  * GPU's buffer: calls that overlap on one GPU (two streams, two threads) race

@@ -193,7 +193,8 @@ def test_long_host_validation_codes(native):
     assert call(ctypes.byref(_args(native, **f16)), 2, ctypes.c_void_p(0x100008), None) == 2  # misaligned
     assert call(ctypes.byref(_args(native, B=0, **f16)), 2, None, None) == 0
     size = lib.kda_chunkwise_long_workspace_size
-    assert size(1, 32768, 16, 128, 128, 8) == 4 * 8 * 16 * 128 * (3 * 128 + 128)
+    # per segment and head: S_loc and Phi (K x (V + K)) and the initial state (K x V), fp32
+    assert size(1, 32768, 16, 128, 128, 8) == 4 * 8 * 16 * 128 * (2 * 128 + 128)
     assert size(1, 64, 1, 64, 64, 0) == 0
 
 
@@ -253,6 +254,18 @@ def test_wrapper_shape_and_chunk_errors(kda_pkg):
         kda_pkg.kda_recurrent(q, q, v, q, torch.zeros(1, 20, 2))
     with pytest.raises(kda_pkg.KdaError, match="state must be"):
         kda_pkg.kda_recurrent(q, q, v, q, beta, state=torch.zeros(1, 1, 64, 32))
+
+
+def test_layer_training_path_refuses_head_dims_its_backward_lacks(kda_pkg):
+    """value_head_dim 256 has a forward but no pre-processing backward: the
+    training path refuses it before any work (here on CPU tensors, which
+    would fail later anyway)."""
+    cfg = kda_pkg.linear_attn_config(hidden_size=256, num_heads=1, head_dim=128, value_head_dim=256,
+                                     gate_low_rank=32, output_gate_low_rank=32)
+    m = kda_pkg.KimiDeltaAttention(cfg)
+    x = torch.zeros(1, 8, 256, requires_grad=True)
+    with pytest.raises(kda_pkg.KdaError, match="training path supports head_dim"):
+        m(x)
 
 
 def test_noalloc_backward_rejects_shapes_beyond_its_buffer(native):

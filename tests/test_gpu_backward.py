@@ -134,6 +134,40 @@ def test_backward_matches_eager_chaining(kda_pkg, wl):
         assert err <= 1e-4, (name, err)
 
 
+@pytest.mark.parametrize("H,K,V,dtype", [(2, 64, 64, torch.float32), (2, 64, 64, torch.float16),
+                                         (1, 128, 128, torch.float16)])
+def test_backward_long_sequence(kda_pkg, wl, H, K, V, dtype):
+    """T = 2048: the state kernel carries dS backwards over 64 checkpoint
+    chunks (with the next chunk fetched while the current one is computed),
+    as in the training workload.  Against the fp64 oracle's autograd (chunk
+    16), and one T = 2048 call against two chained T = 1024 calls."""
+    B, T = 1, 2048
+    print(f"backward long sequence {dtype} B={B} T={T} H={H} K={K} V={V}", flush=True)
+    xs, wo, ws = _case(wl, B, T, H, K, V, seed=300 + K, dtype=dtype, state=True)
+    ref = _ref_grads(xs, wo, ws, 16)
+    got = _native_grads(kda_pkg, xs, wo, ws, 64)
+    tol = 2e-3 if dtype == torch.float32 else 2e-2
+    for name, a, r in zip(NAMES, got, ref):
+        err = _rel(a, r)
+        print(f"  d{name}: rel {err:.2e}", flush=True)
+        assert err <= tol, (name, err)
+    leaves = [x.to(DEV).clone().requires_grad_(True) for x in xs]
+    q, k, v, g, beta, s0 = leaves
+    h = T // 2
+    o1, s1 = kda_pkg.kda_chunkwise(q[:, :h], k[:, :h], v[:, :h], g[:, :h], beta[:, :h],
+                                   initial_state=s0, chunk_size=64, state_dtype=torch.float32)
+    o2, s2 = kda_pkg.kda_chunkwise(q[:, h:], k[:, h:], v[:, h:], g[:, h:], beta[:, h:],
+                                   initial_state=s1, chunk_size=64, state_dtype=torch.float32)
+    o = torch.cat([o1, o2], dim=1)
+    ((o.float() * wo.to(DEV, torch.float32)).sum() + (s2 * ws.to(DEV, torch.float32)).sum()).backward()
+    for name, a, b in zip(NAMES, [x.grad for x in leaves], got):
+        err = _rel(a, b)
+        print(f"  chained vs one call d{name}: rel {err:.2e}", flush=True)
+        # the two halves' checkpoints and gradients are computed as in one call
+        # (the state enters the second half as fp32), up to output rounding
+        assert err <= (1e-4 if dtype == torch.float32 else 2e-3), (name, err)
+
+
 def test_backward_unsupported_head_dims_raise(kda_pkg, wl):
     inp = wl.make_inputs(1, 16, 1, 16, 32, seed=3)
     q = inp["q"].to(DEV).requires_grad_(True)

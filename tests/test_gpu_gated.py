@@ -94,6 +94,43 @@ def test_chunkwise_gated_matches_oracle(kda_pkg, dtype, B, T, H, state):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,T", [(8, 128), (16, 128), (8, 100), (16, 100)])
+def test_chunkwise_gated_wide_launches_match_oracle(kda_pkg, dtype, B, T):
+    """The gated tiles the layer's prefill runs at B=5-16 with 16 heads of 128:
+    128 chains -> 64-column workgroups of four 16-column consumer waves
+    (NC = 4); 256 chains -> 128-column workgroups whose consumer waves own two
+    column groups (NC = 4, CG = 2, the plain output path).  T = 100 ends in a
+    partial block (the layer's tail-free body is a multiple of 64; a direct
+    call need not be).  Three (batch, head) pairs against the oracle, and
+    every sequence's state against the same sequence run alone (16 chains,
+    16-column workgroups: the same per-column arithmetic)."""
+    H, K, V = 16, 128, 128
+    C = 64 if T % 64 == 0 else T
+    print(f"gated chunkwise wide launch {dtype} B={B} T={T} H={H}", flush=True)
+    inp = make(B, T, H, K, V, dtype, seed=B + T, state_std=0.05)
+    d = dev(inp)
+    with torch.no_grad():
+        o, s = kda_pkg.kda_chunkwise_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                           initial_state=d["state"], chunk_size=C, state_dtype=torch.float32)
+        one = {n: (t[B - 1:B] if t is not None and t.dim() >= 3 else t) for n, t in d.items()}
+        o1, s1 = kda_pkg.kda_chunkwise_gated(one["q"], one["k"], one["v"], one["gk"], one["logit"], one["a_log"],
+                                             one["dt_bias"], initial_state=one["state"], chunk_size=C,
+                                             state_dtype=torch.float32)
+    assert torch.equal(o[B - 1:B], o1) and torch.equal(s[B - 1:B], s1)
+    g, beta = oracle_gates(inp)
+    o_tol = O_TOL if dtype == torch.float16 else 8 * O_TOL
+    s_tol = S_TOL if dtype == torch.float16 else 8 * S_TOL
+    for b, h in ((0, 0), (B // 2, 7), (B - 1, 15)):
+        sl = lambda t: t[b:b + 1, :, h:h + 1]  # noqa: E731
+        o_ref, s_ref = kda_chunkwise_ref(sl(inp["q"]), sl(inp["k"]), sl(inp["v"]), sl(g),
+                                         beta[b:b + 1, :, h:h + 1], initial_state=inp["state"][b:b + 1, h:h + 1],
+                                         chunk_size=C, state_dtype=torch.float32)
+        eo, es = max_abs(o[b:b + 1, :, h:h + 1], o_ref), rel(s[b:b + 1, h:h + 1], s_ref)
+        print(f"  b={b} h={h}: o max-abs {eo:.2e} state rel {es:.2e}", flush=True)
+        assert eo <= o_tol and es <= s_tol, (b, h, eo, es)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_chunkwise_gated_equals_ungated_with_the_same_gates(kda_pkg, dtype):
     """The gated kernel and the ungated one fed g, beta from the oracle's formula
     (computed on the host) differ only by the decay's rounding."""

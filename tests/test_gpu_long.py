@@ -125,6 +125,34 @@ def test_long_split_zero_inputs_carry_the_state(kda_pkg, wl, native):
     assert rel(o, o1) <= 1e-3
 
 
+def test_wrapper_split_with_partial_last_chunks(kda_pkg, wl, native):
+    """B=1 T=4160 H=16: the wrapper splits into 4 segments of 1040 tokens, so
+    every segment ends half-way through a 32-token chunk.  The rows past a
+    segment's end must read as zero (not as the next segment's first tokens)
+    in both the transition pass and the output pass: the wrapper's result
+    against one pass and against the oracle on three heads."""
+    kda = __import__("kimi_linear_amd.kda", fromlist=["long_segments"])
+    B, T, H, K, V = 1, 4160, 16, 128, 128
+    assert kda.long_segments(B, T, H, K, V, torch.float16) == 4 and (T // 4) % 32 != 0
+    print(f"long split through the wrapper, B={B} T={T} H={H}: 4 segments of {T // 4} tokens", flush=True)
+    cpu = wl.make_inputs(B, T, H, K, V, seed=51, qkv_dtype=torch.float16, state_std=0.02)
+    cpu["g"] = cpu["g"] * 1e-3                      # weak decay: each segment's initial state matters
+    inp = {n: (t.to(DEV) if t is not None else None) for n, t in cpu.items()}
+    with torch.no_grad():
+        o, s = kda_pkg.kda_chunkwise(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
+                                     initial_state=inp["state"], chunk_size=64, state_dtype=torch.float32)
+        o1, s1 = long_call(native, inp, 1)
+    d_o, d_s = rel(o, o1), rel(s, s1)
+    sub = {n: (t[:, :, 0:16:7] if n != "state" else t[:, 0:16:7]) for n, t in cpu.items()}
+    o_ref, s_ref = kda_chunkwise_ref(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"],
+                                     initial_state=sub["state"], chunk_size=64, state_dtype=torch.float32)
+    eo, es = max_abs(o[:, :, 0:16:7], o_ref), rel(s[:, 0:16:7], s_ref)
+    print(f"  vs oracle: o max-abs {eo:.2e} state rel {es:.2e}; vs one pass: o {d_o:.2e} state {d_s:.2e}",
+          flush=True)
+    assert eo <= O_TOL and es <= S_TOL
+    assert d_o <= 1e-3 and d_s <= 1e-3
+
+
 def test_wrapper_splits_the_config3_shape(kda_pkg):
     """The wrapper picks the split for one long sequence of 16 heads."""
     kda = __import__("kimi_linear_amd.kda", fromlist=["long_segments"])

@@ -269,6 +269,59 @@ def test_config2_decode_graph(kda_pkg, wl):
         assert eo <= O_TOL and es <= 1e-5
 
 
+@pytest.mark.parametrize("in_place", [False, True])
+def test_config2_decode_512_steps_in_one_graph(kda_pkg, wl, in_place):
+    """Configuration 2 as it is timed: 512 consecutive B=64 decode steps
+    captured in ONE hipGraph (each step a fresh state tensor, as the
+    reference's API returns it, or the state updated in place), every step's
+    output kept; replayed twice.  Every step's o and the final state against
+    the oracle's token recurrence (batch rows 0 and 63, all heads), and the
+    whole replay against one eager call over the 512 tokens."""
+    B, H, K, V, steps = 64, 16, 128, 128, 512
+    print(f"cfg2 512 steps in one graph, in_place={in_place}", flush=True)
+    inp = wl.make_inputs(B, steps, H, K, V, device=DEV, seed=2, qkv_dtype=torch.float16,
+                         gate_dtype=torch.float16, state_std=0.02)
+    xs = [inp[n] for n in ("q", "k", "v", "g", "beta")]
+    st = inp["state"].clone()
+    outs = torch.empty(B, steps, H, V, device=DEV, dtype=torch.float16)
+    holder = {}
+
+    def run_all(s_in):
+        cur = s_in
+        for t in range(steps):
+            o, cur = kda_pkg.kda_recurrent(*[a[:, t:t + 1] for a in xs], state=cur, state_dtype=torch.float32,
+                                           state_out=cur if in_place else None)
+            outs[:, t:t + 1].copy_(o)
+        holder["final"] = cur
+
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run_all(st)                                    # warm-up on a side stream
+        torch.cuda.current_stream().wait_stream(side)
+        st.copy_(inp["state"])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_all(st)
+        final = holder["final"]
+        o_all, s_all = kda_pkg.kda_recurrent(*xs, state=inp["state"], state_dtype=torch.float32)
+        for rep in range(2):
+            st.copy_(inp["state"])
+            outs.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(outs, o_all) and torch.equal(final, s_all), rep
+    for b in (0, 63):
+        sub = to_cpu(wl.slice_heads(inp, slice(b, b + 1), slice(0, H)))
+        o_ref, s_ref = ref_recurrent(sub)
+        per_step = (outs[b:b + 1].double().cpu() - o_ref.double()).abs().amax(dim=(0, 2, 3))
+        es = rel(final[b:b + 1], s_ref)
+        report(f"cfg2 one-graph decode b={b} (worst step {int(per_step.argmax())})", per_step.max().item(), es)
+        assert per_step.max().item() <= O_TOL and es <= 1e-5
+    del graph
+
+
 # ----------------------------------------------------------------- configuration 3
 def test_config3_long_context_state(kda_pkg, wl):
     inp = wl.make_inputs(1, 32768, 16, 128, 128, device=DEV, seed=3, qkv_dtype=torch.float16,

@@ -79,3 +79,36 @@ def test_noalloc_backward_equals_workspace_backward(kda_pkg, native):
         for name in ref:
             assert torch.isfinite(ref[name]).all(), name
             assert torch.equal(got[name], ref[name]), name
+
+
+def test_noalloc_backward_under_graph_capture(kda_pkg, native):
+    """The entry is for callers that capture their work: after an eager call on
+    the device (which resolves the scratch address), a captured call replays
+    to the eager gradients three times, with other eager work on the same
+    buffers in between."""
+    B, T, H, K, V, dtype = 1, 96, 4, 128, 128, torch.float16
+    print(f"no-alloc backward under capture B={B} T={T} H={H} K={K} V={V} {dtype}", flush=True)
+    x = _inputs(kda_pkg, B, T, H, K, V, dtype, seed=77)
+    eager = _run(native, "kda_chunkwise_bwd_noalloc", x, B, T, H, K, V, dtype, None)
+    torch.cuda.synchronize()
+    holder = {}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _run(native, "kda_chunkwise_bwd_noalloc", x, B, T, H, K, V, dtype, None)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        holder["outs"] = _run(native, "kda_chunkwise_bwd_noalloc", x, B, T, H, K, V, dtype, None)
+    outs = holder["outs"]
+    for rep in range(3):
+        for t in outs.values():
+            t.fill_(float("nan"))
+        # eager work on the shared scratch between replays (a smaller shape)
+        y = _inputs(kda_pkg, 1, 40, 2, 64, 64, torch.float32, seed=78 + rep)
+        _run(native, "kda_chunkwise_bwd_noalloc", y, 1, 40, 2, 64, 64, torch.float32, None)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name in eager:
+            assert torch.equal(outs[name], eager[name]), (rep, name)
+    del graph
