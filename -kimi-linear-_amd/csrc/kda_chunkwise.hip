@@ -454,6 +454,7 @@ struct Kern {
     // head's first V-tile workgroup only (null otherwise): per 32-token chunk
     // the state, R and P ((K + 64) x V) and then A, L and N (32 x 32 each)
     float* ckm = nullptr;
+    int nblk = 0;                            // blocks of the real chunks (records exist for these)
 
     // A, L, N of the chunk holding block blk (row-major 32 x 32, consecutive)
     __device__ float* ck_mats(int blk) const {
@@ -726,7 +727,7 @@ struct Kern {
         Q = mm_f32(L2, Q, Q);
         Q = mm_f32(L4, Q, Q);
         Q = mm_f32(L8, Q, Q);                    // acc((I + L)^-T) = A-layout of (I + L)^-1
-        if (ckm) {
+        if (ckm && blk < nblk) {
             // the backward's N block: N[ln][4 lg + j] = (I + L)^-1
             float* n = ck_mats(blk) + 2 * CB * BT * CB * BT;
             const int o = BT * (blk % CB);
@@ -806,7 +807,7 @@ struct Kern {
         // the block's sums are complete: A to its operand, G and beta to the
         // solve (and both to the backward's record; block 0 also zeroes the
         // record's blocks above the diagonal)
-        if (ckm) {
+        if (ckm && next - NB < nblk) {
             constexpr int C = CB * BT;
             float* ma = ck_mats(next - NB);
             const int o = BT * bi;
@@ -913,7 +914,7 @@ struct Kern {
                 accG = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o), accG);
                 accA = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o), accA);
             }
-            if (ckm) {
+            if (ckm && blk < nblk) {
                 // the backward's A_10 and L_10: slot j holds row 16 + ln, column 4 lg + j
                 constexpr int C = CB * BT;
                 float* ma = ck_mats(blk);
@@ -1000,21 +1001,28 @@ struct Kern {
         }
     }
 
-    // Four values of one output row to o (TQ): lane (ln, lg) holds row ln of
-    // block blk, columns col + 4lg .. + 3 (rows past T are skipped).
+    // Four values of one output row to o (TQ, [B, T, H, V] contiguous): lane
+    // (ln, lg) holds row ln of block blk, columns col + 4lg .. + 3.  A buffer
+    // store through a descriptor spanning the block's rows before T: the
+    // hardware drops the rows past T, so every lane stores unconditionally.
+    // (A branch around the store would hide the number of outstanding vector
+    // memory operations from the compiler, which then waits for all of them
+    // -- these stores included -- before the next chunk's v tile.)
     __device__ void store_row4(const f4& O, int blk, int64_t col) const {
-        const int64_t row = static_cast<int64_t>(blk) * BT + ln;
-        if (ln >= rows_in(blk)) return;
-        TQ* o = static_cast<TQ*>(a.o) + ((b * T + row) * a.H + h) * a.V + col + 4 * lg;
+        const int64_t rs = a.H * a.V;                    // token row stride, elements
+        const int64_t e = (b * T + static_cast<int64_t>(blk) * BT) * rs + h * a.V;
+        const auto r = make_rsrc(static_cast<TQ*>(a.o) + e,
+                                 static_cast<uint32_t>(rows_in(blk) * rs * static_cast<int64_t>(sizeof(TQ))));
+        const int vo = static_cast<int>((ln * rs + col + 4 * lg) * static_cast<int64_t>(sizeof(TQ)));
         if constexpr (sizeof(TQ) == 4) {
-            *reinterpret_cast<float4*>(o) = float4{O[0], O[1], O[2], O[3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, O), r, vo, 0, 0);
         } else if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
-            *reinterpret_cast<h4*>(o) = to_h4(O);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, to_h4(O)), r, vo, 0, 0);
         } else {
             u2 w;
             w[0] = static_cast<uint32_t>(f32_to_bf16_bits(O[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(O[1])) << 16);
             w[1] = static_cast<uint32_t>(f32_to_bf16_bits(O[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(O[3])) << 16);
-            *reinterpret_cast<u2*>(o) = w;
+            __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, 0, 0);
         }
     }
 
@@ -1283,6 +1291,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     const int nch = static_cast<int>((a.T + BT - 1) / BT);
     const int ncc = (nch + CB - 1) / CB;                 // chunks
     const int nblk = CB * ncc;                           // blocks, padded to whole chunks
+    kn.nblk = nblk;
     if constexpr (CKPT) {
         if (ckpt != nullptr && vt == 0) kn.ckm = ckpt + (kn.b * H + kn.h) * ncc * ckpt_record(K, V);
     }
@@ -1343,33 +1352,45 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
 #pragma unroll
                 for (int j = 0; j < 4; ++j) kn.wn[g][j] = epi.weight[kn.h * V + colw + 16 * g + 4 * kn.lg + j];
         }
-        // First half: the superstep's chunks one after the other; second
-        // half (after the producers' first): the chunks' outputs (EPI: every
-        // wave's row sums are in LDS now) and the solve of block `wave` of the
-        // next superstep.
-        for (int s = -1; s < nss; ++s) {
+        // Superstep -1 (the producers build superstep 0): only the solve of
+        // block `wave` of superstep 0.  Then per superstep, first half: its
+        // chunks one after the other; second half (after the producers'
+        // first): the chunks' outputs (EPI: every wave's row sums are in LDS
+        // now) and the solve of block `wave` of the next superstep.  Both
+        // chunks run in every superstep -- a chunk past T (T / 32 odd) is
+        // built by the producers from zero rows and leaves the state as it is,
+        // its outputs fall past T and are dropped -- so the loop body has no
+        // branch around a chunk: the compiler then counts the outstanding
+        // vector memory operations exactly and waits only for the v tile a
+        // chunk needs, not for the previous chunk's output stores.
+        auto solve_next = [&](int s) {
+            if constexpr (KN::kConsumerSolve) {
+                const int nb = NB * (s + 1) + wave;
+                if (s + 1 < nss) {
+                    ChunkOps<K>& nx = sm.set[(s + 1) & 1][wave / CB];
+                    kn.solve(wave, nb, nx.MH[wave % CB], nx.ML[wave % CB]);
+                }
+            }
+        };
+        __syncthreads();
+        solve_next(-1);
+        __syncthreads();
+        for (int s = 0; s < nss; ++s) {
 #pragma unroll
             for (int cj = 0; cj < NCH; ++cj) {
                 const int cc = NCH * s + cj;
-                if (s >= 0 && cc < ncc) {
-                    // the checkpoint of chunk cc, for the backward
-                    float* ck = CKPT && ckpt ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * ckpt_record(K, V) : nullptr;
-                    kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, colw, ck, pd[cj], wave);
-                }
+                // the checkpoint of chunk cc, for the backward
+                float* ck = CKPT && ckpt && cc < ncc ? ckpt + ((kn.b * H + kn.h) * ncc + cc) * ckpt_record(K, V)
+                                                     : nullptr;
+                kn.consume(sm.set[s & 1][cj], NB * s + CB * cj, vr[cj], vt, S, colw, ck, pd[cj], wave);
             }
             __syncthreads();
             if constexpr (EPI) {
 #pragma unroll
                 for (int cj = 0; cj < NCH; ++cj)
-                    if (s >= 0 && NCH * s + cj < ncc) kn.finish(pd[cj], colw, wave);
+                    if (NCH * s + cj < ncc) kn.finish(pd[cj], colw, wave);
             }
-            if constexpr (KN::kConsumerSolve) {
-                const int nb = NB * (s + 1) + wave;
-                if (nb < nblk) {
-                    ChunkOps<K>& nx = sm.set[(s + 1) & 1][wave / CB];
-                    kn.solve(wave, nb, nx.MH[wave % CB], nx.ML[wave % CB]);
-                }
-            }
+            solve_next(s);
             __syncthreads();
         }
         // a null state_out (the output pass of a split long sequence) keeps no final state
@@ -1394,11 +1415,12 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         kn.load_raw(raw, p);
         if constexpr (KN::kEarlyDecay) kn.decays(raw, w);
         for (int s = -1; s < nss; ++s) {
+            // every block of the supersteps, a padded chunk past T included
             const int blk = NB * (s + 1) + p;
             ChunkOps<K>& co = sm.set[(s + 1) & 1][p / CB];
-            if (blk < nblk) kn.phase1(raw, w, p, co, blk + NB);
+            if (s + 1 < nss) kn.phase1(raw, w, p, co, blk + NB);
             __syncthreads();
-            if (blk < nblk) kn.phase2(p, blk, co);
+            if (s + 1 < nss) kn.phase2(p, blk, co);
             __syncthreads();
         }
     }
