@@ -8,7 +8,8 @@ HIP kernels behind the C ABI in ``include/kda_hip.h``, and the reference's
 
 from .kda import (FP16_MAX_SAFE, KdaError, kda_chunkwise, kda_chunkwise_fused,  # noqa: F401
                   kda_chunkwise_gated, kda_recurrent, kda_recurrent_gated)
-from .layer import HeadwiseRMSNorm, KimiDeltaAttention, ShortConv, linear_attn_config  # noqa: F401
+from .layer import HeadwiseRMSNorm, KimiDeltaAttention, ShortConv, l2norm, linear_attn_config  # noqa: F401
 
 __all__ = ["kda_chunkwise", "kda_recurrent", "kda_chunkwise_gated", "kda_recurrent_gated", "kda_chunkwise_fused",
-           "KdaError", "FP16_MAX_SAFE", "KimiDeltaAttention", "ShortConv", "HeadwiseRMSNorm", "linear_attn_config"]
+           "KdaError", "FP16_MAX_SAFE", "KimiDeltaAttention", "ShortConv", "HeadwiseRMSNorm", "l2norm",
+           "linear_attn_config"]

@@ -6,8 +6,11 @@ rules -- with the core recurrence running on the gfx950 kernels of
 :mod:`kimi_linear_amd.kda`.  The projections are library GEMMs; the
 elementwise work between them and the core (short convolutions with their
 cache, SiLU, L2 norms, gates; RMSNorm and output gate) runs in the two fused
-kernels of :mod:`kimi_linear_amd.layer_ops`.  ``ShortConv`` and
-``HeadwiseRMSNorm`` below only hold parameters under the reference's names.
+kernels of :mod:`kimi_linear_amd.layer_ops`.  ``ShortConv``,
+``HeadwiseRMSNorm`` and :func:`l2norm` keep the reference's names, parameters
+and call signatures, so code that calls them directly (``layer.conv_q(x,
+conv_state, use_cache=True)``, ``layer.g_norm(o)``) keeps working; the layer
+itself never calls their forwards (it runs the fused kernels).
 
 Under grad mode with parameters or x that require grad, ``forward`` runs the
 training path (:meth:`KimiDeltaAttention._train_forward`): the same function,
@@ -55,23 +58,41 @@ from .kda import (KdaError, kda_chunkwise, kda_chunkwise_fused, kda_chunkwise_ga
 from .layer_ops import kda_output, kda_output_train, kda_prep, kda_prep_train
 
 
+def l2norm(x, eps: float):
+    """``kda.py:313-325``: x * min(rsqrt(sum x^2), 1 / eps) over the last
+    dimension, reduced in fp32 and returned in x's dtype.  For callers of the
+    reference's module-level function; the layer's own L2 norms run inside
+    the pre-processing kernel."""
+    src = x.dtype
+    xf = x.float()
+    rstd = (xf * xf).sum(-1, keepdim=True).rsqrt().clamp(max=1.0 / eps)
+    return (xf * rstd).to(src)
+
+
 class HeadwiseRMSNorm(nn.Module):
-    """Holder of the per-head RMSNorm weight ``[H, D]`` and eps
-    (``kda.py:258-279``).  The layer applies the norm inside the fused output
-    kernel (:func:`kimi_linear_amd.layer_ops.kda_output`), so this module has
-    no forward of its own; it keeps the reference's ``g_norm.weight`` key."""
+    """Per-head RMSNorm with a weight ``[H, D]`` (``kda.py:258-279``): the
+    reference's ``g_norm`` parameter and forward.  The layer applies the norm
+    inside the fused output kernel (:func:`kimi_linear_amd.layer_ops.kda_output`)
+    or the chunk kernel's epilogue; this forward serves direct callers."""
 
     def __init__(self, heads: int, dim: int, eps: float):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(heads, dim))
         self.eps = float(eps)
 
+    def forward(self, x):  # x: [B, T, H, D]
+        """x * rsqrt(mean over D of x^2 + eps) * weight in fp32, returned in x's dtype."""
+        dtype = x.dtype
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (xf * self.weight.float()).to(dtype)
+
 
 class ShortConv(nn.Module):
-    """Holder of one causal depthwise convolution's parameters
-    (``kda.py:282-310``): an ``nn.Conv1d`` named ``conv``, so the
-    ``state_dict`` keys (``conv.weight`` ``[D, 1, C]``, ``conv.bias``) match the
-    reference's.  The convolution itself, with its cache, runs inside the fused
+    """One causal depthwise convolution (``kda.py:282-310``): an ``nn.Conv1d``
+    named ``conv``, so the ``state_dict`` keys (``conv.weight`` ``[D, 1, C]``,
+    ``conv.bias``) match the reference's, and its forward for direct callers.
+    The layer runs the convolution, with its cache, inside the fused
     pre-processing kernel (:func:`kimi_linear_amd.layer_ops.kda_prep`)."""
 
     def __init__(self, dim: int, conv_size: int, bias: bool = True):
@@ -79,6 +100,23 @@ class ShortConv(nn.Module):
         self.dim = dim
         self.conv_size = conv_size
         self.conv = nn.Conv1d(dim, dim, conv_size, groups=dim, bias=bias)
+
+    def forward(self, x, conv_state=None, use_cache=False):
+        """x: [B, T, D].  Without ``use_cache``: the causal convolution (left
+        padding of conv_size - 1 zeros), [B, T, D].  With ``use_cache``: x is one
+        token [B, 1, D] and ``conv_state`` the last conv_size - 1 inputs
+        [B, conv_size - 1, D]; the window sum in fp32 (plus the bias), returned
+        in x's dtype with the new state (the window's last conv_size - 1 rows)."""
+        if use_cache:
+            window = torch.cat([conv_state, x], dim=1)
+            w = self.conv.weight.squeeze(1).t().float()            # [C, D]
+            out = (window.float() * w).sum(1)
+            if self.conv.bias is not None:
+                out = out + self.conv.bias.float()
+            new_state = window[:, 1 - self.conv_size:] if self.conv_size > 1 else window[:, :0]
+            return out.to(x.dtype).unsqueeze(1), new_state
+        xt = torch.nn.functional.pad(x.transpose(1, 2), (self.conv_size - 1, 0))
+        return self.conv(xt).transpose(1, 2)
 
 
 def linear_attn_config(**kw) -> SimpleNamespace:
