@@ -21,8 +21,7 @@ LIB_PATH = PKG_DIR / "libkda_hip.so"
 BUILD_DIR = PKG_DIR / "_build"
 
 SOURCES = ["kda_api.hip", "kda_recurrent.hip", "kda_chunkwise.hip", "kda_chunkwise_bwd.hip", "kda_layer_ops.hip",
-           "kda_layer_bwd.hip",
-           "kda_long.hip"]
+           "kda_layer_bwd.hip", "kda_long.hip", "kda_ckpt_fp32.hip"]
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the device code.
 HIPCC_FLAGS = [

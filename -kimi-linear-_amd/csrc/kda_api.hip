@@ -89,11 +89,13 @@ int chunkwise_entry(const kda_fwd_args* args, float* ckpt, const kda_gate_args* 
         // (kimi_linear/kda.py:116), and so does the token recurrence, which
         // gives the same function (the maths is chunk-size invariant) with the
         // state in fp32 registers; the chunk pipeline's operands are fp16.
-        // With checkpoints the pipeline runs first for them and the recurrence
-        // then writes o and the state.
+        // With checkpoints the recurrence also stores the fp32 state before
+        // every 32-token chunk and an fp32 kernel fills the rest of each
+        // record (R, P, A, L, N), so the backward starts from exact records.
         if (ckpt) {
-            const int st = kda::chunkwise_launch(*args, s, ckpt);
+            const int st = kda::recurrent_launch(*args, s, gate, ckpt);
             if (st != KDA_OK) return st;
+            return kda::ckpt_fill_fp32_launch(*args, s, ckpt);
         }
         return kda::recurrent_launch(*args, s, gate);
     }

@@ -9,8 +9,16 @@ namespace kda {
 
 // Token-by-token recurrence (kda_recurrent.hip).
 bool recurrent_supported(int64_t K, int64_t V);
-// gate (nullable): the fused gate of kda_recurrent_gated_fwd
-int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate = nullptr);
+// gate (nullable): the fused gate of kda_recurrent_gated_fwd; ckpt (nullable,
+// K <= 128): the chunk records of kda_chunkwise_fwd_ckpt, whose fp32 state
+// before every 32-token chunk the recurrence stores
+int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate = nullptr,
+                     float* ckpt = nullptr);
+
+// The rest of the fp32 chunk records (kda_ckpt_fp32.hip): R, P, A, L and N
+// of every 32-token chunk from the state the recurrence stored at the
+// record's head and the chunk's fp32 q, k, v, g, beta.
+int ckpt_fill_fp32_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt);
 
 // Chunkwise forward (kda_chunkwise.hip).
 bool chunkwise_supported(int64_t K, int64_t V);

@@ -22,6 +22,11 @@
 // the beta logits instead of g and beta and form, while staging the token,
 // a = exp(-exp(A_log) softplus(gk + dt_bias)) and beta = sigmoid(logit) in
 // fp32 (kimi_linear/kda.py:452-460).
+//
+// CK (the checkpointing forward of fp32 activations, kda_chunkwise_fwd_ckpt):
+// before every 32-token chunk the state is also stored, in fp32, at the head
+// of that chunk's record, so the backward starts from the exact fp32 states
+// of this recurrence (kda_ckpt_fp32.hip fills the rest of each record).
 #include "kda_common.h"
 #include "kda_launch.h"
 
@@ -53,8 +58,9 @@ __device__ __forceinline__ float lanegroup8_sum(float x) {
 // Lane l of a wave holds 4 adjacent state columns (column group l % CPL) of
 // RPL = K CPL / 64 adjacent rows (row group l / CPL); the K-reductions are
 // sums over the lanes of one column group.
-template <int K, int NW, int CPL, bool VEC>
-__global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a, const kda_gate_args gate) {
+template <int K, int NW, int CPL, bool VEC, bool CK = false>
+__global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a, const kda_gate_args gate,
+                                                            float* ckpt) {
     static_assert(CPL == 4 || CPL == 8 || CPL == 16, "column groups per wave");
     constexpr int RPL = K * CPL / 64;           // rows per lane
     constexpr int VT = 4 * CPL * NW;            // columns per workgroup
@@ -135,7 +141,18 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
         }
     }
     const float scale = a.scale;
+    // CK: the records of this (b, h), one per 32-token chunk
+    float* ckh = CK ? ckpt + (b * H + h) * ((T + 31) / 32) * ckpt_record(K, V) : nullptr;
     for (int64_t t = 0; t < T; ++t) {
+        if constexpr (CK) {
+            if (t % 32 == 0) {
+                float* rec = ckh + (t / 32) * ckpt_record(K, V);
+#pragma unroll
+                for (int j = 0; j < RPL; ++j)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) rec[static_cast<int64_t>(r0 + j) * V + col0 + c] = S[j][c];
+            }
+        }
         // ---- stage token t: q~, k, exp(g) for all K rows; v, beta per lane.
         // Every load is issued before any is decoded.
         const int64_t tq = b * a.q_stride[0] + t * a.q_stride[1] + h * a.q_stride[2];
@@ -230,32 +247,39 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(const kda_fwd_args a
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <int K, int NW, int CPL>
-int launch_k_nw(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate) {
+int launch_k_nw(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate, float* ckpt) {
     const dim3 grid(static_cast<unsigned>(a.B * a.H * (a.V / (4 * CPL * NW)))), block(64 * NW);
     const bool vec = (a.V & 3) == 0 && a.state_out_dtype == KDA_DTYPE_F32 && aligned16(a.state_out) &&
                      (a.state_in == nullptr || (a.state_in_dtype == KDA_DTYPE_F32 && aligned16(a.state_in)));
-    if (vec)
-        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, true>), grid, block, 0, stream, a, gate);
-    else
-        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, false>), grid, block, 0, stream, a, gate);
+    if (ckpt != nullptr) {
+        if constexpr (K <= 128) {
+            hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, false, true>), grid, block, 0, stream, a, gate, ckpt);
+        } else {
+            return KDA_ERR_UNSUPPORTED;
+        }
+    } else if (vec) {
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, true>), grid, block, 0, stream, a, gate, nullptr);
+    } else {
+        hipLaunchKernelGGL((recurrent_kernel<K, NW, CPL, false>), grid, block, 0, stream, a, gate, nullptr);
+    }
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
 
 template <int K>
-int launch_k(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate) {
+int launch_k(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args& gate, float* ckpt) {
     // K 128 with V % 64 == 0: one wave of 64 columns (32 rows x 4 columns a
     // lane, 196 VGPRs: the 2048 waves of a B=64 H=16 V=128 step are all
     // resident at once); other K <= 128: one wave of 32 columns (K / 8 rows x
     // 4 columns a lane); K 256: 16 columns a wave (K / 16 rows a lane).
     if constexpr (K == 128) {
-        if (a.V % 64 == 0) return launch_k_nw<K, 1, 16>(a, stream, gate);
+        if (a.V % 64 == 0) return launch_k_nw<K, 1, 16>(a, stream, gate, ckpt);
     }
     if constexpr (K <= 128) {
-        if (a.V % 32 == 0) return launch_k_nw<K, 1, 8>(a, stream, gate);
+        if (a.V % 32 == 0) return launch_k_nw<K, 1, 8>(a, stream, gate, ckpt);
     }
-    if (a.V % 64 == 0) return launch_k_nw<K, 4, 4>(a, stream, gate);
-    if (a.V % 32 == 0) return launch_k_nw<K, 2, 4>(a, stream, gate);
-    return launch_k_nw<K, 1, 4>(a, stream, gate);
+    if (a.V % 64 == 0) return launch_k_nw<K, 4, 4>(a, stream, gate, ckpt);
+    if (a.V % 32 == 0) return launch_k_nw<K, 2, 4>(a, stream, gate, ckpt);
+    return launch_k_nw<K, 1, 4>(a, stream, gate, ckpt);
 }
 
 }  // namespace
@@ -265,13 +289,13 @@ bool recurrent_supported(int64_t K, int64_t V) {
     return V % 16 == 0;
 }
 
-int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate_p) {
+int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate_p, float* ckpt) {
     const kda_gate_args gate = gate_p ? *gate_p : kda_gate_args{nullptr, nullptr};
     switch (a.K) {
-        case 32: return launch_k<32>(a, stream, gate);
-        case 64: return launch_k<64>(a, stream, gate);
-        case 128: return launch_k<128>(a, stream, gate);
-        case 256: return launch_k<256>(a, stream, gate);
+        case 32: return launch_k<32>(a, stream, gate, ckpt);
+        case 64: return launch_k<64>(a, stream, gate, ckpt);
+        case 128: return launch_k<128>(a, stream, gate, ckpt);
+        case 256: return launch_k<256>(a, stream, gate, ckpt);
         default: return KDA_ERR_UNSUPPORTED;
     }
 }

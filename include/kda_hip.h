@@ -198,7 +198,11 @@ int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* wor
  * diagonal blocks): ckpt is [B, H, ceil(T/32), KDA_CKPT_RECORD(K, V)]
  * contiguous, each record (K + 64) x V (rows [0, K) the state, [K, K + 32) R,
  * [K + 32, K + 64) P) followed by three row-major 32 x 32 matrices (the input
- * of kda_chunkwise_bwd).  Same arguments, errors and results otherwise. */
+ * of kda_chunkwise_bwd).  Same arguments, errors and results otherwise.  For
+ * fp16 / bf16 q, k, v the records come from the chunk pipeline (its fp16
+ * operands); for fp32 q, k, v from the fp32 token recurrence (the state) and
+ * an fp32 kernel (the rest, with N whole), fp32-exact like the outputs
+ * (K in {32, 64, 128}). */
 #define KDA_CKPT_RECORD(K, V) (((K) + 64) * (V) + 3 * 32 * 32)
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 

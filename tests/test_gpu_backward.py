@@ -7,9 +7,12 @@ tests/test_oracle_backward.py).  The loss is <o, W_o> + <S_T, W_S> for fixed
 random weights, so every gradient path -- through the outputs, the final
 state and the initial state -- is exercised.
 
-Tolerance: relative L2 error <= 2e-3 per gradient for fp32 inputs (the
-forward's state checkpoints come from the fp16-MFMA forward kernel, relative
-error ~1e-4), 2e-2 for fp16 and bf16 inputs (gradients rounded to that dtype).
+Tolerance: relative L2 error <= 1e-4 per gradient for fp32 inputs (their
+checkpoints are fp32-exact: the fp32 token recurrence's states and an fp32
+kernel's R, P, A, L, N; the backward's products are bf16 pairs, ~2^-17
+relative; measured 4e-6 to 2.4e-5), 2e-2 for fp16 and bf16 inputs (the
+checkpoints come from the fp16-operand chunk pipeline and the gradients are
+rounded to that dtype; measured ~3e-4).
 """
 
 from __future__ import annotations
@@ -82,7 +85,7 @@ def test_backward_fp32(kda_pkg, wl, B, T, H, K, V, chunk, state):
         assert a.dtype == xs[NAMES.index(name)].dtype and a.shape == r.shape
         err = _rel(a, r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
-        assert err <= 2e-3, (name, err)
+        assert err <= 1e-4, (name, err)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -114,7 +117,7 @@ def test_backward_state_only_loss(kda_pkg, wl):
             assert a.grad is None or not a.grad.any(), name
             continue
         err = _rel(a.grad, r.grad)
-        assert err <= 2e-3, (name, err)
+        assert err <= 1e-4, (name, err)
 
 
 def test_backward_matches_eager_chaining(kda_pkg, wl):
@@ -146,7 +149,7 @@ def test_backward_long_sequence(kda_pkg, wl, H, K, V, dtype):
     xs, wo, ws = _case(wl, B, T, H, K, V, seed=300 + K, dtype=dtype, state=True)
     ref = _ref_grads(xs, wo, ws, 16)
     got = _native_grads(kda_pkg, xs, wo, ws, 64)
-    tol = 2e-3 if dtype == torch.float32 else 2e-2
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
     for name, a, r in zip(NAMES, got, ref):
         err = _rel(a, r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
@@ -201,7 +204,7 @@ def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl, B, K, V, dtype):
             err = _rel(a[b:b + 1], r)
             assert err <= 1e-6, (b, name, err)
     ref = _ref_grads([x[:1] for x in xs], wo[:1], ws[:1], 32)
-    tol = 2e-3 if dtype == torch.float32 else 2e-2
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
     for name, a, r in zip(NAMES, wide, ref):
         err = _rel(a[:1], r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
@@ -238,7 +241,7 @@ def test_recurrent_backward(kda_pkg, wl, B, T, H, K, V, dtype, state):
     xs, wo, ws = _case(wl, B, T, H, K, V, seed=200 + T, dtype=dtype, state=state)
     ref = _ref_rec_grads(xs, wo, ws)
     got = _native_rec_grads(kda_pkg, xs, wo, ws)
-    tol = 2e-3 if dtype == torch.float32 else 2e-2
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
     for name, x, a, r in zip(NAMES, xs, got, ref):
         if r is None:
             assert a is None

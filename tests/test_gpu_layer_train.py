@@ -5,10 +5,10 @@ CPU (the oracle's forward is pinned by the reference fixtures; its gradient
 is autograd's).
 
 Tolerances, relative L2 error of each gradient: fp32 inputs 1e-4 for the
-kernels (1e-3 for the layer, whose core backward reads checkpoints computed
-with fp16 operands; measured 3e-4), fp16 4e-3 (5e-3 for the layer, measured
-9e-4), bf16 2e-2 (2e-2, measured 7e-3): the 16-bit paths round every
-activation, and the upstream gradients, to 11 or 8 bits.
+kernels (2e-4 for the layer: its fp32 core checkpoints are exact and the
+parameter gradients sum over every token; measured <= 6e-5), fp16 4e-3 (5e-3
+for the layer, measured 9e-4), bf16 2e-2 (2e-2, measured 7e-3): the 16-bit
+paths round every activation, and the upstream gradients, to 11 or 8 bits.
 """
 
 from __future__ import annotations
@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
 TOL_K = {torch.float32: 1e-4, torch.float16: 4e-3, torch.bfloat16: 2e-2}
-TOL_L = {torch.float32: 1e-3, torch.float16: 5e-3, torch.bfloat16: 2e-2}
+TOL_L = {torch.float32: 2e-4, torch.float16: 5e-3, torch.bfloat16: 2e-2}
 
 
 def rel(a, b):
