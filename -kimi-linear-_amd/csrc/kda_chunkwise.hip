@@ -76,6 +76,17 @@
 // outputs take as operands, are split into fp16 hi + lo; S (in Z and O) and
 // R = V - Z enter their products as single fp16 operands (rounded once per
 // chunk), like q * E, k * E and A.
+//
+// Range (bf16 activations): the state, V, R and P pass through fp16 operands,
+// whose range ends at 65504, while bf16 values reach 3e38.  The chain is
+// linear in (V, S), so each consumer wave carries its state scaled by a power
+// of two sigma (exact): before a chunk it takes the largest |sigma S| and
+// |sigma V| of its columns and, when that passes 2^10 (headroom for Z = (k*E)
+// S and P = M R), divides sigma by the power of two that brings it back
+// under; outputs, checkpoints and the final state are divided by sigma.  With
+// values under 2^10 sigma stays 1 and nothing changes.  fp16 activations keep
+// the fp16 range, as the reference's fp16 path does (it casts the state to
+// the input dtype for its products, kimi_linear/kda.py:174).
 #include <type_traits>
 
 #include "kda_common.h"
@@ -948,6 +959,9 @@ struct Kern {
     // per lane and row set; rows past T read as zero.
     static constexpr int VW = sizeof(TQ) == 2 ? 4 : 8;
     bool vzero = false;                      // TRANS: this wave's columns read v = 0
+    // RANGE (bf16 activations): the wave's power-of-two state scale sigma and 1 / sigma
+    static constexpr bool RANGE = Elem<TQ>::code == KDA_DTYPE_BF16;
+    mutable float sig = 1.f, isig = 1.f;
     __device__ void v_load(uint32_t (&vr)[VW], int chunk, int grp) const {
         if (TRANS && vzero) {
 #pragma unroll
@@ -1106,6 +1120,39 @@ struct Kern {
             v_tile(vraw[g], vt, R[g][0], R[g][1]);
             v_load(vraw[g], blk / CB + NCH, g);
         }
+        if constexpr (RANGE) {
+            // the wave's largest |sigma S| and |V| (R holds V here), then
+            // sigma / 2^k when sigma times it passes 2^10
+            float ms = 0.f, mv = 0.f;
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+#pragma unroll
+                for (int t = 0; t < KT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) ms = fmaxf(ms, fabsf(S[g][t][j]));
+#pragma unroll
+                for (int bk = 0; bk < CB; ++bk)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) mv = fmaxf(mv, fabsf(R[g][bk][j]));
+            }
+            const float m = wave_max(fmaxf(ms, mv * sig));
+            if (m > kRangeMax) {
+                // m = 2^e x 1.f: dividing by 2^(e - 9) leaves it under 2^10
+                const int k = static_cast<int>((__float_as_uint(m) >> 23) & 0xffu) - 127 - 9;
+                const float f = __uint_as_float(static_cast<uint32_t>(127 - k) << 23);
+#pragma unroll
+                for (int g = 0; g < CG; ++g)
+#pragma unroll
+                    for (int t = 0; t < KT; ++t) S[g][t] *= f;
+                sig *= f;
+                isig = 1.f / sig;
+            }
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+                R[g][0] *= sig;
+                R[g][1] *= sig;
+            }
+        }
         const int64_t V = a.V;
         if (ck) {
 #pragma unroll
@@ -1114,7 +1161,8 @@ struct Kern {
                 for (int t = 0; t < KT; ++t)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        __builtin_nontemporal_store(S[g][t][j], &ck[(4 * lg + 16 * t + j) * V + colw + 16 * g + ln]);
+                        __builtin_nontemporal_store(RANGE ? S[g][t][j] * isig : S[g][t][j],
+                                                    &ck[(4 * lg + 16 * t + j) * V + colw + 16 * g + ln]);
         }
         float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
@@ -1165,8 +1213,8 @@ struct Kern {
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    __builtin_nontemporal_store(R[g][0][j], &rp[(4 * lg + j) * V + rc]);
-                    __builtin_nontemporal_store(R[g][1][j], &rp[(16 + 4 * lg + j) * V + rc]);
+                    __builtin_nontemporal_store(RANGE ? R[g][0][j] * isig : R[g][0][j], &rp[(4 * lg + j) * V + rc]);
+                    __builtin_nontemporal_store(RANGE ? R[g][1][j] * isig : R[g][1][j], &rp[(16 + 4 * lg + j) * V + rc]);
                 }
             }
             const h4 r0 = to_h4(R[g][0]);
@@ -1179,8 +1227,8 @@ struct Kern {
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    __builtin_nontemporal_store(P0[j], &rp[(32 + 4 * lg + j) * V + rc]);
-                    __builtin_nontemporal_store(P1[j], &rp[(48 + 4 * lg + j) * V + rc]);
+                    __builtin_nontemporal_store(RANGE ? P0[j] * isig : P0[j], &rp[(32 + 4 * lg + j) * V + rc]);
+                    __builtin_nontemporal_store(RANGE ? P1[j] * isig : P1[j], &rp[(48 + 4 * lg + j) * V + rc]);
                 }
             }
             // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is
@@ -1191,6 +1239,11 @@ struct Kern {
             O[g][0] = mfma16x16x32(cat(p0.hi, p0.lo), cat(a00, a00), O[g][0]);
             O[g][1] = mfma16x16x32(cat(p0.hi, p1.hi), a1, O[g][1]);
             O[g][1] = mfma16x16x32(cat(p0.lo, p1.lo), a1, O[g][1]);
+            if constexpr (RANGE) {
+                // both terms came from the sigma-scaled state and R
+                O[g][0] *= isig;
+                O[g][1] *= isig;
+            }
             ph[g] = cat(p0.hi, p1.hi);
             pl[g] = cat(p0.lo, p1.lo);
         }
@@ -1395,6 +1448,12 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         }
         // a null state_out (the output pass of a split long sequence) keeps no final state
         if (a.state_out != nullptr) {
+            if constexpr (KN::RANGE) {
+#pragma unroll
+                for (int g = 0; g < CG; ++g)
+#pragma unroll
+                    for (int t = 0; t < KT; ++t) S[g][t] *= kn.isig;
+            }
 #pragma unroll
             for (int g = 0; g < CG; ++g)
                 store_state<KT>(S[g], a.state_out, a.state_out_dtype, sbase + (4 * kn.lg) * VS + colw + 16 * g + kn.ln,
@@ -1512,10 +1571,9 @@ int launch_k(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_g
         case KDA_DTYPE_F16: return launch_kq<K, _Float16, GATED>(a, stream, ckpt, gate);
         case KDA_DTYPE_BF16: return launch_kq<K, bf16_t, GATED>(a, stream, ckpt, gate);
         case KDA_DTYPE_F32:
-            // fp32 activations take the token recurrence (gated or not); the
-            // pipeline's fp32 instantiation serves the backward's checkpoints
-            if constexpr (GATED) return KDA_ERR_BAD_DTYPE;
-            else return launch_kq<K, float, false>(a, stream, ckpt, gate);
+            // fp32 activations take the token recurrence (gated or not), with
+            // fp32 checkpoints too (kda_ckpt_fp32.hip): no fp32 pipeline
+            return KDA_ERR_BAD_DTYPE;
         default: return KDA_ERR_BAD_DTYPE;
     }
 }

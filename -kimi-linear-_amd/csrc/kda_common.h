@@ -186,6 +186,29 @@ __device__ __forceinline__ float lanegroup4_sum(float x) {
     return x;
 }
 
+// Largest x over the whole wave (every lane gets it): the lanes of each
+// 16-lane row by DPP rotations, then the permlane swaps of bits 4 and 5.
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xF, 0xF, false)));  // row_ror:1
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xF, 0xF, false)));  // row_ror:2
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false)));  // row_ror:4
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false)));  // row_ror:8
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    {
+        const unsigned u = __float_as_uint(x);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    return x;
+}
+// The bf16 chunk pipeline keeps |sigma S| and |sigma V| of a wave at most this
+// (a power of two), 64 x under the fp16 operands' 65504.
+constexpr float kRangeMax = 1024.f;
+
 // Sum of x over the whole wave (every lane gets it): the four lanes of each
 // quad first (quad_perm xor 1, xor 2), then the 16 quads.
 __device__ __forceinline__ float wave_sum(float x) {

@@ -65,6 +65,12 @@ def dev(inp):
     return {n: (t.to(DEV) if t is not None else None) for n, t in inp.items()}
 
 
+def o_bar(dtype, o_ref):
+    """O_TOL, plus one bf16 ulp of the largest output for bf16 (both outputs
+    are rounded to bf16, 3 mantissa bits fewer than fp16)."""
+    return O_TOL + (2.0 ** -7 * float(o_ref.float().abs().max()) if dtype == torch.bfloat16 else 0.0)
+
+
 def oracle_gates(inp):
     return gates_ref(inp["gk"], inp["logit"], inp["a_log"], inp["dt_bias"])
 
@@ -88,9 +94,7 @@ def test_chunkwise_gated_matches_oracle(kda_pkg, dtype, B, T, H, state):
                                      chunk_size=C, state_dtype=torch.float32)
     eo, es = max_abs(o, o_ref), rel(s, s_ref)
     print(f"gated chunkwise {dtype} B={B} T={T} H={H}: o max-abs {eo:.2e} state rel {es:.2e}", flush=True)
-    o_tol = O_TOL if dtype == torch.float16 else 8 * O_TOL      # bf16 carries 3 fewer mantissa bits
-    s_tol = S_TOL if dtype == torch.float16 else 8 * S_TOL
-    assert eo <= o_tol and es <= s_tol, (eo, es)
+    assert eo <= o_bar(dtype, o_ref) and es <= S_TOL, (eo, es)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -118,8 +122,6 @@ def test_chunkwise_gated_wide_launches_match_oracle(kda_pkg, dtype, B, T):
                                              state_dtype=torch.float32)
     assert torch.equal(o[B - 1:B], o1) and torch.equal(s[B - 1:B], s1)
     g, beta = oracle_gates(inp)
-    o_tol = O_TOL if dtype == torch.float16 else 8 * O_TOL
-    s_tol = S_TOL if dtype == torch.float16 else 8 * S_TOL
     for b, h in ((0, 0), (B // 2, 7), (B - 1, 15)):
         sl = lambda t: t[b:b + 1, :, h:h + 1]  # noqa: E731
         o_ref, s_ref = kda_chunkwise_ref(sl(inp["q"]), sl(inp["k"]), sl(inp["v"]), sl(g),
@@ -127,7 +129,7 @@ def test_chunkwise_gated_wide_launches_match_oracle(kda_pkg, dtype, B, T):
                                          chunk_size=C, state_dtype=torch.float32)
         eo, es = max_abs(o[b:b + 1, :, h:h + 1], o_ref), rel(s[b:b + 1, h:h + 1], s_ref)
         print(f"  b={b} h={h}: o max-abs {eo:.2e} state rel {es:.2e}", flush=True)
-        assert eo <= o_tol and es <= s_tol, (b, h, eo, es)
+        assert eo <= o_bar(dtype, o_ref) and es <= S_TOL, (b, h, eo, es)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

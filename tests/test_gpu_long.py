@@ -98,9 +98,10 @@ def test_long_split_matches_oracle_and_one_pass(kda_pkg, wl, native, K, dtype, s
     d_o, d_s = rel(o, o1), rel(s, s1)
     print(f"  vs oracle: o max-abs {eo:.2e} state rel {es:.2e}; vs one pass: o {d_o:.2e} state {d_s:.2e}",
           flush=True)
-    tol = 1 if dtype == torch.float16 else 8
-    assert eo <= tol * O_TOL and es <= tol * S_TOL
-    assert d_o <= tol * 1e-3 and d_s <= tol * 1e-3
+    # bf16: one output ulp (2^-7 of the largest output) on top of the fp16 bars
+    o_tol = O_TOL + (2.0 ** -7 * float(o_ref.float().abs().max()) if dtype == torch.bfloat16 else 0.0)
+    assert eo <= o_tol and es <= S_TOL
+    assert d_o <= (1e-3 if dtype == torch.float16 else 4e-3) and d_s <= 1e-3
 
 
 def test_long_split_zero_inputs_carry_the_state(kda_pkg, wl, native):
