@@ -332,11 +332,15 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
     const int dv_ = t % VA, dc0 = DPT * (t / VA);
     const uint32_t lo_o = static_cast<uint32_t>(dc0) * HV + dv_;
     const int ai = t % CT, ac0 = APT * (t / CT);
+    // Every fetch is a buffer load through a descriptor whose range ends at
+    // the chunk's last row before T and is empty for n < 0 (the loop fetches
+    // chunk -1 after chunk 0: all zeros, nothing read), issued without a
+    // branch, from descriptors held in scalar registers.
     auto fetch = [&](int n) {
-        const int64_t r0 = static_cast<int64_t>(n) * CT;
-        const int64_t nrow = std::min<int64_t>(CT, T - r0);
+        const int64_t r0 = static_cast<int64_t>(n < 0 ? 0 : n) * CT;
+        const int64_t nrow = n < 0 ? 0 : std::min<int64_t>(CT, T - r0);
         const int64_t base = ((b * T + r0) * H + h) * K;
-        const uint32_t span = static_cast<uint32_t>((nrow - 1) * H * K + K);
+        const uint32_t span = nrow > 0 ? static_cast<uint32_t>((nrow - 1) * H * K + K) : 0u;
         const auto rq = make_rsrc(qp + base, span * SZ), rk = make_rsrc(kp + base, span * SZ);
         const auto rgc = make_rsrc(a.g + base, span * 4);
 #pragma unroll
@@ -351,8 +355,8 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             }
             pg[j] = __builtin_amdgcn_raw_buffer_load_b32(rgc, static_cast<int>(4 * lo_x), static_cast<int>(4 * so), 0);
         }
-        const auto ro = make_rsrc(dop + ((b * T + r0) * H + h) * V + v0,
-                                  static_cast<uint32_t>(((nrow - 1) * H * V + VA) * SZ));
+        const auto ro = make_rsrc_uniform(dop + ((b * T + r0) * H + h) * V + v0,
+                                  nrow > 0 ? static_cast<uint32_t>(((nrow - 1) * H * V + VA) * SZ) : 0u);
 #pragma unroll
         for (int j = 0; j < DPT; ++j) {
             const uint32_t so = static_cast<uint32_t>(j) * HV * SZ;
@@ -361,14 +365,18 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             else
                 pdo[j] = __builtin_amdgcn_raw_buffer_load_b32(ro, static_cast<int>(4 * lo_o), static_cast<int>(so), 0);
         }
-        const float* an = ws.A + (bh * nck + n) * ws.ms;
-        const float* nn = ws.N + (bh * nck + n) * CT * CT;
+        const int64_t cn = bh * nck + r0 / CT;
+        const auto ra = make_rsrc(ws.A + cn * ws.ms, n < 0 ? 0u : static_cast<uint32_t>(CT * CT * 4));
+        const auto rn = make_rsrc(ws.N + cn * CT * CT, n < 0 ? 0u : static_cast<uint32_t>(CT * CT * 4));
 #pragma unroll
         for (int j = 0; j < APT; ++j) {
-            pa[j] = __float_as_uint(an[(ac0 + j) * CT + ai]);
-            pn[j] = __float_as_uint(nn[(ac0 + j) * CT + ai]);
+            const int off = ((ac0 + j) * CT + ai) * 4;
+            pa[j] = __builtin_amdgcn_raw_buffer_load_b32(ra, off, 0, 0);
+            pn[j] = __builtin_amdgcn_raw_buffer_load_b32(rn, off, 0, 0);
         }
-        if (t < CT) pb[0] = r0 + t < T ? __float_as_uint(a.beta[(b * T + r0 + t) * H + h]) : 0u;
+        // beta of row t % CT on every thread (threads t < CT stage it)
+        const auto rb = make_rsrc(a.beta + (b * T + r0) * H + h, static_cast<uint32_t>(nrow * H * 4));
+        pb[0] = __builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<int>((t % CT) * H * 4), 0, 0);
     };
     if (nck > 0) fetch(nck - 1);
 
@@ -406,7 +414,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             put_pairs(&sm.dOT[0][dv_][dc0], &sm.dOT[1][dv_][dc0], vo);
         }
         if (t < CT) sm.beta[t] = __uint_as_float(pb[0]);
-        if (n > 0) fetch(n - 1);
+        fetch(n - 1);
         __syncthreads();
 
         // G, exp(G), exp(G_last - G): the row groups before this thread's and all of them

@@ -235,6 +235,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              static_cast<int>(nbytes), 0x00020000);
 }
 
+// The same descriptor from values the compiler keeps in vector registers
+// (64-bit index arithmetic it hoists out of a loop ends up there): a buffer
+// instruction needs its descriptor in scalar registers, and a vector-register
+// one becomes a loop over the distinct values in the wave, whose control flow
+// also makes every later wait on it a wait for all outstanding memory
+// operations.  The caller guarantees the values are wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_uniform(const void* base, uint32_t nbytes) {
+    const uint64_t u = reinterpret_cast<uint64_t>(base);
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u)));
+    const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32)));
+    return make_rsrc(reinterpret_cast<const void*>(hi << 32 | lo),
+                     static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(nbytes))));
+}
+
 // Values are held raw, one load per register set, and converted only where
 // they are used.  Left alone, the compiler hoists a conversion up to the
 // load, which puts a wait for the whole prefetch right after it is issued.
