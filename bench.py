@@ -386,13 +386,19 @@ def backward_bench(pkg, wl, torch, reps=3):
             fwd += e0.elapsed_time(e1) / reps
             bwd += e1.elapsed_time(e2) / reps
     nbytes = backward_bytes(B1, T1, H1, D1, D1, 2)
+    # the gradient's own I/O per (token, head): q, k, v, dO (2 B) and g (4 B) per
+    # channel and beta read; dq, dk, dv (2 B), dg (4 B) per channel and dbeta written
+    io = B1 * T1 * H1 * (4 * 2 * D1 + 4 * D1 + 4 + 3 * 2 * D1 + 4 * D1 + 4)
     return {"workload": "kda_chunkwise forward (with 32-token checkpoints: state, R, P) + native backward under "
                         "autograd, B=8 T=4096 H=16 dk=dv=128; fp16 q/k/v, fp32 g/beta",
             "forward_ckpt_ms": fwd, "backward_ms": bwd,
             "train_tokens_per_s": B1 * T1 / ((fwd + bwd) * 1e-3),
-            # the three backward kernels' algorithmic HBM bytes over the backward's
-            # wall time (autograd's own work included)
-            "backward_bytes": nbytes, "backward_hbm_frac": nbytes / (bwd * 1e-3) / (HBM_PEAK_GBS * 1e9)}
+            # the gradient I/O over the backward's wall time (autograd's own work
+            # included): the backward's roofline fraction as a function
+            "gradient_io_bytes": io, "backward_hbm_frac": io / (bwd * 1e-3) / (HBM_PEAK_GBS * 1e9),
+            # the bytes this implementation moves (its workspace and the forward's
+            # checkpoint records read back included) over the same time
+            "backward_bytes": nbytes, "backward_bytes_hbm_frac": nbytes / (bwd * 1e-3) / (HBM_PEAK_GBS * 1e9)}
 
 
 def backward_bytes(B, T, H, K, V, sz):

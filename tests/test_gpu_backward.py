@@ -10,9 +10,10 @@ state and the initial state -- is exercised.
 Tolerance: relative L2 error <= 1e-4 per gradient for fp32 inputs (their
 checkpoints are fp32-exact: the fp32 token recurrence's states and an fp32
 kernel's R, P, A, L, N; the backward's products are bf16 pairs, ~2^-17
-relative; measured 4e-6 to 2.4e-5), 2e-2 for fp16 and bf16 inputs (the
-checkpoints come from the fp16-operand chunk pipeline and the gradients are
-rounded to that dtype; measured ~3e-4).
+relative; measured 4e-6 to 2.4e-5), 2e-3 for fp16 inputs and 1e-2 for bf16
+inputs (the checkpoints come from the fp16-operand chunk pipeline and the
+gradients are rounded to that dtype, 2^-11 and 2^-8 relative; measured
+~3.2e-4 and ~2.3e-3).
 """
 
 from __future__ import annotations
@@ -26,6 +27,10 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
 NAMES = ("q", "k", "v", "g", "beta", "s0")
+
+
+def _tol(dtype):
+    return {torch.float32: 1e-4, torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
 
 
 def _rel(a, b):
@@ -99,7 +104,7 @@ def test_backward_half(kda_pkg, wl, dtype):
     for name, a, r in zip(NAMES, got, ref):
         err = _rel(a, r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
-        assert err <= 2e-2, (name, err)
+        assert err <= _tol(dtype), (name, err)
 
 
 def test_backward_state_only_loss(kda_pkg, wl):
@@ -149,7 +154,7 @@ def test_backward_long_sequence(kda_pkg, wl, H, K, V, dtype):
     xs, wo, ws = _case(wl, B, T, H, K, V, seed=300 + K, dtype=dtype, state=True)
     ref = _ref_grads(xs, wo, ws, 16)
     got = _native_grads(kda_pkg, xs, wo, ws, 64)
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    tol = _tol(dtype)
     for name, a, r in zip(NAMES, got, ref):
         err = _rel(a, r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
@@ -204,7 +209,7 @@ def test_backward_wide_launch_matches_per_sequence(kda_pkg, wl, B, K, V, dtype):
             err = _rel(a[b:b + 1], r)
             assert err <= 1e-6, (b, name, err)
     ref = _ref_grads([x[:1] for x in xs], wo[:1], ws[:1], 32)
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    tol = _tol(dtype)
     for name, a, r in zip(NAMES, wide, ref):
         err = _rel(a[:1], r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
@@ -241,7 +246,7 @@ def test_recurrent_backward(kda_pkg, wl, B, T, H, K, V, dtype, state):
     xs, wo, ws = _case(wl, B, T, H, K, V, seed=200 + T, dtype=dtype, state=state)
     ref = _ref_rec_grads(xs, wo, ws)
     got = _native_rec_grads(kda_pkg, xs, wo, ws)
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    tol = _tol(dtype)
     for name, x, a, r in zip(NAMES, xs, got, ref):
         if r is None:
             assert a is None
@@ -281,4 +286,4 @@ def test_recurrent_backward_fp16_clamp(kda_pkg, wl):
     for name, a, r in zip(NAMES[:5], got, ref):
         err = _rel(a, r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
-        assert err <= 2e-2, (name, err)
+        assert err <= _tol(torch.float16), (name, err)

@@ -6,9 +6,10 @@ is autograd's).
 
 Tolerances, relative L2 error of each gradient: fp32 inputs 1e-4 for the
 kernels (2e-4 for the layer: its fp32 core checkpoints are exact and the
-parameter gradients sum over every token; measured <= 6e-5), fp16 4e-3 (5e-3
-for the layer, measured 9e-4), bf16 2e-2 (2e-2, measured 7e-3): the 16-bit
-paths round every activation, and the upstream gradients, to 11 or 8 bits.
+parameter gradients sum over every token; measured <= 6e-5), fp16 1e-3 for the
+kernels (measured <= 2.9e-4) and 2e-3 for the layer (measured <= 9.1e-4), bf16
+6e-3 (measured <= 2.4e-3) and 1.5e-2 (measured <= 6.7e-3): the 16-bit paths
+round every activation, and the upstream gradients, to 11 or 8 bits.
 """
 
 from __future__ import annotations
@@ -22,8 +23,8 @@ from oracle.kda_layer_oracle import (gates_ref, head_rmsnorm_ref, kda_layer_ref,
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
-TOL_K = {torch.float32: 1e-4, torch.float16: 4e-3, torch.bfloat16: 2e-2}
-TOL_L = {torch.float32: 2e-4, torch.float16: 5e-3, torch.bfloat16: 2e-2}
+TOL_K = {torch.float32: 1e-4, torch.float16: 1e-3, torch.bfloat16: 6e-3}
+TOL_L = {torch.float32: 2e-4, torch.float16: 2e-3, torch.bfloat16: 1.5e-2}
 
 
 def rel(a, b):
