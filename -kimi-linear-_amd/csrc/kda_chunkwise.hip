@@ -1542,10 +1542,14 @@ int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_
     // (the producers' chain sets it) and ~10 % longer in a 128-column one
     // (consumer waves of two 16-column groups; 16-bit inputs only, the fp32
     // instantiation serves checkpoints), so the time is about rounds of
-    // workgroups x that factor: pick the cheapest, the narrower tile on a tie
-    // (measured at T=2048 H=16 d=128, gated, one round against 1.5-2: B=3
-    // 178 against 348 us, B=6 182 against 350 us; B=16 220 us in 128-column
-    // workgroups against 368 us in two rounds of 64-column ones).
+    // workgroups x that factor: pick the cheapest (measured at T=2048 H=16
+    // d=128, gated, one round against 1.5-2: B=3 178 against 348 us, B=6 182
+    // against 350 us; B=16 220 us in 128-column workgroups against 368 us in
+    // two rounds of 64-column ones).  On a tie the wider tile wins: the
+    // 64-column one's four consumer waves take the inverse of (I + L) off the
+    // producers' chain, which fewer consumer waves leave there (B=3 and B=4:
+    // 149 against 157-158 us plain, 174 against 180 us gated in 32-column
+    // workgroups; B=1 and B=2 equal to 16-column ones).
     const int64_t w1 = a.V % 16 == 0 ? heads * (a.V / 16) : 0;
     const int64_t w2 = a.V % 32 == 0 ? heads * (a.V / 32) : 0;
     const int64_t w4 = a.V % 64 == 0 ? heads * (a.V / 64) : 0;
@@ -1554,8 +1558,8 @@ int launch_kq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_
     auto cost = [&](int64_t wgs, int64_t tenths) { return ((wgs + kCus - 1) / kCus) * tenths; };
     int best = 1;
     int64_t best_cost = cost(w1, 10);
-    if (w2 > 0 && cost(w2, 10) < best_cost) best = 2, best_cost = cost(w2, 10);
-    if (w4 > 0 && cost(w4, 10) < best_cost) best = 4, best_cost = cost(w4, 10);
+    if (w2 > 0 && cost(w2, 10) <= best_cost) best = 2, best_cost = cost(w2, 10);
+    if (w4 > 0 && cost(w4, 10) <= best_cost) best = 4, best_cost = cost(w4, 10);
     if (w8 > 0 && cost(w8, 11) < best_cost) best = 8, best_cost = cost(w8, 11);
     if constexpr (sizeof(TQ) == 2) {
         if (best == 8) return go(I4{}, I2{});

@@ -79,9 +79,9 @@ def oracle_gates(inp):
 @pytest.mark.parametrize("B,T,H,state", [(2, 256, 4, False), (1, 192, 2, True), (4, 128, 16, False),
                                          (1, 100, 2, True), (2, 10, 3, True)])
 def test_chunkwise_gated_matches_oracle(kda_pkg, dtype, B, T, H, state):
-    """(4, 128, 16): 64 chains of 64 columns -> the 32-column (NC = 2) kernel;
-    the others the 16-column one.  T = 100 and 10 end in a partial block,
-    whose padded rows must leave the state alone (chunk_size = T there)."""
+    """V = 128 in one round of workgroups: the 64-column (NC = 4) kernel.
+    T = 100 and 10 end in a partial block, whose padded rows must leave the
+    state alone (chunk_size = T there)."""
     K = V = 128
     C = 64 if T % 64 == 0 else T
     inp = make(B, T, H, K, V, dtype, seed=1, state_std=0.05 if state else None)
@@ -94,6 +94,28 @@ def test_chunkwise_gated_matches_oracle(kda_pkg, dtype, B, T, H, state):
                                      chunk_size=C, state_dtype=torch.float32)
     eo, es = max_abs(o, o_ref), rel(s, s_ref)
     print(f"gated chunkwise {dtype} B={B} T={T} H={H}: o max-abs {eo:.2e} state rel {es:.2e}", flush=True)
+    assert eo <= o_bar(dtype, o_ref) and es <= S_TOL, (eo, es)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K,V,T", [(64, 96, 128), (128, 32, 100), (64, 16, 64)])
+def test_chunkwise_gated_narrow_tiles_match_oracle(kda_pkg, dtype, K, V, T):
+    """V not a multiple of 64: 32-column (NC = 2: V = 96, 32) and 16-column
+    (NC = 1: V = 16) workgroups, whose producer waves also take the inverse
+    of (I + L); T = 100 ends in a partial block."""
+    B, H = 2, 4
+    C = 64 if T % 64 == 0 else T
+    inp = make(B, T, H, K, V, dtype, seed=7 + V, state_std=0.05)
+    d = dev(inp)
+    with torch.no_grad():
+        o, s = kda_pkg.kda_chunkwise_gated(d["q"], d["k"], d["v"], d["gk"], d["logit"], d["a_log"], d["dt_bias"],
+                                           initial_state=d["state"], chunk_size=C, state_dtype=torch.float32)
+    g, beta = oracle_gates(inp)
+    o_ref, s_ref = kda_chunkwise_ref(inp["q"], inp["k"], inp["v"], g, beta, initial_state=inp["state"],
+                                     chunk_size=C, state_dtype=torch.float32)
+    eo, es = max_abs(o, o_ref), rel(s, s_ref)
+    print(f"gated chunkwise narrow tiles {dtype} K={K} V={V} T={T}: o max-abs {eo:.2e} state rel {es:.2e}",
+          flush=True)
     assert eo <= o_bar(dtype, o_ref) and es <= S_TOL, (eo, es)
 
 

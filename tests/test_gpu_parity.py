@@ -200,10 +200,8 @@ def test_config1_chunk_size_invariance(kda_pkg, cfg1):
 @pytest.mark.parametrize("B,H,T", [(4, 16, 512), (2, 8, 128), (6, 16, 256)])
 def test_chunkwise_mid_head_counts(kda_pkg, wl, B, H, T):
     """64, 16 and 96 (batch, head) chains: the launch picks the column tile by
-    rounds of workgroups (32 columns a workgroup at 64 chains, 16 at 16
-    chains, 64 at 96 chains: 192 workgroups in one round rather than 384
-    32-column ones), each instantiation must agree with the oracle on every
-    head."""
+    rounds of workgroups, the 64-column one on a tie (one round at 64, 16 and
+    96 chains: 128, 32 and 192 workgroups); every head against the oracle."""
     print(f"chunkwise B={B} H={H} T={T} K=V=128 fp16", flush=True)
     inp = wl.make_inputs(B, T, H, 128, 128, seed=B * 100 + H, qkv_dtype=torch.float16, state_std=0.02)
     o, s = run_chunkwise(kda_pkg, to_dev(inp), 64)
