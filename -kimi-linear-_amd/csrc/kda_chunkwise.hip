@@ -1155,16 +1155,45 @@ struct Kern {
         }
         const int64_t V = a.V;
         if (ck) {
+            if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+                // fp16 in accumulator-order tiles (half_tile_offset): slot j
+                // of tile (t, column group) is 64 consecutive halves, the
+                // values the products above take as their fp16 state
+                // (the tile offsets are wave-uniform: scalar offsets of a
+                // buffer store, so no per-tile address is kept in registers)
+                const auto rs = make_rsrc(ck, static_cast<uint32_t>(K * V * 2));
+                const int lo = 2 * (16 * lg + ln);
 #pragma unroll
-            for (int g = 0; g < CG; ++g)
+                for (int g = 0; g < CG; ++g)
 #pragma unroll
-                for (int t = 0; t < KT; ++t)
+                    for (int t = 0; t < KT; ++t)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        __builtin_nontemporal_store(RANGE ? S[g][t][j] * isig : S[g][t][j],
-                                                    &ck[(4 * lg + 16 * t + j) * V + colw + 16 * g + ln]);
+                        for (int j = 0; j < 4; ++j)
+                            __builtin_amdgcn_raw_buffer_store_b16(
+                                __builtin_bit_cast(uint16_t, static_cast<_Float16>(S[g][t][j])), rs, lo,
+                                static_cast<int>(2 * (half_tile_offset(16 * t, colw + 16 * g, V) + 64 * j)), 2);
+            } else {
+#pragma unroll
+                for (int g = 0; g < CG; ++g)
+#pragma unroll
+                    for (int t = 0; t < KT; ++t)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            __builtin_nontemporal_store(RANGE ? S[g][t][j] * isig : S[g][t][j],
+                                                        &ck[(4 * lg + 16 * t + j) * V + colw + 16 * g + ln]);
+            }
         }
         float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
+        // R and P rows through one buffer resource: the lane's part of the
+        // offset in a vector register, the row and column group's
+        // (wave-uniform) part in the scalar offset -- no 64-bit address per
+        // store kept in registers
+        const auto rr = make_rsrc(rp, static_cast<uint32_t>(2 * CB * BT * V * 4));
+        const int rlo = static_cast<int>((4 * lg * V + ln) * 4);
+        auto rp_store = [&](float x, int row, int g) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rr, rlo,
+                                                  static_cast<int>((row * V + colw + 16 * g) * 4), 2);
+        };
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
         // the same fragments as A and B operands the other way round, so that
         // a lane holds four adjacent output columns of one row.  Block 1's
@@ -1207,14 +1236,13 @@ struct Kern {
         h8 ph[CG], pl[CG];
 #pragma unroll
         for (int g = 0; g < CG; ++g) {
-            const int64_t rc = colw + 16 * g + ln;
             R[g][0] -= Z[g][0];
             R[g][1] -= Z[g][1];
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    __builtin_nontemporal_store(RANGE ? R[g][0][j] * isig : R[g][0][j], &rp[(4 * lg + j) * V + rc]);
-                    __builtin_nontemporal_store(RANGE ? R[g][1][j] * isig : R[g][1][j], &rp[(16 + 4 * lg + j) * V + rc]);
+                    rp_store(RANGE ? R[g][0][j] * isig : R[g][0][j], j, g);
+                    rp_store(RANGE ? R[g][1][j] * isig : R[g][1][j], 16 + j, g);
                 }
             }
             const h4 r0 = to_h4(R[g][0]);
@@ -1227,8 +1255,8 @@ struct Kern {
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    __builtin_nontemporal_store(RANGE ? P0[j] * isig : P0[j], &rp[(32 + 4 * lg + j) * V + rc]);
-                    __builtin_nontemporal_store(RANGE ? P1[j] * isig : P1[j], &rp[(48 + 4 * lg + j) * V + rc]);
+                    rp_store(RANGE ? P0[j] * isig : P0[j], 32 + j, g);
+                    rp_store(RANGE ? P1[j] * isig : P1[j], 48 + j, g);
                 }
             }
             // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is

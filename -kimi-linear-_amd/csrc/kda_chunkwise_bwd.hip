@@ -49,6 +49,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "kda_common.h"
 #include "kda_launch.h"
@@ -448,10 +449,21 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             const int ti = w + NWS * m;
             if (ti < NTS) {
                 const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
-                float* dsn = ws.dS + cb * K * V + v0;
+                if constexpr (std::is_same<TI, _Float16>::value) {
+                    // fp16 activations: dS_end in fp16, accumulator-order tiles
+                    // (half_tile_offset), slot j = 64 consecutive halves
+                    _Float16* tile = reinterpret_cast<_Float16*>(ws.dS + cb * K * V) +
+                                     half_tile_offset(r0, v0 + c0, V) + lane;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    __builtin_nontemporal_store(accs[m][j], &dsn[static_cast<uint32_t>(r0 + 4 * lg + j) * V + c0 + ln]);
+                    for (int j = 0; j < 4; ++j)
+                        __builtin_nontemporal_store(static_cast<_Float16>(accs[m][j]), tile + 64 * j);
+                } else {
+                    float* dsn = ws.dS + cb * K * V + v0;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        __builtin_nontemporal_store(accs[m][j],
+                                                    &dsn[static_cast<uint32_t>(r0 + 4 * lg + j) * V + c0 + ln]);
+                }
             }
         }
         if (w < NDP) {
@@ -677,21 +689,37 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     const auto rdr = make_rsrc(ws.dR + cb * CT * V, static_cast<uint32_t>(CT * V * 4));
     const auto rdo = make_rsrc(dop + ((b * T + r0) * H + h) * V,
                                static_cast<uint32_t>(((nrow - 1) * H + 1) * V * SZ));
-    const uint32_t vo_f = static_cast<uint32_t>(x * V + 8 * lg) * 4;
+    // fp16 activations: S and dS as fp16 in accumulator-order tiles
+    // (half_tile_offset): the lane's 8 columns are one 16-byte run, and a
+    // 32-column step moves by two tiles (1 KiB)
+    constexpr bool HALF = std::is_same<TI, _Float16>::value;
+    const uint32_t vo_f = HALF ? static_cast<uint32_t>(2 * half_tile_offset(x, 8 * lg, V))
+                               : static_cast<uint32_t>(x * V + 8 * lg) * 4;
     const int tc = t / VT, tv = t % VT;
     const uint32_t vo_t = static_cast<uint32_t>(tc * V + tv) * 4;
     const uint32_t vo_o = static_cast<uint32_t>(tc * H * V + tv) * SZ;
-    uint32_t fS[8], fdS[8], fR[EPT], fP[EPT], fdP[EPT], fdR[EPT], fdO[EPT];
+    uint32_t fS[HALF ? 4 : 8], fdS[HALF ? 4 : 8], fR[EPT], fP[EPT], fdP[EPT], fdR[EPT], fdO[EPT];
     auto fetch = [&](int vt) {
         const uint32_t v0 = static_cast<uint32_t>(vt) * VT;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const w4 s4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rck, static_cast<int>(vo_f + 16 * u), static_cast<int>(4 * v0), 0));
-            const w4 d4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rds, static_cast<int>(vo_f + 16 * u), static_cast<int>(4 * v0), 0));
+        if constexpr (HALF) {
+            const int so = static_cast<int>(2 * 256 * 2 * (v0 / 32));
+            const w4 s4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rck, static_cast<int>(vo_f), so, 0));
+            const w4 d4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rds, static_cast<int>(vo_f), so, 0));
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                fS[4 * u + e] = s4[e];
-                fdS[4 * u + e] = d4[e];
+                fS[e] = s4[e];
+                fdS[e] = d4[e];
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const w4 s4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rck, static_cast<int>(vo_f + 16 * u), static_cast<int>(4 * v0), 0));
+                const w4 d4 = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rds, static_cast<int>(vo_f + 16 * u), static_cast<int>(4 * v0), 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    fS[4 * u + e] = s4[e];
+                    fdS[4 * u + e] = d4[e];
+                }
             }
         }
 #pragma unroll
@@ -747,8 +775,13 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         float sv[8], dsv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            sv[e] = __uint_as_float(fS[e]);
-            dsv[e] = __uint_as_float(fdS[e]);
+            if constexpr (HALF) {
+                sv[e] = raw_f32<_Float16>(fS[e / 2] >> (16 * (e % 2)));
+                dsv[e] = raw_f32<_Float16>(fdS[e / 2] >> (16 * (e % 2)));
+            } else {
+                sv[e] = __uint_as_float(fS[e]);
+                dsv[e] = __uint_as_float(fdS[e]);
+            }
             deps = fmaf(sv[e], dsv[e], deps);
         }
         split8(sv, sh, sl);

@@ -270,4 +270,19 @@ __device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
 // all V wide, then its A, L and N (32 x 32 each, row-major).
 __host__ __device__ constexpr int64_t ckpt_record(int64_t K, int64_t V) { return (K + 64) * V + 3 * 32 * 32; }
 
+// fp16 activations keep two K x V matrices in fp16: the state at the head of
+// each chunk record and the backward's dS_end per chunk.  fp16 is the dtype
+// the reference's fp16 path takes the state in for its products
+// (kimi_linear/kda.py:174) and the dtype of that cast's gradient.  Each such
+// matrix sits in the first half of its fp32 slot, in 16 x 16 tiles in MFMA
+// accumulator order: tile (r / 16, c / 16) at (r / 16) (V / 16) + c / 16,
+// 256 halves each; inside it, element (r, c) at
+// (r % 4) 64 + ((r / 4) % 4) 16 + c % 16.  An accumulator slot j (rows 4lg + j
+// of column ln in lane 16lg + ln) is then 64 consecutive halves (one 128-byte
+// store), and 8 consecutive columns of one row are 16 contiguous bytes (one
+// load of an MFMA fragment).
+__host__ __device__ constexpr int64_t half_tile_offset(int64_t r, int64_t c, int64_t V) {
+    return ((r / 16) * (V / 16) + c / 16) * 256 + (r % 4) * 64 + ((r / 4) % 4) * 16 + c % 16;
+}
+
 }  // namespace kda

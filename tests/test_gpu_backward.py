@@ -287,3 +287,26 @@ def test_recurrent_backward_fp16_clamp(kda_pkg, wl):
         err = _rel(a, r)
         print(f"  d{name}: rel {err:.2e}", flush=True)
         assert err <= _tol(torch.float16), (name, err)
+
+
+def test_fp16_record_holds_the_state_in_fp16_tiles(kda_pkg, wl):
+    """fp16 activations: each chunk record's state is fp16 in 16 x 16 tiles in
+    accumulator order in the first half of its K x V fp32 rows (element
+    (r, c) at half ((r//16)(V//16) + c//16) 256 + (r%4) 64 + ((r//4)%4) 16 +
+    c%16), as the header documents.  Chunk 0's record holds the initial state
+    as given, rounded to fp16; R's rows follow the state's fp32 rows."""
+    import importlib
+    kda = importlib.import_module("kimi_linear_amd.kda")
+    B, T, H, K, V = 1, 64, 2, 64, 96
+    inp = wl.make_inputs(B, T, H, K, V, seed=61, qkv_dtype=torch.float16, state_std=0.5)
+    d = {n: (x.to(DEV) if x is not None else None) for n, x in inp.items()}
+    with torch.no_grad():
+        _, _, ck = kda._forward("chunkwise", d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"], 64,
+                                torch.float32, ckpt=True)
+    assert ck.shape == (B, H, 2, kda.ckpt_record(K, V))
+    halves = ck[..., : K * V // 2].contiguous().view(torch.float16).cpu()     # [B, H, 2, K * V]
+    r = torch.arange(K)[:, None]
+    c = torch.arange(V)[None, :]
+    off = ((r // 16) * (V // 16) + c // 16) * 256 + (r % 4) * 64 + ((r // 4) % 4) * 16 + c % 16
+    s0 = halves[:, :, 0][..., off]                                             # [B, H, K, V]
+    assert torch.equal(s0, inp["state"].half())
