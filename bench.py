@@ -371,9 +371,17 @@ def backward_bench(pkg, wl, torch, reps=3):
     xs = [inp[n].clone().requires_grad_(True) for n in ("q", "k", "v", "g", "beta")]
     gen = torch.Generator(device="cuda").manual_seed(3)
     d_o = torch.randn(B1, T1, H1, D1, device="cuda", dtype=torch.float16, generator=gen)
-    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-    fwd = bwd = 0.0
-    for i in range(reps + 2):
+    # two untimed steps, then `reps` steps queued back to back (no host
+    # synchronisation between them, as in a training loop), HIP events around
+    # each step's forward and backward on the stream they run on
+    for _ in range(2):
+        for x in xs:
+            x.grad = None
+        o, _ = pkg.kda_chunkwise(*xs, chunk_size=C1, state_dtype=torch.float32)
+        o.backward(d_o)
+    torch.cuda.synchronize()
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(reps)]
+    for e0, e1, e2 in evs:
         for x in xs:
             x.grad = None
         e0.record()
@@ -381,10 +389,9 @@ def backward_bench(pkg, wl, torch, reps=3):
         e1.record()
         o.backward(d_o)
         e2.record()
-        torch.cuda.synchronize()
-        if i >= 2:
-            fwd += e0.elapsed_time(e1) / reps
-            bwd += e1.elapsed_time(e2) / reps
+    torch.cuda.synchronize()
+    fwd = sum(e0.elapsed_time(e1) for e0, e1, _ in evs) / reps
+    bwd = sum(e1.elapsed_time(e2) for _, e1, e2 in evs) / reps
     nbytes = backward_bytes(B1, T1, H1, D1, D1, 2)
     # the gradient's own I/O per (token, head): q, k, v, dO (2 B) and g (4 B) per
     # channel and beta read; dq, dk, dv (2 B), dg (4 B) per channel and dbeta written
