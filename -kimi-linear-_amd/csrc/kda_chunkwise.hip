@@ -1194,6 +1194,15 @@ struct Kern {
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rr, rlo,
                                                   static_cast<int>((row * V + colw + 16 * g) * 4), 2);
         };
+        // fp16 activations: R in fp16 (the single fp16 operand the solve below
+        // takes), row-major halves in the first half of its rows
+        auto r_store = [&](float x, int row, int g) {
+            if constexpr (Elem<TQ>::code == KDA_DTYPE_F16)
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x)), rr,
+                                                      rlo / 2, static_cast<int>((row * V + colw + 16 * g) * 2), 2);
+            else
+                rp_store(x, row, g);
+        };
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
         // the same fragments as A and B operands the other way round, so that
         // a lane holds four adjacent output columns of one row.  Block 1's
@@ -1241,8 +1250,8 @@ struct Kern {
             if (rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    rp_store(RANGE ? R[g][0][j] * isig : R[g][0][j], j, g);
-                    rp_store(RANGE ? R[g][1][j] * isig : R[g][1][j], 16 + j, g);
+                    r_store(RANGE ? R[g][0][j] * isig : R[g][0][j], j, g);
+                    r_store(RANGE ? R[g][1][j] * isig : R[g][1][j], 16 + j, g);
                 }
             }
             const h4 r0 = to_h4(R[g][0]);

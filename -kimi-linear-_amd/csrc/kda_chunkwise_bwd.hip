@@ -474,10 +474,20 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 acc = mm_pair(&sm.kf[0][r0t + ln][32 * u], &sm.kf[1][r0t + ln][32 * u], &sm.dST[0][c0t + ln][32 * u],
                               &sm.dST[1][c0t + ln][32 * u], lg, acc);
             acc = mm_pair(sm.AT[0][r0t + ln], sm.AT[1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[1][c0t + ln], lg, acc);
-            float* dpn = ws.dP + cb * CT * V + v0;
+            if constexpr (std::is_same<TI, _Float16>::value) {
+                // fp16 activations: dP and dR in fp16, row-major halves in the
+                // first half of their fp32 slots
+                _Float16* dpn = reinterpret_cast<_Float16*>(ws.dP + cb * CT * V) + v0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                __builtin_nontemporal_store(acc[j], &dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
+                for (int j = 0; j < 4; ++j)
+                    __builtin_nontemporal_store(static_cast<_Float16>(acc[j]),
+                                                &dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
+            } else {
+                float* dpn = ws.dP + cb * CT * V + v0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    __builtin_nontemporal_store(acc[j], &dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
+            }
             put4_pair(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[1][c0t + ln][r0t + 4 * lg], acc);
         }
 #pragma unroll
@@ -498,11 +508,19 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             const int r0t = 16 * (w / VTL), c0t = 16 * (w % VTL);
             f4 acc = mm_pair(sm.NT_[0][r0t + ln], sm.NT_[1][r0t + ln], sm.dPT[0][c0t + ln], sm.dPT[1][c0t + ln], lg,
                              f4{0.f, 0.f, 0.f, 0.f});
-            float* drn = ws.dR + cb * CT * V + v0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[j] *= sm.beta[r0t + 4 * lg + j];
-                __builtin_nontemporal_store(acc[j], &drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
+            for (int j = 0; j < 4; ++j) acc[j] *= sm.beta[r0t + 4 * lg + j];
+            if constexpr (std::is_same<TI, _Float16>::value) {
+                _Float16* drn = reinterpret_cast<_Float16*>(ws.dR + cb * CT * V) + v0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    __builtin_nontemporal_store(static_cast<_Float16>(acc[j]),
+                                                &drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
+            } else {
+                float* drn = ws.dR + cb * CT * V + v0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    __builtin_nontemporal_store(acc[j], &drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             }
             put4_pair(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[1][c0t + ln][r0t + 4 * lg], acc);
         }
@@ -725,10 +743,17 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 #pragma unroll
         for (int m = 0; m < EPT; ++m) {
             const uint32_t rowo = static_cast<uint32_t>((NTC / VT) * m) * static_cast<uint32_t>(V);
-            fR[m] = __builtin_amdgcn_raw_buffer_load_b32(rck, static_cast<int>(vo_t), static_cast<int>(4 * (K * V + rowo + v0)), 0);
             fP[m] = __builtin_amdgcn_raw_buffer_load_b32(rck, static_cast<int>(vo_t), static_cast<int>(4 * ((K + CT) * V + rowo + v0)), 0);
-            fdP[m] = __builtin_amdgcn_raw_buffer_load_b32(rdp, static_cast<int>(vo_t), static_cast<int>(4 * (rowo + v0)), 0);
-            fdR[m] = __builtin_amdgcn_raw_buffer_load_b32(rdr, static_cast<int>(vo_t), static_cast<int>(4 * (rowo + v0)), 0);
+            if constexpr (HALF) {
+                // R, dP, dR in fp16 (row-major halves in the first half of their rows)
+                fR[m] = __builtin_amdgcn_raw_buffer_load_b16(rck, static_cast<int>(vo_t / 2), static_cast<int>(4 * K * V + 2 * (rowo + v0)), 0);
+                fdP[m] = __builtin_amdgcn_raw_buffer_load_b16(rdp, static_cast<int>(vo_t / 2), static_cast<int>(2 * (rowo + v0)), 0);
+                fdR[m] = __builtin_amdgcn_raw_buffer_load_b16(rdr, static_cast<int>(vo_t / 2), static_cast<int>(2 * (rowo + v0)), 0);
+            } else {
+                fR[m] = __builtin_amdgcn_raw_buffer_load_b32(rck, static_cast<int>(vo_t), static_cast<int>(4 * (K * V + rowo + v0)), 0);
+                fdP[m] = __builtin_amdgcn_raw_buffer_load_b32(rdp, static_cast<int>(vo_t), static_cast<int>(4 * (rowo + v0)), 0);
+                fdR[m] = __builtin_amdgcn_raw_buffer_load_b32(rdr, static_cast<int>(vo_t), static_cast<int>(4 * (rowo + v0)), 0);
+            }
             const uint32_t so = (static_cast<uint32_t>((NTC / VT) * m) * static_cast<uint32_t>(H * V) + v0) * SZ;
             if constexpr (SZ == 2)
                 fdO[m] = __builtin_amdgcn_raw_buffer_load_b16(rdo, static_cast<int>(vo_o), static_cast<int>(so), 0);
@@ -763,14 +788,17 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 #pragma unroll
         for (int m = 0; m < EPT; ++m) {
             const int c = tc + (NTC / VT) * m;
-            split_bf16(__uint_as_float(fR[m]), sm.R[0][c][tv], sm.R[1][c][tv]);
+            // R, dP, dR: fp16 with fp16 activations, fp32 otherwise
+            const float r = HALF ? raw_f32<_Float16>(fR[m]) : __uint_as_float(fR[m]);
+            const float dp = HALF ? raw_f32<_Float16>(fdP[m]) : __uint_as_float(fdP[m]);
+            const float dr = HALF ? raw_f32<_Float16>(fdR[m]) : __uint_as_float(fdR[m]);
+            split_bf16(r, sm.R[0][c][tv], sm.R[1][c][tv]);
             split_bf16(__uint_as_float(fP[m]), sm.P[0][c][tv], sm.P[1][c][tv]);
-            split_bf16(__uint_as_float(fdP[m]), sm.dP[0][c][tv], sm.dP[1][c][tv]);
-            split_bf16(__uint_as_float(fdR[m]), sm.dR[0][c][tv], sm.dR[1][c][tv]);
+            split_bf16(dp, sm.dP[0][c][tv], sm.dP[1][c][tv]);
+            split_bf16(dr, sm.dR[0][c][tv], sm.dR[1][c][tv]);
             split_bf16(raw_f32<TI>(fdO[m]), sm.dO[0][c][tv], sm.dO[1][c][tv]);
             if (c < nrow)
-                Elem<TI>::st(dvp + ((b * T + r0 + c) * H + h) * V + static_cast<int64_t>(vt) * VT + tv,
-                             __uint_as_float(fdR[m]));
+                Elem<TI>::st(dvp + ((b * T + r0 + c) * H + h) * V + static_cast<int64_t>(vt) * VT + tv, dr);
         }
         float sv[8], dsv[8];
 #pragma unroll

@@ -410,19 +410,22 @@ def backward_bench(pkg, wl, torch, reps=3):
 
 def backward_bytes(B, T, H, K, V, sz, half_state=True):
     """Algorithmic HBM bytes of kda_chunkwise_bwd's three kernels (activations of
-    sz bytes; workspace and checkpoints fp32, except the records' state and
-    dS_end, fp16 with fp16 activations (half_state); 32-token chunks): the N
+    sz bytes; workspace and checkpoints fp32, except the records' state and R
+    and the workspace's dS_end, dP and dR, fp16 with fp16 activations
+    (half_state); 32-token chunks): the N
     kernel reads L_10 and N's two diagonal blocks from the checkpoint record and
     block 1's beta, and writes N; the state kernel reads q, k, g, dO, A, N, beta
     and writes dS_end, dP, dR; the chunk kernel reads the checkpoint (S, R, P),
     dS_end, dP, dR, dO, q, k, g, L, N, beta and writes dq, dk, dv, dg, dbeta."""
     nck = -(-T // 32)
     qk, g, v, beta = B * T * H * K * sz, B * T * H * K * 4, B * T * H * V * sz, B * T * H * 4
-    mat, RP = B * H * nck * 32 * 32 * 4, B * H * nck * 32 * V * 4
+    mat = B * H * nck * 32 * 32 * 4
     S = B * H * nck * K * V * (2 if half_state else 4)
+    # per 32 x V matrix: P fp32; R, dP, dR fp16 with fp16 activations
+    RP, RPh = B * H * nck * 32 * V * 4, B * H * nck * 32 * V * (2 if half_state else 4)
     nk = 3 * mat // 4 + beta // 2 + mat
-    state = 2 * qk + g + v + 2 * mat + beta + S + 2 * RP
-    chunk = 2 * S + 4 * RP + v + 2 * qk + g + 2 * mat + beta + 2 * qk + v + g + beta
+    state = 2 * qk + g + v + 2 * mat + beta + S + 2 * RPh
+    chunk = 2 * S + RP + 3 * RPh + v + 2 * qk + g + 2 * mat + beta + 2 * qk + v + g + beta
     return nk + state + chunk
 
 

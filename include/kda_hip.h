@@ -206,7 +206,9 @@ int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* wor
  * dtype the reference's fp16 path casts it to for its products
  * (kimi_linear/kda.py:174), in the first K x V / 2 floats of its rows: 16 x 16
  * tiles, tile (r / 16, c / 16) at (r / 16) (V / 16) + c / 16, 256 halves each,
- * element (r, c) at (r % 4) 64 + ((r / 4) % 4) 16 + c % 16 inside it. */
+ * element (r, c) at (r % 4) 64 + ((r / 4) % 4) 16 + c % 16 inside it; and R
+ * (the single fp16 operand of the forward's solve) as row-major halves in the
+ * first 32 x V / 2 floats of its rows. */
 #define KDA_CKPT_RECORD(K, V) (((K) + 64) * (V) + 3 * 32 * 32)
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 
@@ -240,8 +242,8 @@ typedef struct kda_bwd_args {
 
 /* Bytes of workspace kda_chunkwise_bwd needs: per (b, h) and 32-token chunk,
  * (32 * 32 + K * V + 2 * 32 * V) floats (with fp16 q, k, v the K x V part,
- * the gradient of the state at the chunk's end, is kept in fp16 and uses half
- * of it).  0 for a bad or empty shape. */
+ * the gradient of the state at the chunk's end, and the two 32 x V parts are
+ * kept in fp16 and use half of theirs).  0 for a bad or empty shape. */
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 
 int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
