@@ -91,7 +91,7 @@ int chunkwise_entry(const kda_fwd_args* args, float* ckpt, const kda_gate_args* 
         // state in fp32 registers; the chunk pipeline's operands are fp16.
         // With checkpoints the recurrence also stores the fp32 state before
         // every 32-token chunk and an fp32 kernel fills the rest of each
-        // record (R, P, A, L, N), so the backward starts from exact records.
+        // record (R, A, L, N), so the backward starts from exact records.
         if (ckpt) {
             const int st = kda::recurrent_launch(*args, s, gate, ckpt);
             if (st != KDA_OK) return st;

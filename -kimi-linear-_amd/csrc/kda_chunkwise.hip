@@ -463,13 +463,13 @@ struct Kern {
     uint32_t vo_q, vo_k, vo_g, vo_v, vo_b;   // lane byte offsets
     // kda_chunkwise_fwd_ckpt: the (b, h)'s chunk records, written by the
     // head's first V-tile workgroup only (null otherwise): per 32-token chunk
-    // the state, R and P ((K + 64) x V) and then A, L and N (32 x 32 each)
+    // the state and R ((K + 32) x V) and then A, L and N (32 x 32 each)
     float* ckm = nullptr;
     int nblk = 0;                            // blocks of the real chunks (records exist for these)
 
     // A, L, N of the chunk holding block blk (row-major 32 x 32, consecutive)
     __device__ float* ck_mats(int blk) const {
-        return ckm + static_cast<int64_t>(blk / CB) * ckpt_record(K, a.V) + static_cast<int64_t>(K + 2 * CB * BT) * a.V;
+        return ckm + static_cast<int64_t>(blk / CB) * ckpt_record(K, a.V) + static_cast<int64_t>(K + CB * BT) * a.V;
     }
 
     __device__ Kern(const kda_fwd_args& args, Smem<K, CG, EPI>& s) : a(args), sm(s) {}
@@ -1109,7 +1109,7 @@ struct Kern {
     // groups; the v load of the chunk one superstep later is issued into
     // vraw once its values are in LDS.  ck (or null): the chunk's checkpoint
     // for the backward, in fp32: rows [0, K) the state before it, [K, K + 32)
-    // its R = V - (k * E) S, [K + 32, K + 64) its P.  EPI: the outputs go to
+    // its R = V - (k * E) S.  EPI: the outputs go to
     // pd (and their row sums of squares to LDS) instead of o.
     __device__ void consume(const ChunkOps<K>& co, int blk, uint32_t (&vraw)[CG][VW],
                             uint16_t (*vt)[16], f4 (&S)[CG][KT], int64_t colw, float* ck, Pend& pd,
@@ -1184,24 +1184,20 @@ struct Kern {
             }
         }
         float* rp = ck ? ck + static_cast<int64_t>(K) * V : nullptr;
-        // R and P rows through one buffer resource: the lane's part of the
-        // offset in a vector register, the row and column group's
-        // (wave-uniform) part in the scalar offset -- no 64-bit address per
-        // store kept in registers
-        const auto rr = make_rsrc(rp, static_cast<uint32_t>(2 * CB * BT * V * 4));
+        // R rows through one buffer resource: the lane's part of the offset in
+        // a vector register, the row and column group's (wave-uniform) part
+        // in the scalar offset -- no 64-bit address per store kept in
+        // registers.  fp16 activations: R in fp16 (the single fp16 operand the
+        // solve below takes), row-major halves in the first half of its rows.
+        const auto rr = make_rsrc(rp, static_cast<uint32_t>(CB * BT * V * 4));
         const int rlo = static_cast<int>((4 * lg * V + ln) * 4);
-        auto rp_store = [&](float x, int row, int g) {
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rr, rlo,
-                                                  static_cast<int>((row * V + colw + 16 * g) * 4), 2);
-        };
-        // fp16 activations: R in fp16 (the single fp16 operand the solve below
-        // takes), row-major halves in the first half of its rows
         auto r_store = [&](float x, int row, int g) {
             if constexpr (Elem<TQ>::code == KDA_DTYPE_F16)
                 __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x)), rr,
                                                       rlo / 2, static_cast<int>((row * V + colw + 16 * g) * 2), 2);
             else
-                rp_store(x, row, g);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rr, rlo,
+                                                      static_cast<int>((row * V + colw + 16 * g) * 4), 2);
         };
         // Z_b = (k * E)_b S; the outputs transposed, O_b^T = S^T (q * E)_b^T:
         // the same fragments as A and B operands the other way round, so that
@@ -1261,13 +1257,6 @@ struct Kern {
             const h4 r1 = to_h4(R[g][1]);
             const f4 P1 = mfma16x16x32(m1, cat(r1, r1), f4{0.f, 0.f, 0.f, 0.f});
             const Split4 p1(P1);
-            if (rp) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    rp_store(RANGE ? P0[j] * isig : P0[j], 32 + j, g);
-                    rp_store(RANGE ? P1[j] * isig : P1[j], 48 + j, g);
-                }
-            }
             // O^T = scale S^T (q * E)^T + P^T A^T: P^T's A-operand layout is
             // P's accumulator layout, A^T's B-operand layout is A's A-operand
             // layout

@@ -4,8 +4,8 @@
 // differentiated by autograd (training: scripts/train_musicgpt_fp16.py:519-523).
 // The forward is re-evaluated chunk by chunk from the records that
 // kda_chunkwise_fwd_ckpt writes: per CT = 32-token chunk, the state before it,
-// the chunk's R and P, A, L and the diagonal blocks of N (below), all of which
-// the forward computes anyway.
+// the chunk's R, A, L and the diagonal blocks of N (below), all of which the
+// forward computes anyway; P = M R is formed again from R and N.
 //
 // Per (b, h) and chunk, rows c, i in [0, CT), channels k, state columns v:
 //   G = in-chunk cumulative sum of g,  E = exp(G),  F = exp(G_last - G),
@@ -35,8 +35,8 @@
 //      (fp32) and dS_0.  The next chunk's inputs are fetched while the
 //      current one is computed.
 //   3. bwd_chunk_kernel, one workgroup per (b, h, chunk): writes dv = dR; from
-//      S, R, P (checkpoint), dS_end, dP and dR the sums over all state columns
-//      (VT at a time) of dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain
+//      S, R (checkpoint), P = M R, dS_end, dP and dR the sums over all state
+//      columns (VT at a time) of dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain
 //      through the inverse, the pairwise-decay products and the reverse
 //      cumulative sum: complete dq, dk, dg and dbeta.
 // Rows past T read as zero inputs, which leave the state and every gradient
@@ -47,6 +47,7 @@
 // except A and L for 16-bit activations (fp16 operands, the forward's
 // precision) and N (fp32 matrix cores).
 #include <algorithm>
+#include <cstddef>
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -77,7 +78,7 @@ struct BwdWs {
 BwdWs ws_layout(void* base, const float* ckpt, int64_t BH, int64_t nck, int64_t K, int64_t V) {
     float* p = static_cast<float*>(base);
     BwdWs w;
-    w.A = ckpt + (K + 2 * CT) * V;
+    w.A = ckpt + (K + CT) * V;
     w.L = w.A + CT * CT;
     w.ms = ckpt_record(K, V);
     w.N = p;
@@ -607,10 +608,10 @@ template <int K>
 struct __align__(16) ChunkSmem {
     static constexpr int NW = K / 16;
     uint16_t dO[2][CT][VB];
-    uint16_t R[2][CT][VB];      // R and P from the forward's checkpoint
-    uint16_t P[2][CT][VB];
+    uint16_t R[2][CT][VB];      // R from the forward's checkpoint
     uint16_t dP[2][CT][VB];
     uint16_t dR[2][CT][VB];
+    uint16_t spare[2][CT][VB];  // with the tiles above: the stash after the column steps
     float L[CT][CT + 1];
     float N[CT][CT + 1];
     float dM[CT][CT + 1];       // dM, then dN, then dX
@@ -629,9 +630,11 @@ struct __align__(16) ChunkSmem {
 // 16 w .. 16 w + 15 for all CT rows (two 16-row element tiles), so the
 // state's and its gradient's fragments come straight from HBM into the
 // lanes that use them and the per-element step runs in registers.
-// Column steps of VT state columns: the CT-row tiles (dO, R, P, dP, dR) go
+// Column steps of VT state columns: the CT-row tiles (dO, R, dP, dR) go
 // through LDS as bf16 pairs; every product on the bf16 matrix cores as
-// pairs.  The next step is fetched (raw, through buffer descriptors whose
+// pairs.  P = M R (M = N Diag(beta)) enters through R: the column sums take
+// X = dO R^T and Z = R dS^T, and M is applied once per chunk afterwards
+// (dO P^T = X M^T, P dS^T = M Z) on the fp32 matrix cores.  The next step is fetched (raw, through buffer descriptors whose
 // range stops at the chunk's last row before T) while the current one is
 // computed.  About 60 KiB of LDS at K = 128: two workgroups share a CU, one
 // workgroup's HBM-bound column steps overlapping the other's element step.
@@ -698,10 +701,10 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 
     // column-step fetch: the lane's fragments of S (the checkpointed state
     // before the chunk) and dS (the gradient of the state after it), row x,
-    // columns v0 + 8 lg .. + 7; the thread's EPT elements of R, P (checkpoint),
+    // columns v0 + 8 lg .. + 7; the thread's EPT elements of R (checkpoint),
     // dP, dR (workspace) and dO, rows t / VT + (NTC / VT) m, column t % VT
     const auto rck = make_rsrc(a.ckpt + cb * ckpt_record(K, V),
-                               static_cast<uint32_t>((K + 2 * CT) * V * 4));
+                               static_cast<uint32_t>((K + CT) * V * 4));
     const auto rds = make_rsrc(ws.dS + cb * K * V, static_cast<uint32_t>(K * V * 4));
     const auto rdp = make_rsrc(ws.dP + cb * CT * V, static_cast<uint32_t>(CT * V * 4));
     const auto rdr = make_rsrc(ws.dR + cb * CT * V, static_cast<uint32_t>(CT * V * 4));
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     const int tc = t / VT, tv = t % VT;
     const uint32_t vo_t = static_cast<uint32_t>(tc * V + tv) * 4;
     const uint32_t vo_o = static_cast<uint32_t>(tc * H * V + tv) * SZ;
-    uint32_t fS[HALF ? 4 : 8], fdS[HALF ? 4 : 8], fR[EPT], fP[EPT], fdP[EPT], fdR[EPT], fdO[EPT];
+    uint32_t fS[HALF ? 4 : 8], fdS[HALF ? 4 : 8], fR[EPT], fdP[EPT], fdR[EPT], fdO[EPT];
     auto fetch = [&](int vt) {
         const uint32_t v0 = static_cast<uint32_t>(vt) * VT;
         if constexpr (HALF) {
@@ -743,7 +746,6 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 #pragma unroll
         for (int m = 0; m < EPT; ++m) {
             const uint32_t rowo = static_cast<uint32_t>((NTC / VT) * m) * static_cast<uint32_t>(V);
-            fP[m] = __builtin_amdgcn_raw_buffer_load_b32(rck, static_cast<int>(vo_t), static_cast<int>(4 * ((K + CT) * V + rowo + v0)), 0);
             if constexpr (HALF) {
                 // R, dP, dR in fp16 (row-major halves in the first half of their rows)
                 fR[m] = __builtin_amdgcn_raw_buffer_load_b16(rck, static_cast<int>(vo_t / 2), static_cast<int>(4 * K * V + 2 * (rowo + v0)), 0);
@@ -764,9 +766,10 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     fetch(0);
 
     // ------------------------------------- sums over the state columns
-    // dA += dO P^T, dM += dP R^T (MPW tiles a wave), and per element tile p:
+    // X += dO R^T, dM += dP R^T (MPW tiles a wave), and per element tile p:
     // d(q~E) += dO S^T, d(kE) -= dR S^T (accumulated as + and negated
-    // below), d(kF) += P dS^T; deps += rowsum(dS * S)
+    // below), Z += R dS^T; deps += rowsum(dS * S).  Then dA = tril(X M^T)
+    // and d(kF) = M Z (P = M R).
     f4 accm[MPW];
 #pragma unroll
     for (int m = 0; m < MPW; ++m) accm[m] = f4{0.f, 0.f, 0.f, 0.f};
@@ -781,7 +784,6 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         use_here(fS);
         use_here(fdS);
         use_here(fR);
-        use_here(fP);
         use_here(fdP);
         use_here(fdR);
         use_here(fdO);
@@ -793,7 +795,6 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
             const float dp = HALF ? raw_f32<_Float16>(fdP[m]) : __uint_as_float(fdP[m]);
             const float dr = HALF ? raw_f32<_Float16>(fdR[m]) : __uint_as_float(fdR[m]);
             split_bf16(r, sm.R[0][c][tv], sm.R[1][c][tv]);
-            split_bf16(__uint_as_float(fP[m]), sm.P[0][c][tv], sm.P[1][c][tv]);
             split_bf16(dp, sm.dP[0][c][tv], sm.dP[1][c][tv]);
             split_bf16(dr, sm.dR[0][c][tv], sm.dR[1][c][tv]);
             split_bf16(raw_f32<TI>(fdO[m]), sm.dO[0][c][tv], sm.dO[1][c][tv]);
@@ -820,15 +821,14 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         for (int m = 0; m < MPW; ++m) {
             const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
             const uint16_t (*xa)[CT][VB] = tt < 4 ? sm.dO : sm.dP;
-            const uint16_t (*ya)[CT][VB] = tt < 4 ? sm.P : sm.R;
-            accm[m] = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], ya[0][c0t + ln], ya[1][c0t + ln], lg, accm[m]);
+            accm[m] = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], sm.R[0][c0t + ln], sm.R[1][c0t + ln], lg, accm[m]);
         }
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int er = 16 * p + ln;
             dqe[p] = mm_pair_r(sm.dO[0][er], sm.dO[1][er], sh, sl, lg, dqe[p]);
             dke[p] = mm_pair_r(sm.dR[0][er], sm.dR[1][er], sh, sl, lg, dke[p]);
-            dkf[p] = mm_pair_r(sm.P[0][er], sm.P[1][er], dsh, dsl, lg, dkf[p]);
+            dkf[p] = mm_pair_r(sm.R[0][er], sm.R[1][er], dsh, dsl, lg, dkf[p]);
         }
     };
     for (int vt = 0; vt + 1 < nvt; ++vt) {
@@ -844,10 +844,27 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     __syncthreads();
     products();
     __syncthreads();
+    // d(kF) = M Z: block p of M times the Z tiles (M lower triangular;
+    // xt(p, q) slot u = M[16 p + ln][16 q + 4 lg + u], the A operand of mm_acc)
+    {
+        auto mt = [&](int p, int q) {
+            f4 x;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = 16 * q + 4 * lg + u;
+                x[u] = sm.N[16 * p + ln][i] * sm.beta[i];
+            }
+            return x;
+        };
+        const f4 z0 = dkf[0];
+        dkf[0] = mm_acc(mt(0, 0), z0, f4{0.f, 0.f, 0.f, 0.f});
+        dkf[1] = mm_acc(mt(1, 1), dkf[1], mm_acc(mt(1, 0), z0, f4{0.f, 0.f, 0.f, 0.f}));
+    }
     // block 0's accumulators wait in the (now free) tile area while block 1's
     // element step runs: slot i of thread t at stash[i * NTC + t]
     float* stash = reinterpret_cast<float*>(&sm.dO[0][0][0]);
-    static_assert(12 * NTC * 4 <= 5 * sizeof(sm.dO), "the stash fits the tiles");
+    static_assert(12 * NTC * 4 <= 5 * sizeof(sm.dO) && offsetof(ChunkSmem<K>, spare) == 4 * sizeof(sm.dO),
+                  "the stash fits the tiles");
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         stash[(0 + j) * NTC + t] = dqe[0][j];
@@ -858,22 +875,34 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     // deps of channel x: the shares of the four lanes of the channel
     deps += __shfl_xor(deps, 16);
     deps += __shfl_xor(deps, 32);
+    // X (whole) to Y's area until dA is formed; dM (i <= c)
 #pragma unroll
     for (int m = 0; m < MPW; ++m) {
         const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
-            const float v = i <= c ? accm[m][j] : 0.f;
-            if (tt < 4) {
-                sm.dAr[c][i] = v;
-                sm.dAc[i][c] = v;
-            } else {
-                sm.dM[c][i] = v;
-            }
+            if (tt < 4)
+                sm.Y[c][i] = accm[m][j];
+            else
+                sm.dM[c][i] = i <= c ? accm[m][j] : 0.f;
         }
     }
     __syncthreads();
+    // dA = tril(X M^T), M^T[q][i] = N[i][q] beta[q] (beside the column sums below)
+    for (int tt = __builtin_amdgcn_readfirstlane(w); tt < 4; tt += NW) {
+        const int r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
+        const f4 acc = tile_mm<CT>([&](int r, int q) { return sm.Y[r0t + r][q]; },
+                                   [&](int q, int i) { return sm.N[c0t + i][q] * sm.beta[q]; }, ln, lg,
+                                   f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = r0t + 4 * lg + j, i = c0t + ln;
+            const float v = i <= c ? acc[j] : 0.f;
+            sm.dAr[c][i] = v;
+            sm.dAc[i][c] = v;
+        }
+    }
 
     // ------------------------------- dbeta (M = N Diag(beta)), dN in place
     // column sums of dM * N: over the thread's entries (one column), the two

@@ -10,8 +10,7 @@
 //   G = in-chunk cumulative sum of g,  E = exp(G),  q~ = scale q
 //   A[c,i] = sum_k q~[c,k] k[i,k] exp(G[c,k] - G[i,k])   (i <= c, else 0)
 //   L[c,i] = sum_k  k[c,k] k[i,k] exp(G[c,k] - G[i,k])   (i <  c, else 0)
-//   N = (I + Diag(beta) L)^-1
-//   R = V - (k * E) S,   P = N Diag(beta) R
+//   N = (I + Diag(beta) L)^-1,   R = V - (k * E) S
 // -- the quantities the pipelined forward records from its fp16 operands, so
 // that the backward's gradients of fp32 inputs start from fp32-exact records.
 // One workgroup of 256 threads per (b, h, chunk); rows past T are zero rows
@@ -25,7 +24,7 @@ namespace {
 
 constexpr int CT = 32;          // tokens per record
 constexpr int NT = 256;         // threads per workgroup
-constexpr int VC = NT / 2;      // state columns per pass of the R and P step
+constexpr int VC = NT / 2;      // state columns per pass of the R step
 
 template <int K>
 struct __align__(16) FillSmem {
@@ -35,7 +34,6 @@ struct __align__(16) FillSmem {
     float A[CT][CT + 1];
     float L[CT][CT + 1];
     float N[CT][CT + 1];
-    float R[CT][VC + 1];        // one pass of R columns, for P
     float beta[CT];
 };
 
@@ -114,8 +112,7 @@ __global__ __launch_bounds__(NT) void ckpt_fill_kernel(const kda_fwd_args a, flo
 
     float* rec = ckpt + cb * ckpt_record(K, V);
     float* rr = rec + K * V;                 // R [CT][V]
-    float* rpp = rec + (K + CT) * V;         // P [CT][V]
-    float* ra = rec + (K + 2 * CT) * V;      // A, L, N [CT][CT] each
+    float* ra = rec + (K + CT) * V;          // A, L, N [CT][CT] each
     for (int e = t; e < CT * CT; e += NT) {
         const int c = e / CT, i = e % CT;
         ra[e] = sm.A[c][i];
@@ -123,8 +120,8 @@ __global__ __launch_bounds__(NT) void ckpt_fill_kernel(const kda_fwd_args a, flo
         ra[2 * CT * CT + e] = sm.N[c][i];
     }
 
-    // R = V - (k * E) S and P = N Diag(beta) R, VC columns a pass: thread
-    // (column t % VC, rows 16 (t / VC) .. + 15)
+    // R = V - (k * E) S, VC columns a pass: thread (column t % VC, rows
+    // 16 (t / VC) .. + 15)
     const float* S = rec;                    // the state before the chunk, [K][V]
     const int col = t % VC, hf = t / VC;
     for (int64_t c0 = 0; c0 < V; c0 += VC) {
@@ -143,22 +140,8 @@ __global__ __launch_bounds__(NT) void ckpt_fill_kernel(const kda_fwd_args a, flo
                 for (int r = 0; r < 16; ++r) acc[r] = fmaf(-sm.q[16 * hf + r][x], sv, acc[r]);
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                sm.R[16 * hf + r][col] = acc[r] * sm.beta[16 * hf + r];
-                rr[(16 * hf + r) * V + c] = acc[r];
-            }
+            for (int r = 0; r < 16; ++r) rr[(16 * hf + r) * V + c] = acc[r];
         }
-        __syncthreads();
-        if (live) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 16 * hf + r;
-                float p = 0.f;
-                for (int i = 0; i <= row; ++i) p = fmaf(sm.N[row][i], sm.R[i][col], p);
-                rpp[row * V + c] = p;
-            }
-        }
-        __syncthreads();
     }
 }
 

@@ -266,9 +266,10 @@ __device__ __forceinline__ void use_here(uint32_t (&r)[N][M]) {
 }
 
 // Floats of one 32-token chunk's record in kda_chunkwise_fwd_ckpt's output:
-// the state before the chunk (K rows), the chunk's R and P (32 rows each),
-// all V wide, then its A, L and N (32 x 32 each, row-major).
-__host__ __device__ constexpr int64_t ckpt_record(int64_t K, int64_t V) { return (K + 64) * V + 3 * 32 * 32; }
+// the state before the chunk (K rows) and the chunk's R (32 rows), all V wide,
+// then its A, L and N (32 x 32 each, row-major).  The solve's result
+// P = N Diag(beta) R is not kept: the backward forms it from R and N.
+__host__ __device__ constexpr int64_t ckpt_record(int64_t K, int64_t V) { return (K + 32) * V + 3 * 32 * 32; }
 
 // fp16 activations keep two K x V matrices in fp16: the state at the head of
 // each chunk record and the backward's dS_end per chunk.  fp16 is the dtype

@@ -15,7 +15,7 @@ bool recurrent_supported(int64_t K, int64_t V);
 int recurrent_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate = nullptr,
                      float* ckpt = nullptr);
 
-// The rest of the fp32 chunk records (kda_ckpt_fp32.hip): R, P, A, L and N
+// The rest of the fp32 chunk records (kda_ckpt_fp32.hip): R, A, L and N
 // of every 32-token chunk from the state the recurrence stored at the
 // record's head and the chunk's fp32 q, k, v, g, beta.
 int ckpt_fill_fp32_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt);
@@ -25,7 +25,7 @@ bool chunkwise_supported(int64_t K, int64_t V);
 // Host-side argument checks of the chunkwise contract (gate dtypes, strides);
 // `gated`: g and beta hold gk and the beta logits.
 int chunkwise_check(const kda_fwd_args& a, bool gated = false);
-// ckpt (nullable): fp32 [B, H, ceil(T/32), K + 64, V], the checkpoints of the
+// ckpt (nullable): fp32 [B, H, ceil(T/32), ckpt_record(K, V)], the checkpoints of the
 // backward; gate (nullable): the fused gate of kda_chunkwise_gated_fwd (not
 // with ckpt)
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr,

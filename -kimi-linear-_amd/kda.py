@@ -175,8 +175,8 @@ def _forward(kind, q, k, v, g, beta, state, chunk_size, state_dtype, state_out=N
         epilogue = (og, w_norm.detach().reshape(H, V).to(torch.float32).contiguous(), float(eps))
     o = torch.empty(B, T, H, V, device=dev, dtype=out_dtype)
     s_out = state_out if state_out is not None else torch.empty(B, H, K, V, device=dev, dtype=kernel_s_dtype)
-    # per 32-token chunk a record: the state before it (K rows), the chunk's R and P
-    # (32 rows each), all V wide, then its A, L and N (32 x 32 each)
+    # per 32-token chunk a record: the state before it (K rows) and the chunk's R
+    # (32 rows), all V wide, then its A, L and N (32 x 32 each)
     ck = torch.empty(B, H, (T + CKPT_SPACING - 1) // CKPT_SPACING, ckpt_record(K, V), device=dev,
                      dtype=torch.float32) if ckpt else None
     if B * H == 0:
@@ -279,7 +279,7 @@ CKPT_SPACING = 32   # tokens between the forward's state checkpoints (kda_chunkw
 
 def ckpt_record(K: int, V: int) -> int:
     """Floats of one chunk's record in kda_chunkwise_fwd_ckpt's output."""
-    return (K + 2 * CKPT_SPACING) * V + 3 * CKPT_SPACING * CKPT_SPACING
+    return (K + CKPT_SPACING) * V + 3 * CKPT_SPACING * CKPT_SPACING
 LONG_MIN_SEGMENT = 1024    # shortest segment worth a split (kda_chunkwise_long_fwd)
 CU_COUNT = 256
 

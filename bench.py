@@ -396,7 +396,7 @@ def backward_bench(pkg, wl, torch, reps=3):
     # the gradient's own I/O per (token, head): q, k, v, dO (2 B) and g (4 B) per
     # channel and beta read; dq, dk, dv (2 B), dg (4 B) per channel and dbeta written
     io = B1 * T1 * H1 * (4 * 2 * D1 + 4 * D1 + 4 + 3 * 2 * D1 + 4 * D1 + 4)
-    return {"workload": "kda_chunkwise forward (with 32-token checkpoints: state, R, P) + native backward under "
+    return {"workload": "kda_chunkwise forward (with 32-token checkpoints: state, R, A, L, N) + native backward under "
                         "autograd, B=8 T=4096 H=16 dk=dv=128; fp16 q/k/v, fp32 g/beta",
             "forward_ckpt_ms": fwd, "backward_ms": bwd,
             "train_tokens_per_s": B1 * T1 / ((fwd + bwd) * 1e-3),
@@ -415,17 +415,18 @@ def backward_bytes(B, T, H, K, V, sz, half_state=True):
     (half_state); 32-token chunks): the N
     kernel reads L_10 and N's two diagonal blocks from the checkpoint record and
     block 1's beta, and writes N; the state kernel reads q, k, g, dO, A, N, beta
-    and writes dS_end, dP, dR; the chunk kernel reads the checkpoint (S, R, P),
-    dS_end, dP, dR, dO, q, k, g, L, N, beta and writes dq, dk, dv, dg, dbeta."""
+    and writes dS_end, dP, dR; the chunk kernel reads the checkpoint (S, R),
+    dS_end, dP, dR, dO, q, k, g, L, N, beta (P = N Diag(beta) R is formed in the
+    kernel) and writes dq, dk, dv, dg, dbeta."""
     nck = -(-T // 32)
     qk, g, v, beta = B * T * H * K * sz, B * T * H * K * 4, B * T * H * V * sz, B * T * H * 4
     mat = B * H * nck * 32 * 32 * 4
     S = B * H * nck * K * V * (2 if half_state else 4)
-    # per 32 x V matrix: P fp32; R, dP, dR fp16 with fp16 activations
-    RP, RPh = B * H * nck * 32 * V * 4, B * H * nck * 32 * V * (2 if half_state else 4)
+    # per 32 x V matrix (R, dP, dR): fp16 with fp16 activations
+    RPh = B * H * nck * 32 * V * (2 if half_state else 4)
     nk = 3 * mat // 4 + beta // 2 + mat
     state = 2 * qk + g + v + 2 * mat + beta + S + 2 * RPh
-    chunk = 2 * S + RP + 3 * RPh + v + 2 * qk + g + 2 * mat + beta + 2 * qk + v + g + beta
+    chunk = 2 * S + 3 * RPh + v + 2 * qk + g + 2 * mat + beta + 2 * qk + v + g + beta
     return nk + state + chunk
 
 

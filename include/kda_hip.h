@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 12
+#define KDA_ABI_VERSION 13
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -191,14 +191,14 @@ int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* wor
  * ------------------------------------------------------------------------- */
 
 /* kda_chunkwise_fwd, plus per 32-token chunk a record, in fp32: the state
- * before the chunk, the chunk's R = V - (k * E) S and P = (I + Diag(beta)
- * L)^-1 Diag(beta) R (the solve's result), then its A (scale times the decayed
- * q k^T, i <= c), L (the decayed k k^T, i < c) and N = (I + Diag(beta) L)^-1
- * with its block below the diagonal zero (the solve uses only the 16-row
- * diagonal blocks): ckpt is [B, H, ceil(T/32), KDA_CKPT_RECORD(K, V)]
- * contiguous, each record (K + 64) x V (rows [0, K) the state, [K, K + 32) R,
- * [K + 32, K + 64) P) followed by three row-major 32 x 32 matrices (the input
- * of kda_chunkwise_bwd).  Same arguments, errors and results otherwise.  For
+ * before the chunk and the chunk's R = V - (k * E) S, then its A (scale times
+ * the decayed q k^T, i <= c), L (the decayed k k^T, i < c) and N = (I +
+ * Diag(beta) L)^-1 with its block below the diagonal zero (the solve uses only
+ * the 16-row diagonal blocks): ckpt is [B, H, ceil(T/32), KDA_CKPT_RECORD(K,
+ * V)] contiguous, each record (K + 32) x V (rows [0, K) the state, [K, K + 32)
+ * R) followed by three row-major 32 x 32 matrices (the input of
+ * kda_chunkwise_bwd, which forms the solve's result P = N Diag(beta) R
+ * itself).  Same arguments, errors and results otherwise.  For
  * fp16 / bf16 q, k, v the records come from the chunk pipeline (its fp16
  * operands); for fp32 q, k, v from the fp32 token recurrence (the state) and
  * an fp32 kernel (the rest, with N whole), fp32-exact like the outputs
@@ -209,7 +209,7 @@ int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* wor
  * element (r, c) at (r % 4) 64 + ((r / 4) % 4) 16 + c % 16 inside it; and R
  * (the single fp16 operand of the forward's solve) as row-major halves in the
  * first 32 x V / 2 floats of its rows. */
-#define KDA_CKPT_RECORD(K, V) (((K) + 64) * (V) + 3 * 32 * 32)
+#define KDA_CKPT_RECORD(K, V) (((K) + 32) * (V) + 3 * 32 * 32)
 int kda_chunkwise_fwd_ckpt(const kda_fwd_args* args, float* ckpt, void* stream);
 
 /* Every tensor is contiguous in the forward layout: q, k, g, dq, dk, dg
@@ -421,7 +421,8 @@ int kda_output_bwd(const kda_output_bwd_args* args, void* stream);
 /* Human-readable name of a kda_status code (static storage). */
 const char* kda_status_str(int status);
 
-/* KDA_ABI_VERSION of the built library (layout of the argument structs). */
+/* KDA_ABI_VERSION of the built library (layout of the argument structs and of
+ * the checkpoint records). */
 int kda_abi_version(void);
 
 #ifdef __cplusplus

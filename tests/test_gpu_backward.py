@@ -9,7 +9,7 @@ state and the initial state -- is exercised.
 
 Tolerance: relative L2 error <= 1e-4 per gradient for fp32 inputs (their
 checkpoints are fp32-exact: the fp32 token recurrence's states and an fp32
-kernel's R, P, A, L, N; the backward's products are bf16 pairs, ~2^-17
+kernel's R, A, L, N; the backward's products are bf16 pairs, ~2^-17
 relative; measured 4e-6 to 2.4e-5), 2e-3 for fp16 inputs and 1e-2 for bf16
 inputs (the checkpoints come from the fp16-operand chunk pipeline and the
 gradients are rounded to that dtype, 2^-11 and 2^-8 relative; measured
