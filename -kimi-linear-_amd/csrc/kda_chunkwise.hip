@@ -1420,9 +1420,24 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         }
         uint32_t vr[NCH][CG][KN::VW];
 #pragma unroll
-        for (int j = 0; j < NCH; ++j)
+        for (int j = 0; j < NCH; ++j) {
 #pragma unroll
             for (int g = 0; g < CG; ++g) kn.v_load(vr[j][g], j, g);
+            // a chunk's v loads are followed by its output stores in the loop
+            // below: stores that write nothing (an empty buffer range) stand in
+            // for them here, so that the loop is entered with the pattern of
+            // outstanding vector memory operations it repeats.  The compiler's
+            // count at the loop head is then exact; with the entry path's
+            // smaller count each chunk's wait for its v tile also waited for
+            // the output stores of the chunks before it.
+            if constexpr (!EPI && !TRANS && !CKPT) {
+                // (distinct offsets: identical stores would be merged away)
+                const auto none = make_rsrc(a.o, 0u);
+#pragma unroll
+                for (int i = 0; i < CG * CB; ++i)
+                    __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (CG * CB * j + i), 0);
+            }
+        }
         uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
         typename KN::Pend pd[NCH];
         if constexpr (EPI) {
