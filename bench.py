@@ -364,17 +364,17 @@ def layer_bench(pkg, torch, reps=10):
             "decode_B64_graph_us_per_token": decode_us}
 
 
-def backward_bench(pkg, wl, torch, reps=3):
+def backward_bench(pkg, wl, torch, reps=3, untimed=2):
     """kda_chunkwise forward + native backward under autograd at the chunkwise
     benchmark shape (fp16 q/k/v, fp32 g/beta, fp32 state from zeros)."""
     inp = wl.make_inputs(B1, T1, H1, D1, D1, device="cuda", seed=1, qkv_dtype=torch.float16)
     xs = [inp[n].clone().requires_grad_(True) for n in ("q", "k", "v", "g", "beta")]
     gen = torch.Generator(device="cuda").manual_seed(3)
     d_o = torch.randn(B1, T1, H1, D1, device="cuda", dtype=torch.float16, generator=gen)
-    # two untimed steps, then `reps` steps queued back to back (no host
+    # `untimed` steps, then `reps` steps queued back to back (no host
     # synchronisation between them, as in a training loop), HIP events around
     # each step's forward and backward on the stream they run on
-    for _ in range(2):
+    for _ in range(untimed):
         for x in xs:
             x.grad = None
         o, _ = pkg.kda_chunkwise(*xs, chunk_size=C1, state_dtype=torch.float32)
@@ -577,7 +577,7 @@ def main():
             result.update({"value": us_hbm, "unit": "us/step", "higher_is_better": False,
                            "ms_per_step": us_hbm / 1e3})
     if args.only in (None, "backward"):
-        result["backward"] = backward_bench(pkg, wl, torch)
+        result["backward"] = backward_bench(pkg, wl, torch, reps=max(3, args.steps), untimed=5)
         if "value" not in result:
             result.update({"value": result["backward"]["train_tokens_per_s"], "unit": "tokens/s",
                            "ms_per_step": result["backward"]["forward_ckpt_ms"] + result["backward"]["backward_ms"]})
