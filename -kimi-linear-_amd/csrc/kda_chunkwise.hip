@@ -1040,6 +1040,62 @@ struct Kern {
         }
     }
 
+    // A 16-bit output fragment (4 columns) packed two values a word.
+    static __device__ __forceinline__ u2 pack4(const f4& O) {
+        if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+            return __builtin_bit_cast(u2, to_h4(O));
+        } else {
+            u2 w;
+            w[0] = static_cast<uint32_t>(f32_to_bf16_bits(O[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(O[1])) << 16);
+            w[1] = static_cast<uint32_t>(f32_to_bf16_bits(O[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(O[3])) << 16);
+            return w;
+        }
+    }
+    // Output stores of a chunk, 16-bit TQ: per 16-row tile a lane holds 4
+    // adjacent columns (lane group lg: columns 4 lg .. 4 lg + 3) of two
+    // fragments x and y (CG = 1: the chunk's two blocks; CG = 2: the wave's two
+    // column groups of one block).  One v_permlane16_swap per register trades
+    // x of the odd lane groups for y of the even ones, after which lane group
+    // lg holds 8 adjacent columns 8 (lg / 2) .. + 7 of x (lg even) or y (lg
+    // odd): one 16-byte store instead of two 8-byte ones.
+    static constexpr int kOutStores = sizeof(TQ) == 2 ? (CG == 1 ? 1 : CB * CG / 2) : CB * CG;
+    __device__ void store_pair(const f4& x, const f4& y, __amdgpu_buffer_rsrc_t r, int vo) const {
+        const u2 px = pack4(x), py = pack4(y);
+        const auto s0 = __builtin_amdgcn_permlane16_swap(px[0], py[0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(px[1], py[1], false, false);
+        __builtin_amdgcn_raw_buffer_store_b128(u4{s0[0], s1[0], s0[1], s1[1]}, r, vo, 0, 0);
+    }
+    __device__ void store_chunk(const f4 (&O)[CG][CB], int blk, int64_t colw) const {
+        static_assert(CG == 1 || CG == 2, "output tiles of one or two column groups");
+        if constexpr (sizeof(TQ) == 4) {
+#pragma unroll
+            for (int g = 0; g < CG; ++g) {
+                store_row4(O[g][0], blk, colw + 16 * g);
+                store_row4(O[g][1], blk + 1, colw + 16 * g);
+            }
+        } else {
+            const int64_t rs = a.H * a.V;                    // token row stride, elements
+            const int64_t e = (b * T + static_cast<int64_t>(blk) * BT) * rs + h * a.V;
+            constexpr int64_t es = sizeof(TQ);
+            if constexpr (CG == 1) {
+                // lane group lg: row ln of block lg % 2, columns 8 (lg / 2) ..
+                const auto r = make_rsrc(static_cast<TQ*>(a.o) + e,
+                                         static_cast<uint32_t>((rows_in(blk) + rows_in(blk + 1)) * rs * es));
+                const int vo = static_cast<int>(((ln + BT * (lg & 1)) * rs + colw + 8 * (lg >> 1)) * es);
+                store_pair(O[0][0], O[0][1], r, vo);
+            } else {
+                // lane group lg: row ln, columns 16 (lg % 2) + 8 (lg / 2) ..
+                const int vo = static_cast<int>((ln * rs + colw + 16 * (lg & 1) + 8 * (lg >> 1)) * es);
+#pragma unroll
+                for (int bk = 0; bk < CB; ++bk) {
+                    const auto r = make_rsrc(static_cast<TQ*>(a.o) + e + BT * bk * rs,
+                                             static_cast<uint32_t>(rows_in(blk + bk) * rs * es));
+                    store_pair(O[0][bk], O[1][bk], r, vo);
+                }
+            }
+        }
+    }
+
     // EPI: a chunk's outputs, rounded to TQ as the reference's o_core is and
     // held as TQ bits (two a word) over one barrier while the other consumer
     // waves' row sums of squares arrive, with the output gate's
@@ -1298,11 +1354,7 @@ struct Kern {
             }
             pd.blk = blk;
         } else if constexpr (!TRANS) {
-#pragma unroll
-            for (int g = 0; g < CG; ++g) {
-                store_row4(O[g][0], blk, colw + 16 * g);
-                store_row4(O[g][1], blk + 1, colw + 16 * g);
-            }
+            store_chunk(O, blk, colw);
         }
         // S <- E[31] S + F^T P over both blocks: the k-major line of channel
         // 16t + ln gives tokens 4lg..4lg+3 of block 0 then of block 1, the
@@ -1434,8 +1486,8 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
                 // (distinct offsets: identical stores would be merged away)
                 const auto none = make_rsrc(a.o, 0u);
 #pragma unroll
-                for (int i = 0; i < CG * CB; ++i)
-                    __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (CG * CB * j + i), 0);
+                for (int i = 0; i < KN::kOutStores; ++i)
+                    __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (KN::kOutStores * j + i), 0);
             }
         }
         uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
