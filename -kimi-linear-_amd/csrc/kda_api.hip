@@ -127,7 +127,7 @@ int kda_chunkwise_gated_fwd(const kda_fwd_args* args, const kda_gate_args* gate,
 size_t kda_chunkwise_long_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t segments) {
     if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0 || segments < 1) return 0;
     if (B * H > (int64_t{1} << 31) || K > 4096 || V > 4096 || segments > (int64_t{1} << 20)) return 0;
-    return static_cast<size_t>(kda::long_workspace_bytes(B, H, K, V, segments));
+    return static_cast<size_t>(kda::long_workspace_bytes(B, T, H, K, V, segments));
 }
 
 int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* workspace, void* stream) {

@@ -411,8 +411,12 @@ __device__ __forceinline__ f4 mm_f32(const f4& xt, const f4& y, f4 c) {
 // TRANS: the first pass of a split long sequence (kda_chunkwise_long_fwd):
 // state columns V .. V + K carry the chain's transition -- they start from
 // the identity and see v = 0 -- beside the V columns of its own state from
-// zero; no o is written.
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false>
+// zero; no o is written, unless TOUT: then the outputs of every state column
+// are written in fp32, those of the V columns (the outputs from a zero
+// initial state) to o, those of the transition columns (per token, the
+// coefficients of the initial state in the outputs) to a second buffer.
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false,
+          bool TOUT = false>
 struct Kern {
     static constexpr int KT = K / 16;                   // 16-row state tiles
     static constexpr int KU = K / 32;                   // 32-wide k blocks
@@ -465,6 +469,7 @@ struct Kern {
     // head's first V-tile workgroup only (null otherwise): per 32-token chunk
     // the state and R ((K + 32) x V) and then A, L and N (32 x 32 each)
     float* ckm = nullptr;
+    float* cout = nullptr;                   // TOUT: the transition columns' outputs [B, T, H, K]
     int nblk = 0;                            // blocks of the real chunks (records exist for these)
 
     // A, L, N of the chunk holding block blk (row-major 32 x 32, consecutive)
@@ -1096,6 +1101,25 @@ struct Kern {
         }
     }
 
+    // TOUT: a chunk's outputs in fp32, the V columns' to o ([B, T, H, V]
+    // fp32), the transition columns' to cout ([B, T, H, K]); the choice is
+    // wave-uniform and taken by selecting the base, not by a branch.
+    __device__ void store_fp32_chunk(const f4 (&O)[CG][CB], int blk, int64_t colw) const {
+        const bool tr = vzero;
+        float* base = tr ? cout : static_cast<float*>(a.o);
+        const int64_t W = tr ? K : a.V, col = tr ? colw - a.V : colw;
+        const int64_t rs = a.H * W;
+        const int64_t e = (b * T + static_cast<int64_t>(blk) * BT) * rs + h * W;
+#pragma unroll
+        for (int bk = 0; bk < CB; ++bk) {
+            const auto r = make_rsrc(base + e + BT * bk * rs, static_cast<uint32_t>(rows_in(blk + bk) * rs * 4));
+#pragma unroll
+            for (int g = 0; g < CG; ++g)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, O[g][bk]), r,
+                                                       static_cast<int>((ln * rs + col + 16 * g + 4 * lg) * 4), 0, 0);
+        }
+    }
+
     // EPI: a chunk's outputs, rounded to TQ as the reference's o_core is and
     // held as TQ bits (two a word) over one barrier while the other consumer
     // waves' row sums of squares arrive, with the output gate's
@@ -1353,6 +1377,8 @@ struct Kern {
                 if (lg == 0) sm.rows.p[par][bk][ln][wave] = ss;
             }
             pd.blk = blk;
+        } else if constexpr (TOUT) {
+            store_fp32_chunk(O, blk, colw);
         } else if constexpr (!TRANS) {
             store_chunk(O, blk, colw);
         }
@@ -1381,11 +1407,14 @@ struct Kern {
 // barriers; every prefetch is issued unconditionally (a block past T loads
 // zeros).  The chunks cover T rounded up to whole chunks: a padded block
 // (all rows past T) is neutral and is built like any other.
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false, bool CKPT = false>
+// ckpt: CKPT, the chunk records; TOUT, the transition columns' outputs.
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false, bool CKPT = false,
+          bool TOUT = false>
 __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd_args a, float* ckpt,
                                                                    const kda_gate_args gate,
                                                                    const kda_out_epilogue epi) {
-    using KN = Kern<K, NC, TQ, GATED, CG, EPI, TRANS>;
+    static_assert(!TOUT || TRANS, "fp32 outputs belong to the transition pass");
+    using KN = Kern<K, NC, TQ, GATED, CG, EPI, TRANS, TOUT>;
     constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
     __shared__ Smem<K, CG, EPI> sm;
@@ -1426,6 +1455,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     if constexpr (CKPT) {
         if (ckpt != nullptr && vt == 0) kn.ckm = ckpt + (kn.b * H + kn.h) * ncc * ckpt_record(K, V);
     }
+    if constexpr (TOUT) kn.cout = ckpt;
     const int nss = (ncc + NCH - 1) / NCH;               // supersteps
 
     const bool consumer = wave < NC;
@@ -1482,12 +1512,13 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             // count at the loop head is then exact; with the entry path's
             // smaller count each chunk's wait for its v tile also waited for
             // the output stores of the chunks before it.
-            if constexpr (!EPI && !TRANS && !CKPT) {
+            if constexpr (!EPI && !CKPT && (!TRANS || TOUT)) {
                 // (distinct offsets: identical stores would be merged away)
+                constexpr int ns = TOUT ? CB * CG : KN::kOutStores;
                 const auto none = make_rsrc(a.o, 0u);
 #pragma unroll
-                for (int i = 0; i < KN::kOutStores; ++i)
-                    __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (KN::kOutStores * j + i), 0);
+                for (int i = 0; i < ns; ++i)
+                    __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (ns * j + i), 0);
             }
         }
         uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
@@ -1578,11 +1609,12 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
     }
 }
 
-template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false, bool CKPT = false>
+template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false, bool CKPT = false,
+          bool TOUT = false>
 int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args& gate,
                const kda_out_epilogue& epi = kda_out_epilogue{}) {
     const int64_t blocks = a.B * a.H * ((a.V + (TRANS ? K : 0)) / (16 * NC * CG));
-    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI, TRANS, CKPT>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((chunkwise_kernel<K, NC, TQ, GATED, CG, EPI, TRANS, CKPT, TOUT>), dim3(static_cast<unsigned>(blocks)),
                        dim3(64 * (NC + NB)), 0, stream, a, ckpt, gate, epi);
     return hipGetLastError() == hipSuccess ? KDA_OK : KDA_ERR_LAUNCH;
 }
@@ -1591,10 +1623,14 @@ int launch_knq(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda
 // columns and the K transition columns (128-column tiles when they would
 // outnumber the CUs).
 template <int K, typename TQ>
-int launch_trans(const kda_fwd_args& a, hipStream_t stream) {
+int launch_trans(const kda_fwd_args& a, hipStream_t stream, float* cout) {
     const kda_gate_args none{nullptr, nullptr};
-    if (a.B * a.H * ((a.V + K) / 64) > 256 && (a.V + K) % 128 == 0)
-        return launch_knq<K, 4, TQ, false, 2, false, true>(a, stream, nullptr, none);
+    const bool wide = a.B * a.H * ((a.V + K) / 64) > 256 && (a.V + K) % 128 == 0;
+    if (cout != nullptr) {
+        if (wide) return launch_knq<K, 4, TQ, false, 2, false, true, false, true>(a, stream, cout, none);
+        return launch_knq<K, 4, TQ, false, 1, false, true, false, true>(a, stream, cout, none);
+    }
+    if (wide) return launch_knq<K, 4, TQ, false, 2, false, true>(a, stream, nullptr, none);
     return launch_knq<K, 4, TQ, false, 1, false, true>(a, stream, nullptr, none);
 }
 
@@ -1736,13 +1772,13 @@ bool chunkwise_trans_supported(const kda_fwd_args& a) {
            (a.qkv_dtype == KDA_DTYPE_F16 || a.qkv_dtype == KDA_DTYPE_BF16);
 }
 
-int chunkwise_trans_launch(const kda_fwd_args& a, hipStream_t stream) {
+int chunkwise_trans_launch(const kda_fwd_args& a, hipStream_t stream, float* cout) {
     const int st = chunkwise_check(a, false);
     if (st != KDA_OK) return st;
     if (!chunkwise_trans_supported(a)) return KDA_ERR_UNSUPPORTED;
     if (a.qkv_dtype == KDA_DTYPE_F16)
-        return a.K == 64 ? launch_trans<64, _Float16>(a, stream) : launch_trans<128, _Float16>(a, stream);
-    return a.K == 64 ? launch_trans<64, bf16_t>(a, stream) : launch_trans<128, bf16_t>(a, stream);
+        return a.K == 64 ? launch_trans<64, _Float16>(a, stream, cout) : launch_trans<128, _Float16>(a, stream, cout);
+    return a.K == 64 ? launch_trans<64, bf16_t>(a, stream, cout) : launch_trans<128, bf16_t>(a, stream, cout);
 }
 
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt, const kda_gate_args* gate) {

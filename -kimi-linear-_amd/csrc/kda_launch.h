@@ -31,9 +31,11 @@ int chunkwise_check(const kda_fwd_args& a, bool gated = false);
 int chunkwise_launch(const kda_fwd_args& a, hipStream_t stream, float* ckpt = nullptr,
                      const kda_gate_args* gate = nullptr);
 // The first pass of a split long sequence (kda_chunkwise_long_fwd): per chain
-// the state from zero and the transition, state_out [B, H, K, V + K] fp32.
+// the state from zero and the transition, state_out [B, H, K, V + K] fp32;
+// with cout, also the outputs in fp32: o [B, T, H, V] from the zero state and
+// cout [B, T, H, K] those of the transition columns.
 bool chunkwise_trans_supported(const kda_fwd_args& a);
-int chunkwise_trans_launch(const kda_fwd_args& a, hipStream_t stream);
+int chunkwise_trans_launch(const kda_fwd_args& a, hipStream_t stream, float* cout = nullptr);
 // The chunkwise forward with the layer's output epilogue (kda_chunkwise_fused_fwd).
 bool chunkwise_fused_supported(const kda_fwd_args& a);
 int chunkwise_fused_launch(const kda_fwd_args& a, hipStream_t stream, const kda_gate_args* gate,
@@ -41,7 +43,7 @@ int chunkwise_fused_launch(const kda_fwd_args& a, hipStream_t stream, const kda_
 
 // Long sequences split into segments (kda_long.hip): workspace bytes for P
 // segments, and the three passes (T % P == 0, checked by the caller).
-int64_t long_workspace_bytes(int64_t B, int64_t H, int64_t K, int64_t V, int64_t P);
+int64_t long_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t P);
 int long_launch(const kda_fwd_args& a, int64_t P, void* workspace, hipStream_t stream);
 
 // Chunkwise backward (kda_chunkwise_bwd.hip).

@@ -280,32 +280,46 @@ CKPT_SPACING = 32   # tokens between the forward's state checkpoints (kda_chunkw
 def ckpt_record(K: int, V: int) -> int:
     """Floats of one chunk's record in kda_chunkwise_fwd_ckpt's output."""
     return (K + CKPT_SPACING) * V + 3 * CKPT_SPACING * CKPT_SPACING
-LONG_MIN_SEGMENT = 1024    # shortest segment worth a split (kda_chunkwise_long_fwd)
+LONG_MIN_SEGMENT = 1024    # shortest segment worth the three-pass split (kda_chunkwise_long_fwd)
+FEW_CHAIN_MIN_SEGMENT = 256   # shortest segment of the few-chain form
 CU_COUNT = 256
 
 
 def long_segments(B, T, H, K, V, dtype) -> int:
-    """Segments for kda_chunkwise_long_fwd: the largest power of two that keeps
-    the third pass (every segment's chain from its true initial state) within
-    one round of workgroups on the 256 CUs -- 128-column workgroups when V is a
-    multiple of 128 (the chunk kernel takes them once 64-column ones would
-    outnumber the CUs), else 64-column ones -- and segments of at least
-    LONG_MIN_SEGMENT tokens; 1 (one pass) when the chains alone fill half the
-    CUs, when fewer than 4 segments would result, or when the shape has no
-    split kernel.  At B=1 T=32768 H=16 d=128: 16 segments (0.60 ms against
-    0.68 ms with 8, whose third pass fills one round of 64-column
-    workgroups).  The split pays roughly one superstep of the first pass (the
-    transition columns) and one of the third for every superstep of a
-    segment, against one superstep per 64 tokens in one pass: with 2
-    segments it is slower (B=3 T=2048 H=16: 253 against ~180 us), from 4 on
-    faster (B=1 T=4096: 174 against ~300 us)."""
+    """Segments for kda_chunkwise_long_fwd; 1 (one pass) when the chains alone
+    fill half the CUs or the shape has no split kernel.
+
+    With V + K a multiple of 128 and V <= 256 the split takes its few-chain
+    form whenever its first pass (every segment's state columns and transition
+    columns, 128-column workgroups) fits one round of workgroups: the first
+    pass then also keeps the outputs from a zero state and their initial-state
+    coefficients, and a short pass adds the coefficients times the composed
+    initial states.  So P is the largest power of two with B P H (V + K) / 128
+    <= the CUs and segments of at least FEW_CHAIN_MIN_SEGMENT tokens.
+    Measured (fp16, H=16, d=128, us): B=1 T=32768 543 with 8 segments (600
+    with 16 in three passes), B=1 T=16384 301 (331), B=1 T=4096 95 with 8
+    (293 in one pass), B=2 T=2048 84 with 4 (150), B=3 T=2048 138 with 2
+    (150); B=4 T=2048 161 with 2 against 156 in one pass (the chains fill
+    half the CUs: one pass).
+
+    Otherwise the three-pass form: the largest power of two that keeps the
+    third pass (every segment's chain from its true initial state) within one
+    round of workgroups -- 128-column workgroups when V is a multiple of 128,
+    else 64-column ones -- and segments of at least LONG_MIN_SEGMENT tokens,
+    and 1 when fewer than 4 segments would result (with 2 the split is slower
+    than one pass)."""
     if dtype not in (torch.float16, torch.bfloat16) or K not in (64, 128) or V % 64 != 0:
         return 1
     tiles = B * H * (V // 64)
-    if tiles == 0 or 2 * tiles > CU_COUNT:
+    if tiles == 0 or 2 * tiles >= CU_COUNT:
         return 1
-    units = B * H * (V // 128) if V % 128 == 0 else tiles
     P = 1
+    if (V + K) % 128 == 0 and V <= 256:
+        units = B * H * ((V + K) // 128)
+        while (2 * P * units <= CU_COUNT and T % (2 * P) == 0 and T // (2 * P) >= FEW_CHAIN_MIN_SEGMENT):
+            P *= 2
+        return P
+    units = B * H * (V // 128) if V % 128 == 0 else tiles
     while (2 * P * units <= CU_COUNT and T % (2 * P) == 0 and T // (2 * P) >= LONG_MIN_SEGMENT):
         P *= 2
     return P if P >= 4 else 1

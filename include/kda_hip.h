@@ -172,7 +172,11 @@ int kda_chunkwise_fused_fwd(const kda_fwd_args* args, const kda_gate_args* gate,
  * S_start + S_loc): a first pass computes every segment's S_loc and Phi
  * (K x K), a short sequential pass composes them (the segments' initial
  * states and the final state, fp32), and a second pass writes the outputs
- * from the true initial states.  Same arguments and results as
+ * from the true initial states.  When the first pass fits one round of
+ * workgroups (B * segments * H * (V + K) / 128 <= the compute units), it also
+ * writes the outputs from a zero initial state and, per token, their
+ * coefficients of the initial state, and the second pass is o = those
+ * outputs + coefficients x initial state.  Same arguments and results as
  * kda_chunkwise_fwd (the same function, rounded differently), for q, k, v
  * fp16 or bf16, K in {64, 128}, V a multiple of 64, T % segments == 0 and,
  * with B > 1, each input's batch stride T times its token stride

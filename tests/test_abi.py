@@ -194,7 +194,11 @@ def test_long_host_validation_codes(native):
     assert call(ctypes.byref(_args(native, B=0, **f16)), 2, None, None) == 0
     size = lib.kda_chunkwise_long_workspace_size
     # per segment and head: S_loc and Phi (K x (V + K)) and the initial state (K x V), fp32
-    assert size(1, 32768, 16, 128, 128, 8) == 4 * 8 * 16 * 128 * (2 * 128 + 128)
+    # 16 segments of 16 heads: the first pass takes two rounds of 128-column
+    # workgroups (three passes); 8 segments: one round (the few-chain form,
+    # which also keeps the fp32 outputs and their initial-state coefficients)
+    assert size(1, 32768, 16, 128, 128, 16) == 4 * 16 * 16 * 128 * (2 * 128 + 128)
+    assert size(1, 32768, 16, 128, 128, 8) == 4 * (8 * 16 * 128 * (2 * 128 + 128) + 32768 * 16 * (128 + 128))
     assert size(1, 64, 1, 64, 64, 0) == 0
 
 

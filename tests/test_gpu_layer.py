@@ -186,7 +186,7 @@ def test_layer_fused_output_vs_oracle(kda_pkg, dtype, hd, T):
 
 def test_layer_long_prefill_takes_the_split_core(kda_pkg, monkeypatch):
     """One long sequence over few heads: the pre-processing kernel forms g and
-    beta and the ungated core splits the body into 4 parallel segments (the
+    beta and the ungated core splits the body into parallel segments (the
     gated core has no split).  Output and recurrent state against the oracle
     and against the same layer run with the split turned off."""
     layer_mod = __import__("kimi_linear_amd.layer", fromlist=["long_segments"])
@@ -194,7 +194,7 @@ def test_layer_long_prefill_takes_the_split_core(kda_pkg, monkeypatch):
     m, cfg, p = make_layer(kda_pkg, dtype, seed=5)
     la = cfg.linear_attn_config
     T = 4096 + 22                                   # body of 4096 + recurrent tail
-    assert layer_mod.long_segments(1, 4096, la["num_heads"], la["head_dim"], la["value_head_dim"], dtype) == 4
+    assert layer_mod.long_segments(1, 4096, la["num_heads"], la["head_dim"], la["value_head_dim"], dtype) >= 4
     x = make_x(1, T, 256, dtype, seed=6)
     print(f"[layer long prefill fp16 B=1 T={T} H={la['num_heads']}]", flush=True)
     with torch.no_grad():

@@ -3,7 +3,10 @@
 A long sequence with few (batch, head) chains is cut into segments that run
 in parallel: per segment the state from zero and the K x K transition, a
 sequential composition of the segments in fp32, then the outputs from the
-true initial states.  The result is the same function as one pass, rounded
+true initial states -- with few chains (the first pass in one round of
+workgroups) as the outputs from a zero state, which the first pass keeps in
+fp32, plus their initial-state coefficients (the transition columns'
+outputs) times the composed initial states.  The result is the same function as one pass, rounded
 differently: against the oracle at the core bars (fp16 inputs: o max-abs
 <= 2e-3, state relative error <= 1e-3), against one pass to 1e-3, and the
 transitions are checked on their own by a zero-input case (the state then
@@ -104,6 +107,32 @@ def test_long_split_matches_oracle_and_one_pass(kda_pkg, wl, native, K, dtype, s
     assert d_o <= (1e-3 if dtype == torch.float16 else 4e-3) and d_s <= 1e-3
 
 
+def test_long_split_three_passes_at_many_chains(kda_pkg, wl, native):
+    """64 heads in 4 segments: the first pass takes two rounds of 128-column
+    workgroups, so the outputs come from the third pass over every chain from
+    its true initial state (the cases above, with few chains, take the
+    outputs from a zero state plus their initial-state coefficients times the
+    composed initial states).  Against one pass and, on three heads, the
+    oracle, with weak decays (each segment's initial state matters)."""
+    B, T, H, K, V, segments = 1, 2048, 64, 128, 128, 4
+    print(f"long split B={B} T={T} H={H} K={K} V={V} fp16 segments={segments} (three passes)", flush=True)
+    cpu = wl.make_inputs(B, T, H, K, V, seed=61, qkv_dtype=torch.float16, state_std=0.02)
+    cpu["g"] = cpu["g"] * 1e-3
+    inp = {n: (t.to(DEV) if t is not None else None) for n, t in cpu.items()}
+    with torch.no_grad():
+        o, s = long_call(native, inp, segments)
+        o1, s1 = long_call(native, inp, 1)
+    d_o, d_s = rel(o, o1), rel(s, s1)
+    sub = {n: (t[:, :, 0:64:31] if n != "state" else t[:, 0:64:31]) for n, t in cpu.items()}
+    o_ref, s_ref = kda_chunkwise_ref(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"],
+                                     initial_state=sub["state"], chunk_size=64, state_dtype=torch.float32)
+    eo, es = max_abs(o[:, :, 0:64:31], o_ref), rel(s[:, 0:64:31], s_ref)
+    print(f"  vs oracle: o max-abs {eo:.2e} state rel {es:.2e}; vs one pass: o {d_o:.2e} state {d_s:.2e}",
+          flush=True)
+    assert eo <= O_TOL and es <= S_TOL
+    assert d_o <= 1e-3 and d_s <= 1e-3
+
+
 def test_long_split_zero_inputs_carry_the_state(kda_pkg, wl, native):
     """v = 0 and k = 0: no write, the state only decays -- every segment's
     transition is then Diag(prod a) -- so the split state must be the product
@@ -127,15 +156,15 @@ def test_long_split_zero_inputs_carry_the_state(kda_pkg, wl, native):
 
 
 def test_wrapper_split_with_partial_last_chunks(kda_pkg, wl, native):
-    """B=1 T=4160 H=16: the wrapper splits into 4 segments of 1040 tokens, so
-    every segment ends half-way through a 32-token chunk.  The rows past a
+    """B=1 T=4160 H=16: the wrapper splits into 8 segments of 520 tokens, so
+    every segment ends part-way through a 32-token chunk.  The rows past a
     segment's end must read as zero (not as the next segment's first tokens)
     in both the transition pass and the output pass: the wrapper's result
     against one pass and against the oracle on three heads."""
     kda = __import__("kimi_linear_amd.kda", fromlist=["long_segments"])
     B, T, H, K, V = 1, 4160, 16, 128, 128
-    assert kda.long_segments(B, T, H, K, V, torch.float16) == 4 and (T // 4) % 32 != 0
-    print(f"long split through the wrapper, B={B} T={T} H={H}: 4 segments of {T // 4} tokens", flush=True)
+    assert kda.long_segments(B, T, H, K, V, torch.float16) == 8 and (T // 8) % 32 != 0
+    print(f"long split through the wrapper, B={B} T={T} H={H}: 8 segments of {T // 8} tokens", flush=True)
     cpu = wl.make_inputs(B, T, H, K, V, seed=51, qkv_dtype=torch.float16, state_std=0.02)
     cpu["g"] = cpu["g"] * 1e-3                      # weak decay: each segment's initial state matters
     inp = {n: (t.to(DEV) if t is not None else None) for n, t in cpu.items()}
@@ -157,10 +186,12 @@ def test_wrapper_split_with_partial_last_chunks(kda_pkg, wl, native):
 def test_wrapper_splits_the_config3_shape(kda_pkg):
     """The wrapper picks the split for one long sequence of 16 heads."""
     kda = __import__("kimi_linear_amd.kda", fromlist=["long_segments"])
-    assert kda.long_segments(1, 32768, 16, 128, 128, torch.float16) == 16
-    assert kda.long_segments(1, 32768, 16, 128, 64, torch.float16) == 16
+    assert kda.long_segments(1, 32768, 16, 128, 128, torch.float16) == 8     # few-chain form
+    assert kda.long_segments(1, 32768, 16, 128, 64, torch.float16) == 16     # V + K = 192: three passes
     assert kda.long_segments(1, 8192, 16, 128, 128, torch.float16) == 8
     assert kda.long_segments(8, 4096, 16, 128, 128, torch.float16) == 1
-    assert kda.long_segments(1, 4096, 16, 128, 128, torch.float16) == 4
-    assert kda.long_segments(2, 2048, 16, 128, 128, torch.float16) == 1    # 2 segments: one pass is faster
+    assert kda.long_segments(1, 4096, 16, 128, 128, torch.float16) == 8
+    assert kda.long_segments(2, 2048, 16, 128, 128, torch.float16) == 4
+    assert kda.long_segments(3, 2048, 16, 128, 128, torch.float16) == 2
+    assert kda.long_segments(4, 2048, 16, 128, 128, torch.float16) == 1     # the chains fill half the CUs
     assert kda.long_segments(1, 32768, 16, 128, 128, torch.float32) == 1
