@@ -779,7 +779,12 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     float deps = 0.f;
     // one column step: stage the fetched tiles, then (after the caller's
     // fetch of what comes next and a barrier) the products
+    // fp16 activations: every operand of the column sums (dO, and S, R,
+    // dS_end, dP, dR as recorded) is an fp16 value, so each product is one
+    // fp16 MFMA, exact with fp32 accumulation; the tiles hold the raw fp16
+    // values ([0] only) and the S and dS fragments are used as fetched
     bf8 sh, sl, dsh, dsl;
+    h8 sh16, dsh16;
     auto stage = [&](int vt) {
         use_here(fS);
         use_here(fdS);
@@ -794,10 +799,17 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
             const float r = HALF ? raw_f32<_Float16>(fR[m]) : __uint_as_float(fR[m]);
             const float dp = HALF ? raw_f32<_Float16>(fdP[m]) : __uint_as_float(fdP[m]);
             const float dr = HALF ? raw_f32<_Float16>(fdR[m]) : __uint_as_float(fdR[m]);
-            split_bf16(r, sm.R[0][c][tv], sm.R[1][c][tv]);
-            split_bf16(dp, sm.dP[0][c][tv], sm.dP[1][c][tv]);
-            split_bf16(dr, sm.dR[0][c][tv], sm.dR[1][c][tv]);
-            split_bf16(raw_f32<TI>(fdO[m]), sm.dO[0][c][tv], sm.dO[1][c][tv]);
+            if constexpr (HALF) {
+                sm.R[0][c][tv] = static_cast<uint16_t>(fR[m]);
+                sm.dP[0][c][tv] = static_cast<uint16_t>(fdP[m]);
+                sm.dR[0][c][tv] = static_cast<uint16_t>(fdR[m]);
+                sm.dO[0][c][tv] = static_cast<uint16_t>(fdO[m]);
+            } else {
+                split_bf16(r, sm.R[0][c][tv], sm.R[1][c][tv]);
+                split_bf16(dp, sm.dP[0][c][tv], sm.dP[1][c][tv]);
+                split_bf16(dr, sm.dR[0][c][tv], sm.dR[1][c][tv]);
+                split_bf16(raw_f32<TI>(fdO[m]), sm.dO[0][c][tv], sm.dO[1][c][tv]);
+            }
             if (c < nrow)
                 Elem<TI>::st(dvp + ((b * T + r0 + c) * H + h) * V + static_cast<int64_t>(vt) * VT + tv, dr);
         }
@@ -813,22 +825,37 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
             }
             deps = fmaf(sv[e], dsv[e], deps);
         }
-        split8(sv, sh, sl);
-        split8(dsv, dsh, dsl);
+        if constexpr (HALF) {
+            sh16 = __builtin_bit_cast(h8, w4{fS[0], fS[1], fS[2], fS[3]});
+            dsh16 = __builtin_bit_cast(h8, w4{fdS[0], fdS[1], fdS[2], fdS[3]});
+        } else {
+            split8(sv, sh, sl);
+            split8(dsv, dsh, dsl);
+        }
     };
     auto products = [&]() {
 #pragma unroll
         for (int m = 0; m < MPW; ++m) {
             const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
             const uint16_t (*xa)[CT][VB] = tt < 4 ? sm.dO : sm.dP;
-            accm[m] = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], sm.R[0][c0t + ln], sm.R[1][c0t + ln], lg, accm[m]);
+            if constexpr (HALF)
+                accm[m] = mfma16x16x32(*reinterpret_cast<const h8*>(&xa[0][r0t + ln][8 * lg]),
+                                       *reinterpret_cast<const h8*>(&sm.R[0][c0t + ln][8 * lg]), accm[m]);
+            else
+                accm[m] = mm_pair(xa[0][r0t + ln], xa[1][r0t + ln], sm.R[0][c0t + ln], sm.R[1][c0t + ln], lg, accm[m]);
         }
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int er = 16 * p + ln;
-            dqe[p] = mm_pair_r(sm.dO[0][er], sm.dO[1][er], sh, sl, lg, dqe[p]);
-            dke[p] = mm_pair_r(sm.dR[0][er], sm.dR[1][er], sh, sl, lg, dke[p]);
-            dkf[p] = mm_pair_r(sm.R[0][er], sm.R[1][er], dsh, dsl, lg, dkf[p]);
+            if constexpr (HALF) {
+                dqe[p] = mfma16x16x32(*reinterpret_cast<const h8*>(&sm.dO[0][er][8 * lg]), sh16, dqe[p]);
+                dke[p] = mfma16x16x32(*reinterpret_cast<const h8*>(&sm.dR[0][er][8 * lg]), sh16, dke[p]);
+                dkf[p] = mfma16x16x32(*reinterpret_cast<const h8*>(&sm.R[0][er][8 * lg]), dsh16, dkf[p]);
+            } else {
+                dqe[p] = mm_pair_r(sm.dO[0][er], sm.dO[1][er], sh, sl, lg, dqe[p]);
+                dke[p] = mm_pair_r(sm.dR[0][er], sm.dR[1][er], sh, sl, lg, dke[p]);
+                dkf[p] = mm_pair_r(sm.R[0][er], sm.R[1][er], dsh, dsl, lg, dkf[p]);
+            }
         }
     };
     for (int vt = 0; vt + 1 < nvt; ++vt) {
