@@ -273,6 +273,51 @@ __device__ __forceinline__ void put_pairs(uint16_t* hi, uint16_t* lo, const floa
     }
 }
 
+// fp16 activations run the chain on single fp16 operands (the [0] arrays
+// only, holding fp16 values) and the fp16 matrix cores: the precision of the
+// reference's fp16 path, which takes q E, k E, k F, A, M and the state in
+// fp16 for its products (kimi_linear/kda.py:163-182) and so differentiates
+// them in fp16; dS_end, dP and dR are kept in fp16 for the chunk kernel as
+// it is.  Other dtypes keep the bf16 pairs.
+template <bool H16>
+__device__ __forceinline__ void put4v(uint16_t* hi, uint16_t* lo, const f4& x) {
+    if constexpr (H16) {
+        uint16_t h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x[j]));
+        *reinterpret_cast<uint2*>(hi) = uint2{h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16)};
+        (void)lo;
+    } else {
+        put4_pair(hi, lo, x);
+    }
+}
+template <bool H16, int N>
+__device__ __forceinline__ void put_run(uint16_t* hi, uint16_t* lo, const float (&v)[N]) {
+    if constexpr (H16) {
+        static_assert(N == 2 || N == 4 || N == 8, "run length");
+        uint32_t hw[N / 2];
+#pragma unroll
+        for (int e = 0; e < N / 2; ++e)
+            hw[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * e]))) |
+                    (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * e + 1]))) << 16);
+        if constexpr (N == 2) *reinterpret_cast<uint32_t*>(hi) = hw[0];
+        else if constexpr (N == 4) *reinterpret_cast<w2*>(hi) = w2{hw[0], hw[1]};
+        else *reinterpret_cast<w4*>(hi) = w4{hw[0], hw[1], hw[2], hw[3]};
+        (void)lo;
+    } else {
+        put_pairs(hi, lo, v);
+    }
+}
+// acc += X Y^T over 32 contraction elements (rows xh / yh at the tile's row ln)
+template <bool H16>
+__device__ __forceinline__ f4 mmv(const uint16_t* xh, const uint16_t* xl, const uint16_t* yh, const uint16_t* yl,
+                                 int lg, f4 acc) {
+    if constexpr (H16)
+        return mfma16x16x32(*reinterpret_cast<const h8*>(xh + 8 * lg), *reinterpret_cast<const h8*>(yh + 8 * lg), acc);
+    else
+        return mm_pair(xh, xl, yh, yl, lg, acc);
+}
+
 // One workgroup per (b, h, VA state columns), the chunks in reverse.  dS, the
 // gradient of the state, stays in fp32 accumulators (tile ti = w + 16 m of
 // each wave: channels 16 (ti / VTL), columns 16 (ti % VTL)) and is copied as a
@@ -288,6 +333,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
     constexpr int TPW = (NTS + NWS - 1) / NWS;  // dS tiles per wave
     constexpr int APT = CT * CT / NS;       // elements of A (and of N) per thread
     static_assert(RPT >= 1 && DPT >= 1 && NDP <= NWS, "thread mapping");
+    constexpr bool H16 = std::is_same<TI, _Float16>::value;
     __shared__ StateSmem<K, VA> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
@@ -316,7 +362,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 accs[m][j] = a.d_state_out ? a.d_state_out[(bh * K + r0 + 4 * lg + j) * V + v0 + c0 + ln] : 0.f;
-            put4_pair(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
+            put4v<H16>(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
         }
     }
 
@@ -411,9 +457,9 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             }
 #pragma unroll
             for (int j = 0; j < DPT; ++j) vo[j] = raw_f32<TI>(pdo[j]);
-            put_pairs(&sm.AT[0][ai][ac0], &sm.AT[1][ai][ac0], va);
-            put_pairs(&sm.NT_[0][ai][ac0], &sm.NT_[1][ai][ac0], vn);
-            put_pairs(&sm.dOT[0][dv_][dc0], &sm.dOT[1][dv_][dc0], vo);
+            put_run<H16>(&sm.AT[0][ai][ac0], &sm.AT[1][ai][ac0], va);
+            put_run<H16>(&sm.NT_[0][ai][ac0], &sm.NT_[1][ai][ac0], vn);
+            put_run<H16>(&sm.dOT[0][dv_][dc0], &sm.dOT[1][dv_][dc0], vo);
         }
         if (t < CT) sm.beta[t] = __uint_as_float(pb[0]);
         fetch(n - 1);
@@ -436,10 +482,13 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 const float E = __expf(G), F = __expf(last - G);
                 qe[j] = a.scale * cq[j] * E;
                 ke[j] = ck[j] * E;
-                split_bf16(ck[j] * F, sm.kf[0][c][x], sm.kf[1][c][x]);
+                if constexpr (H16)
+                    sm.kf[0][c][x] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(ck[j] * F));
+                else
+                    split_bf16(ck[j] * F, sm.kf[0][c][x], sm.kf[1][c][x]);
             }
-            put_pairs(&sm.qeT[0][x][RPT * rg], &sm.qeT[1][x][RPT * rg], qe);
-            put_pairs(&sm.keT[0][x][RPT * rg], &sm.keT[1][x][RPT * rg], ke);
+            put_run<H16>(&sm.qeT[0][x][RPT * rg], &sm.qeT[1][x][RPT * rg], qe);
+            put_run<H16>(&sm.keT[0][x][RPT * rg], &sm.keT[1][x][RPT * rg], ke);
             if (rg == 0) sm.eps[x] = __expf(last);
         }
         __syncthreads();
@@ -472,9 +521,9 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < K / 32; ++u)
-                acc = mm_pair(&sm.kf[0][r0t + ln][32 * u], &sm.kf[1][r0t + ln][32 * u], &sm.dST[0][c0t + ln][32 * u],
+                acc = mmv<H16>(&sm.kf[0][r0t + ln][32 * u], &sm.kf[1][r0t + ln][32 * u], &sm.dST[0][c0t + ln][32 * u],
                               &sm.dST[1][c0t + ln][32 * u], lg, acc);
-            acc = mm_pair(sm.AT[0][r0t + ln], sm.AT[1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[1][c0t + ln], lg, acc);
+            acc = mmv<H16>(sm.AT[0][r0t + ln], sm.AT[1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[1][c0t + ln], lg, acc);
             if constexpr (std::is_same<TI, _Float16>::value) {
                 // fp16 activations: dP and dR in fp16, row-major halves in the
                 // first half of their fp32 slots
@@ -489,7 +538,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 for (int j = 0; j < 4; ++j)
                     __builtin_nontemporal_store(acc[j], &dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             }
-            put4_pair(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[1][c0t + ln][r0t + 4 * lg], acc);
+            put4v<H16>(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[1][c0t + ln][r0t + 4 * lg], acc);
         }
 #pragma unroll
         for (int m = 0; m < TPW; ++m) {
@@ -498,7 +547,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) accs[m][j] *= sm.eps[r0 + 4 * lg + j];
-                accs[m] = mm_pair(sm.qeT[0][r0 + ln], sm.qeT[1][r0 + ln], sm.dOT[0][c0 + ln], sm.dOT[1][c0 + ln], lg,
+                accs[m] = mmv<H16>(sm.qeT[0][r0 + ln], sm.qeT[1][r0 + ln], sm.dOT[0][c0 + ln], sm.dOT[1][c0 + ln], lg,
                                   accs[m]);
             }
         }
@@ -507,7 +556,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
         // dR = M^T dP = Diag(beta) N^T dP (= dV, which bwd_chunk_kernel writes out)
         if (w < NDP) {
             const int r0t = 16 * (w / VTL), c0t = 16 * (w % VTL);
-            f4 acc = mm_pair(sm.NT_[0][r0t + ln], sm.NT_[1][r0t + ln], sm.dPT[0][c0t + ln], sm.dPT[1][c0t + ln], lg,
+            f4 acc = mmv<H16>(sm.NT_[0][r0t + ln], sm.NT_[1][r0t + ln], sm.dPT[0][c0t + ln], sm.dPT[1][c0t + ln], lg,
                              f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[j] *= sm.beta[r0t + 4 * lg + j];
@@ -523,7 +572,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 for (int j = 0; j < 4; ++j)
                     __builtin_nontemporal_store(acc[j], &drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             }
-            put4_pair(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[1][c0t + ln][r0t + 4 * lg], acc);
+            put4v<H16>(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[1][c0t + ln][r0t + 4 * lg], acc);
         }
         __syncthreads();
 
@@ -534,10 +583,10 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             const int ti = w + NWS * m;
             if (ti < NTS) {
                 const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
-                const f4 kr = mm_pair(sm.keT[0][r0 + ln], sm.keT[1][r0 + ln], sm.dRT[0][c0 + ln], sm.dRT[1][c0 + ln],
+                const f4 kr = mmv<H16>(sm.keT[0][r0 + ln], sm.keT[1][r0 + ln], sm.dRT[0][c0 + ln], sm.dRT[1][c0 + ln],
                                       lg, f4{0.f, 0.f, 0.f, 0.f});
                 accs[m] -= kr;
-                put4_pair(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
+                put4v<H16>(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
             }
         }
         // the next chunk's staging writes none of keT, dRT, dST before its
