@@ -221,18 +221,19 @@ __global__ __launch_bounds__(256) void bwd_n_kernel(const kda_bwd_args a, const 
 constexpr int NS = 512;         // threads per workgroup of bwd_state_kernel
 constexpr int NWS = NS / 64;    // its waves
 
-template <int K, int VA>
+// NP: 2 (bf16 pairs) or 1 (fp16 activations: single fp16 operands).
+template <int K, int VA, int NP>
 struct __align__(16) StateSmem {
     static constexpr int KB = K + 8, TB = CT + 8;
-    uint16_t qeT[2][K][TB];     // (scale q exp(G))^T: [channel][token]
-    uint16_t keT[2][K][TB];     // (k exp(G))^T
-    uint16_t kf[2][CT][KB];     // k exp(G_last - G): [token][channel]
-    uint16_t dST[2][VA][KB];    // dS^T at the chunk end: [column][channel]
-    uint16_t dOT[2][VA][TB];    // dO^T: [column][token]
-    uint16_t dPT[2][VA][TB];
-    uint16_t dRT[2][VA][TB];
-    uint16_t AT[2][CT][TB];     // A^T: [c][c2] = A[c2][c]
-    uint16_t NT_[2][CT][TB];    // N^T
+    uint16_t qeT[NP][K][TB];    // (scale q exp(G))^T: [channel][token]
+    uint16_t keT[NP][K][TB];    // (k exp(G))^T
+    uint16_t kf[NP][CT][KB];    // k exp(G_last - G): [token][channel]
+    uint16_t dST[NP][VA][KB];   // dS^T at the chunk end: [column][channel]
+    uint16_t dOT[NP][VA][TB];   // dO^T: [column][token]
+    uint16_t dPT[NP][VA][TB];
+    uint16_t dRT[NP][VA][TB];
+    uint16_t AT[NP][CT][TB];    // A^T: [c][c2] = A[c2][c]
+    uint16_t NT_[NP][CT][TB];   // N^T
     float tot[NS / K][K];       // per row group, the sum of its g
     float beta[CT];
     float eps[K];
@@ -334,7 +335,8 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
     constexpr int APT = CT * CT / NS;       // elements of A (and of N) per thread
     static_assert(RPT >= 1 && DPT >= 1 && NDP <= NWS, "thread mapping");
     constexpr bool H16 = std::is_same<TI, _Float16>::value;
-    __shared__ StateSmem<K, VA> sm;
+    constexpr int L1 = H16 ? 0 : 1;         // the lo half of a pair (fp16: unused, aliased to hi)
+    __shared__ StateSmem<K, VA, H16 ? 1 : 2> sm;
     const TI* qp = static_cast<const TI*>(a.q);
     const TI* kp = static_cast<const TI*>(a.k);
     const TI* dop = static_cast<const TI*>(a.d_o);
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 accs[m][j] = a.d_state_out ? a.d_state_out[(bh * K + r0 + 4 * lg + j) * V + v0 + c0 + ln] : 0.f;
-            put4v<H16>(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
+            put4v<H16>(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[L1][c0 + ln][r0 + 4 * lg], accs[m]);
         }
     }
 
@@ -457,9 +459,9 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             }
 #pragma unroll
             for (int j = 0; j < DPT; ++j) vo[j] = raw_f32<TI>(pdo[j]);
-            put_run<H16>(&sm.AT[0][ai][ac0], &sm.AT[1][ai][ac0], va);
-            put_run<H16>(&sm.NT_[0][ai][ac0], &sm.NT_[1][ai][ac0], vn);
-            put_run<H16>(&sm.dOT[0][dv_][dc0], &sm.dOT[1][dv_][dc0], vo);
+            put_run<H16>(&sm.AT[0][ai][ac0], &sm.AT[L1][ai][ac0], va);
+            put_run<H16>(&sm.NT_[0][ai][ac0], &sm.NT_[L1][ai][ac0], vn);
+            put_run<H16>(&sm.dOT[0][dv_][dc0], &sm.dOT[L1][dv_][dc0], vo);
         }
         if (t < CT) sm.beta[t] = __uint_as_float(pb[0]);
         fetch(n - 1);
@@ -485,10 +487,10 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 if constexpr (H16)
                     sm.kf[0][c][x] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(ck[j] * F));
                 else
-                    split_bf16(ck[j] * F, sm.kf[0][c][x], sm.kf[1][c][x]);
+                    split_bf16(ck[j] * F, sm.kf[0][c][x], sm.kf[L1][c][x]);
             }
-            put_run<H16>(&sm.qeT[0][x][RPT * rg], &sm.qeT[1][x][RPT * rg], qe);
-            put_run<H16>(&sm.keT[0][x][RPT * rg], &sm.keT[1][x][RPT * rg], ke);
+            put_run<H16>(&sm.qeT[0][x][RPT * rg], &sm.qeT[L1][x][RPT * rg], qe);
+            put_run<H16>(&sm.keT[0][x][RPT * rg], &sm.keT[L1][x][RPT * rg], ke);
             if (rg == 0) sm.eps[x] = __expf(last);
         }
         __syncthreads();
@@ -521,9 +523,9 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < K / 32; ++u)
-                acc = mmv<H16>(&sm.kf[0][r0t + ln][32 * u], &sm.kf[1][r0t + ln][32 * u], &sm.dST[0][c0t + ln][32 * u],
-                              &sm.dST[1][c0t + ln][32 * u], lg, acc);
-            acc = mmv<H16>(sm.AT[0][r0t + ln], sm.AT[1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[1][c0t + ln], lg, acc);
+                acc = mmv<H16>(&sm.kf[0][r0t + ln][32 * u], &sm.kf[L1][r0t + ln][32 * u], &sm.dST[0][c0t + ln][32 * u],
+                              &sm.dST[L1][c0t + ln][32 * u], lg, acc);
+            acc = mmv<H16>(sm.AT[0][r0t + ln], sm.AT[L1][r0t + ln], sm.dOT[0][c0t + ln], sm.dOT[L1][c0t + ln], lg, acc);
             if constexpr (std::is_same<TI, _Float16>::value) {
                 // fp16 activations: dP and dR in fp16, row-major halves in the
                 // first half of their fp32 slots
@@ -538,7 +540,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 for (int j = 0; j < 4; ++j)
                     __builtin_nontemporal_store(acc[j], &dpn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             }
-            put4v<H16>(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[1][c0t + ln][r0t + 4 * lg], acc);
+            put4v<H16>(&sm.dPT[0][c0t + ln][r0t + 4 * lg], &sm.dPT[L1][c0t + ln][r0t + 4 * lg], acc);
         }
 #pragma unroll
         for (int m = 0; m < TPW; ++m) {
@@ -547,7 +549,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) accs[m][j] *= sm.eps[r0 + 4 * lg + j];
-                accs[m] = mmv<H16>(sm.qeT[0][r0 + ln], sm.qeT[1][r0 + ln], sm.dOT[0][c0 + ln], sm.dOT[1][c0 + ln], lg,
+                accs[m] = mmv<H16>(sm.qeT[0][r0 + ln], sm.qeT[L1][r0 + ln], sm.dOT[0][c0 + ln], sm.dOT[L1][c0 + ln], lg,
                                   accs[m]);
             }
         }
@@ -556,7 +558,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
         // dR = M^T dP = Diag(beta) N^T dP (= dV, which bwd_chunk_kernel writes out)
         if (w < NDP) {
             const int r0t = 16 * (w / VTL), c0t = 16 * (w % VTL);
-            f4 acc = mmv<H16>(sm.NT_[0][r0t + ln], sm.NT_[1][r0t + ln], sm.dPT[0][c0t + ln], sm.dPT[1][c0t + ln], lg,
+            f4 acc = mmv<H16>(sm.NT_[0][r0t + ln], sm.NT_[L1][r0t + ln], sm.dPT[0][c0t + ln], sm.dPT[L1][c0t + ln], lg,
                              f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[j] *= sm.beta[r0t + 4 * lg + j];
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
                 for (int j = 0; j < 4; ++j)
                     __builtin_nontemporal_store(acc[j], &drn[static_cast<uint32_t>(r0t + 4 * lg + j) * V + c0t + ln]);
             }
-            put4v<H16>(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[1][c0t + ln][r0t + 4 * lg], acc);
+            put4v<H16>(&sm.dRT[0][c0t + ln][r0t + 4 * lg], &sm.dRT[L1][c0t + ln][r0t + 4 * lg], acc);
         }
         __syncthreads();
 
@@ -583,10 +585,10 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
             const int ti = w + NWS * m;
             if (ti < NTS) {
                 const int r0 = 16 * (ti / VTL), c0 = 16 * (ti % VTL);
-                const f4 kr = mmv<H16>(sm.keT[0][r0 + ln], sm.keT[1][r0 + ln], sm.dRT[0][c0 + ln], sm.dRT[1][c0 + ln],
+                const f4 kr = mmv<H16>(sm.keT[0][r0 + ln], sm.keT[L1][r0 + ln], sm.dRT[0][c0 + ln], sm.dRT[L1][c0 + ln],
                                       lg, f4{0.f, 0.f, 0.f, 0.f});
                 accs[m] -= kr;
-                put4v<H16>(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[1][c0 + ln][r0 + 4 * lg], accs[m]);
+                put4v<H16>(&sm.dST[0][c0 + ln][r0 + 4 * lg], &sm.dST[L1][c0 + ln][r0 + 4 * lg], accs[m]);
             }
         }
         // the next chunk's staging writes none of keT, dRT, dST before its
