@@ -642,6 +642,35 @@ __device__ __forceinline__ f4 mfma_pair16(const f4& a, const float (&b)[4]) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
 }
 
+// x of lanes ln, ln + 16, ln + 32 and ln + 48 (the four lane groups of the
+// lane's column) on every lane, v[l] from lane group l: three permlane swaps
+// (VALU; permlane16_swap(u, u) gives u of lanes l & ~16 and l | 16,
+// permlane32_swap likewise for bit 5).
+__device__ __forceinline__ void lane_groups(float x, float (&v)[4]) {
+    const unsigned u = __float_as_uint(x);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const auto ra = __builtin_amdgcn_permlane32_swap(r16[0], r16[0], false, false);
+    const auto rb = __builtin_amdgcn_permlane32_swap(r16[1], r16[1], false, false);
+    v[0] = __uint_as_float(ra[0]);
+    v[1] = __uint_as_float(rb[0]);
+    v[2] = __uint_as_float(ra[1]);
+    v[3] = __uint_as_float(rb[1]);
+}
+
+// Sum of x over N aligned consecutive lanes (N = 4, 8 or 16), every lane of
+// the group gets it: DPP quad permutations, then the half-row and row mirrors.
+template <int N>
+__device__ __forceinline__ float lanes_sum(float x) {
+    static_assert(N == 4 || N == 8 || N == 16, "lane group");
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    if constexpr (N >= 8)
+        x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    if constexpr (N >= 16)
+        x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
+    return x;
+}
+
 // acc += X Y^T over the VT = 32 columns of a step: X a bf16 pair tile in LDS
 // (row ln of the tile: xh, xl), Y's fragment in registers (lane (ln, lg):
 // row ln, columns 8 lg .. 8 lg + 7, as a pair).
@@ -951,9 +980,8 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     }
     dke[1] = f4{0.f, 0.f, 0.f, 0.f} - dke[1];
     // deps of channel x: the shares of the four lanes of the channel
-    deps += __shfl_xor(deps, 16);
-    deps += __shfl_xor(deps, 32);
-    // X (whole) to Y's area until dA is formed; dM (i <= c)
+    deps = lanegroup4_sum(deps);
+    // X (whole) to dXc's area until dA is formed; dM (i <= c)
 #pragma unroll
     for (int m = 0; m < MPW; ++m) {
         const int tt = w + NW * m, r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
@@ -961,28 +989,47 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
             if (tt < 4)
-                sm.Y[c][i] = accm[m][j];
+                sm.dXc[c][i] = accm[m][j];
             else
                 sm.dM[c][i] = i <= c ? accm[m][j] : 0.f;
         }
     }
     __syncthreads();
-    // dA = tril(X M^T), M^T[q][i] = N[i][q] beta[q] (beside the column sums below)
-    for (int tt = __builtin_amdgcn_readfirstlane(w); tt < 4; tt += NW) {
-        const int r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
-        const f4 acc = tile_mm<CT>([&](int r, int q) { return sm.Y[r0t + r][q]; },
-                                   [&](int q, int i) { return sm.N[c0t + i][q] * sm.beta[q]; }, ln, lg,
-                                   f4{0.f, 0.f, 0.f, 0.f});
+    // N is lower triangular (N01 = 0), dM lower, so of the 16 x 16 tiles of
+    // dA = tril(X M^T), Y = dN N^T (dN = dM Diag(beta)) and the strictly lower
+    // dX = -N^T Y only the tiles (0,0), (1,0), (1,1) are formed (dX's and
+    // dA's (0,1) tiles are zero and never read, Y's is not needed), over
+    // the contraction blocks where N is not zero: dA and Y tiles of block
+    // column 0 sum over block 0 only, dX tiles of block row 1 over block 1
+    // only.  dA and Y (with the column sums of dM * N) share one phase.
+    for (int tt = __builtin_amdgcn_readfirstlane(w); tt < 6; tt += NW) {
+        // tiles: dA(1,1), Y(1,1), dA(0,0), dA(1,0), Y(0,0), Y(1,0)
+        const bool is_da = tt == 0 || tt == 2 || tt == 3;
+        const int r0t = tt == 2 || tt == 4 ? 0 : 16, c0t = tt < 2 ? 16 : 0;
+        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+        if (is_da) {
+            // dA = tril(X M^T), M^T[q][i] = N[i][q] beta[q]; X in dXc's area
+            auto fx = [&](int r, int q) { return sm.dXc[r0t + r][q]; };
+            auto fm = [&](int q, int i) { return sm.N[c0t + i][q] * sm.beta[q]; };
+            const f4 acc = c0t ? tile_mm<CT>(fx, fm, ln, lg, zero) : tile_mm<16>(fx, fm, ln, lg, zero);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = r0t + 4 * lg + j, i = c0t + ln;
-            const float v = i <= c ? acc[j] : 0.f;
-            sm.dAr[c][i] = v;
-            sm.dAc[i][c] = v;
+            for (int j = 0; j < 4; ++j) {
+                const int c = r0t + 4 * lg + j, i = c0t + ln;
+                const float v = i <= c ? acc[j] : 0.f;
+                sm.dAr[c][i] = v;
+                sm.dAc[i][c] = v;
+            }
+        } else {
+            // Y = dN N^T with dN[r][m] = dM[r][m] beta[m]
+            auto fn = [&](int r, int m) { return sm.dM[r0t + r][m] * sm.beta[m]; };
+            auto ft = [&](int m, int i) { return sm.N[c0t + i][m]; };
+            const f4 acc = c0t ? tile_mm<CT>(fn, ft, ln, lg, zero) : tile_mm<16>(fn, ft, ln, lg, zero);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sm.Y[r0t + 4 * lg + j][c0t + ln] = acc[j];
         }
     }
 
-    // ------------------------------- dbeta (M = N Diag(beta)), dN in place
+    // ------------------------------- dbeta (M = N Diag(beta))
     // column sums of dM * N: over the thread's entries (one column), the two
     // halves of the wave, then the waves
     {
@@ -990,30 +1037,23 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
 #pragma unroll
         for (int m = 0; m < CT * CT / NTC; ++m) {
             const int e = t + NTC * m, c = e / CT, i = e % CT;
-            const float dm = sm.dM[c][i];
-            cs = fmaf(dm, sm.N[c][i], cs);
-            sm.dM[c][i] = dm * sm.beta[i];
+            cs = fmaf(sm.dM[c][i], sm.N[c][i], cs);
         }
-        cs += __shfl_xor(cs, 32);
+        const unsigned u = __float_as_uint(cs);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        cs = __uint_as_float(r[0]) + __uint_as_float(r[1]);
         if (lane < 32) sm.red[w][lane] = cs;
     }
     __syncthreads();
-    // Y = dN N^T
-    for (int tt = w; tt < 4; tt += NW) {
-        const int r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = tile_mm<CT>([&](int r, int m) { return sm.dM[r0t + r][m]; },
-                          [&](int m, int i) { return sm.N[c0t + i][m]; }, ln, lg, acc);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sm.Y[r0t + 4 * lg + j][c0t + ln] = acc[j];
-    }
-    __syncthreads();
-    // dX = -N^T Y, strictly lower (kept in dM and the copies)
-    for (int tt = w; tt < 4; tt += NW) {
-        const int r0t = 16 * ((tt >> 1) & 1), c0t = 16 * (tt & 1);
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = tile_mm<CT>([&](int r, int m) { return sm.N[m][r0t + r]; },
-                          [&](int m, int i) { return sm.Y[m][c0t + i]; }, ln, lg, acc);
+    // dX = -N^T Y, strictly lower (kept in dM and the copies): tiles (0,0)
+    // over both blocks, (1,0) and (1,1) over block 1 (N[m][c] = 0 for m < c)
+    for (int tt = __builtin_amdgcn_readfirstlane(w); tt < 3; tt += NW) {
+        const int r0t = tt ? 16 : 0, c0t = tt == 2 ? 16 : 0;
+        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f4 acc = tt == 0 ? tile_mm<CT>([&](int r, int m) { return sm.N[m][r]; },
+                                             [&](int m, int i) { return sm.Y[m][i]; }, ln, lg, zero)
+                               : tile_mm<16>([&](int r, int m) { return sm.N[16 + m][r0t + r]; },
+                                             [&](int m, int i) { return sm.Y[16 + m][c0t + i]; }, ln, lg, zero);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = r0t + 4 * lg + j, i = c0t + ln;
@@ -1024,19 +1064,20 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         }
     }
     __syncthreads();
-    // dbeta: row sums of dX * L (over the 32 lanes of a row) plus the column sums
+    // dbeta: row sums of dX * L plus the waves' column sums, NTC / CT
+    // consecutive lanes a row
+    {
+        constexpr int TPR = NTC / CT, EPR = CT / TPR;
+        static_assert(NW <= TPR, "a lane per wave's column sum");
+        const int c = t / TPR, part = t % TPR;
+        float s = part < NW ? sm.red[part][c] : 0.f;
 #pragma unroll
-    for (int m = 0; m < CT * CT / NTC; ++m) {
-        const int e = t + NTC * m, c = e / CT, i = e % CT;
-        float p = sm.dM[c][i] * sm.L[c][i];
-#pragma unroll
-        for (int s = 16; s >= 1; s >>= 1) p += __shfl_xor(p, s);
-        if (i == 0 && c < nrow) {
-            float s = p;
-#pragma unroll
-            for (int u = 0; u < NW; ++u) s += sm.red[u][c];
-            a.dbeta[(b * T + r0 + c) * H + h] = s;
+        for (int e = 0; e < EPR; ++e) {
+            const int i = EPR * part + e;
+            s = fmaf(sm.dM[c][i], sm.L[c][i], s);
         }
+        s = lanes_sum<TPR>(s);
+        if (part == 0 && c < nrow) a.dbeta[(b * T + r0 + c) * H + h] = s;
     }
 
     // ---------------------------- per (row, channel): dq, dk and dg
@@ -1067,13 +1108,14 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     }
     {
         // the earlier row groups of the channel (lanes ln + 16 l), block 0 before block 1
-        float pre0 = 0.f, pre1 = 0.f, all0 = 0.f;
+        float pre0 = 0.f, pre1 = 0.f, all0 = 0.f, t0v[4], t1v[4];
+        lane_groups(tot[0], t0v);
+        lane_groups(tot[1], t1v);
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const float t0 = __shfl(tot[0], ln + 16 * l), t1 = __shfl(tot[1], ln + 16 * l);
-            pre0 += l < lg ? t0 : 0.f;
-            pre1 += l < lg ? t1 : 0.f;
-            all0 += t0;
+            pre0 += l < lg ? t0v[l] : 0.f;
+            pre1 += l < lg ? t1v[l] : 0.f;
+            all0 += t0v[l];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1081,7 +1123,14 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
             G[1][j] += all0 + pre1;
         }
     }
-    const float g16 = __shfl(G[1][0], ln), g31 = __shfl(G[1][3], ln + 48);
+    float g16, g31;
+    {
+        float v0[4], v3[4];
+        lane_groups(G[1][0], v0);
+        lane_groups(G[1][3], v3);
+        g16 = v0[0];
+        g31 = v3[3];
+    }
     asm volatile("" ::: "memory");
     // dg = the reverse in-chunk cumulative sum of dG plus deps * eps plus
     // sum_c d(kF)_c k_c F_c (over the channel's lanes)
@@ -1093,8 +1142,7 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
             ls += stash[(8 + j) * NTC + t] * kv[0][j] * __expf(g31 - G[0][j]);
             ls += dkf[1][j] * kv[1][j] * __expf(g31 - G[1][j]);
         }
-        ls += __shfl_xor(ls, 16);
-        ls += __shfl_xor(ls, 32);
+        ls = lanegroup4_sum(ls);
         base = deps * __expf(g31) + ls;
     }
     // block 1 first (its rows' dG sums enter block 0's dg)
@@ -1151,8 +1199,10 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         // k_s e_s (lower s), e = exp(-|G - G_ref|); likewise dX with Z'[s] =
         // beta_s k_s e_s or k_s e_s.  The reference rows are row 3 of lanes
         // ln + 16 l.
-        const float gref3 = __shfl(G[p][3], ln + 16);
-        const float gref2 = __shfl(G[p][3], ln + 16 * (lg & ~1));
+        float g3v[4];
+        lane_groups(G[p][3], g3v);
+        const float gref3 = g3v[1];
+        const float gref2 = lg & 2 ? g3v[2] : g3v[0];
 #pragma unroll
         for (int lev = 2; lev <= 3; ++lev) {
             const bool up = lev == 3 ? lg >= 2 : (lg & 1) != 0;
@@ -1239,12 +1289,12 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         }
         // the later row groups of the channel in this block, then block 1's
         // rows (for block 0)
-        float post = 0.f, all = 0.f;
+        float post = 0.f, all = 0.f, accv[4];
+        lane_groups(acc, accv);
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const float sl = __shfl(acc, ln + 16 * l);
-            post += l > lg ? sl : 0.f;
-            all += sl;
+            post += l > lg ? accv[l] : 0.f;
+            all += accv[l];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
