@@ -469,6 +469,10 @@ struct Kern {
     // head's first V-tile workgroup only (null otherwise): per 32-token chunk
     // the state and R ((K + 32) x V) and then A, L and N (32 x 32 each)
     float* ckm = nullptr;
+    // fp16 activations store the records branch-free (an empty buffer range
+    // where there is no record), so the consumers' loop keeps an exact count
+    // of its outstanding vector memory operations
+    static constexpr bool kFlatRec = Elem<TQ>::code == KDA_DTYPE_F16;
     float* cout = nullptr;                   // TOUT: the transition columns' outputs [B, T, H, K]
     int nblk = 0;                            // blocks of the real chunks (records exist for these)
 
@@ -743,8 +747,17 @@ struct Kern {
         Q = mm_f32(L2, Q, Q);
         Q = mm_f32(L4, Q, Q);
         Q = mm_f32(L8, Q, Q);                    // acc((I + L)^-T) = A-layout of (I + L)^-1
-        if (ckm && blk < nblk) {
+        if constexpr (kFlatRec) {
             // the backward's N block: N[ln][4 lg + j] = (I + L)^-1
+            const bool rec = ckm && blk < nblk;
+            const auto rn = make_rsrc(rec ? ck_mats(blk) + 2 * CB * BT * CB * BT : nullptr,
+                                      rec ? static_cast<uint32_t>(CB * BT * CB * BT * 4) : 0u);
+            const int o = BT * (blk % CB);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Q[j]), rn,
+                                                      ((o + ln) * (CB * BT) + o + 4 * lg + j) * 4, 0, 2);
+        } else if (ckm && blk < nblk) {
             float* n = ck_mats(blk) + 2 * CB * BT * CB * BT;
             const int o = BT * (blk % CB);
 #pragma unroll
@@ -1234,14 +1247,14 @@ struct Kern {
             }
         }
         const int64_t V = a.V;
-        if (ck) {
-            if constexpr (Elem<TQ>::code == KDA_DTYPE_F16) {
+        if constexpr (kFlatRec) {
+            {
                 // fp16 in accumulator-order tiles (half_tile_offset): slot j
                 // of tile (t, column group) is 64 consecutive halves, the
                 // values the products above take as their fp16 state
                 // (the tile offsets are wave-uniform: scalar offsets of a
                 // buffer store, so no per-tile address is kept in registers)
-                const auto rs = make_rsrc(ck, static_cast<uint32_t>(K * V * 2));
+                const auto rs = make_rsrc(ck, ck ? static_cast<uint32_t>(K * V * 2) : 0u);
                 const int lo = 2 * (16 * lg + ln);
 #pragma unroll
                 for (int g = 0; g < CG; ++g)
@@ -1252,7 +1265,9 @@ struct Kern {
                             __builtin_amdgcn_raw_buffer_store_b16(
                                 __builtin_bit_cast(uint16_t, static_cast<_Float16>(S[g][t][j])), rs, lo,
                                 static_cast<int>(2 * (half_tile_offset(16 * t, colw + 16 * g, V) + 64 * j)), 2);
-            } else {
+            }
+        } else if (ck) {
+            {
 #pragma unroll
                 for (int g = 0; g < CG; ++g)
 #pragma unroll
@@ -1269,7 +1284,7 @@ struct Kern {
         // in the scalar offset -- no 64-bit address per store kept in
         // registers.  fp16 activations: R in fp16 (the single fp16 operand the
         // solve below takes), row-major halves in the first half of its rows.
-        const auto rr = make_rsrc(rp, static_cast<uint32_t>(CB * BT * V * 4));
+        const auto rr = make_rsrc(rp, rp ? static_cast<uint32_t>(CB * BT * V * 4) : 0u);
         const int rlo = static_cast<int>((4 * lg * V + ln) * 4);
         auto r_store = [&](float x, int row, int g) {
             if constexpr (Elem<TQ>::code == KDA_DTYPE_F16)
@@ -1323,7 +1338,7 @@ struct Kern {
         for (int g = 0; g < CG; ++g) {
             R[g][0] -= Z[g][0];
             R[g][1] -= Z[g][1];
-            if (rp) {
+            if (kFlatRec || rp) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     r_store(RANGE ? R[g][0][j] * isig : R[g][0][j], j, g);
@@ -1512,9 +1527,10 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             // count at the loop head is then exact; with the entry path's
             // smaller count each chunk's wait for its v tile also waited for
             // the output stores of the chunks before it.
-            if constexpr (!EPI && !CKPT && (!TRANS || TOUT)) {
-                // (distinct offsets: identical stores would be merged away)
-                constexpr int ns = TOUT ? CB * CG : KN::kOutStores;
+            if constexpr (!EPI && (!CKPT || KN::kFlatRec) && (!TRANS || TOUT)) {
+                // (distinct offsets: identical stores would be merged away;
+                // flat records: the chunk's state and R stores as well)
+                constexpr int ns = TOUT ? CB * CG : KN::kOutStores + (CKPT ? CG * (KN::KT + CB) * 4 : 0);
                 const auto none = make_rsrc(a.o, 0u);
 #pragma unroll
                 for (int i = 0; i < ns; ++i)
@@ -1543,7 +1559,10 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
         auto solve_next = [&](int s) {
             if constexpr (KN::kConsumerSolve) {
                 const int nb = NB * (s + 1) + wave;
-                if (s + 1 < nss) {
+                // flat records: also past the last superstep (its N stores
+                // then have an empty range, its M goes to an unused slot), so
+                // the loop body has no branch around them
+                if ((CKPT && KN::kFlatRec) || s + 1 < nss) {
                     ChunkOps<K>& nx = sm.set[(s + 1) & 1][wave / CB];
                     kn.solve(wave, nb, nx.MH[wave % CB], nx.ML[wave % CB]);
                 }
