@@ -416,7 +416,7 @@ __device__ __forceinline__ f4 mm_f32(const f4& xt, const f4& y, f4 c) {
 // initial state) to o, those of the transition columns (per token, the
 // coefficients of the initial state in the outputs) to a second buffer.
 template <int K, int NC, typename TQ, bool GATED, int CG = 1, bool EPI = false, bool TRANS = false,
-          bool TOUT = false>
+          bool TOUT = false, bool CKPT = false>
 struct Kern {
     static constexpr int KT = K / 16;                   // 16-row state tiles
     static constexpr int KU = K / 32;                   // 32-wide k blocks
@@ -469,10 +469,11 @@ struct Kern {
     // head's first V-tile workgroup only (null otherwise): per 32-token chunk
     // the state and R ((K + 32) x V) and then A, L and N (32 x 32 each)
     float* ckm = nullptr;
-    // fp16 activations store the records branch-free (an empty buffer range
-    // where there is no record), so the consumers' loop keeps an exact count
-    // of its outstanding vector memory operations
-    static constexpr bool kFlatRec = Elem<TQ>::code == KDA_DTYPE_F16;
+    // The checkpointing kernel with fp16 activations stores the records
+    // branch-free (an empty buffer range where there is no record), so the
+    // consumers' loop keeps an exact count of its outstanding vector memory
+    // operations; the other kernels have no record stores at all.
+    static constexpr bool kFlatRec = CKPT && Elem<TQ>::code == KDA_DTYPE_F16;
     float* cout = nullptr;                   // TOUT: the transition columns' outputs [B, T, H, K]
     int nblk = 0;                            // blocks of the real chunks (records exist for these)
 
@@ -757,7 +758,7 @@ struct Kern {
             for (int j = 0; j < 4; ++j)
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Q[j]), rn,
                                                       ((o + ln) * (CB * BT) + o + 4 * lg + j) * 4, 0, 2);
-        } else if (ckm && blk < nblk) {
+        } else if (CKPT && ckm && blk < nblk) {
             float* n = ck_mats(blk) + 2 * CB * BT * CB * BT;
             const int o = BT * (blk % CB);
 #pragma unroll
@@ -836,7 +837,7 @@ struct Kern {
         // the block's sums are complete: A to its operand, G and beta to the
         // solve (and both to the backward's record; block 0 also zeroes the
         // record's blocks above the diagonal)
-        if (ckm && next - NB < nblk) {
+        if (CKPT && ckm && next - NB < nblk) {
             constexpr int C = CB * BT;
             float* ma = ck_mats(next - NB);
             const int o = BT * bi;
@@ -943,7 +944,7 @@ struct Kern {
                 accG = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.KE[1][0][0] + o), accG);
                 accA = mfma16x16x32(hf0, *reinterpret_cast<const h8*>(&co.QE[1][0][0] + o), accA);
             }
-            if (ckm && blk < nblk) {
+            if (CKPT && ckm && blk < nblk) {
                 // the backward's A_10 and L_10: slot j holds row 16 + ln, column 4 lg + j
                 constexpr int C = CB * BT;
                 float* ma = ck_mats(blk);
@@ -1429,7 +1430,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
                                                                    const kda_gate_args gate,
                                                                    const kda_out_epilogue epi) {
     static_assert(!TOUT || TRANS, "fp32 outputs belong to the transition pass");
-    using KN = Kern<K, NC, TQ, GATED, CG, EPI, TRANS, TOUT>;
+    using KN = Kern<K, NC, TQ, GATED, CG, EPI, TRANS, TOUT, CKPT>;
     constexpr int KT = KN::KT, VT = KN::VT, CH = KN::CH;
     static_assert(K % 32 == 0 && K <= 128, "chunkwise supports K in {32, 64, 128}");
     __shared__ Smem<K, CG, EPI> sm;
