@@ -1537,6 +1537,22 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
                 for (int i = 0; i < ns; ++i)
                     __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (ns * j + i), 0);
             }
+            if constexpr (EPI) {
+                // a chunk's output-gate loads follow its v loads in the loop
+                constexpr int ng = CB * CG;
+                const auto none = make_rsrc(a.o, 0u);
+#pragma unroll
+                for (int i = 0; i < ng; ++i)
+                    __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (ng * j + i), 0);
+            }
+        }
+        if constexpr (EPI) {
+            // and the superstep's output stores (finish) end the loop body
+            constexpr int nf = NCH * CB * CG;
+            const auto none = make_rsrc(a.o, 0u);
+#pragma unroll
+            for (int i = 0; i < nf; ++i)
+                __builtin_amdgcn_raw_buffer_store_b64(u2{0u, 0u}, none, 0, 8 * (NCH * CB * CG + i), 0);
         }
         uint16_t (*vt)[16] = sm.vt[consumer ? wave : 0];
         typename KN::Pend pd[NCH];
@@ -1585,7 +1601,7 @@ __global__ __launch_bounds__(64 * (NC + NB)) void chunkwise_kernel(const kda_fwd
             if constexpr (EPI) {
 #pragma unroll
                 for (int cj = 0; cj < NCH; ++cj)
-                    if (NCH * s + cj < ncc) kn.finish(pd[cj], colw, wave);
+                    kn.finish(pd[cj], colw, wave);     // a chunk past T: rows dropped by the store's range
             }
             solve_next(s);
             __syncthreads();
