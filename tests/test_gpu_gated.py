@@ -256,7 +256,8 @@ def test_gated_decay_over_the_whole_gate_range(kda_pkg, path):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("K,V,T", [(128, 128, 192), (64, 64, 128), (128, 64, 100), (64, 128, 64)])
+@pytest.mark.parametrize("K,V,T", [(128, 128, 192), (64, 64, 128), (128, 64, 100), (64, 128, 64),
+                                   (128, 128, 96), (64, 128, 160)])   # odd chunk counts: a padded last chunk
 def test_chunkwise_fused_matches_gated_plus_output_kernel(kda_pkg, dtype, K, V, T):
     """The output epilogue on the chunk kernel's tiles (one workgroup per head,
     4 consumer waves of V / 64 column groups) against the gated chunk kernel
