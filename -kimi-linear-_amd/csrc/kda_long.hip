@@ -232,8 +232,9 @@ __global__ __launch_bounds__(1024) void long_correct_kernel(const float* oz, con
         for (int m = 0; m < 2; ++m) {
             const int i = t + nthr * m;
             const int r = i / (K / 4), c4 = i % (K / 4);
-            fc[m] = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rc, static_cast<int>(((tt + r) * hk + 4 * c4) * 4), 0, 0));
+            // a slot past the step's pieces reads past the range: no memory access
+            const int off = i < NP ? static_cast<int>(((tt + r) * hk + 4 * c4) * 4) : 0x7ffffff0;
+            fc[m] = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
         }
     };
     auto stage = [&](int buf) {
@@ -256,13 +257,25 @@ __global__ __launch_bounds__(1024) void long_correct_kernel(const float* oz, con
             }
         }
     };
+    // Every load runs one step ahead of its use: step tt's c rows were
+    // fetched during step tt - 16 and staged at its end, step tt's oz
+    // during step tt - 16; the rows of step tt + 32 are fetched once step
+    // tt + 16's are staged.  (Past the last row the ranges return zeros.)
+    auto oz_row = [&](int tt) { return static_cast<int>((tt + ln) * hv + c0 + 4 * lg); };
     fetch(0);
     stage(0);
+    w4 z = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rz, oz_row(0) * 4, 0, 0));
+    fetch(16);
+    {
+        // the loop issues its output store after these loads: a store that
+        // writes nothing stands in for it, so that the loop is entered with
+        // the pattern of outstanding memory operations it repeats
+        const auto none_o = make_rsrc(o, 0u);
+        __builtin_amdgcn_raw_buffer_store_b32(0u, none_o, 0, 0, 0);
+    }
     int buf = 0;
     for (int tt = 0; tt < rows; tt += 16) {
-        fetch(tt + 16);
-        const int orow = static_cast<int>((tt + ln) * hv + c0 + 4 * lg);
-        const w4 z = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rz, orow * 4, 0, 0));
+        const w4 zn = __builtin_bit_cast(w4, __builtin_amdgcn_raw_buffer_load_b128(rz, oz_row(tt + 16) * 4, 0, 0));
         __syncthreads();                            // this step's rows are staged
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -274,10 +287,12 @@ __global__ __launch_bounds__(1024) void long_correct_kernel(const float* oz, con
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sl[u], ch, acc, 0, 0, 0);
         }
         stage(buf ^ 1);                             // the next step's rows into the other buffer
+        fetch(tt + 32);
         f4 y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) y[j] = acc[j] + __uint_as_float(z[j]);
-        store_out(y, orow);
+        store_out(y, oz_row(tt));
+        z = zn;
         buf ^= 1;
     }
 }
