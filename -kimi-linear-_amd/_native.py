@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1

@@ -26,15 +26,15 @@
 // the reverse in-chunk cumulative sum turns into dg.
 //
 // Only the chain dS_end -> dP -> dR -> dS_start runs from chunk to chunk;
-// everything else is independent per chunk.  Three kernels, one fp32
-// workspace between them:
-//   1. bwd_n_kernel: N of every chunk, its block below the diagonal from the
-//      record's diagonal blocks and L.
-//   2. bwd_state_kernel, one workgroup per (b, h, VA state columns), the chunks
-//      in reverse: the chain above; it stores each chunk's dS_end, dP and dR
-//      (fp32) and dS_0.  The next chunk's inputs are fetched while the
+// everything else is independent per chunk.  Two kernels, one workspace
+// between them:
+//   1. bwd_state_kernel, one workgroup per (b, h, VA state columns), the chunks
+//      in reverse.  First it completes N in the head's chunk records (the
+//      forward's solve left the diagonal blocks; the block below them from
+//      those and L), then the chain above; it stores each chunk's dS_end, dP
+//      and dR and dS_0.  The next chunk's inputs are fetched while the
 //      current one is computed.
-//   3. bwd_chunk_kernel, one workgroup per (b, h, chunk): writes dv = dR; from
+//   2. bwd_chunk_kernel, one workgroup per (b, h, chunk): writes dv = dR; from
 //      S, R (checkpoint), P = M R, dS_end, dP and dR the sums over all state
 //      columns (VT at a time) of dA, dM, d(q~E), d(kE), d(kF) and deps, then the chain
 //      through the inverse, the pairwise-decay products and the reverse
@@ -62,9 +62,10 @@ namespace {
 constexpr int CT = 32;          // tokens per chunk = the forward's checkpoint spacing
 constexpr int VT = 32;          // state columns per step of bwd_chunk_kernel
 
-// Per (b, h) and chunk (index cb = (b H + h) nck + n): A and L (32 x 32)
-// from the forward's chunk record (records of ms floats), and in the fp32
-// workspace N (32 x 32), dS_end [K][V], dP and dR [CT][V].
+// Per (b, h) and chunk (index cb = (b H + h) nck + n): A, L and N (32 x 32)
+// from the forward's chunk record (records of ms floats; the forward leaves
+// N's block below the diagonal to bwd_state_kernel, which completes it in
+// place), and in the workspace dS_end [K][V], dP and dR [CT][V].
 struct BwdWs {
     const float* A;
     const float* L;
@@ -80,9 +81,9 @@ BwdWs ws_layout(void* base, const float* ckpt, int64_t BH, int64_t nck, int64_t 
     BwdWs w;
     w.A = ckpt + (K + CT) * V;
     w.L = w.A + CT * CT;
+    w.N = const_cast<float*>(w.A) + 2 * CT * CT;
     w.ms = ckpt_record(K, V);
-    w.N = p;
-    w.dS = p + BH * nck * CT * CT;
+    w.dS = p;
     w.dP = w.dS + BH * nck * K * V;
     w.dR = w.dP + BH * nck * CT * V;
     return w;
@@ -178,38 +179,45 @@ __device__ __forceinline__ float raw_f32(uint32_t w) {
     }
 }
 
-// N = (I + Diag(beta) L)^-1 of every chunk into the workspace.  The
-// forward's solve left the diagonal blocks N00, N11 in the chunk record;
-// N10 = -N11 X10 N00 with X10 = Diag(beta_1) L10 on the fp32 matrix cores.
-// One wave per chunk, four chunks a workgroup; no barriers.
-__global__ __launch_bounds__(256) void bwd_n_kernel(const kda_bwd_args a, const BwdWs ws, int64_t nchunks) {
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
-    const int64_t cb = static_cast<int64_t>(blockIdx.x) * 4 + w;
-    if (cb >= nchunks) return;
-    const int64_t H = a.H, T = a.T;
-    const int64_t nck = (T + CT - 1) / CT;
-    const int64_t bh = cb / nck, b = bh / H, h = bh % H, r0 = (cb % nck) * CT;
-    const float* L = ws.L + cb * ws.ms;
-    const float* Nr = ws.A + cb * ws.ms + 2 * CT * CT;      // the record's N
-    float* N = ws.N + cb * CT * CT;
-    const int64_t row1 = r0 + 16 + ln;
-    const float b1 = row1 < T ? a.beta[(b * T + row1) * H + h] : 0.f;
-    f4 xt, n00, n11t;
+// N = (I + Diag(beta) L)^-1 of the chunks n = n0, n0 + step, ... of head bh,
+// completed in its records: the forward's solve left the diagonal blocks
+// N00, N11 there (and zeroed N01); N10 = -N11 X10 N00 with X10 = Diag(beta_1)
+// L10 on the fp32 matrix cores, written to the record's N10 block.  One wave,
+// four chunks in flight (their operands fetched together).
+__device__ __forceinline__ void complete_n(const kda_bwd_args& a, const BwdWs& ws, int64_t bh, int nck, int n0,
+                                           int step, int ln, int lg) {
+    const int64_t H = a.H, T = a.T, b = bh / H, h = bh % H;
+    constexpr int NF = 4;
+    for (int nb = n0; nb < nck; nb += NF * step) {
+        f4 xt[NF], n00[NF], n11t[NF];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        xt[u] = b1 * L[(16 + ln) * CT + 4 * lg + u];          // X10[ln][4 lg + u]
-        n00[u] = Nr[(4 * lg + u) * CT + ln];                  // N00[4 lg + u][ln]
-        n11t[u] = Nr[(16 + ln) * CT + 16 + 4 * lg + u];       // N11[ln][4 lg + u]
+        for (int f = 0; f < NF; ++f) {
+            const int n = nb + f * step;
+            const bool on = n < nck;
+            const int64_t cb = bh * nck + (on ? n : 0);
+            const float* L = ws.L + cb * ws.ms;
+            const float* N = ws.N + cb * ws.ms;
+            const int64_t row1 = static_cast<int64_t>(n) * CT + 16 + ln;
+            const float b1 = on && row1 < T ? a.beta[(b * T + row1) * H + h] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                xt[f][u] = b1 * L[(16 + ln) * CT + 4 * lg + u];       // X10[ln][4 lg + u]
+                n00[f][u] = N[(4 * lg + u) * CT + ln];                // N00[4 lg + u][ln]
+                n11t[f][u] = N[(16 + ln) * CT + 16 + 4 * lg + u];     // N11[ln][4 lg + u]
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const int n = nb + f * step;
+            const f4 y = mm_acc(xt[f], n00[f], f4{0.f, 0.f, 0.f, 0.f});      // X10 N00
+            const f4 n10 = mm_acc(n11t[f], y, f4{0.f, 0.f, 0.f, 0.f});       // N11 X10 N00
+            if (n < nck) {
+                float* N = ws.N + (bh * nck + n) * ws.ms;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) N[(16 + 4 * lg + j) * CT + ln] = -n10[j];
+            }
+        }
     }
-    const f4 y = mm_acc(xt, n00, f4{0.f, 0.f, 0.f, 0.f});    // X10 N00
-    const f4 n10 = mm_acc(n11t, y, f4{0.f, 0.f, 0.f, 0.f});  // N11 X10 N00
-#pragma unroll
-    for (int m = 0; m < CT * CT / 64; ++m) {
-        const int e = lane + 64 * m, r = e / CT, c = e % CT;
-        if (r < 16 || c >= 16) N[e] = r < 16 && c >= 16 ? 0.f : Nr[e];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) N[(16 + 4 * lg + j) * CT + ln] = -n10[j];
 }
 
 // ------------------------------------------------------------------ kernel 2
@@ -354,6 +362,11 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, ln = lane & 15, lg = lane >> 4;
     const int x = t % K, rg = t / K;
 
+    // N of every chunk of this head completed in its records (both V-tile
+    // workgroups of the head write the same values), before the chain reads it
+    complete_n(a, ws, bh, nck, w, NWS, ln, lg);
+    __syncthreads();
+
     // dS at the end of the sequence into the accumulators and its pair copy
     f4 accs[TPW];
 #pragma unroll
@@ -417,7 +430,7 @@ __global__ __launch_bounds__(NS) void bwd_state_kernel(const kda_bwd_args a, con
         }
         const int64_t cn = bh * nck + r0 / CT;
         const auto ra = make_rsrc(ws.A + cn * ws.ms, n < 0 ? 0u : static_cast<uint32_t>(CT * CT * 4));
-        const auto rn = make_rsrc(ws.N + cn * CT * CT, n < 0 ? 0u : static_cast<uint32_t>(CT * CT * 4));
+        const auto rn = make_rsrc(ws.N + cn * ws.ms, n < 0 ? 0u : static_cast<uint32_t>(CT * CT * 4));
 #pragma unroll
         for (int j = 0; j < APT; ++j) {
             const int off = ((ac0 + j) * CT + ai) * 4;
@@ -775,7 +788,7 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
     for (int m = 0; m < CT * CT / NTC; ++m) {
         const int e = t + NTC * m;
         sm.L[e / CT][e % CT] = ws.L[cb * ws.ms + e];
-        sm.N[e / CT][e % CT] = ws.N[cb * CT * CT + e];
+        sm.N[e / CT][e % CT] = ws.N[cb * ws.ms + e];
     }
     if (t < CT) sm.beta[t] = t < nrow ? a.beta[(b * T + r0 + t) * H + h] : 0.f;
 
@@ -1319,11 +1332,6 @@ int launch_bwd(const kda_bwd_args& a, hipStream_t stream) {
     const int64_t BH = a.B * a.H;
     const int64_t nck = (a.T + CT - 1) / CT;
     const BwdWs ws = ws_layout(a.workspace, a.ckpt, BH, nck, a.K, a.V);
-    if (nck > 0) {
-        hipLaunchKernelGGL(bwd_n_kernel, dim3(static_cast<unsigned>((BH * nck + 3) / 4)), dim3(256), 0, stream, a, ws,
-                           BH * nck);
-        if (hipGetLastError() != hipSuccess) return KDA_ERR_LAUNCH;
-    }
     // 64 state columns a workgroup, or 32 when that leaves compute units idle
     // and the 32-column workgroups still fit one round (the chain is
     // sequential: more, narrower workgroups shorten it, a second round
@@ -1363,7 +1371,7 @@ bool chunkwise_bwd_supported(int64_t K, int64_t V) {
 
 int64_t chunkwise_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
     const int64_t nck = (T + CT - 1) / CT;
-    return B * H * nck * (CT * CT + K * V + 2 * CT * V) * static_cast<int64_t>(sizeof(float));
+    return B * H * nck * (K * V + 2 * CT * V) * static_cast<int64_t>(sizeof(float));
 }
 
 // Static scratch of kda_chunkwise_bwd_noalloc: the workspace of the

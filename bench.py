@@ -409,22 +409,22 @@ def backward_bench(pkg, wl, torch, reps=3, untimed=2):
 
 
 def backward_bytes(B, T, H, K, V, sz, half_state=True):
-    """Algorithmic HBM bytes of kda_chunkwise_bwd's three kernels (activations of
+    """Algorithmic HBM bytes of kda_chunkwise_bwd's two kernels (activations of
     sz bytes; workspace and checkpoints fp32, except the records' state and R
     and the workspace's dS_end, dP and dR, fp16 with fp16 activations
-    (half_state); 32-token chunks): the N
-    kernel reads L_10 and N's two diagonal blocks from the checkpoint record and
-    block 1's beta, and writes N; the state kernel reads q, k, g, dO, A, N, beta
-    and writes dS_end, dP, dR; the chunk kernel reads the checkpoint (S, R),
-    dS_end, dP, dR, dO, q, k, g, L, N, beta (P = N Diag(beta) R is formed in the
-    kernel) and writes dq, dk, dv, dg, dbeta."""
+    (half_state); 32-token chunks): the state kernel completes N in the
+    records (reads L_10 and N's two diagonal blocks and block 1's beta, writes
+    N_10), reads q, k, g, dO, A, N, beta and writes dS_end, dP, dR; the chunk
+    kernel reads the checkpoint (S, R), dS_end, dP, dR, dO, q, k, g, L, N, beta
+    (P = N Diag(beta) R is formed in the kernel) and writes dq, dk, dv, dg,
+    dbeta."""
     nck = -(-T // 32)
     qk, g, v, beta = B * T * H * K * sz, B * T * H * K * 4, B * T * H * V * sz, B * T * H * 4
     mat = B * H * nck * 32 * 32 * 4
     S = B * H * nck * K * V * (2 if half_state else 4)
     # per 32 x V matrix (R, dP, dR): fp16 with fp16 activations
     RPh = B * H * nck * 32 * V * (2 if half_state else 4)
-    nk = 3 * mat // 4 + beta // 2 + mat
+    nk = 3 * mat // 4 + beta // 2 + mat // 4
     state = 2 * qk + g + v + 2 * mat + beta + S + 2 * RPh
     chunk = 2 * S + 3 * RPh + v + 2 * qk + g + 2 * mat + beta + 2 * qk + v + g + beta
     return nk + state + chunk

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 13
+#define KDA_ABI_VERSION 14
 
 /* Element types accepted at the boundary. */
 typedef enum kda_dtype {
@@ -197,8 +197,9 @@ int kda_chunkwise_long_fwd(const kda_fwd_args* args, int64_t segments, void* wor
 /* kda_chunkwise_fwd, plus per 32-token chunk a record, in fp32: the state
  * before the chunk and the chunk's R = V - (k * E) S, then its A (scale times
  * the decayed q k^T, i <= c), L (the decayed k k^T, i < c) and N = (I +
- * Diag(beta) L)^-1 with its block below the diagonal zero (the solve uses only
- * the 16-row diagonal blocks): ckpt is [B, H, ceil(T/32), KDA_CKPT_RECORD(K,
+ * Diag(beta) L)^-1, of which the forward's solve writes the 16-row diagonal
+ * blocks and zeroes the block above them; kda_chunkwise_bwd completes the
+ * block below them in place: ckpt is [B, H, ceil(T/32), KDA_CKPT_RECORD(K,
  * V)] contiguous, each record (K + 32) x V (rows [0, K) the state, [K, K + 32)
  * R) followed by three row-major 32 x 32 matrices (the input of
  * kda_chunkwise_bwd, which forms the solve's result P = N Diag(beta) R
@@ -230,7 +231,9 @@ typedef struct kda_bwd_args {
     const void* v;                 /* not read: R comes from the checkpoint     */
     const float* g;
     const float* beta;
-    const float* ckpt;             /* from kda_chunkwise_fwd_ckpt on the same inputs */
+    float* ckpt;                   /* from kda_chunkwise_fwd_ckpt on the same inputs;
+                                      the backward completes each record's N in place
+                                      (idempotent: a second call writes the same) */
     const void* d_o;               /* dL/do                                      */
     const float* d_state_out;      /* dL/d(final state), or NULL for zeros       */
     void* dq;                      /* [B, T, H, K] */
@@ -245,7 +248,7 @@ typedef struct kda_bwd_args {
 } kda_bwd_args;
 
 /* Bytes of workspace kda_chunkwise_bwd needs: per (b, h) and 32-token chunk,
- * (32 * 32 + K * V + 2 * 32 * V) floats (with fp16 q, k, v the K x V part,
+ * (K * V + 2 * 32 * V) floats (with fp16 q, k, v the K x V part,
  * the gradient of the state at the chunk's end, and the two 32 x V parts are
  * kept in fp16 and use half of theirs).  0 for a bad or empty shape. */
 size_t kda_chunkwise_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
@@ -260,7 +263,7 @@ int kda_chunkwise_bwd(const kda_bwd_args* args, void* stream);
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory -- code under hipGraph capture, tight serving or training
  * loops, harnesses that forbid hipMalloc.  args->workspace is ignored; the
- * three kernels use instead a static device buffer of KDA_BWD_SCRATCH_BYTES
+ * two kernels use instead a static device buffer of KDA_BWD_SCRATCH_BYTES
  * that the library holds on every GPU it runs on until the process ends
  * (resolved once per device, on the first call with that device current;
  * `stream` must belong to the current device).  That first call resolves a

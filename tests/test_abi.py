@@ -75,10 +75,11 @@ def test_struct_layout_matches_header(native, tmp_path, struct, cname):
 
 
 def test_backward_workspace_size(native):
-    """(32 * 32 + K * V + 2 * 32 * V) floats per (b, h) and 32-token chunk; 0 for bad shapes."""
+    """(K * V + 2 * 32 * V) floats per (b, h) and 32-token chunk (N is completed in
+    the checkpoint records, not the workspace); 0 for bad shapes."""
     size = native.load().kda_chunkwise_bwd_workspace_size
-    assert size(8, 4096, 16, 128, 128) == 8 * 16 * 128 * (1024 + 128 * 128 + 64 * 128) * 4
-    assert size(2, 80, 3, 64, 32) == 2 * 3 * 3 * (1024 + 64 * 32 + 64 * 32) * 4    # ragged: 3 chunks
+    assert size(8, 4096, 16, 128, 128) == 8 * 16 * 128 * (128 * 128 + 64 * 128) * 4
+    assert size(2, 80, 3, 64, 32) == 2 * 3 * 3 * (64 * 32 + 64 * 32) * 4    # ragged: 3 chunks
     assert size(1, 0, 1, 64, 64) == 0
     assert size(-1, 16, 1, 64, 64) == 0 and size(1, 16, 1, 0, 64) == 0
 
