@@ -310,3 +310,37 @@ def test_fp16_record_holds_the_state_in_fp16_tiles(kda_pkg, wl):
     off = ((r // 16) * (V // 16) + c // 16) * 256 + (r % 4) * 64 + ((r // 4) % 4) * 16 + c % 16
     s0 = halves[:, :, 0][..., off]                                             # [B, H, K, V]
     assert torch.equal(s0, inp["state"].half())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_backward_completes_n_in_the_records(kda_pkg, wl, dtype):
+    """The forward's records hold N's diagonal blocks (and zeros above them);
+    kda_chunkwise_bwd completes the block below them in place.  After a
+    backward every record's N is (I + Diag(beta) L)^-1 of that record's L,
+    with beta = 0 past T (a ragged last chunk here), and a second backward
+    over the same record returns the same gradients."""
+    import importlib
+    kda = importlib.import_module("kimi_linear_amd.kda")
+    B, T, H, K, V = 2, 100, 3, 64, 64
+    inp = wl.make_inputs(B, T, H, K, V, seed=71, qkv_dtype=dtype, state_std=0.1)
+    d = {n: (x.to(DEV) if x is not None else None) for n, x in inp.items()}
+    with torch.no_grad():
+        _, _, ck = kda._forward("chunkwise", d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"], 4,
+                                torch.float32, ckpt=True)
+        d_o = torch.randn(B, T, H, V, generator=torch.Generator().manual_seed(72)).to(dtype).to(DEV)
+        g1 = kda._chunkwise_backward(d["q"], d["k"], d["v"], d["g"], d["beta"], ck, d_o, None, True)
+        g2 = kda._chunkwise_backward(d["q"], d["k"], d["v"], d["g"], d["beta"], ck, d_o, None, True)
+    torch.cuda.synchronize()
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+    nck = -(-T // 32)
+    mats = ck[..., (K + 32) * V:].reshape(B, H, nck, 3, 32, 32).double().cpu()
+    L, N = mats[:, :, :, 1].tril(-1), mats[:, :, :, 2]
+    beta = torch.zeros(B, H, nck * 32, dtype=torch.float64)
+    beta[:, :, :T] = inp["beta"].double().permute(0, 2, 1)
+    beta = beta.view(B, H, nck, 32)
+    eye = torch.eye(32, dtype=torch.float64)
+    resid = (N @ (eye + beta[..., :, None] * L) - eye).abs().max().item()
+    print(f"record N {dtype}: max |N (I + Diag(beta) L) - I| {resid:.2e}", flush=True)
+    assert resid < 1e-4, resid
