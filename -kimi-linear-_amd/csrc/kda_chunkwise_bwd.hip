@@ -784,14 +784,6 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
                 rg[p][j] = __builtin_amdgcn_raw_buffer_load_b32(dg, static_cast<int>(4 * vo), static_cast<int>(4 * so), 0);
             }
     };
-#pragma unroll
-    for (int m = 0; m < CT * CT / NTC; ++m) {
-        const int e = t + NTC * m;
-        sm.L[e / CT][e % CT] = ws.L[cb * ws.ms + e];
-        sm.N[e / CT][e % CT] = ws.N[cb * ws.ms + e];
-    }
-    if (t < CT) sm.beta[t] = t < nrow ? a.beta[(b * T + r0 + t) * H + h] : 0.f;
-
     // column-step fetch: the lane's fragments of S (the checkpointed state
     // before the chunk) and dS (the gradient of the state after it), row x,
     // columns v0 + 8 lg .. + 7; the thread's EPT elements of R (checkpoint),
@@ -857,6 +849,15 @@ __global__ __launch_bounds__(4 * K) __attribute__((amdgpu_waves_per_eu(4))) void
         }
     };
     fetch(0);
+    // L, N and beta to LDS (read after the column steps), fetched after the
+    // first step's tiles so that both fetches are in flight together
+#pragma unroll
+    for (int m = 0; m < CT * CT / NTC; ++m) {
+        const int e = t + NTC * m;
+        sm.L[e / CT][e % CT] = ws.L[cb * ws.ms + e];
+        sm.N[e / CT][e % CT] = ws.N[cb * ws.ms + e];
+    }
+    if (t < CT) sm.beta[t] = t < nrow ? a.beta[(b * T + r0 + t) * H + h] : 0.f;
 
     // ------------------------------------- sums over the state columns
     // X += dO R^T, dM += dP R^T (MPW tiles a wave), and per element tile p:
