@@ -183,11 +183,11 @@ __device__ __forceinline__ float raw_f32(uint32_t w) {
 // completed in its records: the forward's solve left the diagonal blocks
 // N00, N11 there (and zeroed N01); N10 = -N11 X10 N00 with X10 = Diag(beta_1)
 // L10 on the fp32 matrix cores, written to the record's N10 block.  One wave,
-// four chunks in flight (their operands fetched together).
+// eight chunks in flight (their operands fetched together).
 __device__ __forceinline__ void complete_n(const kda_bwd_args& a, const BwdWs& ws, int64_t bh, int nck, int n0,
                                            int step, int ln, int lg) {
     const int64_t H = a.H, T = a.T, b = bh / H, h = bh % H;
-    constexpr int NF = 4;
+    constexpr int NF = 8;
     for (int nb = n0; nb < nck; nb += NF * step) {
         f4 xt[NF], n00[NF], n11t[NF];
 #pragma unroll
